@@ -1,0 +1,202 @@
+"""Benchmark: batched decode attention of the Needle KV-cache path on one
+MI355X (the headline workload: 4096 independent sequences, 8 heads x 64,
+fp16 K/V, ragged lengths uniform in [213, 1024], one new token per sequence
+through 8 layers).
+
+A step = for each of 8 layers: KV append of the new token (nda_kv_append) and
+single-token attention (nda_decode), then pos += 1 (nda_advance); inputs are
+resident in HBM before the timed region. Prints one JSON line.
+
+    python bench.py [--steps K] [--warmup W] [--no-cpu]
+"""
+import argparse
+import json
+import os
+import sys
+import time
+
+import numpy as np
+
+REPO = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, os.path.join(REPO, "esp32-needle-3_amd"))
+sys.path.insert(0, os.path.join(REPO, "oracle"))
+
+HBM_PEAK_GBS = 8000.0
+B, H, D, LAYERS = 4096, 8, 64, 8
+LMIN, LMAX = 213, 1024
+SEED = 20261201
+
+
+def log(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+def cpu_baseline(lens_all, seconds, nthreads):
+    """The oracle's fp16 decode (the engine's attn_heads restated, fp16 KV)
+    on a bounded sample of the same workload, threaded over sequences as the
+    engine's nd_parallel_rows seam splits rows. Returns decode tokens/s."""
+    import ndoracle as O
+
+    rng = np.random.default_rng(SEED + 1)
+    S = 128
+    lens = np.ascontiguousarray(rng.choice(lens_all, S), np.uint32)
+    koff = np.zeros(S, np.uint64)
+    koff[1:] = np.cumsum(lens[:-1].astype(np.uint64) * H * D)
+    tot = int(lens.sum()) * H * D
+    kbase = rng.standard_normal(tot, dtype=np.float32).astype(np.float16).view(np.uint16)
+    vbase = rng.standard_normal(tot, dtype=np.float32).astype(np.float16).view(np.uint16)
+    q = rng.standard_normal(S * H * D, dtype=np.float32)
+    kn = rng.standard_normal(S * H * D, dtype=np.float32)
+    vn = rng.standard_normal(S * H * D, dtype=np.float32)
+    out = np.zeros(S * H * D, np.float32)
+    # one call = one decode token for S sequences on one layer
+    O.decode_batch_f16(H, H, D, D, lens, kbase, vbase, koff, koff, q, kn, vn, None, out, nthreads)
+    calls, t0 = 0, time.perf_counter()
+    while True:
+        O.decode_batch_f16(H, H, D, D, lens, kbase, vbase, koff, koff, q, kn, vn, None, out, nthreads)
+        calls += 1
+        el = time.perf_counter() - t0
+        if el >= seconds and calls >= 2:
+            break
+    # tokens per second through all LAYERS layers
+    tok_s = calls * S / el / LAYERS
+    return tok_s, "%d sequences (L mean %.0f) x %d layer-calls, %.1f s" % (S, lens.mean(), calls, el)
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--cpu-seconds", type=float, default=12.0)
+    ap.add_argument("--split-chunk", type=int, default=0)
+    ap.add_argument("--page-size", type=int, default=16)
+    args = ap.parse_args()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
+        print("bench.py measures one GPU: this build has no multi-GPU path "
+              "(decode shards by sequence with no exchange; see DESIGN.md)", file=sys.stderr)
+        sys.exit(2)
+
+    import ndattn as N
+
+    name, cus = N.device_info()
+    log("device:", name, "CUs:", cus)
+    rng = np.random.default_rng(SEED)
+    lens = rng.integers(LMIN, LMAX + 1, B)          # positions attended at the first step
+    total_steps = args.warmup + args.steps
+    window = LMAX + total_steps + 16
+    P = args.page_size
+    need_pages = int(sum((int(L) + total_steps + P - 1) // P for L in lens)) + 64
+    ctx = N.Context(LAYERS, H, H, D, D, window, kv_dtype=N.KV_F16, max_seqs=B, page_size=P,
+                    max_pages=need_pages, split_chunk=args.split_chunk)
+    log("pool GiB: %.1f" % (ctx.device_bytes / 2 ** 30))
+    stream = N.vp()
+    N._check(N.lib().nda_stream_create(N.C.byref(stream)))
+    for b in range(B):
+        ctx.seq_set_pos(b, int(lens[b]) - 1)
+        ctx.seq_reserve(b, total_steps + 1)
+    ctx.kv_fill_normal(B, seed=SEED, stream=stream)
+    # per-layer q, new k/v, out: resident in HBM
+    q = [N.DevBuf(B * H * D * 4) for _ in range(LAYERS)]
+    kn = [N.DevBuf(B * H * D * 4) for _ in range(LAYERS)]
+    vn = [N.DevBuf(B * H * D * 4) for _ in range(LAYERS)]
+    out = [N.DevBuf(B * H * D * 4) for _ in range(LAYERS)]
+    for li in range(LAYERS):
+        q[li].fill_normal(B * H * D, 0, SEED + 10 * li + 1, stream=stream)
+        kn[li].fill_normal(B * H * D, 0, SEED + 10 * li + 2, stream=stream)
+        vn[li].fill_normal(B * H * D, 0, SEED + 10 * li + 3, stream=stream)
+    ctx.sync(stream)
+
+    def step():
+        for li in range(LAYERS):
+            ctx.kv_append(li, B, kn[li], vn[li], stream=stream)
+            ctx.decode(li, B, q[li], out[li], stream=stream)
+        ctx.advance(B, None, 1, stream=stream)
+
+    for _ in range(args.warmup):
+        step()
+    ctx.sync(stream)
+    N.device_sync()
+    # algorithmic bytes of the timed steps: lengths grow by one per step
+    base = lens + args.warmup
+    attended = sum(int(base.sum()) + s * B for s in range(args.steps))   # positions read, per layer
+    row = H * 2 * D * 2                                   # K + V bytes per position, all heads
+    qo = B * H * D * 4 * 2                                # q read + out write per layer launch
+    dec_bytes = attended * row + args.steps * qo          # per layer, all timed steps
+    app_bytes = B * (2 * H * D * 4 + 2 * H * D * 2)       # read k,v fp32 + write fp16, per launch
+
+    ctx.prof_enable(True)
+    ctx.prof_read(reset=True)
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        step()
+    ctx.sync(stream)
+    N.device_sync()
+    el = time.perf_counter() - t0
+    ms, launches = ctx.prof_read(reset=True)
+    ctx.prof_enable(False)
+
+    ms_per_step = el * 1e3 / args.steps
+    tok_s = B * args.steps / el
+    dec_ms = ms[N.K_DECODE] / max(1, launches[N.K_DECODE])
+    app_ms = ms[N.K_APPEND] / max(1, launches[N.K_APPEND])
+    dec_bytes_per_launch = dec_bytes / args.steps
+    achieved = dec_bytes_per_launch / (dec_ms * 1e-3) / 1e9
+    step_bytes = LAYERS * (dec_bytes_per_launch + app_bytes)
+    log("step %.3f ms | decode kernel %.3f ms (%d launches) %.0f GB/s | append %.4f ms | combine %d" %
+        (ms_per_step, dec_ms, launches[N.K_DECODE], achieved, app_ms, launches[N.K_COMBINE]))
+
+    # sampled parity of the last step against the oracle (not timed)
+    import ndoracle as O
+    worst = 0.0
+    qh = q[LAYERS - 1].to_array(np.float32, (B, H * D))
+    oh = out[LAYERS - 1].to_array(np.float32, (B, H * D))
+    for b in rng.choice(B, 8, replace=False):
+        pos = ctx.seq_state(int(b))[0] - 1            # the last decode attended [0, pos]
+        k, v, _, _ = ctx.kv_read(LAYERS - 1, int(b), 0, pos + 1)
+        kv = O.kv_view(k, v, None, None, H, pos + 1, 0, pos, O.KV_F16)
+        want = O.attend_view(kv, qh[b], None)
+        worst = max(worst, float(np.abs(want - oh[b]).max()))
+    log("sampled max |delta| vs oracle: %.3g" % worst)
+
+    cpu = None
+    if not args.no_cpu:
+        ncores = min(16, os.cpu_count() or 1)
+        c_tok, sample = cpu_baseline(lens, args.cpu_seconds, ncores)
+        cpu = {"value": round(c_tok, 1), "unit": "tokens/s", "cores": ncores, "kind": "port",
+               "sample": sample + ", fp16 KV, no gate, oracle attn_heads restatement"}
+        log("cpu baseline: %.1f tok/s on %d threads" % (c_tok, ncores))
+
+    res = {
+        "metric": "decode attn tokens/s + HBM GB/s (% peak) at B=4096; prefill TFLOP/s",
+        "value": round(tok_s, 1),
+        "unit": "tokens/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_per_step, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f16",
+        "data": "synthetic: K/V N(0,1) from a counter-based generator on device, q/k_new/v_new N(0,1)",
+        "config": {"workload": "batched decode: 4096 sequences, 8 heads x 64, fp16 K/V, "
+                               "L ~ U[213,1024], 1 token x 8 layers (append + attend)",
+                   "global_batch": B, "layers": LAYERS, "heads": H, "head_dim": D,
+                   "kv_len": [LMIN, LMAX], "page_size": P, "seed": SEED,
+                   "step_GB": round(step_bytes / 1e9, 3),
+                   "step_GBps": round(step_bytes / (ms_per_step * 1e-3) / 1e9, 1)},
+        "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
+                     "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
+                     "kernel": "attend_kernel<f16,64,64,rep1>", "kernel_ms": round(dec_ms, 4),
+                     "bytes_per_launch": int(dec_bytes_per_launch)},
+        "cpu_baseline": cpu,
+        "max_abs_delta_sampled": worst,
+        "device": name,
+    }
+    print(json.dumps(res), flush=True)
+
+
+if __name__ == "__main__":
+    main()

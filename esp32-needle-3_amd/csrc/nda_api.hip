@@ -1,0 +1,1204 @@
+// nda_api.hip - the C ABI of libndattn (include/nda.h): context, paged KV
+// pool, per-sequence session state, shared prefix segments and launches.
+//
+// The host keeps the authoritative copy of every sequence's state (pos,
+// n_sink, attached prefix) and of the page tables, the way the engine keeps
+// them in nd_model (engine/include/nd_model.h:132-148); the device copies are
+// refreshed on the caller's stream right before the launch that reads them.
+#include "nda.h"
+#include "nda_internal.h"
+
+#include <algorithm>
+#include <cmath>
+#include <cstdarg>
+#include <cstdio>
+#include <cstring>
+#include <new>
+#include <string>
+#include <vector>
+
+using namespace nda;
+
+namespace {
+
+constexpr uint32_t MIN_RECENT = 64;   // ND_MIN_RECENT, engine/src/nd_model.c:1311-1312
+
+struct Prefix {
+    bool used = false;
+    uint32_t len = 0;       // positions stored: [0, len)
+    uint32_t n_sink = 0;    // pinned count (clamped len)
+    uint32_t refs = 0;      // sequences attached
+};
+
+struct SeqHost {
+    uint32_t pos = 0, n_sink = 0;
+    int32_t prefix = -1;
+    bool has_snap = false;
+    uint32_t snap_pos = 0;
+};
+
+struct ProfRec {
+    int kind;
+    hipEvent_t a, b;
+};
+
+} // namespace
+
+struct nda_ctx {
+    nda_config cfg{};
+    Geo geo{};
+    PageGeom pg{};
+    uint64_t max_pages = 0;
+    uint32_t chunk = 0;
+
+    uint8_t *pool = nullptr;            // n_layers * layer_bytes
+    int32_t *d_pages = nullptr;         // [max_seqs][pps]
+    int32_t *d_prefix_pages = nullptr;  // [max_prefixes][pps]
+    SeqDev *d_seqs = nullptr;
+    uint32_t *d_rows = nullptr;         // row_seq | row_t staging
+    size_t rows_cap = 0;
+    float *d_part = nullptr;
+    size_t part_cap = 0;                // floats
+    uint8_t *d_stage = nullptr;
+    size_t stage_cap = 0;
+    uint64_t dev_bytes = 0;
+
+    std::vector<int32_t> pages, prefix_pages;
+    std::vector<SeqHost> seqs;
+    std::vector<Prefix> prefixes;
+    std::vector<int32_t> free_pages;
+    bool seqs_dirty = true;
+    uint32_t dirty_lo = UINT32_MAX, dirty_hi = 0;   // page-table rows to upload
+    bool prefix_dirty = true;
+
+    bool prof = false;
+    std::vector<ProfRec> prof_pending;
+    std::vector<hipEvent_t> ev_free;
+    double prof_ms[NDA_K_COUNT] = {};
+    uint64_t prof_n[NDA_K_COUNT] = {};
+
+    std::string err;
+};
+
+namespace {
+
+int fail(nda_ctx *c, int code, const char *fmt, ...)
+{
+    if (c) {
+        char buf[512];
+        va_list ap;
+        va_start(ap, fmt);
+        vsnprintf(buf, sizeof buf, fmt, ap);
+        va_end(ap);
+        c->err = buf;
+    }
+    return code;
+}
+
+int hip_fail(nda_ctx *c, hipError_t e, const char *what)
+{
+    return fail(c, e == hipErrorOutOfMemory ? NDA_ERR_NOMEM : NDA_ERR_HIP, "%s: %s", what,
+                hipGetErrorString(e));
+}
+
+#define HIPC(c, call)                                      \
+    do {                                                   \
+        hipError_t e_ = (call);                            \
+        if (e_ != hipSuccess)                              \
+            return hip_fail((c), e_, #call);               \
+    } while (0)
+
+inline uint32_t clamp_sink(uint32_t window, uint32_t n)
+{
+    uint32_t cap = window > MIN_RECENT ? window - MIN_RECENT : 0;
+    return n < cap ? n : cap;
+}
+
+// Same mapping as the kernels' own_slot (kv_slot, nd_model.c:1302-1309).
+inline uint32_t own_slot(const SeqHost &s, uint32_t p, uint32_t window)
+{
+    if (s.prefix >= 0)
+        return (p - s.n_sink) % (window - s.n_sink);
+    if (p < s.n_sink)
+        return p;
+    return s.n_sink + (p - s.n_sink) % (window - s.n_sink);
+}
+
+struct Vis {
+    uint32_t n_sh, n_own;
+};
+
+inline Vis visible(const SeqHost &s, uint32_t p, uint32_t window)
+{
+    uint32_t sinks = std::min(s.n_sink, p + 1);
+    uint32_t rcap = window - s.n_sink;
+    uint32_t rcount = (p + 1 <= s.n_sink) ? 0 : std::min(p + 1 - s.n_sink, rcap);
+    Vis v;
+    v.n_sh = s.prefix >= 0 ? sinks : 0;
+    v.n_own = s.prefix >= 0 ? rcount : sinks + rcount;
+    return v;
+}
+
+inline void mark_rows(nda_ctx *c, uint32_t seq)
+{
+    c->dirty_lo = std::min(c->dirty_lo, seq);
+    c->dirty_hi = std::max(c->dirty_hi, seq + 1);
+}
+
+void release_pages(nda_ctx *c, uint32_t seq)
+{
+    int32_t *row = &c->pages[(size_t)seq * c->pg.pages_per_seq];
+    for (uint32_t i = 0; i < c->pg.pages_per_seq; i++) {
+        if (row[i] >= 0) {
+            c->free_pages.push_back(row[i]);
+            row[i] = -1;
+        }
+    }
+    mark_rows(c, seq);
+}
+
+// Back own slots [s0, s1) of a sequence with pages. All-or-nothing.
+int back_slots(nda_ctx *c, uint32_t seq, uint32_t s0, uint32_t s1)
+{
+    if (s1 <= s0)
+        return NDA_OK;
+    int32_t *row = &c->pages[(size_t)seq * c->pg.pages_per_seq];
+    uint32_t p0 = s0 >> c->pg.log2_page, p1 = (s1 - 1) >> c->pg.log2_page;
+    size_t need = 0;
+    for (uint32_t i = p0; i <= p1; i++)
+        need += row[i] < 0;
+    if (need > c->free_pages.size())
+        return fail(c, NDA_ERR_NOMEM, "page pool exhausted: need %zu pages, %zu free", need,
+                    c->free_pages.size());
+    for (uint32_t i = p0; i <= p1; i++) {
+        if (row[i] < 0) {
+            row[i] = c->free_pages.back();
+            c->free_pages.pop_back();
+            mark_rows(c, seq);
+        }
+    }
+    return NDA_OK;
+}
+
+// Back the own slot(s) of positions [p0, p0 + n) (no wrap inside, n >= 1).
+int back_positions(nda_ctx *c, uint32_t seq, uint32_t p0, uint32_t n)
+{
+    const SeqHost &s = c->seqs[seq];
+    const uint32_t W = c->pg.window;
+    // Positions map to consecutive slots until the ring wraps; walk in runs.
+    uint32_t p = p0, end = p0 + n;
+    while (p < end) {
+        uint32_t sl = own_slot(s, p, W);
+        uint32_t run;
+        if (s.prefix < 0 && p < s.n_sink)
+            run = std::min(end, s.n_sink) - p;
+        else {
+            uint32_t ring_end = (s.prefix >= 0 ? 0u : s.n_sink) + (W - s.n_sink);
+            run = std::min(end - p, ring_end - sl);
+        }
+        int rc = back_slots(c, seq, sl, sl + run);
+        if (rc)
+            return rc;
+        p += run;
+    }
+    return NDA_OK;
+}
+
+int sync_tables(nda_ctx *c, hipStream_t st)
+{
+    if (c->seqs_dirty) {
+        std::vector<SeqDev> tmp(c->seqs.size());
+        for (size_t i = 0; i < tmp.size(); i++) {
+            tmp[i].pos = (int32_t)c->seqs[i].pos;
+            tmp[i].n_sink = (int32_t)c->seqs[i].n_sink;
+            tmp[i].prefix = c->seqs[i].prefix;
+            tmp[i].pad = 0;
+        }
+        HIPC(c, hipMemcpyAsync(c->d_seqs, tmp.data(), tmp.size() * sizeof(SeqDev), hipMemcpyHostToDevice, st));
+        c->seqs_dirty = false;
+    }
+    if (c->dirty_lo < c->dirty_hi) {
+        size_t off = (size_t)c->dirty_lo * c->pg.pages_per_seq;
+        size_t n = (size_t)(c->dirty_hi - c->dirty_lo) * c->pg.pages_per_seq;
+        HIPC(c, hipMemcpyAsync(c->d_pages + off, c->pages.data() + off, n * sizeof(int32_t),
+                               hipMemcpyHostToDevice, st));
+        c->dirty_lo = UINT32_MAX;
+        c->dirty_hi = 0;
+    }
+    if (c->prefix_dirty) {
+        HIPC(c, hipMemcpyAsync(c->d_prefix_pages, c->prefix_pages.data(),
+                               c->prefix_pages.size() * sizeof(int32_t), hipMemcpyHostToDevice, st));
+        c->prefix_dirty = false;
+    }
+    return NDA_OK;
+}
+
+int ensure_rows(nda_ctx *c, size_t rows)
+{
+    if (rows * 2 <= c->rows_cap)
+        return NDA_OK;
+    if (c->d_rows) {
+        hipDeviceSynchronize();   // launches still reading the old staging
+        hipFree(c->d_rows);
+        c->dev_bytes -= c->rows_cap * sizeof(uint32_t);
+        c->d_rows = nullptr;
+    }
+    size_t cap = std::max<size_t>(rows * 2, 8192);
+    HIPC(c, hipMalloc(&c->d_rows, cap * sizeof(uint32_t)));
+    c->rows_cap = cap;
+    c->dev_bytes += cap * sizeof(uint32_t);
+    return NDA_OK;
+}
+
+int ensure_part(nda_ctx *c, size_t floats)
+{
+    if (floats <= c->part_cap)
+        return NDA_OK;
+    if (c->d_part) {
+        hipDeviceSynchronize();
+        hipFree(c->d_part);
+        c->dev_bytes -= c->part_cap * sizeof(float);
+        c->d_part = nullptr;
+    }
+    HIPC(c, hipMalloc(&c->d_part, floats * sizeof(float)));
+    c->part_cap = floats;
+    c->dev_bytes += floats * sizeof(float);
+    return NDA_OK;
+}
+
+int ensure_stage(nda_ctx *c, size_t bytes)
+{
+    if (bytes <= c->stage_cap)
+        return NDA_OK;
+    if (c->d_stage) {
+        hipDeviceSynchronize();
+        hipFree(c->d_stage);
+        c->dev_bytes -= c->stage_cap;
+        c->d_stage = nullptr;
+    }
+    HIPC(c, hipMalloc(&c->d_stage, bytes));
+    c->stage_cap = bytes;
+    c->dev_bytes += bytes;
+    return NDA_OK;
+}
+
+hipEvent_t take_event(nda_ctx *c)
+{
+    if (!c->ev_free.empty()) {
+        hipEvent_t e = c->ev_free.back();
+        c->ev_free.pop_back();
+        return e;
+    }
+    hipEvent_t e = nullptr;
+    if (hipEventCreate(&e) != hipSuccess)
+        return nullptr;
+    return e;
+}
+
+struct ProfScope {
+    nda_ctx *c;
+    int kind;
+    hipStream_t st;
+    hipEvent_t a = nullptr, b = nullptr;
+    ProfScope(nda_ctx *c_, int k, hipStream_t s) : c(c_), kind(k), st(s)
+    {
+        if (c->prof) {
+            a = take_event(c);
+            b = take_event(c);
+            if (a && b)
+                hipEventRecord(a, st);
+        }
+    }
+    ~ProfScope()
+    {
+        if (a && b) {
+            hipEventRecord(b, st);
+            c->prof_pending.push_back({kind, a, b});
+        } else {
+            if (a)
+                c->ev_free.push_back(a);
+            if (b)
+                c->ev_free.push_back(b);
+        }
+    }
+};
+
+int check_seq(nda_ctx *c, uint32_t seq)
+{
+    if (seq >= c->cfg.max_seqs)
+        return fail(c, NDA_ERR_ARG, "sequence %u out of range (max_seqs %u)", seq, c->cfg.max_seqs);
+    return NDA_OK;
+}
+
+int check_ids(nda_ctx *c, uint32_t nseq, const uint32_t *ids)
+{
+    if (nseq > c->cfg.max_seqs)
+        return fail(c, NDA_ERR_ARG, "nseq %u > max_seqs %u", nseq, c->cfg.max_seqs);
+    if (ids)
+        for (uint32_t b = 0; b < nseq; b++)
+            if (ids[b] >= c->cfg.max_seqs)
+                return fail(c, NDA_ERR_ARG, "seq_ids[%u] = %u out of range", b, ids[b]);
+    return NDA_OK;
+}
+
+inline uint32_t sid(const uint32_t *ids, uint32_t b) { return ids ? ids[b] : b; }
+
+// Upload seq ids (and optional per-row offsets) for a launch; returns device
+// pointers, null when the identity mapping applies.
+int upload_rows(nda_ctx *c, uint32_t rows, const uint32_t *row_seq, const uint32_t *row_t,
+                hipStream_t st, const uint32_t **d_seq, const uint32_t **d_t)
+{
+    *d_seq = nullptr;
+    *d_t = nullptr;
+    if (!row_seq && !row_t)
+        return NDA_OK;
+    int rc = ensure_rows(c, rows);
+    if (rc)
+        return rc;
+    if (row_seq) {
+        HIPC(c, hipMemcpyAsync(c->d_rows, row_seq, rows * sizeof(uint32_t), hipMemcpyHostToDevice, st));
+        *d_seq = c->d_rows;
+    }
+    if (row_t) {
+        HIPC(c, hipMemcpyAsync(c->d_rows + rows, row_t, rows * sizeof(uint32_t), hipMemcpyHostToDevice, st));
+        *d_t = c->d_rows + rows;
+    }
+    return NDA_OK;
+}
+
+AttnArgs attn_args(nda_ctx *c, uint32_t layer, uint32_t rows, const float *q, const float *gate,
+                   float *out, uint32_t max_total)
+{
+    AttnArgs a{};
+    a.q = q;
+    a.gate = gate;
+    a.out = out;
+    a.pool = c->pool + (uint64_t)layer * c->pg.layer_bytes;
+    a.page_table = c->d_pages;
+    a.prefix_pages = c->d_prefix_pages;
+    a.seqs = c->d_seqs;
+    a.part = c->d_part;
+    a.pg = c->pg;
+    a.rows = rows;
+    a.nh = c->cfg.n_heads;
+    a.chunk = c->chunk;
+    // grid.y and the partial-buffer stride: chunks of the longest row.
+    a.max_chunks = std::max<uint32_t>(1, (max_total + c->chunk - 1) / c->chunk);
+    a.qscale = (float)(1.4426950408889634 / std::sqrt((double)c->cfg.qk_head_dim));
+    return a;
+}
+
+int run_attend(nda_ctx *c, AttnArgs &a, hipStream_t st)
+{
+    if (a.max_chunks > 1) {
+        int rc = ensure_part(c, (size_t)a.rows * a.nh * a.max_chunks * (c->cfg.v_head_dim + 2));
+        if (rc)
+            return rc;
+        a.part = c->d_part;
+    }
+    {
+        ProfScope ps(c, NDA_K_DECODE, st);
+        hipError_t e = launch_attend(c->geo, a, st);
+        if (e != hipSuccess)
+            return hip_fail(c, e, "attend kernel launch");
+    }
+    if (a.max_chunks > 1) {
+        ProfScope ps(c, NDA_K_COMBINE, st);
+        hipError_t e = launch_combine(c->geo, a, st);
+        if (e != hipSuccess)
+            return hip_fail(c, e, "combine kernel launch");
+    }
+    return NDA_OK;
+}
+
+} // namespace
+
+// ===================================================================== ABI
+
+extern "C" {
+
+int nda_create(const nda_config *cfg_in, nda_ctx **out)
+{
+    if (!cfg_in || !out)
+        return NDA_ERR_ARG;
+    *out = nullptr;
+    nda_config cfg = *cfg_in;
+    if (cfg.page_size == 0)
+        cfg.page_size = 16;
+    if (cfg.max_prefixes == 0)
+        cfg.max_prefixes = 16;
+    if (!cfg.n_layers || !cfg.n_heads || !cfg.n_kv_heads || cfg.n_heads % cfg.n_kv_heads ||
+        !cfg.window || !cfg.max_seqs || cfg.kv_dtype > NDA_KV_F16)
+        return NDA_ERR_ARG;
+    if (cfg.page_size != 16 && cfg.page_size != 32 && cfg.page_size != 64)
+        return NDA_ERR_ARG;
+    if (cfg.window > (1u << 30))
+        return NDA_ERR_ARG;
+    Geo geo{(int)(cfg.kv_dtype == NDA_KV_F16), (int)cfg.qk_head_dim, (int)cfg.v_head_dim,
+            (int)(cfg.n_heads / cfg.n_kv_heads)};
+    if (!geometry_supported(geo))
+        return NDA_ERR_UNSUPPORTED;
+
+    int ndev = 0;
+    if (hipGetDeviceCount(&ndev) != hipSuccess || ndev <= 0)
+        return NDA_ERR_NODEV;
+
+    nda_ctx *c = new (std::nothrow) nda_ctx();
+    if (!c)
+        return NDA_ERR_NOMEM;
+    c->cfg = cfg;
+    c->geo = geo;
+    const uint32_t P = cfg.page_size;
+    uint32_t lg = 0;
+    while ((1u << lg) < P)
+        lg++;
+    const uint64_t es = cfg.kv_dtype == NDA_KV_F16 ? 2 : 1;
+    c->pg.log2_page = lg;
+    c->pg.pages_per_seq = (cfg.window + P - 1) / P;
+    c->pg.head_bytes = (uint64_t)P * (cfg.qk_head_dim + cfg.v_head_dim) * es + (es == 1 ? 8ull * P : 0ull);
+    c->pg.page_bytes = c->pg.head_bytes * cfg.n_kv_heads;
+    c->pg.window = cfg.window;
+    c->pg.nkv = cfg.n_kv_heads;
+    c->max_pages = cfg.max_pages ? cfg.max_pages
+                                 : (uint64_t)(cfg.max_seqs + cfg.max_prefixes) * c->pg.pages_per_seq;
+    if (c->max_pages > (uint64_t)INT32_MAX) {
+        delete c;
+        return NDA_ERR_ARG;
+    }
+    c->pg.layer_bytes = c->pg.page_bytes * c->max_pages;
+
+    // Split-KV: a sequence longer than `chunk` visible positions is split into
+    // chunks merged by the combine kernel. Visible positions <= 2 * window
+    // (shared sinks + own slots).
+    c->chunk = cfg.split_chunk ? cfg.split_chunk : 1024;
+    if (c->chunk % 64)
+        c->chunk = (c->chunk + 63) / 64 * 64;
+    if ((2ull * cfg.window + c->chunk - 1) / c->chunk > 65535) {
+        delete c;
+        return NDA_ERR_ARG;
+    }
+
+    const uint64_t pool_bytes = c->pg.layer_bytes * cfg.n_layers;
+    hipError_t e = hipMalloc(&c->pool, pool_bytes);
+    if (e != hipSuccess) {
+        delete c;
+        return e == hipErrorOutOfMemory ? NDA_ERR_NOMEM : NDA_ERR_HIP;
+    }
+    c->dev_bytes = pool_bytes;
+    const size_t pt = (size_t)cfg.max_seqs * c->pg.pages_per_seq;
+    const size_t ppt = (size_t)cfg.max_prefixes * c->pg.pages_per_seq;
+    if (hipMalloc(&c->d_pages, pt * 4) != hipSuccess ||
+        hipMalloc(&c->d_prefix_pages, ppt * 4) != hipSuccess ||
+        hipMalloc(&c->d_seqs, (size_t)cfg.max_seqs * sizeof(SeqDev)) != hipSuccess) {
+        nda_destroy(c);
+        return NDA_ERR_NOMEM;
+    }
+    c->dev_bytes += pt * 4 + ppt * 4 + (size_t)cfg.max_seqs * sizeof(SeqDev);
+    try {
+        c->pages.assign(pt, -1);
+        c->prefix_pages.assign(ppt, -1);
+        c->seqs.assign(cfg.max_seqs, SeqHost());
+        c->prefixes.assign(cfg.max_prefixes, Prefix());
+        c->free_pages.resize(c->max_pages);
+    } catch (...) {
+        nda_destroy(c);
+        return NDA_ERR_NOMEM;
+    }
+    // Hand out low page ids first.
+    for (uint64_t i = 0; i < c->max_pages; i++)
+        c->free_pages[i] = (int32_t)(c->max_pages - 1 - i);
+    c->dirty_lo = 0;
+    c->dirty_hi = cfg.max_seqs;
+    *out = c;
+    return NDA_OK;
+}
+
+void nda_destroy(nda_ctx *c)
+{
+    if (!c)
+        return;
+    hipDeviceSynchronize();
+    for (auto &r : c->prof_pending) {
+        hipEventDestroy(r.a);
+        hipEventDestroy(r.b);
+    }
+    for (auto e : c->ev_free)
+        hipEventDestroy(e);
+    hipFree(c->pool);
+    hipFree(c->d_pages);
+    hipFree(c->d_prefix_pages);
+    hipFree(c->d_seqs);
+    hipFree(c->d_rows);
+    hipFree(c->d_part);
+    hipFree(c->d_stage);
+    delete c;
+}
+
+const char *nda_last_error(const nda_ctx *c) { return c ? c->err.c_str() : "null context"; }
+
+uint64_t nda_device_bytes(const nda_ctx *c) { return c ? c->dev_bytes : 0; }
+
+int nda_seq_reset(nda_ctx *c, uint32_t seq)
+{
+    if (!c)
+        return NDA_ERR_ARG;
+    if (int rc = check_seq(c, seq))
+        return rc;
+    SeqHost &s = c->seqs[seq];
+    if (s.prefix >= 0)
+        c->prefixes[s.prefix].refs--;
+    release_pages(c, seq);
+    s = SeqHost();
+    c->seqs_dirty = true;
+    return NDA_OK;
+}
+
+int nda_seq_set_sink(nda_ctx *c, uint32_t seq, uint32_t n)
+{
+    if (!c)
+        return NDA_ERR_ARG;
+    if (int rc = check_seq(c, seq))
+        return rc;
+    SeqHost &s = c->seqs[seq];
+    if (s.prefix >= 0)
+        return fail(c, NDA_ERR_STATE, "sequence %u reads its sinks from prefix %d", seq, s.prefix);
+    s.n_sink = clamp_sink(c->cfg.window, n);
+    c->seqs_dirty = true;
+    return NDA_OK;
+}
+
+int nda_seq_state(const nda_ctx *c, uint32_t seq, uint32_t *pos, uint32_t *n_sink, int32_t *prefix_id)
+{
+    if (!c || seq >= c->cfg.max_seqs)
+        return NDA_ERR_ARG;
+    const SeqHost &s = c->seqs[seq];
+    if (pos)
+        *pos = s.pos;
+    if (n_sink)
+        *n_sink = s.n_sink;
+    if (prefix_id)
+        *prefix_id = s.prefix;
+    return NDA_OK;
+}
+
+int nda_seq_set_pos(nda_ctx *c, uint32_t seq, uint32_t pos)
+{
+    if (!c)
+        return NDA_ERR_ARG;
+    if (int rc = check_seq(c, seq))
+        return rc;
+    SeqHost &s = c->seqs[seq];
+    if (s.prefix >= 0 && pos < s.n_sink)
+        return fail(c, NDA_ERR_RANGE, "pos %u inside the shared prefix (%u)", pos, s.n_sink);
+    s.pos = pos;
+    c->seqs_dirty = true;
+    return NDA_OK;
+}
+
+int nda_seq_reserve(nda_ctx *c, uint32_t seq, uint32_t n)
+{
+    if (!c)
+        return NDA_ERR_ARG;
+    if (int rc = check_seq(c, seq))
+        return rc;
+    if (n == 0)
+        return NDA_OK;
+    const SeqHost &s = c->seqs[seq];
+    // Once the ring is full every slot is backed; cap at one full cycle.
+    uint32_t cap = c->cfg.window - (s.prefix >= 0 ? s.n_sink : 0);
+    return back_positions(c, seq, s.pos, std::min(n, cap));
+}
+
+int nda_advance(nda_ctx *c, uint32_t nseq, const uint32_t *ids, uint32_t n, void *stream)
+{
+    if (!c)
+        return NDA_ERR_ARG;
+    if (int rc = check_ids(c, nseq, ids))
+        return rc;
+    if (nseq == 0 || n == 0)
+        return NDA_OK;
+    for (uint32_t b = 0; b < nseq; b++)
+        c->seqs[sid(ids, b)].pos += n;
+    if (c->seqs_dirty)      // a full upload is pending anyway
+        return NDA_OK;
+    // Same increment on the device copy, in stream order, so steady-state
+    // decoding uploads nothing.
+    hipStream_t st = (hipStream_t)stream;
+    const uint32_t *d_seq, *d_t;
+    if (int rc = upload_rows(c, nseq, ids, nullptr, st, &d_seq, &d_t))
+        return rc;
+    hipError_t e = launch_advance(c->d_seqs, d_seq, nseq, n, st);
+    if (e != hipSuccess)
+        return hip_fail(c, e, "advance kernel launch");
+    return NDA_OK;
+}
+
+int nda_prefix_build(nda_ctx *c, uint32_t seq, int32_t *prefix_id, void *stream)
+{
+    if (!c || !prefix_id)
+        return NDA_ERR_ARG;
+    if (int rc = check_seq(c, seq))
+        return rc;
+    hipStream_t st = (hipStream_t)stream;
+    SeqHost &s = c->seqs[seq];
+    const uint32_t len = s.pos;
+    if (len == 0)
+        return fail(c, NDA_ERR_STATE, "sequence %u holds no positions", seq);
+    if (len > c->cfg.window)
+        return fail(c, NDA_ERR_RANGE, "prefix of %u positions exceeds the window %u", len, c->cfg.window);
+    int32_t id = -1;
+    for (uint32_t i = 0; i < c->cfg.max_prefixes; i++)
+        if (!c->prefixes[i].used) {
+            id = (int32_t)i;
+            break;
+        }
+    if (id < 0)
+        return fail(c, NDA_ERR_NOMEM, "all %u prefix segments in use", c->cfg.max_prefixes);
+    const uint32_t npages = (len + c->cfg.page_size - 1) / c->cfg.page_size;
+    if (npages > c->free_pages.size())
+        return fail(c, NDA_ERR_NOMEM, "page pool exhausted building a prefix");
+    int32_t *prow = &c->prefix_pages[(size_t)id * c->pg.pages_per_seq];
+    for (uint32_t i = 0; i < npages; i++) {
+        prow[i] = c->free_pages.back();
+        c->free_pages.pop_back();
+    }
+    c->prefix_dirty = true;
+    if (int rc = sync_tables(c, st))
+        return rc;
+
+    // Copy positions [0, len): shared part (if this sequence is itself
+    // attached) then its own slots (no wrap: len <= window).
+    const Vis v = visible(s, len - 1, c->cfg.window);
+    CopyArgs ca{};
+    ca.pool = c->pool;
+    ca.n_layers = c->cfg.n_layers;
+    ca.pg = c->pg;
+    ca.dst_pages = c->d_prefix_pages + (size_t)id * c->pg.pages_per_seq;
+    if (v.n_sh) {
+        ca.src_pages = c->d_prefix_pages + (size_t)s.prefix * c->pg.pages_per_seq;
+        ca.src_slot0 = 0;
+        ca.dst_slot0 = 0;
+        ca.count = v.n_sh;
+        hipError_t e = launch_copy(c->geo, ca, st);
+        if (e != hipSuccess)
+            return hip_fail(c, e, "prefix copy");
+    }
+    if (v.n_own) {
+        ca.src_pages = c->d_pages + (size_t)seq * c->pg.pages_per_seq;
+        ca.src_slot0 = 0;
+        ca.dst_slot0 = v.n_sh;
+        ca.count = v.n_own;
+        hipError_t e = launch_copy(c->geo, ca, st);
+        if (e != hipSuccess)
+            return hip_fail(c, e, "prefix copy");
+    }
+    Prefix &pf = c->prefixes[id];
+    pf.used = true;
+    pf.len = len;
+    pf.n_sink = clamp_sink(c->cfg.window, len);
+    pf.refs = 0;
+    // nd_model_snapshot: the builder pins its own positions as sinks.
+    if (s.prefix < 0)
+        s.n_sink = pf.n_sink;
+    s.has_snap = true;
+    s.snap_pos = len;
+    c->seqs_dirty = true;
+    *prefix_id = id;
+    return NDA_OK;
+}
+
+int nda_seq_attach(nda_ctx *c, uint32_t seq, int32_t id, void *stream)
+{
+    if (!c)
+        return NDA_ERR_ARG;
+    if (int rc = check_seq(c, seq))
+        return rc;
+    if (id < 0 || (uint32_t)id >= c->cfg.max_prefixes || !c->prefixes[id].used)
+        return fail(c, NDA_ERR_ARG, "prefix %d does not exist", id);
+    hipStream_t st = (hipStream_t)stream;
+    SeqHost &s = c->seqs[seq];
+    if (s.prefix >= 0)
+        c->prefixes[s.prefix].refs--;
+    release_pages(c, seq);
+    const Prefix &pf = c->prefixes[id];
+    s = SeqHost();
+    s.prefix = id;
+    s.n_sink = pf.n_sink;
+    s.pos = pf.len;
+    s.has_snap = true;
+    s.snap_pos = pf.len;
+    c->prefixes[id].refs++;
+    c->seqs_dirty = true;
+    // Positions past the sink clamp live in the ring: copy them in, as the
+    // engine's restore copies every live slot.
+    if (pf.len > pf.n_sink) {
+        const uint32_t tail = pf.len - pf.n_sink;
+        if (int rc = back_slots(c, seq, 0, tail))
+            return rc;
+        if (int rc = sync_tables(c, st))
+            return rc;
+        CopyArgs ca{};
+        ca.pool = c->pool;
+        ca.n_layers = c->cfg.n_layers;
+        ca.pg = c->pg;
+        ca.src_pages = c->d_prefix_pages + (size_t)id * c->pg.pages_per_seq;
+        ca.dst_pages = c->d_pages + (size_t)seq * c->pg.pages_per_seq;
+        ca.src_slot0 = pf.n_sink;
+        ca.dst_slot0 = 0;
+        ca.count = tail;
+        hipError_t e = launch_copy(c->geo, ca, st);
+        if (e != hipSuccess)
+            return hip_fail(c, e, "prefix tail copy");
+    }
+    return NDA_OK;
+}
+
+int nda_seq_rewind(nda_ctx *c, uint32_t seq)
+{
+    if (!c)
+        return NDA_ERR_ARG;
+    if (int rc = check_seq(c, seq))
+        return rc;
+    SeqHost &s = c->seqs[seq];
+    if (!s.has_snap)
+        return nda_seq_reset(c, seq);
+    s.pos = s.snap_pos;
+    c->seqs_dirty = true;
+    return NDA_OK;
+}
+
+int nda_prefix_free(nda_ctx *c, int32_t id)
+{
+    if (!c)
+        return NDA_ERR_ARG;
+    if (id < 0 || (uint32_t)id >= c->cfg.max_prefixes || !c->prefixes[id].used)
+        return fail(c, NDA_ERR_ARG, "prefix %d does not exist", id);
+    if (c->prefixes[id].refs)
+        return fail(c, NDA_ERR_STATE, "prefix %d is attached to %u sequences", id, c->prefixes[id].refs);
+    int32_t *prow = &c->prefix_pages[(size_t)id * c->pg.pages_per_seq];
+    for (uint32_t i = 0; i < c->pg.pages_per_seq; i++)
+        if (prow[i] >= 0) {
+            c->free_pages.push_back(prow[i]);
+            prow[i] = -1;
+        }
+    c->prefixes[id] = Prefix();
+    c->prefix_dirty = true;
+    return NDA_OK;
+}
+
+int nda_kv_append(nda_ctx *c, uint32_t layer, uint32_t nseq, const uint32_t *ids, const float *k,
+                  const float *v, void *stream)
+{
+    if (!c || (nseq && (!k || !v)))
+        return c ? fail(c, NDA_ERR_ARG, "null k/v") : NDA_ERR_ARG;
+    if (layer >= c->cfg.n_layers)
+        return fail(c, NDA_ERR_ARG, "layer %u out of range", layer);
+    if (int rc = check_ids(c, nseq, ids))
+        return rc;
+    hipStream_t st = (hipStream_t)stream;
+    for (uint32_t b = 0; b < nseq; b++) {
+        const uint32_t q = sid(ids, b);
+        if (int rc = back_positions(c, q, c->seqs[q].pos, 1))
+            return rc;
+    }
+    if (int rc = sync_tables(c, st))
+        return rc;
+    const uint32_t *d_seq, *d_t;
+    if (int rc = upload_rows(c, nseq, ids, nullptr, st, &d_seq, &d_t))
+        return rc;
+    AppendArgs a{};
+    a.k = k;
+    a.v = v;
+    a.pool = c->pool + (uint64_t)layer * c->pg.layer_bytes;
+    a.page_table = c->d_pages;
+    a.seqs = c->d_seqs;
+    a.row_seq = d_seq;
+    a.row_t = d_t;
+    a.pg = c->pg;
+    a.rows = nseq;
+    ProfScope ps(c, NDA_K_APPEND, st);
+    hipError_t e = launch_append(c->geo, a, st);
+    if (e != hipSuccess)
+        return hip_fail(c, e, "append kernel launch");
+    return NDA_OK;
+}
+
+int nda_decode(nda_ctx *c, uint32_t layer, uint32_t nseq, const uint32_t *ids, const float *q,
+               const float *gate, float *out, void *stream)
+{
+    if (!c || (nseq && (!q || !out)))
+        return c ? fail(c, NDA_ERR_ARG, "null q/out") : NDA_ERR_ARG;
+    if (layer >= c->cfg.n_layers)
+        return fail(c, NDA_ERR_ARG, "layer %u out of range", layer);
+    if (int rc = check_ids(c, nseq, ids))
+        return rc;
+    hipStream_t st = (hipStream_t)stream;
+    // Every visible slot must be backed (written by an append, a write or an
+    // attach); an unbacked one means the caller skipped the append.
+    uint32_t max_total = 0;
+    for (uint32_t b = 0; b < nseq; b++) {
+        const uint32_t qq = sid(ids, b);
+        const SeqHost &s = c->seqs[qq];
+        const Vis v = visible(s, s.pos, c->cfg.window);
+        max_total = std::max(max_total, v.n_sh + v.n_own);
+        if (v.n_own) {
+            const int32_t *row = &c->pages[(size_t)qq * c->pg.pages_per_seq];
+            if (row[(v.n_own - 1) >> c->pg.log2_page] < 0 || row[0] < 0)
+                return fail(c, NDA_ERR_STATE, "sequence %u: slot of position %u never stored", qq, s.pos);
+        }
+    }
+    if (int rc = sync_tables(c, st))
+        return rc;
+    const uint32_t *d_seq, *d_t;
+    if (int rc = upload_rows(c, nseq, ids, nullptr, st, &d_seq, &d_t))
+        return rc;
+    AttnArgs a = attn_args(c, layer, nseq, q, gate, out, max_total);
+    a.row_seq = d_seq;
+    a.row_t = d_t;
+    return run_attend(c, a, st);
+}
+
+int nda_step(nda_ctx *c, uint32_t layer, uint32_t nseq, const uint32_t *ids, const float *q,
+             const float *k, const float *v, const float *gate, float *out, void *stream)
+{
+    int rc = nda_kv_append(c, layer, nseq, ids, k, v, stream);
+    if (rc)
+        return rc;
+    return nda_decode(c, layer, nseq, ids, q, gate, out, stream);
+}
+
+int nda_prefill(nda_ctx *c, uint32_t layer, uint32_t nseq, const uint32_t *ids, const uint32_t *n_tokens,
+                const float *q, const float *k, const float *v, const float *gate, float *out, void *stream)
+{
+    if (!c || (nseq && (!n_tokens || !q || !k || !v || !out)))
+        return c ? fail(c, NDA_ERR_ARG, "null argument") : NDA_ERR_ARG;
+    if (layer >= c->cfg.n_layers)
+        return fail(c, NDA_ERR_ARG, "layer %u out of range", layer);
+    if (int rc = check_ids(c, nseq, ids))
+        return rc;
+    hipStream_t st = (hipStream_t)stream;
+    uint64_t rows = 0;
+    uint32_t max_total = 0;
+    for (uint32_t b = 0; b < nseq; b++) {
+        const uint32_t qq = sid(ids, b);
+        const SeqHost &s = c->seqs[qq];
+        if ((uint64_t)s.pos + n_tokens[b] > c->cfg.window)
+            return fail(c, NDA_ERR_RANGE,
+                        "sequence %u: prefill of %u tokens at position %u would wrap the ring (window %u)",
+                        qq, n_tokens[b], s.pos, c->cfg.window);
+        if (s.prefix >= 0 && s.pos < s.n_sink)
+            return fail(c, NDA_ERR_STATE, "sequence %u positioned inside its shared prefix", qq);
+        if (n_tokens[b]) {
+            const Vis v = visible(s, s.pos + n_tokens[b] - 1, c->cfg.window);
+            max_total = std::max(max_total, v.n_sh + v.n_own);
+        }
+        rows += n_tokens[b];
+    }
+    if (rows == 0)
+        return NDA_OK;
+    if (rows > (1u << 26))
+        return fail(c, NDA_ERR_ARG, "too many prefill tokens (%llu)", (unsigned long long)rows);
+    for (uint32_t b = 0; b < nseq; b++) {
+        const uint32_t qq = sid(ids, b);
+        if (n_tokens[b])
+            if (int rc = back_positions(c, qq, c->seqs[qq].pos, n_tokens[b]))
+                return rc;
+    }
+    std::vector<uint32_t> rseq(rows), rt(rows);
+    for (uint32_t b = 0, r = 0; b < nseq; b++)
+        for (uint32_t t = 0; t < n_tokens[b]; t++, r++) {
+            rseq[r] = sid(ids, b);
+            rt[r] = t;
+        }
+    if (int rc = sync_tables(c, st))
+        return rc;
+    const uint32_t *d_seq, *d_t;
+    if (int rc = upload_rows(c, (uint32_t)rows, rseq.data(), rt.data(), st, &d_seq, &d_t))
+        return rc;
+    {
+        AppendArgs a{};
+        a.k = k;
+        a.v = v;
+        a.pool = c->pool + (uint64_t)layer * c->pg.layer_bytes;
+        a.page_table = c->d_pages;
+        a.seqs = c->d_seqs;
+        a.row_seq = d_seq;
+        a.row_t = d_t;
+        a.pg = c->pg;
+        a.rows = (uint32_t)rows;
+        ProfScope ps(c, NDA_K_APPEND, st);
+        hipError_t e = launch_append(c->geo, a, st);
+        if (e != hipSuccess)
+            return hip_fail(c, e, "append kernel launch");
+    }
+    AttnArgs a = attn_args(c, layer, (uint32_t)rows, q, gate, out, max_total);
+    a.row_seq = d_seq;
+    a.row_t = d_t;
+    return run_attend(c, a, st);
+}
+
+int nda_sync(nda_ctx *c, void *stream)
+{
+    hipError_t e = hipStreamSynchronize((hipStream_t)stream);
+    if (e != hipSuccess)
+        return hip_fail(c, e, "hipStreamSynchronize");
+    return NDA_OK;
+}
+
+// Page and in-page slot of `count` positions from p0 of one sequence.
+static int locate(nda_ctx *c, uint32_t seq, uint32_t p0, uint32_t count, bool for_write,
+                  std::vector<int32_t> &pg, std::vector<uint32_t> &off)
+{
+    SeqHost &s = c->seqs[seq];
+    pg.resize(count);
+    off.resize(count);
+    const uint32_t P = c->cfg.page_size;
+    for (uint32_t i = 0; i < count; i++) {
+        const uint32_t p = p0 + i;
+        if (s.prefix >= 0 && p < s.n_sink) {
+            if (for_write)
+                return fail(c, NDA_ERR_STATE, "position %u belongs to the shared prefix", p);
+            pg[i] = c->prefix_pages[(size_t)s.prefix * c->pg.pages_per_seq + p / P];
+            off[i] = p % P;
+            continue;
+        }
+        if (!for_write) {
+            // readable iff still inside the window seen from pos (or pos-1)
+            const uint32_t top = std::max(s.pos, p);
+            const uint32_t rcap = c->cfg.window - s.n_sink;
+            if (p >= s.n_sink && top - p >= rcap)
+                return fail(c, NDA_ERR_RANGE, "position %u has left the ring", p);
+        }
+        const uint32_t sl = own_slot(s, p, c->cfg.window);
+        if (for_write)
+            if (int rc = back_slots(c, seq, sl, sl + 1))
+                return rc;
+        pg[i] = c->pages[(size_t)seq * c->pg.pages_per_seq + sl / P];
+        off[i] = sl % P;
+        if (pg[i] < 0)
+            return fail(c, NDA_ERR_STATE, "position %u was never stored", p);
+    }
+    return NDA_OK;
+}
+
+static int kv_stage(nda_ctx *c, uint32_t layer, uint32_t seq, uint32_t p0, uint32_t count, void *k, void *v,
+                    float *ks, float *vs, bool write)
+{
+    if (!c)
+        return NDA_ERR_ARG;
+    if (int rc = check_seq(c, seq))
+        return rc;
+    if (layer >= c->cfg.n_layers || !k || !v)
+        return fail(c, NDA_ERR_ARG, "bad layer or null buffer");
+    if (count == 0)
+        return NDA_OK;
+    std::vector<int32_t> pg;
+    std::vector<uint32_t> off;
+    if (int rc = locate(c, seq, p0, count, write, pg, off))
+        return rc;
+    const size_t es = c->cfg.kv_dtype == NDA_KV_F16 ? 2 : 1;
+    const size_t nkv = c->cfg.n_kv_heads;
+    const size_t kb = count * nkv * c->cfg.qk_head_dim * es, vb = count * nkv * c->cfg.v_head_dim * es;
+    const size_t sb = count * nkv * sizeof(float);
+    const size_t ib = count * (sizeof(int32_t) + sizeof(uint32_t));
+    const size_t total = kb + vb + 2 * sb + ib + 64;
+    if (int rc = ensure_stage(c, total))
+        return rc;
+    uint8_t *d = c->d_stage;
+    StageArgs a{};
+    a.pool = c->pool + (uint64_t)layer * c->pg.layer_bytes;
+    a.stage_ks = reinterpret_cast<float *>(d);
+    a.stage_vs = reinterpret_cast<float *>(d + sb);
+    a.pages_for_slot = reinterpret_cast<int32_t *>(d + 2 * sb);
+    a.slot_in_page = reinterpret_cast<uint32_t *>(d + 2 * sb + count * 4);
+    a.stage_k = d + 2 * sb + count * 8;
+    a.stage_v = a.stage_k + kb;
+    a.count = count;
+    a.pg = c->pg;
+    if (int rc = sync_tables(c, nullptr))
+        return rc;
+    HIPC(c, hipMemcpy((void *)a.pages_for_slot, pg.data(), count * 4, hipMemcpyHostToDevice));
+    HIPC(c, hipMemcpy((void *)a.slot_in_page, off.data(), count * 4, hipMemcpyHostToDevice));
+    if (write) {
+        HIPC(c, hipMemcpy(a.stage_k, k, kb, hipMemcpyHostToDevice));
+        HIPC(c, hipMemcpy(a.stage_v, v, vb, hipMemcpyHostToDevice));
+        if (c->cfg.kv_dtype == NDA_KV_INT8) {
+            if (!ks || !vs)
+                return fail(c, NDA_ERR_ARG, "int8 write needs scales");
+            HIPC(c, hipMemcpy(a.stage_ks, ks, sb, hipMemcpyHostToDevice));
+            HIPC(c, hipMemcpy(a.stage_vs, vs, sb, hipMemcpyHostToDevice));
+        }
+        hipError_t e = launch_scatter(c->geo, a, nullptr);
+        if (e != hipSuccess)
+            return hip_fail(c, e, "scatter");
+        HIPC(c, hipDeviceSynchronize());
+    } else {
+        hipError_t e = launch_gather(c->geo, a, nullptr);
+        if (e != hipSuccess)
+            return hip_fail(c, e, "gather");
+        HIPC(c, hipDeviceSynchronize());
+        HIPC(c, hipMemcpy(k, a.stage_k, kb, hipMemcpyDeviceToHost));
+        HIPC(c, hipMemcpy(v, a.stage_v, vb, hipMemcpyDeviceToHost));
+        if (ks)
+            HIPC(c, hipMemcpy(ks, a.stage_ks, sb, hipMemcpyDeviceToHost));
+        if (vs)
+            HIPC(c, hipMemcpy(vs, a.stage_vs, sb, hipMemcpyDeviceToHost));
+    }
+    return NDA_OK;
+}
+
+int nda_kv_read(nda_ctx *c, uint32_t layer, uint32_t seq, uint32_t p0, uint32_t count, void *k, void *v,
+                float *ks, float *vs)
+{
+    return kv_stage(c, layer, seq, p0, count, k, v, ks, vs, false);
+}
+
+int nda_kv_write(nda_ctx *c, uint32_t layer, uint32_t seq, uint32_t p0, uint32_t count, const void *k,
+                 const void *v, const float *ks, const float *vs)
+{
+    return kv_stage(c, layer, seq, p0, count, const_cast<void *>(k), const_cast<void *>(v),
+                    const_cast<float *>(ks), const_cast<float *>(vs), true);
+}
+
+int nda_kv_fill_normal(nda_ctx *c, uint32_t nseq, const uint32_t *ids, uint64_t seed, void *stream)
+{
+    if (!c)
+        return NDA_ERR_ARG;
+    if (c->cfg.kv_dtype != NDA_KV_F16)
+        return fail(c, NDA_ERR_UNSUPPORTED, "synthetic fill is fp16 only");
+    if (int rc = check_ids(c, nseq, ids))
+        return rc;
+    hipStream_t st = (hipStream_t)stream;
+    for (uint32_t b = 0; b < nseq; b++) {
+        const uint32_t qq = sid(ids, b);
+        const SeqHost &s = c->seqs[qq];
+        if (s.pos == 0)
+            continue;
+        const Vis v = visible(s, s.pos - 1, c->cfg.window);
+        if (int rc = back_slots(c, qq, 0, v.n_own))
+            return rc;
+    }
+    if (int rc = sync_tables(c, st))
+        return rc;
+    const uint32_t *d_seq, *d_t;
+    if (int rc = upload_rows(c, nseq, ids, nullptr, st, &d_seq, &d_t))
+        return rc;
+    FillKvArgs a{};
+    a.pool = c->pool;
+    a.page_table = c->d_pages;
+    a.prefix_pages = c->d_prefix_pages;
+    a.seqs = c->d_seqs;
+    a.seq_list = d_seq;
+    a.nseq = nseq;
+    a.n_layers = c->cfg.n_layers;
+    a.seed = seed;
+    a.pg = c->pg;
+    hipError_t e = launch_fill_kv(c->geo, a, st);
+    if (e != hipSuccess)
+        return hip_fail(c, e, "fill kernel launch");
+    return NDA_OK;
+}
+
+int nda_dev_alloc(void **ptr, size_t bytes)
+{
+    if (!ptr)
+        return NDA_ERR_ARG;
+    hipError_t e = hipMalloc(ptr, bytes ? bytes : 1);
+    return e == hipSuccess ? NDA_OK : (e == hipErrorOutOfMemory ? NDA_ERR_NOMEM : NDA_ERR_HIP);
+}
+
+int nda_dev_free(void *ptr) { return hipFree(ptr) == hipSuccess ? NDA_OK : NDA_ERR_HIP; }
+
+int nda_h2d(void *dst, const void *src, size_t bytes)
+{
+    return hipMemcpy(dst, src, bytes, hipMemcpyHostToDevice) == hipSuccess ? NDA_OK : NDA_ERR_HIP;
+}
+
+int nda_d2h(void *dst, const void *src, size_t bytes)
+{
+    return hipMemcpy(dst, src, bytes, hipMemcpyDeviceToHost) == hipSuccess ? NDA_OK : NDA_ERR_HIP;
+}
+
+int nda_memset(void *dst, int value, size_t bytes)
+{
+    return hipMemset(dst, value, bytes) == hipSuccess ? NDA_OK : NDA_ERR_HIP;
+}
+
+int nda_fill_normal(void *dst, uint64_t n, int dtype, uint64_t seed, float scale, void *stream)
+{
+    if (!dst || (dtype != 0 && dtype != 1))
+        return NDA_ERR_ARG;
+    return launch_fill_normal(dst, n, dtype, seed, scale, (hipStream_t)stream) == hipSuccess ? NDA_OK
+                                                                                             : NDA_ERR_HIP;
+}
+
+int nda_stream_create(void **stream)
+{
+    if (!stream)
+        return NDA_ERR_ARG;
+    hipStream_t s = nullptr;
+    if (hipStreamCreateWithFlags(&s, hipStreamNonBlocking) != hipSuccess)
+        return NDA_ERR_HIP;
+    *stream = s;
+    return NDA_OK;
+}
+
+int nda_stream_destroy(void *stream)
+{
+    return hipStreamDestroy((hipStream_t)stream) == hipSuccess ? NDA_OK : NDA_ERR_HIP;
+}
+
+int nda_device_sync(void) { return hipDeviceSynchronize() == hipSuccess ? NDA_OK : NDA_ERR_HIP; }
+
+int nda_device_info(char *name, size_t name_len, int *cu_count)
+{
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess)
+        return NDA_ERR_NODEV;
+    hipDeviceProp_t p;
+    if (hipGetDeviceProperties(&p, dev) != hipSuccess)
+        return NDA_ERR_HIP;
+    if (name && name_len) {
+        snprintf(name, name_len, "%s (%s)", p.name, p.gcnArchName);
+    }
+    if (cu_count)
+        *cu_count = p.multiProcessorCount;
+    return NDA_OK;
+}
+
+int nda_prof_enable(nda_ctx *c, int on)
+{
+    if (!c)
+        return NDA_ERR_ARG;
+    c->prof = on != 0;
+    return NDA_OK;
+}
+
+int nda_prof_read(nda_ctx *c, double ms[NDA_K_COUNT], uint64_t launches[NDA_K_COUNT], int reset)
+{
+    if (!c)
+        return NDA_ERR_ARG;
+    for (auto &r : c->prof_pending) {
+        float t = 0.0f;
+        if (hipEventSynchronize(r.b) == hipSuccess && hipEventElapsedTime(&t, r.a, r.b) == hipSuccess) {
+            c->prof_ms[r.kind] += t;
+            c->prof_n[r.kind]++;
+        }
+        c->ev_free.push_back(r.a);
+        c->ev_free.push_back(r.b);
+    }
+    c->prof_pending.clear();
+    for (int i = 0; i < NDA_K_COUNT; i++) {
+        if (ms)
+            ms[i] = c->prof_ms[i];
+        if (launches)
+            launches[i] = c->prof_n[i];
+        if (reset) {
+            c->prof_ms[i] = 0;
+            c->prof_n[i] = 0;
+        }
+    }
+    return NDA_OK;
+}
+
+} // extern "C"

@@ -1,0 +1,120 @@
+/* nda_internal.h - shared definitions between the C-ABI layer (nda_api.hip)
+ * and the gfx950 kernels (nda_kernels.hip). Not installed. */
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace nda {
+
+/* Per-sequence state as the kernels see it. pos is the position being
+ * stored/attended (the engine's m->pos), n_sink the pinned count, prefix the
+ * shared segment id or -1. */
+struct SeqDev {
+    int32_t pos;
+    int32_t n_sink;
+    int32_t prefix;
+    int32_t pad;
+};
+
+/* Page geometry of one layer pool. A page holds page_size consecutive slots
+ * of one sequence (or prefix) for every kv-head:
+ *   page + g*head_bytes:  K codes   [page_size][dk]
+ *                         V codes   [page_size][dv]
+ *                         K scales  [page_size] fp32   (int8 only)
+ *                         V scales  [page_size] fp32   (int8 only)      */
+struct PageGeom {
+    uint32_t log2_page;     /* page_size = 1 << log2_page */
+    uint32_t pages_per_seq; /* page-table row length = ceil(window / page_size) */
+    uint64_t head_bytes;
+    uint64_t page_bytes;
+    uint64_t layer_bytes;   /* page_bytes * max_pages */
+    uint32_t window;
+    uint32_t nkv;
+};
+
+/* One launch of the decode / causal kernel. A "row" is one query token of
+ * one sequence: batch index b = row_seq_idx, visible position = pos + row_t. */
+struct AttnArgs {
+    const float *q;          /* [rows][nh][dk] */
+    const float *gate;       /* [rows][nh][dv] or null */
+    float *out;              /* [rows][nh][dv] */
+    const uint8_t *pool;     /* this layer's pool base */
+    const int32_t *page_table;
+    const int32_t *prefix_pages;
+    const SeqDev *seqs;
+    const uint32_t *row_seq; /* [rows] sequence id per row, or null: row -> seq_ids/identity */
+    const uint32_t *row_t;   /* [rows] offset from pos, or null: 0 */
+    float *part;             /* split partials [rows][nh][max_chunks][dv + 2] */
+    PageGeom pg;
+    uint32_t rows;
+    uint32_t nh;
+    uint32_t chunk;          /* positions per work item */
+    uint32_t max_chunks;
+    float qscale;            /* log2(e) / sqrt(dk) */
+};
+
+struct AppendArgs {
+    const float *k;          /* [rows][nkv][dk] */
+    const float *v;          /* [rows][nkv][dv] */
+    uint8_t *pool;
+    const int32_t *page_table;
+    const SeqDev *seqs;
+    const uint32_t *row_seq;
+    const uint32_t *row_t;
+    PageGeom pg;
+    uint32_t rows;
+};
+
+/* Copy of `count` slots between two page lists (prefix build / attach). */
+struct CopyArgs {
+    uint8_t *pool;           /* layer 0 base; layers at + l * layer_bytes */
+    const int32_t *src_pages;
+    const int32_t *dst_pages;
+    uint32_t src_slot0, dst_slot0, count, n_layers;
+    PageGeom pg;
+};
+
+/* Gather / scatter of positions to a contiguous staging buffer (inspection). */
+struct StageArgs {
+    uint8_t *pool;
+    const int32_t *pages_for_slot; /* [count] page id per position */
+    const uint32_t *slot_in_page;  /* [count] */
+    uint8_t *stage_k, *stage_v;    /* [count][nkv][d] */
+    float *stage_ks, *stage_vs;    /* [count][nkv] */
+    uint32_t count;
+    PageGeom pg;
+};
+
+struct FillKvArgs {
+    uint8_t *pool;
+    const int32_t *page_table;
+    const int32_t *prefix_pages;
+    const SeqDev *seqs;
+    const uint32_t *seq_list;
+    uint32_t nseq, n_layers;
+    uint64_t seed;
+    PageGeom pg;
+};
+
+/* Kernel geometry key. */
+struct Geo {
+    int kv_f16;
+    int dk, dv, rep;
+};
+
+/* Launchers (nda_kernels.hip). Return hipSuccess or the launch error;
+ * hipErrorNotSupported for a geometry without an instantiation. */
+hipError_t launch_append(const Geo &g, const AppendArgs &a, hipStream_t s);
+hipError_t launch_attend(const Geo &g, const AttnArgs &a, hipStream_t s);
+hipError_t launch_combine(const Geo &g, const AttnArgs &a, hipStream_t s);
+hipError_t launch_copy(const Geo &g, const CopyArgs &a, hipStream_t s);
+hipError_t launch_gather(const Geo &g, const StageArgs &a, hipStream_t s);
+hipError_t launch_scatter(const Geo &g, const StageArgs &a, hipStream_t s);
+hipError_t launch_fill_kv(const Geo &g, const FillKvArgs &a, hipStream_t s);
+hipError_t launch_advance(SeqDev *seqs, const uint32_t *seq_list, uint32_t nseq, uint32_t n, hipStream_t s);
+hipError_t launch_fill_normal(void *dst, uint64_t n, int dtype, uint64_t seed, float scale,
+                              hipStream_t s);
+bool geometry_supported(const Geo &g);
+
+} // namespace nda

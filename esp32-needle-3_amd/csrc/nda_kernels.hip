@@ -1,0 +1,823 @@
+// nda_kernels.hip - gfx950 kernels of the Needle attention / KV-cache path.
+//
+// Decode attention (attend_kernel) is HBM-bound: every K/V byte is read once.
+// A work-group of NW waves owns one (row, kv-head) unit (a row is one query
+// token of one sequence) or one split-KV chunk of it. Inside a wave, G lanes
+// share one KV position: each lane loads its 16-byte slice of the K and V row
+// straight into registers (global_load_dwordx4, a wave moves 1 KiB per load)
+// and 64/G positions are in flight per wave per step. The q.k partial dots
+// are summed over the G lanes with DPP row permutes; every lane group keeps
+// its own online-softmax state (running max, denominator, accumulator), so no
+// wave-wide reduction happens inside the KV loop. The states are merged once
+// at the end (shuffles across lane groups, LDS across waves). With no reuse
+// of K/V rows between lanes (rep 1) there is nothing to gain from staging
+// K/V in LDS; for GQA the rep query heads of a group reuse each loaded row
+// from registers.
+//
+// Semantics follow the engine's attn_heads (engine/src/nd_model.c:2105-2359):
+// the visited positions are the sinks plus the recent ring (:2451-2483), the
+// current token included, emit (acc / denom) * sigmoid(gate) (:2085-2103).
+// The online softmax is evaluated in base 2 (q pre-scaled by log2(e)/sqrt(dk))
+// with fp32 accumulation; results match the engine's fp32 CPU attention to
+// rounding (tests bound max |delta| at 1e-3).
+#include "nda_internal.h"
+
+#include <float.h>
+
+namespace nda {
+
+// ---------------------------------------------------------------- helpers
+
+__device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
+
+__device__ __forceinline__ float sigmoid_dev(float x) { return 1.0f / (1.0f + __expf(-x)); }
+
+template <int CTRL>
+__device__ __forceinline__ float dpp_mov(float x)
+{
+    return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, x), CTRL,
+                                                                 0xF, 0xF, false));
+}
+
+// Sum over aligned groups of G lanes; every lane of a group gets the same
+// bits (each step adds a commutative pair).
+template <int G>
+__device__ __forceinline__ float group_sum(float x)
+{
+    if constexpr (G >= 2)
+        x += dpp_mov<0xB1>(x);    // quad_perm [1,0,3,2]
+    if constexpr (G >= 4)
+        x += dpp_mov<0x4E>(x);    // quad_perm [2,3,0,1]
+    if constexpr (G >= 8)
+        x += dpp_mov<0x141>(x);   // row_half_mirror
+    if constexpr (G >= 16)
+        x += dpp_mov<0x140>(x);   // row_mirror
+    static_assert(G <= 16, "group_sum: G <= 16");
+    return x;
+}
+
+__device__ __forceinline__ float wave_max(float x)
+{
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1)
+        x = fmaxf(x, __shfl_xor(x, o, 64));
+    return x;
+}
+
+// Which positions a row sees (the dispatch arithmetic of attention(),
+// engine/src/nd_model.c:2451-2483), split into the shared-prefix run and
+// the sequence's own slots. Own slots [0, n_own) are contiguous: without a
+// shared prefix they are the sinks [0, n_sink) followed by the ring
+// [n_sink, n_sink + rcount); with one they are ring indices [0, rcount).
+struct Visible {
+    int n_sh, n_own;
+};
+
+__device__ __forceinline__ Visible visible(const SeqDev &s, int p, int window)
+{
+    int sinks = min(s.n_sink, p + 1);
+    int rcap = window - s.n_sink;
+    int rcount = (p + 1 <= s.n_sink) ? 0 : min(p + 1 - s.n_sink, rcap);
+    Visible v;
+    v.n_sh = s.prefix >= 0 ? sinks : 0;
+    v.n_own = s.prefix >= 0 ? rcount : sinks + rcount;
+    return v;
+}
+
+// Own slot of position p (kv_slot, engine/src/nd_model.c:1302-1309, with the
+// sinks of a shared prefix living outside the sequence's pages).
+__device__ __forceinline__ int own_slot(const SeqDev &s, int p, int window)
+{
+    if (s.prefix >= 0)
+        return (p - s.n_sink) % (window - s.n_sink);
+    if (p < s.n_sink)
+        return p;
+    return s.n_sink + (p - s.n_sink) % (window - s.n_sink);
+}
+
+// ----------------------------------------------------- fixed-size loads
+
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+
+template <int NB>
+struct Words {
+    static_assert(NB % 4 == 0, "row slices are whole dwords");
+    uint32_t w[NB / 4];
+};
+
+template <int NB>
+__device__ __forceinline__ void load_words(Words<NB> &d, const uint8_t *p)
+{
+    if constexpr (NB % 16 == 0) {
+#pragma unroll
+        for (int i = 0; i < NB / 16; i++) {
+            u32x4 x = __builtin_nontemporal_load(reinterpret_cast<const u32x4 *>(p) + i);
+            d.w[4 * i + 0] = x.x;
+            d.w[4 * i + 1] = x.y;
+            d.w[4 * i + 2] = x.z;
+            d.w[4 * i + 3] = x.w;
+        }
+    } else if constexpr (NB % 8 == 0) {
+#pragma unroll
+        for (int i = 0; i < NB / 8; i++) {
+            u32x2 x = __builtin_nontemporal_load(reinterpret_cast<const u32x2 *>(p) + i);
+            d.w[2 * i + 0] = x.x;
+            d.w[2 * i + 1] = x.y;
+        }
+    } else {
+#pragma unroll
+        for (int i = 0; i < NB / 4; i++)
+            d.w[i] = __builtin_nontemporal_load(reinterpret_cast<const uint32_t *>(p) + i);
+    }
+}
+
+// Element e of a loaded slice as float: int8 code or fp16 value.
+template <int ES>
+__device__ __forceinline__ float elem(const uint32_t *w, int e)
+{
+    if constexpr (ES == 1) {
+        return (float)(int8_t)(w[e >> 2] >> (8 * (e & 3)));
+    } else {
+        uint16_t h = (uint16_t)(w[e >> 1] >> (16 * (e & 1)));
+        return (float)__builtin_bit_cast(_Float16, h);
+    }
+}
+
+// -------------------------------------------------------- decode / causal
+
+template <int ES, int DK, int DV, int REP, int G, int NP, int NW>
+struct AttnCfg {
+    static constexpr int EK = DK / G;          // K elements per lane
+    static constexpr int EV = DV / G;          // V elements per lane
+    static constexpr int PW = 64 / G;          // positions per wave step (lane groups)
+    static constexpr int KB = EK * ES;         // K bytes per lane
+    static constexpr int VB = EV * ES;
+    static_assert(DK % G == 0 && DV % G == 0, "head dims split over G lanes");
+    static_assert(KB % 4 == 0 && VB % 4 == 0, "lane slices are whole dwords");
+};
+
+template <int ES, int DK, int DV, int REP, int G, int NP, int NW>
+struct AttnState {
+    using C = AttnCfg<ES, DK, DV, REP, G, NP, NW>;
+    float qr[REP][C::EK];
+    float m[REP], l[REP];
+    float acc[REP][C::EV];
+};
+
+// One wave step over positions blk0 + j*PW + grp, j < NP, of a page list.
+template <bool MASK, int ES, int DK, int DV, int REP, int G, int NP, int NW>
+__device__ __forceinline__ void attn_step(AttnState<ES, DK, DV, REP, G, NP, NW> &st,
+                                          const AttnArgs &a, const int32_t *pages, uint32_t g,
+                                          int blk0, int s0, int s1, int grp, int li)
+{
+    using C = AttnCfg<ES, DK, DV, REP, G, NP, NW>;
+    const int P = 1 << a.pg.log2_page;
+    Words<C::KB> kw[NP];
+    Words<C::VB> vw[NP];
+    float ks[NP], vs[NP];
+    bool valid[NP];
+
+#pragma unroll
+    for (int j = 0; j < NP; j++) {
+        const int blk = blk0 + j * C::PW;
+        const int s = blk + grp;
+        valid[j] = !MASK || (s >= s0 && s < s1);
+        // The whole block of PW slots lies in one page (page_size % PW == 0)
+        // and intersects [s0, s1), so its page is backed; an unbacked page
+        // (never stored) reads as masked instead of faulting.
+        const int32_t page = (!MASK || blk < s1) ? pages[blk >> a.pg.log2_page] : -1;
+        if (page >= 0) {
+            const uint8_t *hb = a.pool + (uint64_t)page * a.pg.page_bytes + (uint64_t)g * a.pg.head_bytes;
+            const int off = s & (P - 1);
+            load_words<C::KB>(kw[j], hb + (uint64_t)off * DK * ES + li * C::KB);
+            load_words<C::VB>(vw[j], hb + (uint64_t)P * DK * ES + (uint64_t)off * DV * ES + li * C::VB);
+            if constexpr (ES == 1) {
+                const float *sc = reinterpret_cast<const float *>(hb + (uint64_t)P * (DK + DV));
+                ks[j] = sc[off];
+                vs[j] = sc[P + off];
+            } else {
+                ks[j] = 1.0f;
+                vs[j] = 1.0f;
+            }
+        } else {
+#pragma unroll
+            for (int i = 0; i < C::KB / 4; i++)
+                kw[j].w[i] = 0;
+#pragma unroll
+            for (int i = 0; i < C::VB / 4; i++)
+                vw[j].w[i] = 0;
+            ks[j] = 0.0f;
+            vs[j] = 0.0f;
+            valid[j] = false;
+        }
+        if constexpr (MASK && ES == 2) {
+            // Unwritten slots may hold any bits (inf/nan in fp16): zero them.
+#pragma unroll
+            for (int i = 0; i < C::VB / 4; i++)
+                vw[j].w[i] = valid[j] ? vw[j].w[i] : 0u;
+        }
+    }
+
+    float vf[NP][C::EV];
+#pragma unroll
+    for (int j = 0; j < NP; j++)
+#pragma unroll
+        for (int e = 0; e < C::EV; e++)
+            vf[j][e] = elem<ES>(vw[j].w, e);
+
+#pragma unroll
+    for (int t = 0; t < REP; t++) {
+        float sc[NP];
+#pragma unroll
+        for (int j = 0; j < NP; j++) {
+            float d = 0.0f;
+#pragma unroll
+            for (int e = 0; e < C::EK; e++)
+                d = fmaf(st.qr[t][e], elem<ES>(kw[j].w, e), d);
+            d = group_sum<G>(d);
+            if constexpr (ES == 1)
+                d *= ks[j];
+            sc[j] = (MASK && !valid[j]) ? -INFINITY : d;
+        }
+        float mx = st.m[t];
+#pragma unroll
+        for (int j = 0; j < NP; j++)
+            mx = fmaxf(mx, sc[j]);
+        const float r = fast_exp2(st.m[t] - mx);
+        st.m[t] = mx;
+        st.l[t] *= r;
+#pragma unroll
+        for (int e = 0; e < C::EV; e++)
+            st.acc[t][e] *= r;
+#pragma unroll
+        for (int j = 0; j < NP; j++) {
+            const float p = fast_exp2(sc[j] - mx);
+            st.l[t] += p;
+            float pv = ES == 1 ? p * vs[j] : p;
+            if constexpr (MASK)
+                pv = valid[j] ? pv : 0.0f;
+#pragma unroll
+            for (int e = 0; e < C::EV; e++)
+                st.acc[t][e] = fmaf(pv, vf[j][e], st.acc[t][e]);
+        }
+    }
+}
+
+template <int ES, int DK, int DV, int REP, int G, int NP, int NW>
+__device__ __forceinline__ void attn_run(AttnState<ES, DK, DV, REP, G, NP, NW> &st, const AttnArgs &a,
+                                         const int32_t *pages, uint32_t g, int s0, int s1, int wave,
+                                         int grp, int li)
+{
+    using C = AttnCfg<ES, DK, DV, REP, G, NP, NW>;
+    constexpr int BLK = C::PW * NP;
+    const int start = (s0 / C::PW) * C::PW;
+    for (int it = start + wave * BLK; it < s1; it += NW * BLK) {
+        if (it >= s0 && it + BLK <= s1)
+            attn_step<false>(st, a, pages, g, it, s0, s1, grp, li);
+        else
+            attn_step<true>(st, a, pages, g, it, s0, s1, grp, li);
+    }
+}
+
+// Merge online-softmax state (m, l, acc) of another lane group / wave.
+__device__ __forceinline__ void merge_state(float &m, float &l, float *acc, int n, float m2, float l2,
+                                            const float *acc2)
+{
+    const float M = fmaxf(m, m2);
+    const float ca = fast_exp2(m - M), cb = fast_exp2(m2 - M);
+    l = l * ca + l2 * cb;
+    for (int e = 0; e < n; e++)
+        acc[e] = acc[e] * ca + acc2[e] * cb;
+    m = M;
+}
+
+template <int ES, int DK, int DV, int REP, int G, int NP, int NW>
+__global__ __launch_bounds__(64 * NW) void attend_kernel(AttnArgs a)
+{
+    using C = AttnCfg<ES, DK, DV, REP, G, NP, NW>;
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int grp = lane / G, li = lane % G;
+    const uint32_t nkv = a.pg.nkv;
+    const uint32_t unit = blockIdx.x;
+    const uint32_t row = unit / nkv, g = unit % nkv;
+    const uint32_t chunk = blockIdx.y;
+
+    const uint32_t seq = a.row_seq ? a.row_seq[row] : row;
+    const SeqDev sd = a.seqs[seq];
+    const int p = sd.pos + (a.row_t ? (int)a.row_t[row] : 0);
+    const Visible vis = visible(sd, p, (int)a.pg.window);
+    const int total = vis.n_sh + vis.n_own;
+    const int nchunks = (total + (int)a.chunk - 1) / (int)a.chunk;
+    if ((int)chunk >= nchunks)
+        return;
+    const int c0 = (int)chunk * (int)a.chunk, c1 = min(total, c0 + (int)a.chunk);
+
+    AttnState<ES, DK, DV, REP, G, NP, NW> st;
+#pragma unroll
+    for (int t = 0; t < REP; t++) {
+        const float *qh = a.q + ((uint64_t)row * a.nh + g * REP + t) * DK + li * C::EK;
+#pragma unroll
+        for (int e = 0; e < C::EK; e++)
+            st.qr[t][e] = qh[e] * a.qscale;
+        st.m[t] = -FLT_MAX;
+        st.l[t] = 0.0f;
+#pragma unroll
+        for (int e = 0; e < C::EV; e++)
+            st.acc[t][e] = 0.0f;
+    }
+
+    if (c0 < vis.n_sh)
+        attn_run(st, a, a.prefix_pages + (uint64_t)sd.prefix * a.pg.pages_per_seq, g, c0,
+                 min(c1, vis.n_sh), wave, grp, li);
+    if (c1 > vis.n_sh)
+        attn_run(st, a, a.page_table + (uint64_t)seq * a.pg.pages_per_seq, g,
+                 max(c0, vis.n_sh) - vis.n_sh, c1 - vis.n_sh, wave, grp, li);
+
+    // Merge the lane groups of this wave: lanes li, li+G, li+2G, ...
+#pragma unroll
+    for (int t = 0; t < REP; t++) {
+#pragma unroll
+        for (int o = G; o < 64; o <<= 1) {
+            float acc2[C::EV];
+            const float m2 = __shfl_xor(st.m[t], o, 64);
+            const float l2 = __shfl_xor(st.l[t], o, 64);
+#pragma unroll
+            for (int e = 0; e < C::EV; e++)
+                acc2[e] = __shfl_xor(st.acc[t][e], o, 64);
+            merge_state(st.m[t], st.l[t], st.acc[t], C::EV, m2, l2, acc2);
+        }
+    }
+
+    // Merge the waves through LDS: [wave][t][li][EV + 2].
+    constexpr int REC = C::EV + 2;
+    __shared__ float lds[NW][REP][G][REC];
+    if (NW > 1) {
+        if (lane < G) {
+#pragma unroll
+            for (int t = 0; t < REP; t++) {
+                float *r = lds[wave][t][li];
+                r[0] = st.m[t];
+                r[1] = st.l[t];
+#pragma unroll
+                for (int e = 0; e < C::EV; e++)
+                    r[2 + e] = st.acc[t][e];
+            }
+        }
+        __syncthreads();
+        if (wave != 0)
+            return;
+        if (lane < G) {
+#pragma unroll
+            for (int w = 1; w < NW; w++)
+#pragma unroll
+                for (int t = 0; t < REP; t++) {
+                    const float *r = lds[w][t][li];
+                    merge_state(st.m[t], st.l[t], st.acc[t], C::EV, r[0], r[1], r + 2);
+                }
+        }
+    }
+    if (lane >= G)
+        return;
+
+#pragma unroll
+    for (int t = 0; t < REP; t++) {
+        const uint32_t h = g * REP + t;
+        if (nchunks == 1) {
+            const float inv = 1.0f / st.l[t];
+            float *o = a.out + ((uint64_t)row * a.nh + h) * DV + li * C::EV;
+            const float *gt = a.gate ? a.gate + ((uint64_t)row * a.nh + h) * DV + li * C::EV : nullptr;
+#pragma unroll
+            for (int e = 0; e < C::EV; e++) {
+                float z = st.acc[t][e] * inv;
+                if (gt)
+                    z *= sigmoid_dev(gt[e]);
+                o[e] = z;
+            }
+        } else {
+            float *r = a.part + (((uint64_t)row * a.nh + h) * a.max_chunks + chunk) * (DV + 2);
+#pragma unroll
+            for (int e = 0; e < C::EV; e++)
+                r[li * C::EV + e] = st.acc[t][e];
+            if (li == 0) {
+                r[DV] = st.m[t];
+                r[DV + 1] = st.l[t];
+            }
+        }
+    }
+}
+
+// Split-KV merge: one wave per (row, head), lane = output element.
+template <int DV>
+__global__ __launch_bounds__(256) void combine_kernel(AttnArgs a)
+{
+    const int lane = threadIdx.x & 63;
+    const uint64_t wid = (uint64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (wid >= (uint64_t)a.rows * a.nh)
+        return;
+    const uint32_t row = (uint32_t)(wid / a.nh), h = (uint32_t)(wid % a.nh);
+    const uint32_t seq = a.row_seq ? a.row_seq[row] : row;
+    const SeqDev sd = a.seqs[seq];
+    const int p = sd.pos + (a.row_t ? (int)a.row_t[row] : 0);
+    const Visible vis = visible(sd, p, (int)a.pg.window);
+    const int nchunks = (vis.n_sh + vis.n_own + (int)a.chunk - 1) / (int)a.chunk;
+    if (nchunks <= 1)
+        return;
+    const float *base = a.part + ((uint64_t)row * a.nh + h) * a.max_chunks * (DV + 2);
+    float M = -FLT_MAX;
+    for (int c = 0; c < nchunks; c++)
+        M = fmaxf(M, base[(uint64_t)c * (DV + 2) + DV]);
+    float L = 0.0f, o = 0.0f;
+    for (int c = 0; c < nchunks; c++) {
+        const float *r = base + (uint64_t)c * (DV + 2);
+        const float w = fast_exp2(r[DV] - M);
+        L += r[DV + 1] * w;
+        if (lane < DV)
+            o += r[lane] * w;
+    }
+    if (lane < DV) {
+        float z = o * (1.0f / L);
+        if (a.gate)
+            z *= sigmoid_dev(a.gate[((uint64_t)row * a.nh + h) * DV + lane]);
+        a.out[((uint64_t)row * a.nh + h) * DV + lane] = z;
+    }
+}
+
+// ------------------------------------------------------------- KV append
+
+// One wave per (row, kv-head), lane = element. INT8: absmax over the row,
+// scale = absmax/127 (1 for a zero row), then the engine's store
+// (engine/src/nd_model.c:2426-2449 and kv_store_int8 :1819-1866) step for
+// step: r = 1/scale, y = x*r, e = fma(-scale, y, x), q = fma(e, r, y) (a plain
+// divide for |x| >= 1e30), clamp +-127, round half-to-even; a NaN quotient
+// (scale below 2^-127, where 1/scale overflows) stores 0 as the host build
+// does. F16: round to nearest even.
+__device__ __forceinline__ int8_t quant_code(float x, float scale, float r)
+{
+    float q;
+    if (x > -1e30f && x < 1e30f) {
+        const float y = x * r;
+        const float e = __builtin_fmaf(-scale, y, x);
+        q = __builtin_fmaf(e, r, y);
+    } else {
+        q = __fdiv_rn(x, scale);
+    }
+    if (q != q)
+        return 0;
+    q = q > 127.0f ? 127.0f : q;
+    q = q < -127.0f ? -127.0f : q;
+    return (int8_t)(int)__builtin_rintf(q);
+}
+
+template <int ES, int DK, int DV>
+__global__ __launch_bounds__(256) void append_kernel(AppendArgs a)
+{
+    static_assert(DK <= 64 && DV <= 64, "one lane per element");
+    const int lane = threadIdx.x & 63;
+    const uint64_t unit = (uint64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+    const uint32_t nkv = a.pg.nkv;
+    if (unit >= (uint64_t)a.rows * nkv)
+        return;
+    const uint32_t row = (uint32_t)(unit / nkv), g = (uint32_t)(unit % nkv);
+    const uint32_t seq = a.row_seq ? a.row_seq[row] : row;
+    const SeqDev sd = a.seqs[seq];
+    const int p = sd.pos + (a.row_t ? (int)a.row_t[row] : 0);
+    const int slot = own_slot(sd, p, (int)a.pg.window);
+    const int P = 1 << a.pg.log2_page;
+    const int32_t page = a.page_table[(uint64_t)seq * a.pg.pages_per_seq + (slot >> a.pg.log2_page)];
+    if (page < 0)
+        return;   // the host backs every appended slot; never taken
+    uint8_t *hb = a.pool + (uint64_t)page * a.pg.page_bytes + (uint64_t)g * a.pg.head_bytes;
+    const int off = slot & (P - 1);
+
+    const float kx = lane < DK ? a.k[((uint64_t)row * nkv + g) * DK + lane] : 0.0f;
+    const float vx = lane < DV ? a.v[((uint64_t)row * nkv + g) * DV + lane] : 0.0f;
+    if constexpr (ES == 2) {
+        if (lane < DK)
+            reinterpret_cast<_Float16 *>(hb + (uint64_t)off * DK * 2)[lane] = (_Float16)kx;
+        if (lane < DV)
+            reinterpret_cast<_Float16 *>(hb + (uint64_t)P * DK * 2 + (uint64_t)off * DV * 2)[lane] = (_Float16)vx;
+    } else {
+        const float ak = wave_max(fabsf(kx)), av = wave_max(fabsf(vx));
+        const float sk = ak > 0.0f ? __fdiv_rn(ak, 127.0f) : 1.0f;
+        const float sv = av > 0.0f ? __fdiv_rn(av, 127.0f) : 1.0f;
+        const float rk = __fdiv_rn(1.0f, sk), rv = __fdiv_rn(1.0f, sv);
+        if (lane < DK)
+            reinterpret_cast<int8_t *>(hb + (uint64_t)off * DK)[lane] = quant_code(kx, sk, rk);
+        if (lane < DV)
+            reinterpret_cast<int8_t *>(hb + (uint64_t)P * DK + (uint64_t)off * DV)[lane] = quant_code(vx, sv, rv);
+        if (lane == 0) {
+            float *sc = reinterpret_cast<float *>(hb + (uint64_t)P * (DK + DV));
+            sc[off] = sk;
+            sc[P + off] = sv;
+        }
+    }
+}
+
+// ------------------------------------------------------ copies and staging
+
+// Bytes of one slot of one kv-head: K row, V row (+ the two scales).
+template <int ES, int DK, int DV>
+__device__ __forceinline__ void copy_slot(uint8_t *dhb, int doff, const uint8_t *shb, int soff, int P,
+                                          int tid, int nthr)
+{
+    const uint32_t *sk = reinterpret_cast<const uint32_t *>(shb + (uint64_t)soff * DK * ES);
+    uint32_t *dk = reinterpret_cast<uint32_t *>(dhb + (uint64_t)doff * DK * ES);
+    for (int i = tid; i < DK * ES / 4; i += nthr)
+        dk[i] = sk[i];
+    const uint32_t *sv = reinterpret_cast<const uint32_t *>(shb + (uint64_t)P * DK * ES + (uint64_t)soff * DV * ES);
+    uint32_t *dv = reinterpret_cast<uint32_t *>(dhb + (uint64_t)P * DK * ES + (uint64_t)doff * DV * ES);
+    for (int i = tid; i < DV * ES / 4; i += nthr)
+        dv[i] = sv[i];
+    if (ES == 1 && tid == 0) {
+        const float *ss = reinterpret_cast<const float *>(shb + (uint64_t)P * (DK + DV));
+        float *ds = reinterpret_cast<float *>(dhb + (uint64_t)P * (DK + DV));
+        ds[doff] = ss[soff];
+        ds[P + doff] = ss[P + soff];
+    }
+}
+
+// grid (count, n_layers), one block per (slot, layer), heads in a loop.
+template <int ES, int DK, int DV>
+__global__ __launch_bounds__(64) void copy_kernel(CopyArgs a)
+{
+    const uint32_t i = blockIdx.x, l = blockIdx.y;
+    if (i >= a.count || l >= a.n_layers)
+        return;
+    const int P = 1 << a.pg.log2_page;
+    const uint32_t ss = a.src_slot0 + i, ds = a.dst_slot0 + i;
+    const int32_t spg = a.src_pages[ss >> a.pg.log2_page], dpg = a.dst_pages[ds >> a.pg.log2_page];
+    if (spg < 0 || dpg < 0)
+        return;
+    const uint8_t *sp = a.pool + l * a.pg.layer_bytes + (uint64_t)spg * a.pg.page_bytes;
+    uint8_t *dp = a.pool + l * a.pg.layer_bytes + (uint64_t)dpg * a.pg.page_bytes;
+    for (uint32_t g = 0; g < a.pg.nkv; g++)
+        copy_slot<ES, DK, DV>(dp + g * a.pg.head_bytes, ds & (P - 1), sp + g * a.pg.head_bytes,
+                              ss & (P - 1), P, threadIdx.x, blockDim.x);
+}
+
+// One block per staged position: pool <-> [count][nkv][d] staging.
+template <int ES, int DK, int DV, bool SCATTER>
+__global__ __launch_bounds__(64) void stage_kernel(StageArgs a)
+{
+    const uint32_t i = blockIdx.x;
+    if (i >= a.count)
+        return;
+    const int P = 1 << a.pg.log2_page;
+    const int off = (int)a.slot_in_page[i];
+    uint8_t *pp = a.pool + (uint64_t)a.pages_for_slot[i] * a.pg.page_bytes;
+    for (uint32_t g = 0; g < a.pg.nkv; g++) {
+        uint8_t *hb = pp + g * a.pg.head_bytes;
+        uint8_t *kr = hb + (uint64_t)off * DK * ES;
+        uint8_t *vr = hb + (uint64_t)P * DK * ES + (uint64_t)off * DV * ES;
+        uint8_t *sk = a.stage_k + ((uint64_t)i * a.pg.nkv + g) * DK * ES;
+        uint8_t *sv = a.stage_v + ((uint64_t)i * a.pg.nkv + g) * DV * ES;
+        for (int b = threadIdx.x; b < DK * ES; b += blockDim.x) {
+            if (SCATTER)
+                kr[b] = sk[b];
+            else
+                sk[b] = kr[b];
+        }
+        for (int b = threadIdx.x; b < DV * ES; b += blockDim.x) {
+            if (SCATTER)
+                vr[b] = sv[b];
+            else
+                sv[b] = vr[b];
+        }
+        if (threadIdx.x == 0) {
+            float *sc = reinterpret_cast<float *>(hb + (uint64_t)P * (DK + DV));
+            float *dks = a.stage_ks + (uint64_t)i * a.pg.nkv + g;
+            float *dvs = a.stage_vs + (uint64_t)i * a.pg.nkv + g;
+            if (ES == 1) {
+                if (SCATTER) {
+                    sc[off] = *dks;
+                    sc[P + off] = *dvs;
+                } else {
+                    *dks = sc[off];
+                    *dvs = sc[P + off];
+                }
+            } else if (!SCATTER) {
+                *dks = 1.0f;
+                *dvs = 1.0f;
+            }
+        }
+    }
+}
+
+// pos += n for the listed sequences (the engine's pos++, nd_model.c:3094).
+__global__ __launch_bounds__(256) void advance_kernel(SeqDev *seqs, const uint32_t *seq_list, uint32_t nseq,
+                                                      uint32_t n)
+{
+    const uint32_t b = blockIdx.x * blockDim.x + threadIdx.x;
+    if (b < nseq)
+        seqs[seq_list ? seq_list[b] : b].pos += (int32_t)n;
+}
+
+// --------------------------------------------------------- synthetic data
+
+__device__ __forceinline__ uint64_t splitmix64(uint64_t z)
+{
+    z += 0x9E3779B97F4A7C15ull;
+    z = (z ^ (z >> 30)) * 0xBF58476D1CE4E5B9ull;
+    z = (z ^ (z >> 27)) * 0x94D049BB133111EBull;
+    return z ^ (z >> 31);
+}
+
+// N(0,1) from one 64-bit hash: Box-Muller on two 24-bit uniforms.
+__device__ __forceinline__ float normal_from(uint64_t h)
+{
+    const float u1 = ((float)(uint32_t)(h >> 40) + 0.5f) * (1.0f / 16777216.0f);
+    const float u2 = (float)(uint32_t)(h & 0xFFFFFFu) * (1.0f / 16777216.0f);
+    return sqrtf(-2.0f * __logf(u1)) * __cosf(6.28318530717958647f * u2);
+}
+
+__global__ __launch_bounds__(256) void fill_normal_kernel(void *dst, uint64_t n, int dtype, uint64_t seed,
+                                                          float scale)
+{
+    for (uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n;
+         i += (uint64_t)gridDim.x * blockDim.x) {
+        const float x = normal_from(splitmix64(seed ^ splitmix64(i))) * scale;
+        if (dtype == 0)
+            static_cast<float *>(dst)[i] = x;
+        else
+            static_cast<_Float16 *>(dst)[i] = (_Float16)x;
+    }
+}
+
+// Fill own slots [0, n_own) of every listed sequence (fp16). The value of
+// (layer, seq, slot, head, element) depends on those indices only.
+template <int DK, int DV>
+__global__ __launch_bounds__(256) void fill_kv_kernel(FillKvArgs a)
+{
+    const uint32_t bi = blockIdx.x, l = blockIdx.y;
+    if (bi >= a.nseq || l >= a.n_layers)
+        return;
+    const uint32_t seq = a.seq_list ? a.seq_list[bi] : bi;
+    const SeqDev sd = a.seqs[seq];
+    if (sd.pos <= 0)
+        return;
+    const Visible vis = visible(sd, sd.pos - 1, (int)a.pg.window);
+    const int P = 1 << a.pg.log2_page;
+    const uint32_t nkv = a.pg.nkv;
+    const uint64_t per_slot = (uint64_t)nkv * (DK + DV);
+    const uint64_t total = (uint64_t)vis.n_own * per_slot;
+    const uint64_t key = a.seed ^ splitmix64(((uint64_t)l << 40) ^ ((uint64_t)seq << 8) ^ 0x5a5aull);
+    uint8_t *lp = a.pool + l * a.pg.layer_bytes;
+    const int32_t *pages = a.page_table + (uint64_t)seq * a.pg.pages_per_seq;
+    for (uint64_t i = threadIdx.x; i < total; i += blockDim.x) {
+        const uint32_t slot = (uint32_t)(i / per_slot);
+        const uint32_t rem = (uint32_t)(i % per_slot);
+        const uint32_t g = rem / (DK + DV), e = rem % (DK + DV);
+        const int32_t pg = pages[slot >> a.pg.log2_page];
+        if (pg < 0)
+            continue;
+        uint8_t *hb = lp + (uint64_t)pg * a.pg.page_bytes + g * a.pg.head_bytes;
+        const int off = slot & (P - 1);
+        const _Float16 x = (_Float16)normal_from(splitmix64(key + i));
+        if (e < DK)
+            reinterpret_cast<_Float16 *>(hb + (uint64_t)off * DK * 2)[e] = x;
+        else
+            reinterpret_cast<_Float16 *>(hb + (uint64_t)P * DK * 2 + (uint64_t)off * DV * 2)[e - DK] = x;
+    }
+}
+
+// ------------------------------------------------------------- dispatch
+
+// Lanes per KV position: 16-byte slices of a 64-element row.
+template <int ES>
+constexpr int lanes_per_pos() { return ES == 2 ? 8 : 4; }
+
+constexpr int ATT_NW = 4;
+constexpr int ATT_NP = 2;
+
+#define NDA_FOR_GEOMETRIES(X) \
+    X(2, 64, 64, 1) X(2, 64, 64, 2) X(2, 64, 64, 4) X(2, 64, 64, 6) X(2, 64, 64, 8) \
+    X(2, 48, 64, 1) X(2, 48, 64, 2) X(2, 48, 64, 6) \
+    X(1, 64, 64, 1) X(1, 64, 64, 2) X(1, 64, 64, 4) X(1, 64, 64, 6) X(1, 64, 64, 8) \
+    X(1, 48, 64, 1) X(1, 48, 64, 2) X(1, 48, 64, 6)
+
+static inline int es_of(const Geo &g) { return g.kv_f16 ? 2 : 1; }
+
+bool geometry_supported(const Geo &g)
+{
+#define X(ES, DK, DV, REP) if (es_of(g) == ES && g.dk == DK && g.dv == DV && g.rep == REP) return true;
+    NDA_FOR_GEOMETRIES(X)
+#undef X
+    return false;
+}
+
+static inline unsigned blocks_for(uint64_t waves) { return (unsigned)((waves + 3) / 4); }
+
+hipError_t launch_attend(const Geo &g, const AttnArgs &a, hipStream_t s)
+{
+    if (a.rows == 0)
+        return hipSuccess;
+    dim3 grid(a.rows * a.pg.nkv, a.max_chunks);
+#define X(ES, DK, DV, REP)                                                                      \
+    if (es_of(g) == ES && g.dk == DK && g.dv == DV && g.rep == REP) {                          \
+        hipLaunchKernelGGL((attend_kernel<ES, DK, DV, REP, lanes_per_pos<ES>(), ATT_NP, ATT_NW>), \
+                           grid, dim3(64 * ATT_NW), 0, s, a);                                   \
+        return hipGetLastError();                                                               \
+    }
+    NDA_FOR_GEOMETRIES(X)
+#undef X
+    return hipErrorNotSupported;
+}
+
+hipError_t launch_combine(const Geo &g, const AttnArgs &a, hipStream_t s)
+{
+    if (a.rows == 0 || a.max_chunks <= 1)
+        return hipSuccess;
+    if (g.dv != 64)
+        return hipErrorNotSupported;
+    hipLaunchKernelGGL(combine_kernel<64>, dim3(blocks_for((uint64_t)a.rows * a.nh)), dim3(256), 0, s, a);
+    return hipGetLastError();
+}
+
+#define NDA_FOR_SHAPES(X) X(2, 64, 64) X(2, 48, 64) X(1, 64, 64) X(1, 48, 64)
+
+hipError_t launch_append(const Geo &g, const AppendArgs &a, hipStream_t s)
+{
+    if (a.rows == 0)
+        return hipSuccess;
+    const unsigned nb = blocks_for((uint64_t)a.rows * a.pg.nkv);
+#define X(ES, DK, DV)                                                                          \
+    if (es_of(g) == ES && g.dk == DK && g.dv == DV) {                                         \
+        hipLaunchKernelGGL((append_kernel<ES, DK, DV>), dim3(nb), dim3(256), 0, s, a);         \
+        return hipGetLastError();                                                              \
+    }
+    NDA_FOR_SHAPES(X)
+#undef X
+    return hipErrorNotSupported;
+}
+
+hipError_t launch_copy(const Geo &g, const CopyArgs &a, hipStream_t s)
+{
+    if (a.count == 0 || a.n_layers == 0)
+        return hipSuccess;
+#define X(ES, DK, DV)                                                                          \
+    if (es_of(g) == ES && g.dk == DK && g.dv == DV) {                                         \
+        hipLaunchKernelGGL((copy_kernel<ES, DK, DV>), dim3(a.count, a.n_layers), dim3(64), 0, s, a); \
+        return hipGetLastError();                                                              \
+    }
+    NDA_FOR_SHAPES(X)
+#undef X
+    return hipErrorNotSupported;
+}
+
+static hipError_t launch_stage(const Geo &g, const StageArgs &a, hipStream_t s, bool scatter)
+{
+    if (a.count == 0)
+        return hipSuccess;
+#define X(ES, DK, DV)                                                                          \
+    if (es_of(g) == ES && g.dk == DK && g.dv == DV) {                                         \
+        if (scatter)                                                                           \
+            hipLaunchKernelGGL((stage_kernel<ES, DK, DV, true>), dim3(a.count), dim3(64), 0, s, a); \
+        else                                                                                   \
+            hipLaunchKernelGGL((stage_kernel<ES, DK, DV, false>), dim3(a.count), dim3(64), 0, s, a); \
+        return hipGetLastError();                                                              \
+    }
+    NDA_FOR_SHAPES(X)
+#undef X
+    return hipErrorNotSupported;
+}
+
+hipError_t launch_gather(const Geo &g, const StageArgs &a, hipStream_t s) { return launch_stage(g, a, s, false); }
+hipError_t launch_scatter(const Geo &g, const StageArgs &a, hipStream_t s) { return launch_stage(g, a, s, true); }
+
+hipError_t launch_fill_kv(const Geo &g, const FillKvArgs &a, hipStream_t s)
+{
+    if (!g.kv_f16)
+        return hipErrorNotSupported;
+    if (a.nseq == 0 || a.n_layers == 0)
+        return hipSuccess;
+    dim3 grid(a.nseq, a.n_layers);
+    if (g.dk == 64 && g.dv == 64)
+        hipLaunchKernelGGL((fill_kv_kernel<64, 64>), grid, dim3(256), 0, s, a);
+    else if (g.dk == 48 && g.dv == 64)
+        hipLaunchKernelGGL((fill_kv_kernel<48, 64>), grid, dim3(256), 0, s, a);
+    else
+        return hipErrorNotSupported;
+    return hipGetLastError();
+}
+
+hipError_t launch_advance(SeqDev *seqs, const uint32_t *seq_list, uint32_t nseq, uint32_t n, hipStream_t s)
+{
+    if (nseq == 0)
+        return hipSuccess;
+    hipLaunchKernelGGL(advance_kernel, dim3((nseq + 255) / 256), dim3(256), 0, s, seqs, seq_list, nseq, n);
+    return hipGetLastError();
+}
+
+hipError_t launch_fill_normal(void *dst, uint64_t n, int dtype, uint64_t seed, float scale, hipStream_t s)
+{
+    if (n == 0)
+        return hipSuccess;
+    uint64_t nb = (n + 255) / 256;
+    if (nb > 65536)
+        nb = 65536;
+    hipLaunchKernelGGL(fill_normal_kernel, dim3((unsigned)nb), dim3(256), 0, s, dst, n, dtype, seed, scale);
+    return hipGetLastError();
+}
+
+} // namespace nda

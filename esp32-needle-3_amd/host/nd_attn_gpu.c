@@ -1,0 +1,230 @@
+/* nd_attn_gpu.c - the engine-side C shim over libndattn (see nd_attn_gpu.h).
+ *
+ * One engine session = sequence 0 of a one-sequence context. Snapshot and
+ * prefix caches map onto the library's shared prefix segments: a snapshot
+ * builds a segment from the live KV, a saved prefix holds a reference to one,
+ * and a restore attaches the session to it (a pointer switch on the device,
+ * where the engine memcpy's every live slot back, nd_model.c:1543-1553).
+ */
+#include "nd_attn_gpu.h"
+
+#include <stdlib.h>
+#include <string.h>
+
+struct nd_gpu_model {
+    nda_ctx *ctx;
+    uint32_t nh, nkv, qk_hd, v_hd, window;
+    int has_snap;
+    int32_t snap_prefix;      /* segment holding the snapshot's KV, -1 none */
+    uint32_t snap_pos;
+    /* Segments whose prefix handle was freed while the session still read
+     * them; released once the session detaches. */
+    int32_t orphan[64];
+    uint32_t n_orphan;
+    /* device staging for one token */
+    float *d_q, *d_k, *d_v, *d_gate, *d_out;
+};
+
+struct nd_gpu_prefix {
+    const nd_gpu_model *owner;
+    int32_t segment;
+    uint32_t pos;
+};
+
+nd_gpu_model *nd_gpu_open(uint32_t n_layers, uint32_t n_heads, uint32_t n_kv_heads,
+                          uint32_t qk_head_dim, uint32_t v_head_dim, uint32_t window,
+                          uint32_t kv_dtype, uint32_t max_prefixes)
+{
+    nda_config cfg;
+    nd_gpu_model *m = (nd_gpu_model *)calloc(1, sizeof *m);
+    if (!m)
+        return NULL;
+    memset(&cfg, 0, sizeof cfg);
+    cfg.n_layers = n_layers;
+    cfg.n_heads = n_heads;
+    cfg.n_kv_heads = n_kv_heads;
+    cfg.qk_head_dim = qk_head_dim;
+    cfg.v_head_dim = v_head_dim;
+    cfg.window = window;
+    cfg.page_size = 16;
+    cfg.kv_dtype = kv_dtype;
+    cfg.max_seqs = 1;
+    cfg.max_prefixes = max_prefixes ? max_prefixes + 1u : 8u;
+    if (nda_create(&cfg, &m->ctx) != NDA_OK) {
+        free(m);
+        return NULL;
+    }
+    m->nh = n_heads;
+    m->nkv = n_kv_heads;
+    m->qk_hd = qk_head_dim;
+    m->v_hd = v_head_dim;
+    m->window = window;
+    m->snap_prefix = -1;
+    if (nda_dev_alloc((void **)&m->d_q, sizeof(float) * n_heads * qk_head_dim) ||
+        nda_dev_alloc((void **)&m->d_k, sizeof(float) * n_kv_heads * qk_head_dim) ||
+        nda_dev_alloc((void **)&m->d_v, sizeof(float) * n_kv_heads * v_head_dim) ||
+        nda_dev_alloc((void **)&m->d_gate, sizeof(float) * n_heads * v_head_dim) ||
+        nda_dev_alloc((void **)&m->d_out, sizeof(float) * n_heads * v_head_dim)) {
+        nd_gpu_close(m);
+        return NULL;
+    }
+    return m;
+}
+
+void nd_gpu_close(nd_gpu_model *m)
+{
+    if (!m)
+        return;
+    nda_dev_free(m->d_q);
+    nda_dev_free(m->d_k);
+    nda_dev_free(m->d_v);
+    nda_dev_free(m->d_gate);
+    nda_dev_free(m->d_out);
+    nda_destroy(m->ctx);
+    free(m);
+}
+
+nda_ctx *nd_gpu_ctx(nd_gpu_model *m) { return m->ctx; }
+
+uint32_t nd_gpu_pos(const nd_gpu_model *m)
+{
+    uint32_t pos = 0;
+    nda_seq_state(m->ctx, 0, &pos, NULL, NULL);
+    return pos;
+}
+
+uint32_t nd_gpu_n_sink(const nd_gpu_model *m)
+{
+    uint32_t n = 0;
+    nda_seq_state(m->ctx, 0, NULL, &n, NULL);
+    return n;
+}
+
+/* Free orphaned segments the session no longer reads. */
+static void sweep_orphans(nd_gpu_model *m)
+{
+    uint32_t i, kept = 0;
+    for (i = 0; i < m->n_orphan; i++)
+        if (nda_prefix_free(m->ctx, m->orphan[i]) != NDA_OK)
+            m->orphan[kept++] = m->orphan[i];
+    m->n_orphan = kept;
+}
+
+static void orphan(nd_gpu_model *m, int32_t seg)
+{
+    if (seg < 0)
+        return;
+    if (nda_prefix_free(m->ctx, seg) == NDA_OK)
+        return;
+    if (m->n_orphan < sizeof m->orphan / sizeof m->orphan[0])
+        m->orphan[m->n_orphan++] = seg;
+}
+
+void nd_gpu_reset(nd_gpu_model *m)
+{
+    nda_seq_reset(m->ctx, 0);
+    orphan(m, m->snap_prefix);
+    m->snap_prefix = -1;
+    m->has_snap = 0;
+    sweep_orphans(m);
+}
+
+void nd_gpu_set_sink(nd_gpu_model *m, uint32_t n)
+{
+    nda_seq_set_sink(m->ctx, 0, n);
+}
+
+/* The snapshot pins pos as sinks and keeps the KV up to pos in a segment;
+ * the session then continues attached to that segment. */
+int nd_gpu_snapshot(nd_gpu_model *m)
+{
+    int32_t id = -1;
+    int32_t old = m->snap_prefix;
+    if (nda_prefix_build(m->ctx, 0, &id, NULL) != NDA_OK)
+        return -1;
+    if (nda_seq_attach(m->ctx, 0, id, NULL) != NDA_OK) {
+        nda_prefix_free(m->ctx, id);
+        return -1;
+    }
+    orphan(m, old);
+    sweep_orphans(m);
+    m->snap_prefix = id;
+    m->snap_pos = nd_gpu_pos(m);
+    m->has_snap = 1;
+    return 0;
+}
+
+void nd_gpu_rewind(nd_gpu_model *m)
+{
+    if (!m->has_snap) {
+        nd_gpu_reset(m);
+        return;
+    }
+    nda_seq_rewind(m->ctx, 0);
+}
+
+nd_gpu_prefix *nd_gpu_prefix_save(nd_gpu_model *m)
+{
+    nd_gpu_prefix *p;
+    if (!m->has_snap || nd_gpu_pos(m) != m->snap_pos)
+        return NULL;
+    p = (nd_gpu_prefix *)malloc(sizeof *p);
+    if (!p)
+        return NULL;
+    p->owner = m;
+    p->segment = m->snap_prefix;
+    p->pos = m->snap_pos;
+    m->snap_prefix = -1;      /* the saved prefix now owns the segment */
+    return p;
+}
+
+int nd_gpu_prefix_restore(nd_gpu_model *m, const nd_gpu_prefix *p)
+{
+    int32_t old;
+    if (!p || p->owner != m)
+        return -1;
+    old = m->snap_prefix;
+    if (nda_seq_attach(m->ctx, 0, p->segment, NULL) != NDA_OK)
+        return -1;
+    if (old != p->segment)
+        orphan(m, old);
+    m->snap_prefix = -1;
+    sweep_orphans(m);
+    m->has_snap = 1;
+    m->snap_pos = p->pos;
+    return 0;
+}
+
+void nd_gpu_prefix_free(nd_gpu_prefix *p)
+{
+    if (!p)
+        return;
+    /* A segment the session still reads is released when it detaches. */
+    orphan((nd_gpu_model *)p->owner, p->segment);
+    free(p);
+}
+
+int nd_gpu_attention(nd_gpu_model *m, uint32_t li, const float *q, const float *k,
+                     const float *v, const float *gate, float *out)
+{
+    int rc;
+    if (nda_h2d(m->d_q, q, sizeof(float) * m->nh * m->qk_hd) ||
+        nda_h2d(m->d_k, k, sizeof(float) * m->nkv * m->qk_hd) ||
+        nda_h2d(m->d_v, v, sizeof(float) * m->nkv * m->v_hd))
+        return NDA_ERR_HIP;
+    if (gate && nda_h2d(m->d_gate, gate, sizeof(float) * m->nh * m->v_hd))
+        return NDA_ERR_HIP;
+    rc = nda_step(m->ctx, li, 1, NULL, m->d_q, m->d_k, m->d_v, gate ? m->d_gate : NULL,
+                  m->d_out, NULL);
+    if (rc)
+        return rc;
+    rc = nda_sync(m->ctx, NULL);
+    if (rc)
+        return rc;
+    return nda_d2h(out, m->d_out, sizeof(float) * m->nh * m->v_hd);
+}
+
+void nd_gpu_step_end(nd_gpu_model *m)
+{
+    nda_advance(m->ctx, 1, NULL, 1, NULL);
+}

@@ -1,0 +1,209 @@
+/* nda.h - C ABI of libndattn: the Needle engine's attention / KV-cache hot
+ * path on MI355X (gfx950).
+ *
+ * The engine (iammrduncan/esp32-needle-3) keeps one session's KV cache as a
+ * per-layer ring of `window` int8 slots with an fp32 scale per (slot, kv-head)
+ * and attends with attn_heads behind the nd_parallel_rows row seam. This
+ * library holds the KV of many independent sequences in paged HBM and runs
+ * the same operations batched across them. Every entry point below names the
+ * reference interface it replaces.
+ *
+ * Conventions (engine/include/nd_model.h:191-236, nd_model.c:760-767):
+ *   - every function returns 0 on success or a negative NDA_ERR_* code; no C++
+ *     exception or HIP error crosses the ABI; nda_last_error() explains the
+ *     last failure on a context;
+ *   - q, k, v, gate and out are DEVICE pointers (fp32) unless stated;
+ *     seq_ids and n_tokens are HOST arrays (NULL seq_ids = sequences 0..nseq-1);
+ *   - stream is a hipStream_t passed as void* (NULL = the default stream);
+ *   - a context is used by one host thread at a time; calls on it are serial.
+ *     Kernels launched by one call write disjoint (sequence, head) outputs.
+ */
+#ifndef NDA_H
+#define NDA_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define NDA_OK               0
+#define NDA_ERR_ARG         -1   /* bad argument or geometry */
+#define NDA_ERR_NOMEM       -2   /* device memory or page pool exhausted */
+#define NDA_ERR_HIP         -3   /* a HIP runtime call failed */
+#define NDA_ERR_RANGE       -4   /* position / length outside what the window holds */
+#define NDA_ERR_STATE       -5   /* call not valid in the sequence's current state */
+#define NDA_ERR_UNSUPPORTED -6   /* geometry has no compiled kernel */
+#define NDA_ERR_NODEV       -7   /* no usable gfx950 device */
+
+/* KV element types. INT8: symmetric int8 codes + fp32 scale per (slot,
+ * kv-head), the engine's own format (nd_model.h:17-20, :134-137). F16: IEEE
+ * half, scale 1 (the fp16 variant of the same path). */
+#define NDA_KV_INT8 0
+#define NDA_KV_F16  1
+
+typedef struct nda_ctx nda_ctx;
+
+/* Geometry and capacities. Mirrors the engine's model shape fields
+ * (nd_model.h:89-90: n_layers, n_heads, n_kv_heads, qk_head_dim, v_head_dim,
+ * window) plus the batched-serving capacities the engine does not have. */
+typedef struct {
+    uint32_t n_layers;
+    uint32_t n_heads;        /* query heads */
+    uint32_t n_kv_heads;     /* n_heads % n_kv_heads == 0 (GQA) */
+    uint32_t qk_head_dim;    /* 48 or 64 */
+    uint32_t v_head_dim;     /* 64 */
+    uint32_t window;         /* KV slots per sequence per layer (sinks + ring) */
+    uint32_t page_size;      /* positions per page: 16, 32 or 64 (0 = 16) */
+    uint32_t kv_dtype;       /* NDA_KV_INT8 | NDA_KV_F16 */
+    uint32_t max_seqs;       /* sequence slots */
+    uint32_t max_prefixes;   /* shared prefix segments (0 = 16) */
+    uint64_t max_pages;      /* page pool size per layer (0 = enough for every
+                                sequence's full window plus the prefixes) */
+    uint32_t split_chunk;    /* positions per split-KV work item (0 = auto) */
+    uint32_t reserved;
+} nda_config;
+
+/* ---- lifecycle ---- */
+
+/* Allocates the paged KV pool and tables on the current HIP device.
+ * Replaces the KV part of nd_model_open (nd_model.c:1142-1144, :1195-1198). */
+int  nda_create(const nda_config *cfg, nda_ctx **out);
+void nda_destroy(nda_ctx *ctx);
+const char *nda_last_error(const nda_ctx *ctx);
+/* Bytes of device memory the context holds (pool + tables + scratch). */
+uint64_t nda_device_bytes(const nda_ctx *ctx);
+
+/* ---- per-sequence session state (host-side mirror, uploaded lazily) ---- */
+
+/* nd_model_reset (nd_model.c:1557-1581), KV part: pos = 0, n_sink = 0, no
+ * snapshot, detached from any shared prefix, pages returned to the pool. */
+int nda_seq_reset(nda_ctx *ctx, uint32_t seq);
+/* nd_model_set_sink (nd_model.c:1314-1321): pin the first n positions,
+ * clamped to window - 64. */
+int nda_seq_set_sink(nda_ctx *ctx, uint32_t seq, uint32_t n);
+int nda_seq_state(const nda_ctx *ctx, uint32_t seq, uint32_t *pos, uint32_t *n_sink,
+                  int32_t *prefix_id);
+/* Sets pos directly (a sequence whose KV was written through nda_kv_write). */
+int nda_seq_set_pos(nda_ctx *ctx, uint32_t seq, uint32_t pos);
+/* Back the slots of positions [pos, pos + n) with pages now, so that later
+ * appends allocate nothing. No counterpart in the engine (its cache is one
+ * flat allocation). */
+int nda_seq_reserve(nda_ctx *ctx, uint32_t seq, uint32_t n);
+/* End of a token for these sequences: pos += n. The engine does pos++ at the
+ * end of nd_model_step_hidden (nd_model.c:3094), after every layer. The
+ * device copy is incremented in stream order (no upload). */
+int nda_advance(nda_ctx *ctx, uint32_t nseq, const uint32_t *seq_ids, uint32_t n, void *stream);
+
+/* ---- shared prefix (schema) segments ---- */
+
+/* nd_model_snapshot + nd_model_prefix_save (nd_model.c:1395-1434, :1531-1541):
+ * pins the sequence's current positions as sinks and copies its live KV into
+ * a read-only segment any number of sequences can then share. */
+int nda_prefix_build(nda_ctx *ctx, uint32_t seq, int32_t *prefix_id, void *stream);
+/* nd_model_prefix_restore (nd_model.c:1543-1553): the sequence resumes at the
+ * prefix's position with its sinks read from the shared segment - no copy of
+ * the pinned positions. Positions past the sink clamp are copied into the
+ * sequence's own ring, as the engine restores them. */
+int nda_seq_attach(nda_ctx *ctx, uint32_t seq, int32_t prefix_id, void *stream);
+/* nd_model_rewind (nd_model.c:1436-1460), KV part: back to the attached
+ * prefix's position (or reset when none). */
+int nda_seq_rewind(nda_ctx *ctx, uint32_t seq);
+/* nd_model_prefix_free. Fails with NDA_ERR_STATE while sequences use it. */
+int nda_prefix_free(nda_ctx *ctx, int32_t prefix_id);
+
+/* ---- the hot path ---- */
+
+/* Store each sequence's K/V for its current position into layer `layer`:
+ * k [nseq][n_kv_heads][qk_head_dim], v [nseq][n_kv_heads][v_head_dim] fp32.
+ * INT8 quantises per kv-head exactly as the engine does (absmax/127 scale,
+ * correctly rounded divide, clamp, round-half-even; nd_model.c:2426-2449 and
+ * kv_store_int8 :1819-1866); F16 rounds to nearest even. Allocates a page
+ * when the slot's page is not backed yet. */
+int nda_kv_append(nda_ctx *ctx, uint32_t layer, uint32_t nseq, const uint32_t *seq_ids,
+                  const float *k, const float *v, void *stream);
+
+/* Single-token attention at each sequence's current position over its sinks
+ * and recent ring, GQA, online softmax, gated emit:
+ * q [nseq][n_heads][qk_head_dim], gate [nseq][n_heads][v_head_dim] or NULL
+ * (no output gate), out [nseq][n_heads][v_head_dim] fp32.
+ * Replaces nd_parallel_rows(attn_heads, &actx, nh) in attention()
+ * (nd_model.c:2451-2483, attn_heads :2105-2359). */
+int nda_decode(nda_ctx *ctx, uint32_t layer, uint32_t nseq, const uint32_t *seq_ids,
+               const float *q, const float *gate, float *out, void *stream);
+
+/* nda_kv_append + nda_decode in one launch sequence (the order attention()
+ * runs them: store first, the current token is attended). */
+int nda_step(nda_ctx *ctx, uint32_t layer, uint32_t nseq, const uint32_t *seq_ids,
+             const float *q, const float *k, const float *v, const float *gate,
+             float *out, void *stream);
+
+/* Causal prefill of n_tokens[b] new tokens per sequence at positions
+ * [pos, pos + n): appends their K/V, then token t attends exactly what a
+ * decode at position pos + t would (the engine prefills by repeated
+ * nd_model_step_hidden: esp32/main/main.c:233-234, :312-315). Inputs are
+ * packed token-major per sequence, sequence b's rows starting at
+ * sum(n_tokens[0..b)): q [T][n_heads][qk_head_dim], k [T][n_kv_heads][qk_head_dim],
+ * v [T][n_kv_heads][v_head_dim], gate/out [T][n_heads][v_head_dim].
+ * Requires pos + n <= window (no ring wrap inside the chunk): NDA_ERR_RANGE
+ * otherwise. Does not advance pos. */
+int nda_prefill(nda_ctx *ctx, uint32_t layer, uint32_t nseq, const uint32_t *seq_ids,
+                const uint32_t *n_tokens, const float *q, const float *k, const float *v,
+                const float *gate, float *out, void *stream);
+
+int nda_sync(nda_ctx *ctx, void *stream);
+
+/* ---- inspection (tests, tools) ---- */
+
+/* Copies the stored K/V of `count` consecutive positions starting at
+ * position p0 of one sequence and layer to HOST buffers:
+ * k [count][n_kv_heads][qk_head_dim] and v [...][v_head_dim] in the KV
+ * element type (int8 or fp16 bits), k_scale/v_scale [count][n_kv_heads]
+ * (NULL allowed; all 1.0 for F16). Positions must be currently visible. */
+int nda_kv_read(nda_ctx *ctx, uint32_t layer, uint32_t seq, uint32_t p0, uint32_t count,
+                void *k, void *v, float *k_scale, float *v_scale);
+/* The reverse: write stored-format K/V for positions [p0, p0+count) (pages are
+ * allocated as needed). Used to load an existing cache. */
+int nda_kv_write(nda_ctx *ctx, uint32_t layer, uint32_t seq, uint32_t p0, uint32_t count,
+                 const void *k, const void *v, const float *k_scale, const float *v_scale);
+
+/* Fills the stored K/V of positions [0, pos) of every listed sequence, every
+ * layer, with N(0,1) values from a counter-based generator keyed by (seed,
+ * layer, sequence, position, head, element) - independent of page placement.
+ * F16 only (INT8: NDA_ERR_UNSUPPORTED). Synthetic benchmark data. */
+int nda_kv_fill_normal(nda_ctx *ctx, uint32_t nseq, const uint32_t *seq_ids, uint64_t seed,
+                       void *stream);
+
+/* ---- device plumbing for hosts without their own allocator ---- */
+int nda_dev_alloc(void **ptr, size_t bytes);
+int nda_dev_free(void *ptr);
+int nda_h2d(void *dst, const void *src, size_t bytes);
+int nda_d2h(void *dst, const void *src, size_t bytes);
+int nda_memset(void *dst, int value, size_t bytes);
+/* dst[i] = N(0,1) * scale as fp32 (dtype 0) or fp16 (dtype 1), i < n;
+ * counter-based (seed, i). */
+int nda_fill_normal(void *dst, uint64_t n, int dtype, uint64_t seed, float scale, void *stream);
+int nda_stream_create(void **stream);
+int nda_stream_destroy(void *stream);
+int nda_device_sync(void);
+/* Device name and compute-unit count of the current device. */
+int nda_device_info(char *name, size_t name_len, int *cu_count);
+
+/* ---- kernel timing (the engine's ND_PROFILE phases, nd_model.h:238-269) ----
+ * When enabled, every launch is bracketed by HIP events on its own stream and
+ * the elapsed device time is accumulated per kernel kind. */
+#define NDA_K_APPEND  0   /* ND_P_KVST */
+#define NDA_K_DECODE  1   /* ND_P_ATTN */
+#define NDA_K_COMBINE 2   /* split-KV merge */
+#define NDA_K_PREFILL 3
+#define NDA_K_COUNT   4
+int nda_prof_enable(nda_ctx *ctx, int on);
+/* Synchronises outstanding timed launches, then returns per kind the summed
+ * milliseconds and launch counts; resets when reset != 0. */
+int nda_prof_read(nda_ctx *ctx, double ms[NDA_K_COUNT], uint64_t launches[NDA_K_COUNT], int reset);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* NDA_H */

@@ -1,0 +1,143 @@
+/* nd_oracle.h - CPU restatement of the Needle engine's attention / KV-cache path.
+ *
+ * TEST INFRASTRUCTURE ONLY. This is the checker the HIP library is compared
+ * against; only tests/, the package smoke check and bench.py's cpu_baseline leg
+ * may load it. The product (libndattn) never links or calls it.
+ *
+ * Every function restates the behaviour of the reference engine
+ * (iammrduncan/esp32-needle-3) in code written for this project; each cites the
+ * reference file:line it follows. Floating-point evaluation order matches the
+ * reference statement for statement (build with -ffp-contract=off), so on the
+ * int8 path the outputs are bit-identical to the reference's host build. That
+ * claim is pinned by tests against a harness compiled from the reference's own
+ * sources (oracle/ref_harness.c), not by reading this file.
+ *
+ * Pinning status per function:
+ *   ndo_kv_slot, ndo_clamp_sink           - pinned: reference harness + brute force
+ *   ndo_expf, ndo_expf_pair, ndo_sigmoid  - pinned: reference harness + exp_pairs fixture + libm bound
+ *   ndo_kv_quant_row                      - pinned: reference harness (bit-exact), closed form
+ *   ndo_attend (int8)                     - pinned: reference harness (bit-exact), float64 textbook
+ *   ndo_attend (fp16)                     - pinned: float64 textbook + special cases (the reference
+ *                                           has no fp16 KV path)
+ *   session/prefix functions              - pinned: reference harness session replay
+ */
+#ifndef ND_ORACLE_H
+#define ND_ORACLE_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Recent slots kept free by the sink clamp (nd_model.c:1311-1312). */
+#define NDO_MIN_RECENT 64u
+
+enum { NDO_KV_INT8 = 0, NDO_KV_F16 = 1 };
+
+/* ---- scalar primitives ---- */
+uint32_t ndo_kv_slot(uint32_t window, uint32_t n_sink, uint32_t p);
+uint32_t ndo_clamp_sink(uint32_t window, uint32_t n);
+float    ndo_expf(float x);
+void     ndo_expf_pair(float x0, float x1, float *r0, float *r1);
+float    ndo_sigmoid(float x);
+float    ndo_f16_to_f32(uint16_t h);
+uint16_t ndo_f32_to_f16(float f);                 /* round to nearest even */
+
+/* Per-(slot, kv-head) symmetric int8 row quantisation: returns the scale and
+ * writes n codes. nd_model.c:2426-2449 (absmax, scale) + :1819-1866 (store). */
+float    ndo_kv_quant_row(const float *x, uint32_t n, int8_t *dst);
+/* The store alone, for a given scale (nd_model.c:1819-1866). */
+void     ndo_kv_store_int8(int8_t *dst, const float *src, uint32_t n, float scale);
+
+/* ---- one layer's attention over an explicit KV view ----
+ *
+ * The KV view is the engine's per-layer slot array: slot s of kv-head g holds
+ * k at k + (s*nkv + g)*qk_hd (int8 or fp16 by kv_dtype), its scale at
+ * k_scale[s*nkv + g] (int8 only), and likewise for v. */
+typedef struct {
+    uint32_t nh, nkv, qk_hd, v_hd, window, n_sink, pos;
+    int      kv_dtype;
+    const void  *k, *v;
+    const float *k_scale, *v_scale;
+} ndo_kv_view;
+
+/* attn_heads for all query heads + the attention() dispatch arithmetic
+ * (nd_model.c:2105-2359, :2451-2483). q [nh*qk_hd], gate [nh*v_hd] or NULL
+ * (NULL: no output gate), out [nh*v_hd]. */
+void ndo_attend(const ndo_kv_view *kv, const float *q, const float *gate, float *out);
+
+/* Same, over an explicit position list instead of the sink/ring runs: every
+ * listed slot is visited in order, pairs restarting at each run boundary given
+ * in run_len[] (sum = n_pos). Used for the shared-prefix layout checks. */
+void ndo_attend_runs(const ndo_kv_view *kv, const uint32_t *slots, const uint32_t *run_len,
+                     uint32_t n_runs, const float *q, const float *gate, float *out);
+
+/* Float64 textbook attention over the same (dequantised) KV, positions listed
+ * explicitly: out = softmax(q.k * scale_k / sqrt(qk_hd)) . (v * scale_v) * sigmoid(gate). */
+void ndo_attend_f64(const ndo_kv_view *kv, const uint32_t *slots, uint32_t n_pos,
+                    const float *q, const float *gate, double *out);
+
+/* ---- session: the engine's KV state for one sequence (nd_model.h:132-148) ---- */
+typedef struct {
+    uint32_t n_layers, nh, nkv, qk_hd, v_hd, window;
+    int      kv_dtype;
+    uint32_t pos, n_sink;
+    int      has_snap;
+    uint32_t snap_pos;
+    void    *k_cache, *v_cache;       /* [layer][window][nkv*hd] int8 or fp16 */
+    float   *k_scale, *v_scale;       /* [layer][window][nkv] (int8 only)   */
+} ndo_session;
+
+int  ndo_session_init(ndo_session *s, uint32_t n_layers, uint32_t nh, uint32_t nkv,
+                      uint32_t qk_hd, uint32_t v_hd, uint32_t window, int kv_dtype);
+void ndo_session_free(ndo_session *s);
+void ndo_reset(ndo_session *s);                      /* nd_model.c:1557-1581 (KV part) */
+void ndo_set_sink(ndo_session *s, uint32_t n);       /* nd_model.c:1314-1321 */
+int  ndo_snapshot(ndo_session *s);                   /* nd_model.c:1395-1434 (KV part) */
+void ndo_rewind(ndo_session *s);                     /* nd_model.c:1436-1460 */
+
+typedef struct ndo_prefix ndo_prefix;
+ndo_prefix *ndo_prefix_save(ndo_session *s);        /* nd_model.c:1531-1541 */
+int  ndo_prefix_restore(ndo_session *s, const ndo_prefix *p); /* nd_model.c:1543-1553 */
+void ndo_prefix_free(ndo_prefix *p);
+
+/* Store this position's K/V for layer li (k [nkv*qk_hd], v [nkv*v_hd] fp32;
+ * int8: quantised per kv-head, fp16: rounded to nearest even) and attend.
+ * nd_model.c:2426-2483. Does not advance pos. */
+void ndo_attention(ndo_session *s, uint32_t li, const float *q, const float *k,
+                   const float *v, const float *gate, float *out);
+void ndo_kv_store(ndo_session *s, uint32_t li, const float *k, const float *v);
+void ndo_attend_session(const ndo_session *s, uint32_t li, const float *q,
+                        const float *gate, float *out);
+void ndo_step_end(ndo_session *s);                   /* pos++ (nd_model.c:3094) */
+void ndo_view(const ndo_session *s, uint32_t li, ndo_kv_view *kv);
+
+/* ---- CPU baseline: batched fp16 decode, threaded over sequences ----
+ *
+ * Independent sequences b in [0, nseq): K/V in a contiguous per-sequence slot
+ * array k[b] = kbase + koff[b] (elements), window = len[b] slots, n_sink 0,
+ * pos = len[b]-1. The new token's K/V (k_new/v_new fp32) is stored at slot
+ * len[b]-1 first, as the engine does, then attended. nthreads workers take whole
+ * sequences (the nd_parallel_rows seam, nd_quant.h:213-230). */
+typedef struct {
+    uint32_t nseq, nh, nkv, qk_hd, v_hd;
+    const uint32_t *len;
+    const uint64_t *koff, *voff;
+    uint16_t *kbase, *vbase;
+    const float *q, *k_new, *v_new, *gate;   /* per sequence: nh*qk_hd, nkv*qk_hd, nkv*v_hd, nh*v_hd */
+    float *out;                              /* nseq*nh*v_hd */
+} ndo_batch_f16;
+
+int ndo_decode_batch_f16(const ndo_batch_f16 *b, int nthreads);
+
+/* Causal prefill restated as the engine runs it: one token at a time through
+ * ndo_attention (esp32/main/main.c:312-315). q/k/v/gate/out are [n][...]. */
+void ndo_prefill_tokens(ndo_session *s, uint32_t li, uint32_t n, const float *q,
+                        const float *k, const float *v, const float *gate, float *out);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

@@ -1,0 +1,158 @@
+"""Writes tests/golden/golden.npz from the reference engine's own attention
+code (oracle/_ref/libndref.so, compiled by oracle/ref.mk from the reference
+sources). Run in the build container, where the reference tree exists:
+
+    make -C oracle && python tests/golden/gen_golden.py
+
+Inputs are integer-derived (detgen.py), so the fixture stores seeds and
+outputs only. The exp_pairs vectors take their inputs from the reference's
+own fixture esp32/main/exp_pairs.h (1024 real softmax argument pairs),
+read here as data.
+"""
+import os
+import re
+import sys
+
+import numpy as np
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+REPO = os.path.dirname(os.path.dirname(HERE))
+sys.path.insert(0, os.path.join(REPO, "oracle"))
+sys.path.insert(0, HERE)
+import ctypes as C  # noqa: E402
+
+import ndoracle as O  # noqa: E402
+from detgen import Stream, det_normal  # noqa: E402
+
+REF = os.environ.get("REF", "/root/reference")
+
+# Session scripts. Each event: ("tok", gated) store+attend one token on every
+# layer then pos++, ("snap",), ("sink", n), ("save", slot), ("restore", slot),
+# ("reset",). Outputs are recorded for the token steps listed in `record`.
+SESSIONS = {
+    # one layer, MHA 8x64, 213-token pinned prefix + 16 prompt tokens
+    "cfg1": dict(geom=(1, 8, 8, 64, 64, 256), seed=101,
+                 script=[("tok", True)] * 213 + [("snap",)] + [("tok", True)] * 16,
+                 record=list(range(213, 229))),
+    # the archive's shapes: 12 q / 2 kv heads, qk 48, v 64, window 384, ring wraps
+    "engine": dict(geom=(2, 12, 2, 48, 64, 384), seed=202,
+                   script=[("tok", True)] * 200 + [("snap",)] + [("tok", True)] * 260,
+                   record=list(range(0, 460, 23)) + [459]),
+    # GQA rep 4, tiny window with 10 sinks: many wraps, one ungated token in 3
+    "wrap": dict(geom=(1, 8, 2, 64, 64, 100), seed=303,
+                 script=[("tok", True)] * 10 + [("sink", 10)] +
+                        [("tok", i % 3 != 0) for i in range(250)],
+                 record=list(range(0, 260, 13)) + [259]),
+    # window <= 64: the sink clamp pins nothing; plain sliding window
+    "small": dict(geom=(1, 4, 4, 64, 64, 40), seed=404,
+                  script=[("tok", True)] * 5 + [("sink", 5)] + [("tok", True)] * 60,
+                  record=list(range(0, 65, 8)) + [64]),
+    # nd_ptest's flow: two 2-token prefixes restored alternately
+    "ptest": dict(geom=(1, 12, 2, 48, 64, 384), seed=505,
+                  script=[("reset",), ("tok", True), ("tok", True), ("snap",), ("save", 0), ("tok", True),
+                          ("reset",), ("tok", True), ("tok", True), ("snap",), ("save", 1), ("tok", True),
+                          ("restore", 0), ("tok", True), ("restore", 1), ("tok", True),
+                          ("restore", 0), ("tok", True), ("restore", 1), ("tok", True)],
+                  record="all"),
+    # config 2's shape on 2 layers: causal prefill of 256 tokens, window 256
+    "prefill": dict(geom=(2, 8, 8, 64, 64, 256), seed=606,
+                    script=[("tok", True)] * 256, record=list(range(0, 256, 17)) + [255]),
+}
+
+
+def run_session(S, spec):
+    L, nh, nkv, qk, vd, W = spec["geom"]
+    st = Stream(spec["seed"])
+    outs, saved = [], {}
+    ntok = 0
+    rec = spec["record"]
+    for ev in spec["script"]:
+        if ev[0] == "tok":
+            for li in range(L):
+                q = st.take(nh * qk)
+                k = st.take(nkv * qk)
+                v = st.take(nkv * vd)
+                g = st.take(nh * vd) if ev[1] else None
+                o = S.attention(li, q, k, v, g)
+                if rec == "all" or ntok in rec:
+                    outs.append(o.copy())
+            S.step_end()
+            ntok += 1
+        elif ev[0] == "snap":
+            assert S.snapshot() == 0
+        elif ev[0] == "sink":
+            S.set_sink(ev[1])
+        elif ev[0] == "save":
+            saved[ev[1]] = S.prefix_save()
+            assert saved[ev[1]]
+        elif ev[0] == "restore":
+            assert S.prefix_restore(saved[ev[1]]) == 0
+        elif ev[0] == "reset":
+            S.reset()
+    return np.stack(outs), saved
+
+
+def exp_pairs_inputs():
+    text = open(os.path.join(REF, "esp32/main/exp_pairs.h")).read()
+    body = text[text.index("{", text.index("kb_exp_pairs")) + 1: text.index("};")]
+    vals = [float(x.rstrip("f")) for x in re.findall(r"-?\d+\.?\d*(?:e-?\d+)?f", body)]
+    return np.array(vals, np.float32)
+
+
+def main():
+    R = O.ref()
+    out = {}
+    # exp on the reference's captured softmax arguments, paired form
+    xp = exp_pairs_inputs()
+    assert xp.size == 2048, xp.size
+    r0, r1 = C.c_float(), C.c_float()
+    ep = np.zeros_like(xp)
+    for i in range(0, xp.size, 2):
+        R.ref_expf_pair(float(xp[i]), float(xp[i + 1]), C.byref(r0), C.byref(r1))
+        ep[i], ep[i + 1] = r0.value, r1.value
+    out["exp_pairs_in"], out["exp_pairs_out"] = xp, ep
+    # exp / sigmoid over a sweep including the clamps and rounding boundaries
+    xs = np.concatenate([np.linspace(-100, 100, 4001, dtype=np.float32),
+                         np.array([-88.0, 88.0, -88.00001, 88.00001, 0.0, -0.0, 0.5, -0.5,
+                                   0.34657359, -0.34657359, 1e-30, -1e-30], np.float32),
+                         det_normal(7, 2000) * 8]).astype(np.float32)
+    out["exp_in"] = xs
+    out["exp_out"] = np.array([R.ref_expf(float(x)) for x in xs], np.float32)
+    out["sig_out"] = np.array([R.ref_sigmoid(float(x)) for x in xs], np.float32)
+    # int8 store: random rows, exact ties, zero rows, +-absmax, tiny values
+    rows = [det_normal(11, 64), det_normal(12, 48) * 1000, np.zeros(64, np.float32),
+            np.array([127 * 0.5 + 0.5 * i for i in range(64)], np.float32) / 127,
+            np.array([(i - 32) + 0.5 for i in range(64)], np.float32),
+            np.array([1e-38 * (i - 32) for i in range(64)], np.float32),
+            det_normal(13, 64) * 1e-20]
+    codes, scales = [], []
+    for r in rows:
+        r = np.ascontiguousarray(r, np.float32)
+        amax = float(np.max(np.abs(r)))
+        sc = np.float32(amax) / np.float32(127.0) if amax > 0 else np.float32(1.0)
+        d = np.zeros(r.size, np.int8)
+        R.ref_kv_store_int8(d, r, r.size, float(sc))
+        codes.append(np.pad(d, (0, 64 - d.size)))
+        scales.append(sc)
+    out["store_rows"] = np.stack([np.pad(r, (0, 64 - r.size)) for r in rows]).astype(np.float32)
+    out["store_len"] = np.array([r.size for r in rows], np.int32)
+    out["store_codes"] = np.stack(codes)
+    out["store_scales"] = np.array(scales, np.float32)
+    # attention sessions on the reference
+    for name, spec in SESSIONS.items():
+        S = O.RefSession(*spec["geom"])
+        o, saved = run_session(S, spec)
+        out["sess_" + name] = o.astype(np.float32)
+        k, v, ks, vs = S.cache()
+        out["sess_" + name + "_kvsum"] = np.array(
+            [int(k.astype(np.int64).sum()), int(v.astype(np.int64).sum()),
+             int(np.abs(k.astype(np.int64)).sum()), int(np.abs(v.astype(np.int64)).sum())], np.int64)
+        for p in saved.values():
+            O.ref().ref_prefix_free(p)
+        S.close()
+    np.savez_compressed(os.path.join(HERE, "golden.npz"), **out)
+    print("wrote", os.path.join(HERE, "golden.npz"), {k: v.shape for k, v in out.items()})
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,468 @@
+"""GPU parity: libndattn (through its C ABI and the C engine shim) against the
+oracle on identical inputs. Output tolerance max |delta| <= 1e-3 (fp32
+accumulate, the bar the engine's attention is held to); stored int8 codes and
+scales bit-exact."""
+import os
+import sys
+
+import numpy as np
+import pytest
+
+import ndoracle as O
+
+pytestmark = pytest.mark.gpu
+
+TOL = 1e-3
+
+
+def nda():
+    import ndattn
+    return ndattn
+
+
+def say(*a):
+    print("[gpu-case]", *a, flush=True)
+    sys.stdout.flush()
+
+
+def maxdiff(a, b):
+    return float(np.abs(np.asarray(a, np.float64) - np.asarray(b, np.float64)).max())
+
+
+# ------------------------------------------------------------ engine session
+
+def replay(geom, script, seed, kv_dtype=O.KV_INT8, scale=1.0):
+    """Same token stream through the oracle session and the GPU shim."""
+    N = nda()
+    rng = np.random.default_rng(seed)
+    L, nh, nkv, qk, vd, W = geom
+    o = O.OracleSession(*geom, kv_dtype=kv_dtype)
+    g = N.GpuSession(*geom, kv_dtype=kv_dtype)
+    worst = 0.0
+    saved_o, saved_g = {}, {}
+    outs = []
+    for ev in script:
+        if ev[0] == "tok":
+            for li in range(L):
+                q = (rng.standard_normal(nh * qk) * scale).astype(np.float32)
+                k = (rng.standard_normal(nkv * qk) * scale).astype(np.float32)
+                v = rng.standard_normal(nkv * vd).astype(np.float32)
+                gt = rng.standard_normal(nh * vd).astype(np.float32) if ev[1] else None
+                a = o.attention(li, q, k, v, gt)
+                b = g.attention(li, q, k, v, gt)
+                worst = max(worst, maxdiff(a, b))
+                outs.append(b)
+            o.step_end()
+            g.step_end()
+        elif ev[0] == "snap":
+            assert o.snapshot() == 0 and g.snapshot() == 0
+        elif ev[0] == "sink":
+            o.set_sink(ev[1])
+            g.set_sink(ev[1])
+        elif ev[0] == "save":
+            saved_o[ev[1]], saved_g[ev[1]] = o.prefix_save(), g.prefix_save()
+            assert saved_o[ev[1]] and saved_g[ev[1]]
+        elif ev[0] == "restore":
+            assert o.prefix_restore(saved_o[ev[1]]) == 0
+            assert g.prefix_restore(saved_g[ev[1]]) == 0
+        elif ev[0] == "rewind":
+            o.rewind()
+            g.rewind()
+        elif ev[0] == "reset":
+            o.reset()
+            g.reset()
+        assert (g.pos, g.n_sink) == (o.pos, o.n_sink), ev
+    return o, g, worst, outs
+
+
+def check_cache(o, g, layers, positions):
+    """GPU-stored codes and scales of every listed position == oracle's."""
+    N = nda()
+    ctx = N.Context.__new__(N.Context)
+    ctx.h = N.vp(N.host_lib().nd_gpu_ctx(g.m))
+    L, nh, nkv, qk, vd, W = o.geom
+    ctx.cfg = N.Config(L, nh, nkv, qk, vd, W, 16, o.kv_dtype, 1, 0, 0, 0, 0)
+    ok, ov, oks, ovs = o.cache()
+    for li in layers:
+        for p in positions:
+            sl = O.lib().ndo_kv_slot(W, o.n_sink, p)
+            k, v, ks, vs = ctx.kv_read(li, 0, p, 1)
+            assert np.array_equal(k[0], ok[li, sl]), (li, p)
+            assert np.array_equal(v[0], ov[li, sl]), (li, p)
+            if o.kv_dtype == O.KV_INT8:
+                assert np.array_equal(ks[0].view(np.uint32), oks[li, sl].view(np.uint32)), (li, p)
+                assert np.array_equal(vs[0].view(np.uint32), ovs[li, sl].view(np.uint32)), (li, p)
+    ctx.h = N.vp()   # borrowed handle: the shim owns it
+
+
+def test_cfg1_prefix_plus_prompt_int8():
+    """One layer, MHA 8x64, 213 pinned schema positions + 16 prompt tokens,
+    int8 KV as the engine stores it."""
+    say("cfg1 int8 session 229 tokens")
+    script = [("tok", True)] * 213 + [("snap",)] + [("tok", True)] * 16
+    o, g, worst, _ = replay((1, 8, 8, 64, 64, 256), script, seed=1)
+    assert worst <= TOL, worst
+    check_cache(o, g, [0], range(229))
+
+
+def test_engine_shapes_ring_wrap_int8():
+    """The archive's geometry (12 q / 2 kv heads, qk 48, v 64, window 384)
+    with 200 pinned positions and a ring that wraps."""
+    say("engine shapes 460 tokens ring wrap")
+    script = [("tok", True)] * 200 + [("snap",)] + [("tok", i % 4 != 0) for i in range(260)]
+    o, g, worst, _ = replay((2, 12, 2, 48, 64, 384), script, seed=2, scale=2.0)
+    assert worst <= TOL, worst
+    check_cache(o, g, [0, 1], list(range(200)) + list(range(460 - 184, 460)))
+
+
+def test_sliding_window_and_small_window():
+    say("small windows")
+    script = [("tok", True)] * 10 + [("sink", 10)] + [("tok", True)] * 150
+    o, g, worst, _ = replay((1, 8, 2, 64, 64, 100), script, seed=3)
+    assert worst <= TOL, worst
+    script = [("tok", True)] * 5 + [("sink", 5)] + [("tok", True)] * 60
+    o, g, worst, _ = replay((1, 4, 4, 64, 64, 40), script, seed=4)
+    assert worst <= TOL, worst
+    assert g.n_sink == 0
+
+
+def test_prefix_switching_reproduces():
+    """host/nd_ptest.c's flow: two prefixes restored alternately give
+    identical outputs for the same next token."""
+    say("prefix switching")
+    N = nda()
+    geom = (1, 12, 2, 48, 64, 384)
+    rng = np.random.default_rng(5)
+    L, nh, nkv, qk, vd, W = geom
+    g = N.GpuSession(*geom)
+    o = O.OracleSession(*geom)
+    pre_g, pre_o, expect = [], [], []
+    toks = [[rng.standard_normal(n).astype(np.float32) for n in (nh * qk, nkv * qk, nkv * vd, nh * vd)]
+            for _ in range(5)]
+    for i in range(2):
+        g.reset()
+        o.reset()
+        for t in (toks[i], toks[i + 2]):
+            g.attention(0, *t)
+            o.attention(0, *t)
+            g.step_end()
+            o.step_end()
+        assert g.snapshot() == 0 and o.snapshot() == 0
+        pre_g.append(g.prefix_save())
+        pre_o.append(o.prefix_save())
+        expect.append(g.attention(0, *toks[4]))
+        assert maxdiff(expect[-1], o.attention(0, *toks[4])) <= TOL
+    for n in range(4):
+        i = n % 2
+        assert g.prefix_restore(pre_g[i]) == 0
+        assert (g.pos, g.n_sink) == (2, 2)
+        got = g.attention(0, *toks[4])
+        assert np.array_equal(got.view(np.uint32), expect[i].view(np.uint32))
+    for p in pre_g:
+        g.prefix_free(p)
+
+
+def test_rewind_and_long_outliers():
+    say("rewind + outliers")
+    script = ([("tok", True)] * 30 + [("snap",), ("save", 0)] + [("tok", True)] * 50 + [("rewind",)] +
+              [("tok", True)] * 20 + [("restore", 0)] + [("tok", False)] * 10)
+    o, g, worst, _ = replay((1, 12, 2, 48, 64, 384), script, seed=6, scale=3.0)
+    assert worst <= TOL, worst
+
+
+# ----------------------------------------------------------- batched decode
+
+def _ragged_decode(kv_dtype, lens, window, seed, nh=8, nkv=8, qk=64, vd=64, split_chunk=0,
+                   outlier_p=0.0, gated=True):
+    N = nda()
+    rng = np.random.default_rng(seed)
+    B = len(lens)
+    ctx = N.Context(1, nh, nkv, qk, vd, window, kv_dtype=kv_dtype, max_seqs=B, split_chunk=split_chunk)
+    # history positions [0, L-1) written in stored format, new token appended
+    hist = []
+    for b, L in enumerate(lens):
+        kf = rng.standard_normal((L - 1, nkv, qk)).astype(np.float32)
+        if outlier_p:
+            mask = rng.random((L - 1, nkv)) < outlier_p
+            kf[mask] *= np.float32(8.0)
+        vf = rng.standard_normal((L - 1, nkv, vd)).astype(np.float32)
+        if kv_dtype == O.KV_F16:
+            k, v, ks, vs = O.f32_to_f16_bits(kf), O.f32_to_f16_bits(vf), None, None
+        else:
+            k = np.zeros(kf.shape, np.int8)
+            v = np.zeros(vf.shape, np.int8)
+            ks = np.zeros((L - 1, nkv), np.float32)
+            vs = np.zeros((L - 1, nkv), np.float32)
+            for p in range(L - 1):
+                for gg in range(nkv):
+                    ks[p, gg] = O.lib().ndo_kv_quant_row(np.ascontiguousarray(kf[p, gg]), qk, k[p, gg])
+                    vs[p, gg] = O.lib().ndo_kv_quant_row(np.ascontiguousarray(vf[p, gg]), vd, v[p, gg])
+        if L > 1:
+            ctx.kv_write(0, b, 0, k, v, ks, vs)
+        ctx.seq_set_pos(b, L - 1)
+        hist.append(L)
+    q = rng.standard_normal((B, nh, qk)).astype(np.float32)
+    kn = rng.standard_normal((B, nkv, qk)).astype(np.float32)
+    vn = rng.standard_normal((B, nkv, vd)).astype(np.float32)
+    gate = rng.standard_normal((B, nh, vd)).astype(np.float32) if gated else None
+    dq, dk, dv = N.DevBuf.from_array(q), N.DevBuf.from_array(kn), N.DevBuf.from_array(vn)
+    dg = N.DevBuf.from_array(gate) if gated else None
+    dout = N.DevBuf(B * nh * vd * 4)
+    ctx.step(0, B, dq, dk, dv, dout, gate=dg)
+    ctx.sync()
+    out = dout.to_array(np.float32, (B, nh, vd))
+    worst = 0.0
+    for b, L in enumerate(lens):
+        k, v, ks, vs = ctx.kv_read(0, b, 0, L)
+        kv = O.kv_view(k, v, ks if kv_dtype == O.KV_INT8 else None, vs if kv_dtype == O.KV_INT8 else None,
+                       nh, L, 0, L - 1, kv_dtype)
+        want = O.attend_view(kv, q[b].ravel(), None if gate is None else gate[b].ravel())
+        worst = max(worst, maxdiff(out[b].ravel(), want))
+        # the appended token was stored as the oracle stores it
+        if kv_dtype == O.KV_F16:
+            assert np.array_equal(k[L - 1], O.f32_to_f16_bits(kn[b]))
+        else:
+            for gg in range(nkv):
+                c = np.zeros(qk, np.int8)
+                sc = O.lib().ndo_kv_quant_row(np.ascontiguousarray(kn[b, gg]), qk, c)
+                assert np.array_equal(c, k[L - 1, gg]) and np.float32(sc) == ks[L - 1, gg]
+    return worst
+
+
+@pytest.mark.parametrize("kv_dtype", [O.KV_F16, O.KV_INT8])
+def test_batched_ragged_decode(kv_dtype):
+    say("ragged decode dtype", kv_dtype)
+    rng = np.random.default_rng(7)
+    lens = [1, 2, 3, 15, 16, 17, 31, 64, 213, 229] + list(rng.integers(1, 1025, 22))
+    worst = _ragged_decode(kv_dtype, lens, 1024, seed=8)
+    assert worst <= TOL, worst
+
+
+def test_gqa_decode_engine_shapes():
+    say("gqa decode 12/2 48/64")
+    lens = [1, 5, 100, 384, 383, 200]
+    for dt in (O.KV_INT8, O.KV_F16):
+        worst = _ragged_decode(dt, lens, 384, seed=9, nh=12, nkv=2, qk=48, vd=64)
+        assert worst <= TOL, worst
+
+
+def test_split_kv_long_context_with_outliers():
+    """Split-KV with the LSE merge, lengths past the split size, 8-sigma keys."""
+    say("split-kv long context")
+    lens = [8192, 5000, 1025, 1024, 513, 7]
+    worst = _ragged_decode(O.KV_F16, lens, 8192, seed=10, split_chunk=512, outlier_p=1e-3)
+    assert worst <= TOL, worst
+
+
+def test_no_gate_and_rep_variants():
+    say("rep variants")
+    for nh, nkv in ((8, 4), (8, 1), (16, 2), (6, 1)):
+        worst = _ragged_decode(O.KV_F16, [3, 77, 300], 512, seed=nh * 10 + nkv, nh=nh, nkv=nkv, gated=False)
+        assert worst <= TOL, (nh, nkv, worst)
+
+
+# ------------------------------------------------------ prefill and prefixes
+
+def test_cfg2_causal_prefill_int8_all_layers():
+    """8 layers x 256-token causal prefill through nda_prefill against the
+    engine's token-by-token prefill; codes bit-exact."""
+    say("cfg2 prefill 8x256 int8")
+    N = nda()
+    Lyr, nh, nkv, d, S = 8, 8, 8, 64, 256
+    rng = np.random.default_rng(11)
+    ctx = N.Context(Lyr, nh, nkv, d, d, S, kv_dtype=O.KV_INT8, max_seqs=1)
+    o = O.OracleSession(Lyr, nh, nkv, d, d, S, O.KV_INT8)
+    worst = 0.0
+    for li in range(Lyr):
+        q = rng.standard_normal((S, nh, d)).astype(np.float32)
+        k = rng.standard_normal((S, nkv, d)).astype(np.float32)
+        v = rng.standard_normal((S, nkv, d)).astype(np.float32)
+        want = np.zeros((S, nh * d), np.float32)
+        O.lib().ndo_prefill_tokens(O.C.byref(o.s), li, S, q.ctypes.data, k.ctypes.data, v.ctypes.data,
+                                   None, want.ctypes.data)
+        dq, dk, dv = N.DevBuf.from_array(q), N.DevBuf.from_array(k), N.DevBuf.from_array(v)
+        dout = N.DevBuf(S * nh * d * 4)
+        ctx.prefill(li, [S], dq, dk, dv, dout)
+        ctx.sync()
+        got = dout.to_array(np.float32, (S, nh * d))
+        worst = max(worst, maxdiff(got, want))
+        kk, vv, ks, vs = ctx.kv_read(li, 0, 0, S)
+        ok, ov, oks, ovs = o.cache()
+        assert np.array_equal(kk, ok[li]) and np.array_equal(vv, ov[li])
+        assert np.array_equal(ks, oks[li]) and np.array_equal(vs, ovs[li])
+    assert worst <= TOL, worst
+
+
+def _views_for(ctx, li, seq, pos, nh, dtype):
+    k, v, ks, vs = ctx.kv_read(li, seq, 0, pos + 1)
+    if dtype == O.KV_F16:
+        ks = vs = None
+    return O.kv_view(k, v, ks, vs, nh, pos + 1, 0, pos, dtype), (k, v, ks, vs)
+
+
+@pytest.mark.parametrize("kv_dtype", [O.KV_F16, O.KV_INT8])
+def test_shared_prefix_prefill_then_decode(kv_dtype):
+    """Config 4's structure at small batch: one 213-token prefix built once,
+    shared by every sequence; ragged causal suffixes; decode steps."""
+    say("shared prefix dtype", kv_dtype)
+    N = nda()
+    nh = nkv = 8
+    d, W, B, npre = 64, 384, 12, 213
+    rng = np.random.default_rng(12)
+    ctx = N.Context(2, nh, nkv, d, d, W, kv_dtype=kv_dtype, max_seqs=B + 1)
+    # build the prefix on sequence B by prefilling it
+    for li in range(2):
+        q = rng.standard_normal((npre, nh, d)).astype(np.float32)
+        k = rng.standard_normal((npre, nkv, d)).astype(np.float32)
+        v = rng.standard_normal((npre, nkv, d)).astype(np.float32)
+        dout = N.DevBuf(npre * nh * d * 4)
+        ctx.prefill(li, [npre], N.DevBuf.from_array(q), N.DevBuf.from_array(k), N.DevBuf.from_array(v),
+                    dout, seq_ids=[B])
+    ctx.advance(1, [B], npre)
+    pid = ctx.prefix_build(B)
+    for b in range(B):
+        ctx.seq_attach(b, pid)
+        assert ctx.seq_state(b) == (npre, npre, pid)
+    with pytest.raises(N.NdaError):
+        ctx.prefix_free(pid)       # attached: refused
+    n = rng.integers(32, 65, B)
+    worst = 0.0
+    for li in range(2):
+        T = int(n.sum())
+        q = rng.standard_normal((T, nh, d)).astype(np.float32)
+        k = rng.standard_normal((T, nkv, d)).astype(np.float32)
+        v = rng.standard_normal((T, nkv, d)).astype(np.float32)
+        g = rng.standard_normal((T, nh, d)).astype(np.float32)
+        dout = N.DevBuf(T * nh * d * 4)
+        ctx.prefill(li, n, N.DevBuf.from_array(q), N.DevBuf.from_array(k), N.DevBuf.from_array(v), dout,
+                    gate=N.DevBuf.from_array(g), seq_ids=list(range(B)))
+        ctx.sync()
+        got = dout.to_array(np.float32, (T, nh * d))
+        r = 0
+        for b in range(B):
+            view, keep = _views_for(ctx, li, b, npre + int(n[b]) - 1, nh, kv_dtype)
+            for t in range(int(n[b])):
+                pos = npre + t
+                slots = np.arange(pos + 1)
+                want = O.attend_runs(view, slots, [npre, pos + 1 - npre], q[r], g[r])
+                worst = max(worst, maxdiff(got[r], want))
+                r += 1
+    for b in range(B):
+        ctx.advance(1, [b], int(n[b]))
+    for step in range(3):
+        for li in range(2):
+            q = rng.standard_normal((B, nh, d)).astype(np.float32)
+            k = rng.standard_normal((B, nkv, d)).astype(np.float32)
+            v = rng.standard_normal((B, nkv, d)).astype(np.float32)
+            dout = N.DevBuf(B * nh * d * 4)
+            ctx.step(li, B, N.DevBuf.from_array(q), N.DevBuf.from_array(k), N.DevBuf.from_array(v), dout)
+            ctx.sync()
+            got = dout.to_array(np.float32, (B, nh * d))
+            for b in range(B):
+                pos = ctx.seq_state(b)[0]
+                view, keep = _views_for(ctx, li, b, pos, nh, kv_dtype)
+                want = O.attend_runs(view, np.arange(pos + 1), [npre, pos + 1 - npre], q[b], None)
+                worst = max(worst, maxdiff(got[b], want))
+        ctx.advance(B, None, 1)
+    assert worst <= TOL, worst
+    for b in range(B):
+        ctx.seq_reset(b)
+    ctx.prefix_free(pid)
+
+
+def test_int8_store_edge_rows():
+    """Exact .5 ties, zero rows, +-absmax, subnormal scales: codes and scales
+    identical to the oracle's (which is pinned to the reference's store)."""
+    say("int8 store edge rows")
+    N = nda()
+    rows = []
+    rng = np.random.default_rng(13)
+    rows.append(np.zeros(64, np.float32))
+    rows.append(np.array([(i - 32) + 0.5 for i in range(64)], np.float32))
+    rows.append(np.array([1e-38 * (i - 32) for i in range(64)], np.float32))
+    rows.append((rng.standard_normal(64) * 1e-20).astype(np.float32))
+    sc = np.float32(0.37)
+    t = (rng.integers(-254, 255, 64) / 2.0).astype(np.float32)
+    rows.append((t * sc).astype(np.float32))
+    for _ in range(59):
+        rows.append((rng.standard_normal(64) * 10 ** rng.uniform(-8, 8)).astype(np.float32))
+    n = len(rows)
+    ctx = N.Context(1, 1, 1, 64, 64, 128, kv_dtype=O.KV_INT8, max_seqs=n)
+    kin = np.stack(rows).reshape(n, 1, 64)
+    vin = kin[::-1].copy()
+    ctx.kv_append(0, n, N.DevBuf.from_array(kin), N.DevBuf.from_array(vin))
+    ctx.sync()
+    for b in range(n):
+        k, v, ks, vs = ctx.kv_read(0, b, 0, 1)
+        for src, code, scl in ((kin[b, 0], k[0, 0], ks[0, 0]), (vin[b, 0], v[0, 0], vs[0, 0])):
+            c = np.zeros(64, np.int8)
+            s = O.lib().ndo_kv_quant_row(np.ascontiguousarray(src), 64, c)
+            assert np.array_equal(c, code), b
+            assert np.float32(s).view(np.uint32) == np.float32(scl).view(np.uint32), b
+
+
+# ------------------------------------------------------------ error handling
+
+def test_error_paths():
+    say("error paths")
+    N = nda()
+    ctx = N.Context(2, 4, 2, 64, 64, 64, kv_dtype=O.KV_F16, max_seqs=2, max_pages=5)
+    z = N.DevBuf(1 << 16)
+    with pytest.raises(N.NdaError) as e:
+        ctx.decode(0, 1, z, z)                       # nothing stored yet
+    assert e.value.code == -5
+    with pytest.raises(N.NdaError) as e:
+        ctx.kv_append(2, 1, z, z)                    # bad layer
+    assert e.value.code == -1
+    with pytest.raises(N.NdaError) as e:
+        ctx.prefill(0, [65], z, z, z, z)              # would wrap the ring
+    assert e.value.code == -4
+    ctx.prefill(0, [64], z, z, z, z)                  # exactly the window: fine
+    with pytest.raises(N.NdaError) as e:
+        ctx.prefill(0, [64], z, z, z, z, seq_ids=[1])  # 4 more pages, 1 left
+    assert e.value.code == -2
+    assert ctx.seq_state(1)[0] == 0
+    ctx.kv_append(0, 0, None, None)                   # empty batch
+    ctx.decode(0, 0, None, None)
+    with pytest.raises(N.NdaError):
+        ctx.seq_attach(0, 3)                          # no such prefix
+    with pytest.raises(N.NdaError):
+        N.Context(1, 6, 4, 64, 64, 64)                 # heads not a multiple
+    with pytest.raises(N.NdaError) as e:
+        N.Context(1, 4, 4, 80, 64, 64)                 # no kernel for dk 80
+    assert e.value.code == -6
+
+
+# --------------------------------------------------- full-size sampled check
+
+def test_cfg3_full_shape_one_layer_sampled():
+    """Config 3's full shape on one layer (4096 ragged sequences, L in
+    [213, 1024], fp16): the whole batch decodes, and 24 sampled sequences match
+    the oracle; a second step after advance matches too."""
+    say("cfg3 full shape 1 layer")
+    N = nda()
+    B, nh, d, W = 4096, 8, 64, 1024
+    rng = np.random.default_rng(14)
+    lens = rng.integers(213, 1025, B)
+    ctx = N.Context(1, nh, nh, d, d, W + 8, kv_dtype=O.KV_F16, max_seqs=B)
+    for b in range(B):
+        ctx.seq_set_pos(b, int(lens[b]) - 1)
+        ctx.seq_reserve(b, 2)
+    ctx.kv_fill_normal(B, seed=77)
+    dq, dk, dv, dout = (N.DevBuf(B * nh * d * 4) for _ in range(4))
+    for buf, s in ((dq, 1), (dk, 2), (dv, 3)):
+        buf.fill_normal(B * nh * d, 0, s)
+    sample = rng.choice(B, 24, replace=False)
+    for step in range(2):
+        ctx.step(0, B, dq, dk, dv, dout)
+        ctx.sync()
+        out = dout.to_array(np.float32, (B, nh * d))
+        assert np.isfinite(out).all()
+        q = dq.to_array(np.float32, (B, nh * d))
+        for b in sample:
+            pos = ctx.seq_state(int(b))[0]
+            k, v, _, _ = ctx.kv_read(0, int(b), 0, pos + 1)
+            kv = O.kv_view(k, v, None, None, nh, pos + 1, 0, pos, O.KV_F16)
+            want = O.attend_view(kv, q[b], None)
+            assert maxdiff(out[b], want) <= TOL, (step, b)
+        ctx.advance(B, None, 1)
