@@ -35,6 +35,7 @@ struct SeqHost {
     int32_t prefix = -1;
     bool has_snap = false;
     uint32_t snap_pos = 0;
+    uint32_t stored_end = 0;   // one past the highest position stored
 };
 
 struct ProfRec {
@@ -61,6 +62,8 @@ struct nda_ctx {
     size_t part_cap = 0;                // floats
     uint8_t *d_stage = nullptr;
     size_t stage_cap = 0;
+    uint32_t *d_pf = nullptr;           // prefill work list staging
+    size_t pf_cap = 0;                  // uint32 entries
     uint64_t dev_bytes = 0;
 
     std::vector<int32_t> pages, prefix_pages;
@@ -263,6 +266,23 @@ int ensure_part(nda_ctx *c, size_t floats)
     HIPC(c, hipMalloc(&c->d_part, floats * sizeof(float)));
     c->part_cap = floats;
     c->dev_bytes += floats * sizeof(float);
+    return NDA_OK;
+}
+
+int ensure_pf(nda_ctx *c, size_t n)
+{
+    if (n <= c->pf_cap)
+        return NDA_OK;
+    if (c->d_pf) {
+        hipDeviceSynchronize();
+        hipFree(c->d_pf);
+        c->dev_bytes -= c->pf_cap * sizeof(uint32_t);
+        c->d_pf = nullptr;
+    }
+    size_t cap = std::max<size_t>(n * 2, 16384);
+    HIPC(c, hipMalloc(&c->d_pf, cap * sizeof(uint32_t)));
+    c->pf_cap = cap;
+    c->dev_bytes += cap * sizeof(uint32_t);
     return NDA_OK;
 }
 
@@ -531,6 +551,7 @@ void nda_destroy(nda_ctx *c)
     hipFree(c->d_rows);
     hipFree(c->d_part);
     hipFree(c->d_stage);
+    hipFree(c->d_pf);
     delete c;
 }
 
@@ -727,6 +748,7 @@ int nda_seq_attach(nda_ctx *c, uint32_t seq, int32_t id, void *stream)
     s.pos = pf.len;
     s.has_snap = true;
     s.snap_pos = pf.len;
+    s.stored_end = pf.len;
     c->prefixes[id].refs++;
     c->seqs_dirty = true;
     // Positions past the sink clamp live in the ring: copy them in, as the
@@ -800,6 +822,10 @@ int nda_kv_append(nda_ctx *c, uint32_t layer, uint32_t nseq, const uint32_t *ids
         const uint32_t q = sid(ids, b);
         if (int rc = back_positions(c, q, c->seqs[q].pos, 1))
             return rc;
+    }
+    for (uint32_t b = 0; b < nseq; b++) {
+        SeqHost &s = c->seqs[sid(ids, b)];
+        s.stored_end = std::max(s.stored_end, s.pos + 1);
     }
     if (int rc = sync_tables(c, st))
         return rc;
@@ -904,6 +930,11 @@ int nda_prefill(nda_ctx *c, uint32_t layer, uint32_t nseq, const uint32_t *ids, 
             if (int rc = back_positions(c, qq, c->seqs[qq].pos, n_tokens[b]))
                 return rc;
     }
+    for (uint32_t b = 0; b < nseq; b++) {
+        SeqHost &s = c->seqs[sid(ids, b)];
+        if (n_tokens[b])
+            s.stored_end = std::max(s.stored_end, s.pos + n_tokens[b]);
+    }
     std::vector<uint32_t> rseq(rows), rt(rows);
     for (uint32_t b = 0, r = 0; b < nseq; b++)
         for (uint32_t t = 0; t < n_tokens[b]; t++, r++) {
@@ -931,10 +962,57 @@ int nda_prefill(nda_ctx *c, uint32_t layer, uint32_t nseq, const uint32_t *ids, 
         if (e != hipSuccess)
             return hip_fail(c, e, "append kernel launch");
     }
-    AttnArgs a = attn_args(c, layer, (uint32_t)rows, q, gate, out, max_total);
-    a.row_seq = d_seq;
-    a.row_t = d_t;
-    return run_attend(c, a, st);
+    if (c->cfg.flags & NDA_FLAG_PREFILL_VALU) {
+        AttnArgs a = attn_args(c, layer, (uint32_t)rows, q, gate, out, max_total);
+        a.row_seq = d_seq;
+        a.row_t = d_t;
+        return run_attend(c, a, st);
+    }
+    // MFMA path: work items = (batch index, tile of 32*W query rows).
+    const uint32_t rep = c->cfg.n_heads / c->cfg.n_kv_heads;
+    uint32_t max_rows = 0;
+    for (uint32_t b = 0; b < nseq; b++)
+        max_rows = std::max(max_rows, n_tokens[b] * rep);
+    const int waves = max_rows <= 64 ? 2 : 4;
+    const uint32_t trows = 32u * waves;
+    std::vector<uint32_t> host(3 * (size_t)nseq);
+    std::vector<uint32_t> items;
+    for (uint32_t b = 0, tok = 0; b < nseq; b++) {
+        host[b] = sid(ids, b);
+        host[nseq + b] = tok;
+        host[2 * nseq + b] = n_tokens[b];
+        tok += n_tokens[b];
+        const uint32_t nt = (n_tokens[b] * rep + trows - 1) / trows;
+        for (uint32_t t = 0; t < nt; t++) {
+            items.push_back(b);
+            items.push_back(t);
+        }
+    }
+    if (int rc = ensure_pf(c, host.size() + items.size()))
+        return rc;
+    HIPC(c, hipMemcpyAsync(c->d_pf, host.data(), host.size() * 4, hipMemcpyHostToDevice, st));
+    HIPC(c, hipMemcpyAsync(c->d_pf + host.size(), items.data(), items.size() * 4, hipMemcpyHostToDevice, st));
+    PrefillArgs pa{};
+    pa.q = q;
+    pa.gate = gate;
+    pa.out = out;
+    pa.pool = c->pool + (uint64_t)layer * c->pg.layer_bytes;
+    pa.page_table = c->d_pages;
+    pa.prefix_pages = c->d_prefix_pages;
+    pa.seqs = c->d_seqs;
+    pa.bseq = c->d_pf;
+    pa.btok0 = c->d_pf + nseq;
+    pa.bntok = c->d_pf + 2 * (size_t)nseq;
+    pa.items = c->d_pf + host.size();
+    pa.pg = c->pg;
+    pa.n_items = (uint32_t)(items.size() / 2);
+    pa.nh = c->cfg.n_heads;
+    pa.qscale = (float)(1.4426950408889634 / std::sqrt((double)c->cfg.qk_head_dim));
+    ProfScope ps(c, NDA_K_PREFILL, st);
+    hipError_t e = launch_prefill(c->geo, pa, waves, st);
+    if (e != hipSuccess)
+        return hip_fail(c, e, "prefill kernel launch");
+    return NDA_OK;
 }
 
 int nda_sync(nda_ctx *c, void *stream)
@@ -963,10 +1041,11 @@ static int locate(nda_ctx *c, uint32_t seq, uint32_t p0, uint32_t count, bool fo
             continue;
         }
         if (!for_write) {
-            // readable iff still inside the window seen from pos (or pos-1)
-            const uint32_t top = std::max(s.pos, p);
+            // readable iff stored and not yet overwritten by the ring
             const uint32_t rcap = c->cfg.window - s.n_sink;
-            if (p >= s.n_sink && top - p >= rcap)
+            if (p >= s.stored_end)
+                return fail(c, NDA_ERR_RANGE, "position %u was never stored", p);
+            if (p >= s.n_sink && s.stored_end - p > rcap)
                 return fail(c, NDA_ERR_RANGE, "position %u has left the ring", p);
         }
         const uint32_t sl = own_slot(s, p, c->cfg.window);
@@ -1032,6 +1111,8 @@ static int kv_stage(nda_ctx *c, uint32_t layer, uint32_t seq, uint32_t p0, uint3
         if (e != hipSuccess)
             return hip_fail(c, e, "scatter");
         HIPC(c, hipDeviceSynchronize());
+        SeqHost &sw = c->seqs[seq];
+        sw.stored_end = std::max(sw.stored_end, p0 + count);
     } else {
         hipError_t e = launch_gather(c->geo, a, nullptr);
         if (e != hipSuccess)
@@ -1077,6 +1158,10 @@ int nda_kv_fill_normal(nda_ctx *c, uint32_t nseq, const uint32_t *ids, uint64_t 
         const Vis v = visible(s, s.pos - 1, c->cfg.window);
         if (int rc = back_slots(c, qq, 0, v.n_own))
             return rc;
+    }
+    for (uint32_t b = 0; b < nseq; b++) {
+        SeqHost &s = c->seqs[sid(ids, b)];
+        s.stored_end = std::max(s.stored_end, s.pos);
     }
     if (int rc = sync_tables(c, st))
         return rc;

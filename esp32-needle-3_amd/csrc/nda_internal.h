@@ -54,6 +54,26 @@ struct AttnArgs {
     float qscale;            /* log2(e) / sqrt(dk) */
 };
 
+/* One launch of the MFMA causal-prefill kernel. A work item is one tile of
+ * 32*waves query rows (token, head-of-group) of one sequence and kv-head. */
+struct PrefillArgs {
+    const float *q;          /* [T][nh][dk] packed tokens */
+    const float *gate;       /* [T][nh][dv] or null */
+    float *out;              /* [T][nh][dv] */
+    const uint8_t *pool;
+    const int32_t *page_table;
+    const int32_t *prefix_pages;
+    const SeqDev *seqs;
+    const uint32_t *items;   /* [n_items][2]: batch index, row tile */
+    const uint32_t *bseq;    /* [nseq] sequence id per batch index */
+    const uint32_t *btok0;   /* [nseq] first packed token of the batch index */
+    const uint32_t *bntok;   /* [nseq] tokens of the batch index */
+    PageGeom pg;
+    uint32_t n_items;
+    uint32_t nh;
+    float qscale;
+};
+
 struct AppendArgs {
     const float *k;          /* [rows][nkv][dk] */
     const float *v;          /* [rows][nkv][dv] */
@@ -107,6 +127,7 @@ struct Geo {
  * hipErrorNotSupported for a geometry without an instantiation. */
 hipError_t launch_append(const Geo &g, const AppendArgs &a, hipStream_t s);
 hipError_t launch_attend(const Geo &g, const AttnArgs &a, hipStream_t s);
+hipError_t launch_prefill(const Geo &g, const PrefillArgs &a, int waves, hipStream_t s);
 hipError_t launch_combine(const Geo &g, const AttnArgs &a, hipStream_t s);
 hipError_t launch_copy(const Geo &g, const CopyArgs &a, hipStream_t s);
 hipError_t launch_gather(const Geo &g, const StageArgs &a, hipStream_t s);

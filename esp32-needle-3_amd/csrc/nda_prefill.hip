@@ -1,0 +1,290 @@
+// nda_prefill.hip - causal prefill attention on MFMA (gfx950).
+//
+// The engine prefills one token at a time (esp32/main/main.c:233-234,
+// :312-315): token t of a chunk attends every stored position <= pos + t. Over
+// a chunk that is causal attention of n query tokens against pos + n keys, a
+// dense contraction wherever a key tile lies below the earliest query of a
+// row tile; only tiles that cross the diagonal are masked, tiles above it are
+// never visited.
+//
+// A work-group owns 32*W query rows of one (sequence, kv-head); a row is one
+// (token, query head of the group) pair, so GQA heads share every K/V tile.
+// Key tiles of 32 are staged through LDS (K row-major, V transposed), then per
+// wave and tile:
+//   S^T[32 keys x 32 rows]  = K . Q^T           v_mfma_f32_32x32x16_f16
+//   O^T[64 dims x 32 rows] += V^T . P^T         v_mfma_f32_32x32x16_f16
+// Computing the transposes puts one query row in each lane (lane l and l+32
+// hold halves of the keys), so the online-softmax state of a row is lane
+// local, and the S^T accumulator registers are, slot for slot, the P^T
+// operand of the next MFMA. Q and P are carried as fp16 hi + lo pairs (two
+// MFMAs each) so the result keeps fp32-level accuracy: fp16 alone would leave
+// ~2^-12 relative error on a dominant softmax weight.
+//
+// K/V are the cache's own fp16 values, or int8 codes (exact in fp16) with the
+// per-(slot, kv-head) scales applied to S (k scale) and folded into P (v
+// scale), the engine's dequantisation (engine/src/nd_model.c:2179-2180,
+// :2250-2252).
+#include "nda_device.h"
+
+#include <float.h>
+
+namespace nda {
+
+typedef _Float16 half8 __attribute__((ext_vector_type(8)));
+typedef _Float16 half4 __attribute__((ext_vector_type(4)));
+typedef float float16v __attribute__((ext_vector_type(16)));
+
+constexpr int PF_KT = 32;   // keys per tile
+
+__device__ __forceinline__ float16v mfma32(half8 a, half8 b, float16v c)
+{
+    return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
+}
+
+template <int ES, int DK, int DV>
+struct PfTile {
+    static constexpr int KPAD = DK + 8;        // halves per K row in LDS
+    static constexpr int VPAD = PF_KT + 4;     // halves per V^T row in LDS
+    static constexpr int KCH = DK * ES / 4;    // dwords per stored K row
+    static constexpr int VCH = DV * ES / 4;
+};
+
+// Element i of a dword as a half: fp16 lane or an int8 code (exact in fp16).
+template <int ES>
+__device__ __forceinline__ _Float16 code_at(uint32_t w, int i)
+{
+    if constexpr (ES == 1)
+        return (_Float16)(float)(int8_t)(w >> (8 * i));
+    else
+        return __builtin_bit_cast(_Float16, (uint16_t)(w >> (16 * i)));
+}
+
+template <int ES, int DK, int DV, int REP, int W>
+__global__ __launch_bounds__(64 * W) void prefill_kernel(PrefillArgs a)
+{
+    using T = PfTile<ES, DK, DV>;
+    static_assert(DK % 16 == 0 && DV == 64, "prefill tiles: dk multiple of 16, dv 64");
+    constexpr int ROWS = 32 * W;
+    constexpr int NKB = DK / 16;               // k-blocks of the QK MFMA
+    constexpr int NTHR = 64 * W;
+
+    __shared__ __attribute__((aligned(16))) _Float16 Ks[PF_KT][T::KPAD];
+    __shared__ __attribute__((aligned(16))) _Float16 Vt[DV][T::VPAD];
+    __shared__ float Ksc[PF_KT], Vsc[PF_KT];
+
+    const int tid = threadIdx.x;
+    const int lane = tid & 63, wave = tid >> 6;
+    const int jh = lane >> 5, ln = lane & 31;
+    const uint32_t b = a.items[2 * blockIdx.x], rtile = a.items[2 * blockIdx.x + 1];
+    const uint32_t g = blockIdx.y;
+    const uint32_t seq = a.bseq[b];
+    const SeqDev sd = a.seqs[seq];
+    const int ntok = (int)a.bntok[b];
+    const int nrows = ntok * REP;
+    const int r0 = (int)rtile * ROWS;
+    const int pos = sd.pos;
+    const Visible vis0 = visible(sd, pos, (int)a.pg.window);
+    const int n_sh = vis0.n_sh;                 // shared-prefix keys (fixed over the chunk)
+
+    // this lane's query row
+    const int r = r0 + wave * 32 + ln;
+    const bool rvalid = r < nrows;
+    const int tok = rvalid ? r / REP : 0;
+    const int h = (int)g * REP + (rvalid ? r % REP : 0);
+    const int qpos = pos + tok;                 // keys [0, qpos] visible
+    const uint64_t qrow = (uint64_t)(a.btok0[b] + tok) * a.nh + h;
+
+    // Q^T operand, hi and lo halves, slots = dims 16*kb + 8*jh + s
+    half8 qh[NKB], ql[NKB];
+#pragma unroll
+    for (int kb = 0; kb < NKB; kb++) {
+#pragma unroll
+        for (int s = 0; s < 8; s++) {
+            const float x = rvalid ? a.q[qrow * DK + 16 * kb + 8 * jh + s] * a.qscale : 0.0f;
+            const _Float16 hi = (_Float16)x;
+            qh[kb][s] = hi;
+            ql[kb][s] = (_Float16)(x - (float)hi);
+        }
+    }
+
+    // rows of this tile: keys up to the last valid row's position
+    const int last_r = min(r0 + ROWS, nrows) - 1;
+    const int kmax = pos + last_r / REP + 1;        // keys [0, kmax) are touched
+    const int kfull = pos + r0 / REP + 1;           // keys [0, kfull) visible to every row
+
+    float16v acc0 = {}, acc1 = {};
+    float m = -FLT_MAX, lsum = 0.0f;
+
+    const int32_t *own_pages = a.page_table + (uint64_t)seq * a.pg.pages_per_seq;
+    const int32_t *pre_pages = sd.prefix >= 0 ? a.prefix_pages + (uint64_t)sd.prefix * a.pg.pages_per_seq
+                                              : nullptr;
+    const int P = 1 << a.pg.log2_page;
+
+    for (int kt = 0; kt < kmax; kt += PF_KT) {
+        // ---- stage the tile: K codes row-major, V codes transposed
+        for (int c = tid; c < PF_KT * (T::KCH + T::VCH); c += NTHR) {
+            const int isv = c >= PF_KT * T::KCH;
+            const int cc = isv ? c - PF_KT * T::KCH : c;
+            const int rowlen = isv ? T::VCH : T::KCH;
+            const int kl = cc / rowlen, wd = cc % rowlen;
+            const int key = kt + kl;
+            uint32_t w = 0;
+            float sc = 0.0f;
+            if (key < kmax) {
+                int32_t page;
+                int off;
+                if (key < n_sh) {
+                    page = pre_pages[key >> a.pg.log2_page];
+                    off = key & (P - 1);
+                } else {
+                    const int s = key - n_sh;
+                    page = own_pages[s >> a.pg.log2_page];
+                    off = s & (P - 1);
+                }
+                if (page >= 0) {
+                    const uint8_t *hb = a.pool + (uint64_t)page * a.pg.page_bytes + (uint64_t)g * a.pg.head_bytes;
+                    const uint8_t *src = isv ? hb + (uint64_t)P * DK * ES + (uint64_t)off * DV * ES
+                                             : hb + (uint64_t)off * DK * ES;
+                    w = reinterpret_cast<const uint32_t *>(src)[wd];
+                    if (ES == 1 && wd == 0)
+                        sc = reinterpret_cast<const float *>(hb + (uint64_t)P * (DK + DV))[(isv ? P : 0) + off];
+                }
+            }
+            constexpr int EPW = 4 / ES;        // elements per dword
+            if (!isv) {
+#pragma unroll
+                for (int i = 0; i < EPW; i++)
+                    Ks[kl][wd * EPW + i] = code_at<ES>(w, i);
+                if (ES == 1 && wd == 0)
+                    Ksc[kl] = sc;
+            } else {
+#pragma unroll
+                for (int i = 0; i < EPW; i++)
+                    Vt[wd * EPW + i][kl] = code_at<ES>(w, i);
+                if (ES == 1 && wd == 0)
+                    Vsc[kl] = sc;
+            }
+        }
+        __syncthreads();
+
+        // ---- S^T = K . Q^T (keys x rows), accumulate hi then lo
+        float16v st = {};
+#pragma unroll
+        for (int kb = 0; kb < NKB; kb++) {
+            const half8 ka = *reinterpret_cast<const half8 *>(&Ks[ln][16 * kb + 8 * jh]);
+            st = mfma32(ka, qh[kb], st);
+            st = mfma32(ka, ql[kb], st);
+        }
+        // register i holds key 8*(i/4) + 4*jh + (i%4) of the tile, row ln
+        const bool need_mask = (kt + PF_KT > kfull) || !rvalid;
+        float mt = -FLT_MAX;
+#pragma unroll
+        for (int i = 0; i < 16; i++) {
+            const int kl = 8 * (i >> 2) + 4 * jh + (i & 3);
+            float s = st[i];
+            if constexpr (ES == 1)
+                s *= Ksc[kl];
+            if (need_mask && (!rvalid || kt + kl > qpos))
+                s = -INFINITY;
+            st[i] = s;
+            mt = fmaxf(mt, s);
+        }
+        mt = fmaxf(mt, __shfl_xor(mt, 32, 64));
+        const float mnew = fmaxf(m, mt);
+        const float rs = fast_exp2(m - mnew);
+        m = mnew;
+        lsum *= rs;
+#pragma unroll
+        for (int i = 0; i < 16; i++) {
+            acc0[i] *= rs;
+            acc1[i] *= rs;
+        }
+        // P^T operand (hi, lo) for the two 16-key blocks: slots = registers 8*kb2 + s
+        half8 ph[2], pl[2];
+#pragma unroll
+        for (int i = 0; i < 16; i++) {
+            const float p = fast_exp2(st[i] - mnew);
+            lsum += p;
+            float pv = p;
+            if constexpr (ES == 1)
+                pv *= Vsc[8 * (i >> 2) + 4 * jh + (i & 3)];
+            const _Float16 hi = (_Float16)pv;
+            ph[i >> 3][i & 7] = hi;
+            pl[i >> 3][i & 7] = (_Float16)(pv - (float)hi);
+        }
+        // ---- O^T += V^T . P^T; V^T slots = keys 16*kb2 + 8*(s/4) + 4*jh + (s%4)
+#pragma unroll
+        for (int kb2 = 0; kb2 < 2; kb2++) {
+#pragma unroll
+            for (int dt = 0; dt < 2; dt++) {
+                const _Float16 *vr = &Vt[32 * dt + ln][16 * kb2 + 4 * jh];
+                const half4 v0 = *reinterpret_cast<const half4 *>(vr);
+                const half4 v1 = *reinterpret_cast<const half4 *>(vr + 8);
+                const half8 va = {v0[0], v0[1], v0[2], v0[3], v1[0], v1[1], v1[2], v1[3]};
+                if (dt == 0) {
+                    acc0 = mfma32(va, ph[kb2], acc0);
+                    acc0 = mfma32(va, pl[kb2], acc0);
+                } else {
+                    acc1 = mfma32(va, ph[kb2], acc1);
+                    acc1 = mfma32(va, pl[kb2], acc1);
+                }
+            }
+        }
+        __syncthreads();
+    }
+
+    // ---- emit: lane holds row ln, dims 32*dt + 8*(i/4) + 4*jh + (i%4)
+    lsum += __shfl_xor(lsum, 32, 64);
+    if (!rvalid)
+        return;
+    const float inv = 1.0f / lsum;
+    float *o = a.out + qrow * DV;
+    const float *gt = a.gate ? a.gate + qrow * DV : nullptr;
+#pragma unroll
+    for (int dt = 0; dt < 2; dt++) {
+#pragma unroll
+        for (int i4 = 0; i4 < 4; i4++) {
+            const int d0 = 32 * dt + 8 * i4 + 4 * jh;
+            float4 z;
+            const float16v &acc = dt == 0 ? acc0 : acc1;
+            z.x = acc[4 * i4 + 0] * inv;
+            z.y = acc[4 * i4 + 1] * inv;
+            z.z = acc[4 * i4 + 2] * inv;
+            z.w = acc[4 * i4 + 3] * inv;
+            if (gt) {
+                z.x *= sigmoid_dev(gt[d0 + 0]);
+                z.y *= sigmoid_dev(gt[d0 + 1]);
+                z.z *= sigmoid_dev(gt[d0 + 2]);
+                z.w *= sigmoid_dev(gt[d0 + 3]);
+            }
+            *reinterpret_cast<float4 *>(o + d0) = z;
+        }
+    }
+}
+
+#define NDA_PF_GEOMETRIES(X) \
+    X(2, 64, 64, 1) X(2, 64, 64, 2) X(2, 64, 64, 4) X(2, 64, 64, 6) X(2, 64, 64, 8) \
+    X(2, 48, 64, 1) X(2, 48, 64, 2) X(2, 48, 64, 6) \
+    X(1, 64, 64, 1) X(1, 64, 64, 2) X(1, 64, 64, 4) X(1, 64, 64, 6) X(1, 64, 64, 8) \
+    X(1, 48, 64, 1) X(1, 48, 64, 2) X(1, 48, 64, 6)
+
+hipError_t launch_prefill(const Geo &g, const PrefillArgs &a, int waves, hipStream_t s)
+{
+    if (a.n_items == 0)
+        return hipSuccess;
+    const int es = g.kv_f16 ? 2 : 1;
+    dim3 grid(a.n_items, a.pg.nkv);
+#define X(ES, DK, DV, REP)                                                                      \
+    if (es == ES && g.dk == DK && g.dv == DV && g.rep == REP) {                                 \
+        if (waves == 2)                                                                          \
+            hipLaunchKernelGGL((prefill_kernel<ES, DK, DV, REP, 2>), grid, dim3(128), 0, s, a);  \
+        else                                                                                     \
+            hipLaunchKernelGGL((prefill_kernel<ES, DK, DV, REP, 4>), grid, dim3(256), 0, s, a);  \
+        return hipGetLastError();                                                                \
+    }
+    NDA_PF_GEOMETRIES(X)
+#undef X
+    return hipErrorNotSupported;
+}
+
+} // namespace nda

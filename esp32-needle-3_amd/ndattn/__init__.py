@@ -19,6 +19,7 @@ ERRORS = {-1: "NDA_ERR_ARG", -2: "NDA_ERR_NOMEM", -3: "NDA_ERR_HIP", -4: "NDA_ER
           -5: "NDA_ERR_STATE", -6: "NDA_ERR_UNSUPPORTED", -7: "NDA_ERR_NODEV"}
 KV_INT8, KV_F16 = 0, 1
 K_APPEND, K_DECODE, K_COMBINE, K_PREFILL = 0, 1, 2, 3
+FLAG_PREFILL_VALU = 1
 
 # Every symbol include/nda.h declares (checked by the CPU test suite).
 ABI_SYMBOLS = [
@@ -50,7 +51,7 @@ class Config(C.Structure):
                 ("qk_head_dim", C.c_uint32), ("v_head_dim", C.c_uint32), ("window", C.c_uint32),
                 ("page_size", C.c_uint32), ("kv_dtype", C.c_uint32), ("max_seqs", C.c_uint32),
                 ("max_prefixes", C.c_uint32), ("max_pages", C.c_uint64),
-                ("split_chunk", C.c_uint32), ("reserved", C.c_uint32)]
+                ("split_chunk", C.c_uint32), ("flags", C.c_uint32)]
 
 
 _lib = None
@@ -226,17 +227,27 @@ class Context:
 
     def __init__(self, n_layers, n_heads, n_kv_heads, qk_head_dim, v_head_dim, window,
                  kv_dtype=KV_INT8, max_seqs=1, page_size=16, max_prefixes=16, max_pages=0,
-                 split_chunk=0):
+                 split_chunk=0, flags=0):
         cfg = Config(n_layers, n_heads, n_kv_heads, qk_head_dim, v_head_dim, window, page_size,
-                     kv_dtype, max_seqs, max_prefixes, max_pages, split_chunk, 0)
+                     kv_dtype, max_seqs, max_prefixes, max_pages, split_chunk, flags)
         self.h = vp()
+        self.owned = True
         _check(lib().nda_create(C.byref(cfg), C.byref(self.h)))
         self.cfg = cfg
 
+    @classmethod
+    def borrow(cls, handle, cfg):
+        """View of a context owned elsewhere (e.g. by the C shim): never destroyed here."""
+        c = cls.__new__(cls)
+        c.h = vp(handle)
+        c.owned = False
+        c.cfg = cfg
+        return c
+
     def close(self):
-        if self.h and self.h.value:
+        if self.h and self.h.value and self.owned:
             lib().nda_destroy(self.h)
-            self.h = vp()
+        self.h = vp()
 
     def __del__(self):
         try:
@@ -357,6 +368,13 @@ class GpuSession:
         if not self.m:
             raise NdaError(-1, "nd_gpu_open failed")
         self.geom = (n_layers, nh, nkv, qk_hd, v_hd, window)
+        self.kv_dtype = kv_dtype
+
+    def context(self):
+        """The session's nda_ctx (sequence 0), borrowed."""
+        L, nh, nkv, qk, vd, W = self.geom
+        return Context.borrow(host_lib().nd_gpu_ctx(self.m),
+                              Config(L, nh, nkv, qk, vd, W, 16, self.kv_dtype, 1, 0, 0, 0, 0))
 
     def close(self):
         if self.m:

@@ -62,8 +62,12 @@ typedef struct {
     uint64_t max_pages;      /* page pool size per layer (0 = enough for every
                                 sequence's full window plus the prefixes) */
     uint32_t split_chunk;    /* positions per split-KV work item (0 = auto) */
-    uint32_t reserved;
+    uint32_t flags;          /* NDA_FLAG_* */
 } nda_config;
+
+/* Prefill through the per-row VALU decode kernel instead of the MFMA
+ * kernel (same results within rounding; for comparison and tiny chunks). */
+#define NDA_FLAG_PREFILL_VALU 1u
 
 /* ---- lifecycle ---- */
 

@@ -77,11 +77,8 @@ def replay(geom, script, seed, kv_dtype=O.KV_INT8, scale=1.0):
 
 def check_cache(o, g, layers, positions):
     """GPU-stored codes and scales of every listed position == oracle's."""
-    N = nda()
-    ctx = N.Context.__new__(N.Context)
-    ctx.h = N.vp(N.host_lib().nd_gpu_ctx(g.m))
+    ctx = g.context()
     L, nh, nkv, qk, vd, W = o.geom
-    ctx.cfg = N.Config(L, nh, nkv, qk, vd, W, 16, o.kv_dtype, 1, 0, 0, 0, 0)
     ok, ov, oks, ovs = o.cache()
     for li in layers:
         for p in positions:
@@ -92,7 +89,6 @@ def check_cache(o, g, layers, positions):
             if o.kv_dtype == O.KV_INT8:
                 assert np.array_equal(ks[0].view(np.uint32), oks[li, sl].view(np.uint32)), (li, p)
                 assert np.array_equal(vs[0].view(np.uint32), ovs[li, sl].view(np.uint32)), (li, p)
-    ctx.h = N.vp()   # borrowed handle: the shim owns it
 
 
 def test_cfg1_prefix_plus_prompt_int8():
@@ -466,3 +462,102 @@ def test_cfg3_full_shape_one_layer_sampled():
             want = O.attend_view(kv, q[b], None)
             assert maxdiff(out[b], want) <= TOL, (step, b)
         ctx.advance(B, None, 1)
+
+
+# ------------------------------------------------------- MFMA prefill kernel
+
+def _prefill_case(kv_dtype, nh, nkv, qk, hist, ntok, seed, flags=0, outlier_p=0.0, gated=True):
+    """Sequences with `hist[b]` stored positions prefill `ntok[b]` tokens in one
+    call; every token's output against the oracle over positions [0, pos+t]."""
+    N = nda()
+    vd = 64
+    rng = np.random.default_rng(seed)
+    B = len(hist)
+    W = max(h + n for h, n in zip(hist, ntok)) + 16
+    ctx = N.Context(1, nh, nkv, qk, vd, W, kv_dtype=kv_dtype, max_seqs=B, flags=flags)
+    for b, L in enumerate(hist):
+        if L:
+            kf = rng.standard_normal((L, nkv, qk)).astype(np.float32)
+            if outlier_p:
+                kf[rng.random((L, nkv)) < outlier_p] *= np.float32(8.0)
+            vf = rng.standard_normal((L, nkv, vd)).astype(np.float32)
+            if kv_dtype == O.KV_F16:
+                ctx.kv_write(0, b, 0, O.f32_to_f16_bits(kf), O.f32_to_f16_bits(vf))
+            else:
+                k = np.zeros(kf.shape, np.int8)
+                v = np.zeros(vf.shape, np.int8)
+                ks = np.zeros((L, nkv), np.float32)
+                vs = np.zeros((L, nkv), np.float32)
+                for p in range(L):
+                    for gg in range(nkv):
+                        ks[p, gg] = O.lib().ndo_kv_quant_row(np.ascontiguousarray(kf[p, gg]), qk, k[p, gg])
+                        vs[p, gg] = O.lib().ndo_kv_quant_row(np.ascontiguousarray(vf[p, gg]), vd, v[p, gg])
+                ctx.kv_write(0, b, 0, k, v, ks, vs)
+        ctx.seq_set_pos(b, L)
+    T = int(sum(ntok))
+    q = rng.standard_normal((T, nh, qk)).astype(np.float32)
+    k = rng.standard_normal((T, nkv, qk)).astype(np.float32)
+    v = rng.standard_normal((T, nkv, vd)).astype(np.float32)
+    g = rng.standard_normal((T, nh, vd)).astype(np.float32) if gated else None
+    dout = N.DevBuf(max(1, T) * nh * vd * 4)
+    ctx.prefill(0, ntok, N.DevBuf.from_array(q), N.DevBuf.from_array(k), N.DevBuf.from_array(v), dout,
+                gate=None if g is None else N.DevBuf.from_array(g))
+    ctx.sync()
+    got = dout.to_array(np.float32, (T, nh * vd))
+    worst, r = 0.0, 0
+    for b in range(B):
+        n = int(ntok[b])
+        if n == 0:
+            continue
+        end = hist[b] + n
+        kk, vv, ks, vs = ctx.kv_read(0, b, 0, end)
+        if kv_dtype == O.KV_F16:
+            ks = vs = None
+        for t in range(n):
+            pos = hist[b] + t
+            kv = O.kv_view(kk, vv, ks, vs, nh, end, 0, pos, kv_dtype)
+            want = O.attend_view(kv, q[r].ravel(), None if g is None else g[r].ravel())
+            worst = max(worst, maxdiff(got[r], want))
+            r += 1
+    return worst, got
+
+
+@pytest.mark.parametrize("kv_dtype", [O.KV_F16, O.KV_INT8])
+def test_prefill_mfma_ragged_batch(kv_dtype):
+    """Row tiles with partial fills (1, 31, 32, 33, 64, 65, 129 tokens),
+    existing history (0 to 700 positions), tile/diagonal boundaries."""
+    say("prefill mfma ragged dtype", kv_dtype)
+    hist = [0, 0, 5, 31, 100, 213, 700, 64, 1]
+    ntok = [1, 129, 31, 32, 33, 64, 65, 200, 0]
+    worst, _ = _prefill_case(kv_dtype, 8, 8, 64, hist, ntok, seed=21)
+    assert worst <= TOL, worst
+
+
+@pytest.mark.parametrize("kv_dtype", [O.KV_F16, O.KV_INT8])
+def test_prefill_mfma_gqa_engine_shapes(kv_dtype):
+    """12 query / 2 kv heads, qk 48: rows of a tile interleave the 6 heads."""
+    say("prefill mfma gqa dtype", kv_dtype)
+    worst, _ = _prefill_case(kv_dtype, 12, 2, 48, [0, 10, 213], [40, 7, 16], seed=22)
+    assert worst <= TOL, worst
+
+
+def test_prefill_mfma_rep_variants_and_no_gate():
+    say("prefill mfma rep variants")
+    for nh, nkv in ((8, 4), (8, 1), (16, 2)):
+        worst, _ = _prefill_case(O.KV_F16, nh, nkv, 64, [3, 50], [20, 70], seed=nh + nkv, gated=False)
+        assert worst <= TOL, (nh, nkv, worst)
+
+
+def test_prefill_mfma_long_context_outliers():
+    """A 512-token chunk over 4000 stored positions with 8-sigma keys."""
+    say("prefill mfma long context")
+    worst, _ = _prefill_case(O.KV_F16, 8, 8, 64, [4000], [512], seed=23, outlier_p=1e-3)
+    assert worst <= TOL, worst
+
+
+def test_prefill_mfma_matches_valu_path():
+    say("prefill mfma vs valu")
+    hist, ntok = [17, 300], [90, 45]
+    _, a = _prefill_case(O.KV_F16, 8, 8, 64, hist, ntok, seed=24)
+    _, b = _prefill_case(O.KV_F16, 8, 8, 64, hist, ntok, seed=24, flags=1)
+    assert maxdiff(a, b) <= 2e-6
