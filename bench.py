@@ -63,6 +63,63 @@ def cpu_baseline(lens_all, seconds, nthreads):
     return tok_s, "%d sequences (L mean %.0f) x %d layer-calls, %.1f s" % (S, lens.mean(), calls, el)
 
 
+def prefill_leg(N, stream, nseq=256, lmin=8192, lmax=32768, chunk=512, reps=3):
+    """Config 5's prefill: nseq sequences with L ~ U[lmin, lmax] stored
+    positions each take a `chunk`-token causal prefill (append + MFMA attention)
+    on one layer. FLOPs count the unmasked causal pairs only:
+    sum_s H * 2 * (dk + dv) * (chunk * L_s + chunk * (chunk + 1) / 2)."""
+    rng = np.random.default_rng(SEED + 5)
+    lens = rng.integers(lmin, lmax + 1, nseq)
+    P = 16
+    window = lmax + chunk + 16
+    need = int(sum((int(L) + chunk + P) // P for L in lens)) + 64
+    ctx = N.Context(1, H, H, D, D, window, kv_dtype=N.KV_F16, max_seqs=nseq, page_size=P, max_pages=need)
+    for b in range(nseq):
+        ctx.seq_set_pos(b, int(lens[b]))         # the fill stores positions [0, pos)
+    ctx.kv_fill_normal(nseq, seed=SEED + 6, stream=stream)
+    T = nseq * chunk
+    q, k, v, out = (N.DevBuf(T * H * D * 4) for _ in range(4))
+    for i, buf in enumerate((q, k, v)):
+        buf.fill_normal(T * H * D, 0, SEED + 70 + i, stream=stream)
+    ntok = np.full(nseq, chunk, np.uint32)
+    ctx.prefill(0, ntok, q, k, v, out, stream=stream)       # warm-up
+    ctx.sync(stream)
+    ctx.prof_enable(True)
+    ctx.prof_read(reset=True)
+    t0 = time.perf_counter()
+    for _ in range(reps):
+        ctx.prefill(0, ntok, q, k, v, out, stream=stream)
+    ctx.sync(stream)
+    el = time.perf_counter() - t0
+    ms, launches = ctx.prof_read(reset=True)
+    ctx.prof_enable(False)
+    flops = float(sum(H * 2 * (D + D) * (chunk * int(L) + chunk * (chunk + 1) / 2) for L in lens))
+    pf_ms = ms[N.K_PREFILL] / max(1, launches[N.K_PREFILL])
+    tflops = flops / (pf_ms * 1e-3) / 1e12
+    # sampled parity: two rows of one sequence against the oracle
+    import ndoracle as O
+    qh = q.to_array(np.float32, (T, H * D))
+    oh = out.to_array(np.float32, (T, H * D))
+    worst = 0.0
+    b = int(rng.integers(0, nseq))
+    L = int(lens[b])
+    kk, vv, _, _ = ctx.kv_read(0, b, 0, L + chunk)
+    for t in (0, chunk - 1):
+        kv = O.kv_view(kk, vv, None, None, H, L + chunk, 0, L + t, O.KV_F16)
+        want = O.attend_view(kv, qh[b * chunk + t], None)
+        worst = max(worst, float(np.abs(want - oh[b * chunk + t]).max()))
+    ctx.close()
+    return {"workload": "causal prefill chunk: %d sequences, %d new tokens each over L ~ U[%d,%d] "
+                        "stored positions, 8 heads x 64, fp16 K/V, 1 layer (append + attention)"
+                        % (nseq, chunk, lmin, lmax),
+            "tflops": round(tflops, 1), "unit": "TFLOP/s", "bound": "mfma",
+            "peak": 2500.0, "frac": round(tflops / 2500.0, 4),
+            "kernel": "prefill_kernel<f16,64,64,rep1,W4>", "kernel_ms": round(pf_ms, 3),
+            "flop_per_launch": flops, "append_ms": round(ms[N.K_APPEND] / max(1, launches[N.K_APPEND]), 4),
+            "call_ms": round(el * 1e3 / reps, 3), "max_abs_delta_sampled": worst,
+            "note": "unmasked causal FLOPs; the kernel issues 2x this on MFMA (fp16 hi+lo for Q and P)"}
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -72,6 +129,7 @@ def main():
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--split-chunk", type=int, default=0)
     ap.add_argument("--page-size", type=int, default=16)
+    ap.add_argument("--no-prefill", action="store_true")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py measures one GPU: this build has no multi-GPU path "
@@ -160,6 +218,16 @@ def main():
         worst = max(worst, float(np.abs(want - oh[b]).max()))
     log("sampled max |delta| vs oracle: %.3g" % worst)
 
+    ctx.close()
+    for bufs in (q, kn, vn, out):
+        for bb in bufs:
+            bb.free()
+    prefill = None
+    if not args.no_prefill:
+        prefill = prefill_leg(N, stream)
+        log("prefill: %.1f TFLOP/s (%.3f of 2.5 PF), kernel %.3f ms, sampled max |delta| %.3g" %
+            (prefill["tflops"], prefill["frac"], prefill["kernel_ms"], prefill["max_abs_delta_sampled"]))
+
     cpu = None
     if not args.no_cpu:
         ncores = min(16, os.cpu_count() or 1)
@@ -192,6 +260,7 @@ def main():
                      "kernel": "attend_kernel<f16,64,64,rep1>", "kernel_ms": round(dec_ms, 4),
                      "bytes_per_launch": int(dec_bytes_per_launch)},
         "cpu_baseline": cpu,
+        "prefill": prefill,
         "max_abs_delta_sampled": worst,
         "device": name,
     }

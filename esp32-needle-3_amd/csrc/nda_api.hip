@@ -983,10 +983,17 @@ int nda_prefill(nda_ctx *c, uint32_t layer, uint32_t nseq, const uint32_t *ids, 
         host[2 * nseq + b] = n_tokens[b];
         tok += n_tokens[b];
         const uint32_t nt = (n_tokens[b] * rep + trows - 1) / trows;
-        for (uint32_t t = 0; t < nt; t++) {
-            items.push_back(b);
-            items.push_back(t);
-        }
+        for (uint32_t g = 0; g < c->cfg.n_kv_heads; g++)
+            for (uint32_t t = 0; t < nt; t++) {
+                items.push_back(b);
+                items.push_back(g);
+                items.push_back(t);
+            }
+    }
+    while ((items.size() / 3) % 8) {   // the kernel's XCD remap needs a multiple of 8
+        items.push_back(0xFFFFFFFFu);
+        items.push_back(0);
+        items.push_back(0);
     }
     if (int rc = ensure_pf(c, host.size() + items.size()))
         return rc;
@@ -1005,7 +1012,7 @@ int nda_prefill(nda_ctx *c, uint32_t layer, uint32_t nseq, const uint32_t *ids, 
     pa.bntok = c->d_pf + 2 * (size_t)nseq;
     pa.items = c->d_pf + host.size();
     pa.pg = c->pg;
-    pa.n_items = (uint32_t)(items.size() / 2);
+    pa.n_items = (uint32_t)(items.size() / 3);
     pa.nh = c->cfg.n_heads;
     pa.qscale = (float)(1.4426950408889634 / std::sqrt((double)c->cfg.qk_head_dim));
     ProfScope ps(c, NDA_K_PREFILL, st);

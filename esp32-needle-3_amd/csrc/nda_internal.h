@@ -64,7 +64,7 @@ struct PrefillArgs {
     const int32_t *page_table;
     const int32_t *prefix_pages;
     const SeqDev *seqs;
-    const uint32_t *items;   /* [n_items][2]: batch index, row tile */
+    const uint32_t *items;   /* [n_items][3]: batch index (~0: empty), kv-head, row tile */
     const uint32_t *bseq;    /* [nseq] sequence id per batch index */
     const uint32_t *btok0;   /* [nseq] first packed token of the batch index */
     const uint32_t *bntok;   /* [nseq] tokens of the batch index */

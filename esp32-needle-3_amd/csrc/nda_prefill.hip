@@ -41,12 +41,25 @@ __device__ __forceinline__ float16v mfma32(half8 a, half8 b, float16v c)
     return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
 }
 
-template <int ES, int DK, int DV>
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+
+template <int ES, int DK, int DV, int NTHR>
 struct PfTile {
     static constexpr int KPAD = DK + 8;        // halves per K row in LDS
     static constexpr int VPAD = PF_KT + 4;     // halves per V^T row in LDS
-    static constexpr int KCH = DK * ES / 4;    // dwords per stored K row
-    static constexpr int VCH = DV * ES / 4;
+    static constexpr int KC = DK * ES / 16;    // 16-byte chunks per stored K row
+    static constexpr int VC = DV * ES / 16;
+    static constexpr int EPC = 16 / ES;        // elements per chunk
+    static constexpr int NCHUNK = PF_KT * (KC + VC);
+    static constexpr int CPT = (NCHUNK + NTHR - 1) / NTHR;   // chunks per thread
+    static_assert(DK * ES % 16 == 0 && DV * ES % 16 == 0, "rows are whole 16-byte chunks");
+};
+
+// One thread's share of a K/V tile in flight: raw 16-byte chunks + scales.
+template <int CPT>
+struct Staged {
+    u32x4 w[CPT];
+    float sc[CPT];
 };
 
 // Element i of a dword as a half: fp16 lane or an int8 code (exact in fp16).
@@ -62,7 +75,7 @@ __device__ __forceinline__ _Float16 code_at(uint32_t w, int i)
 template <int ES, int DK, int DV, int REP, int W>
 __global__ __launch_bounds__(64 * W) void prefill_kernel(PrefillArgs a)
 {
-    using T = PfTile<ES, DK, DV>;
+    using T = PfTile<ES, DK, DV, 64 * W>;
     static_assert(DK % 16 == 0 && DV == 64, "prefill tiles: dk multiple of 16, dv 64");
     constexpr int ROWS = 32 * W;
     constexpr int NKB = DK / 16;               // k-blocks of the QK MFMA
@@ -75,8 +88,15 @@ __global__ __launch_bounds__(64 * W) void prefill_kernel(PrefillArgs a)
     const int tid = threadIdx.x;
     const int lane = tid & 63, wave = tid >> 6;
     const int jh = lane >> 5, ln = lane & 31;
-    const uint32_t b = a.items[2 * blockIdx.x], rtile = a.items[2 * blockIdx.x + 1];
-    const uint32_t g = blockIdx.y;
+    // XCD-aware order: work-group w runs on XCD w % 8, so consecutive work
+    // items (the row tiles of one sequence and kv-head, which read the same
+    // K/V) are given to work-groups of one XCD and share its L2.
+    const uint32_t nwg = gridDim.x, wg = blockIdx.x;
+    const uint32_t item = (wg % 8u) * (nwg / 8u) + wg / 8u;
+    const uint32_t b = a.items[3 * item];
+    if (b == 0xFFFFFFFFu)
+        return;
+    const uint32_t g = a.items[3 * item + 1], rtile = a.items[3 * item + 2];
     const uint32_t seq = a.bseq[b];
     const SeqDev sd = a.seqs[seq];
     const int ntok = (int)a.bntok[b];
@@ -120,52 +140,82 @@ __global__ __launch_bounds__(64 * W) void prefill_kernel(PrefillArgs a)
                                               : nullptr;
     const int P = 1 << a.pg.log2_page;
 
-    for (int kt = 0; kt < kmax; kt += PF_KT) {
-        // ---- stage the tile: K codes row-major, V codes transposed
-        for (int c = tid; c < PF_KT * (T::KCH + T::VCH); c += NTHR) {
-            const int isv = c >= PF_KT * T::KCH;
-            const int cc = isv ? c - PF_KT * T::KCH : c;
-            const int rowlen = isv ? T::VCH : T::KCH;
-            const int kl = cc / rowlen, wd = cc % rowlen;
+    // Chunk c of a tile: K chunks [key][KC] first, then V chunks [key][VC].
+    auto load_tile = [&](int kt, Staged<T::CPT> &sg) {
+#pragma unroll
+        for (int i = 0; i < T::CPT; i++) {
+            const int c = tid + i * NTHR;
+            const bool isv = c >= PF_KT * T::KC;
+            const int cc = isv ? c - PF_KT * T::KC : c;
+            const int kl = isv ? cc / T::VC : cc / T::KC;
+            const int ch = isv ? cc % T::VC : cc % T::KC;
             const int key = kt + kl;
-            uint32_t w = 0;
-            float sc = 0.0f;
-            if (key < kmax) {
+            sg.w[i] = u32x4{0u, 0u, 0u, 0u};
+            sg.sc[i] = 0.0f;
+            if (c < T::NCHUNK && key < kmax) {
                 int32_t page;
                 int off;
                 if (key < n_sh) {
                     page = pre_pages[key >> a.pg.log2_page];
                     off = key & (P - 1);
                 } else {
-                    const int s = key - n_sh;
-                    page = own_pages[s >> a.pg.log2_page];
-                    off = s & (P - 1);
+                    const int sl = key - n_sh;
+                    page = own_pages[sl >> a.pg.log2_page];
+                    off = sl & (P - 1);
                 }
                 if (page >= 0) {
                     const uint8_t *hb = a.pool + (uint64_t)page * a.pg.page_bytes + (uint64_t)g * a.pg.head_bytes;
                     const uint8_t *src = isv ? hb + (uint64_t)P * DK * ES + (uint64_t)off * DV * ES
                                              : hb + (uint64_t)off * DK * ES;
-                    w = reinterpret_cast<const uint32_t *>(src)[wd];
-                    if (ES == 1 && wd == 0)
-                        sc = reinterpret_cast<const float *>(hb + (uint64_t)P * (DK + DV))[(isv ? P : 0) + off];
+                    sg.w[i] = __builtin_nontemporal_load(reinterpret_cast<const u32x4 *>(src) + ch);
+                    if (ES == 1 && ch == 0)
+                        sg.sc[i] = reinterpret_cast<const float *>(hb + (uint64_t)P * (DK + DV))[(isv ? P : 0) + off];
                 }
             }
-            constexpr int EPW = 4 / ES;        // elements per dword
-            if (!isv) {
+        }
+    };
+    auto store_tile = [&](const Staged<T::CPT> &sg) {
 #pragma unroll
-                for (int i = 0; i < EPW; i++)
-                    Ks[kl][wd * EPW + i] = code_at<ES>(w, i);
-                if (ES == 1 && wd == 0)
-                    Ksc[kl] = sc;
+        for (int i = 0; i < T::CPT; i++) {
+            const int c = tid + i * NTHR;
+            if (c >= T::NCHUNK)
+                continue;
+            const bool isv = c >= PF_KT * T::KC;
+            const int cc = isv ? c - PF_KT * T::KC : c;
+            const int kl = isv ? cc / T::VC : cc / T::KC;
+            const int ch = isv ? cc % T::VC : cc % T::KC;
+            if (!isv) {
+                if constexpr (ES == 2) {
+                    *reinterpret_cast<u32x4 *>(&Ks[kl][ch * 8]) = sg.w[i];
+                } else {
+                    half8 lo, hi;
+#pragma unroll
+                    for (int e = 0; e < 8; e++) {
+                        lo[e] = code_at<1>(sg.w[i][e >> 2], e & 3);
+                        hi[e] = code_at<1>(sg.w[i][2 + (e >> 2)], e & 3);
+                    }
+                    *reinterpret_cast<half8 *>(&Ks[kl][ch * 16]) = lo;
+                    *reinterpret_cast<half8 *>(&Ks[kl][ch * 16 + 8]) = hi;
+                    if (ch == 0)
+                        Ksc[kl] = sg.sc[i];
+                }
             } else {
 #pragma unroll
-                for (int i = 0; i < EPW; i++)
-                    Vt[wd * EPW + i][kl] = code_at<ES>(w, i);
-                if (ES == 1 && wd == 0)
-                    Vsc[kl] = sc;
+                for (int e = 0; e < T::EPC; e++)
+                    Vt[ch * T::EPC + e][kl] = code_at<ES>(sg.w[i][e / (4 / ES)], e % (4 / ES));
+                if (ES == 1 && ch == 0)
+                    Vsc[kl] = sg.sc[i];
             }
         }
+    };
+
+    Staged<T::CPT> sg;
+    load_tile(0, sg);
+    for (int kt = 0; kt < kmax; kt += PF_KT) {
+        store_tile(sg);
         __syncthreads();
+        if (kt + PF_KT < kmax)
+            load_tile(kt + PF_KT, sg);      // in flight while this tile computes
 
         // ---- S^T = K . Q^T (keys x rows), accumulate hi then lo
         float16v st = {};
@@ -273,7 +323,7 @@ hipError_t launch_prefill(const Geo &g, const PrefillArgs &a, int waves, hipStre
     if (a.n_items == 0)
         return hipSuccess;
     const int es = g.kv_f16 ? 2 : 1;
-    dim3 grid(a.n_items, a.pg.nkv);
+    dim3 grid(a.n_items);     // n_items: a multiple of 8 (padded with empty items)
 #define X(ES, DK, DV, REP)                                                                      \
     if (es == ES && g.dk == DK && g.dv == DV && g.rep == REP) {                                 \
         if (waves == 2)                                                                          \
