@@ -130,6 +130,8 @@ def main():
     ap.add_argument("--split-chunk", type=int, default=0)
     ap.add_argument("--page-size", type=int, default=16)
     ap.add_argument("--no-prefill", action="store_true")
+    ap.add_argument("--calib", action="store_true",
+                    help="first run a 4 GiB device copy (known traffic, for counter calibration)")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py measures one GPU: this build has no multi-GPU path "
@@ -140,6 +142,16 @@ def main():
 
     name, cus = N.device_info()
     log("device:", name, "CUs:", cus)
+    if args.calib:
+        nb = 4 << 30
+        src, dst = N.DevBuf(nb), N.DevBuf(nb)
+        src.fill_normal(nb // 4, 0, 1)
+        for _ in range(3):
+            N._check(N.lib().nda_d2d(dst.value, src.value, nb, None))
+        N.device_sync()
+        log("calibration copy: 3 x %d bytes read + written" % nb)
+        src.free()
+        dst.free()
     rng = np.random.default_rng(SEED)
     lens = rng.integers(LMIN, LMAX + 1, B)          # positions attended at the first step
     total_steps = args.warmup + args.steps

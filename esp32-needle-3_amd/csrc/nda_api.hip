@@ -1211,6 +1211,13 @@ int nda_d2h(void *dst, const void *src, size_t bytes)
     return hipMemcpy(dst, src, bytes, hipMemcpyDeviceToHost) == hipSuccess ? NDA_OK : NDA_ERR_HIP;
 }
 
+int nda_d2d(void *dst, const void *src, size_t bytes, void *stream)
+{
+    return hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToDevice, (hipStream_t)stream) == hipSuccess
+               ? NDA_OK
+               : NDA_ERR_HIP;
+}
+
 int nda_memset(void *dst, int value, size_t bytes)
 {
     return hipMemset(dst, value, bytes) == hipSuccess ? NDA_OK : NDA_ERR_HIP;

@@ -143,36 +143,51 @@ __global__ __launch_bounds__(64 * W) void prefill_kernel(PrefillArgs a)
     const int P = 1 << a.pg.log2_page;
 
     // Chunk c of a tile: K chunks [key][KC] first, then V chunks [key][VC].
-    auto load_tile = [&](int kt, Staged<T::CPT> &sg) {
+    // Page ids of a tile are fetched one iteration before its data, so no
+    // data load waits on a page-table round trip.
+    struct PageRef {
+        int32_t page[T::CPT];
+        int off[T::CPT];
+    };
+    auto fetch_pages = [&](int kt, PageRef &pr) {
 #pragma unroll
         for (int i = 0; i < T::CPT; i++) {
             const int c = tid + i * NTHR;
             const bool isv = c >= PF_KT * T::KC;
             const int cc = isv ? c - PF_KT * T::KC : c;
             const int kl = isv ? cc / T::VC : cc / T::KC;
-            const int ch = isv ? cc % T::VC : cc % T::KC;
             const int key = kt + kl;
-            sg.w[i] = u32x4{0u, 0u, 0u, 0u};
-            sg.sc[i] = 0.0f;
+            pr.page[i] = -1;
+            pr.off[i] = 0;
             if (c < T::NCHUNK && key < kmax) {
-                int32_t page;
-                int off;
                 if (key < n_sh) {
-                    page = pre_pages[key >> a.pg.log2_page];
-                    off = key & (P - 1);
+                    pr.page[i] = pre_pages[key >> a.pg.log2_page];
+                    pr.off[i] = key & (P - 1);
                 } else {
                     const int sl = key - n_sh;
-                    page = own_pages[sl >> a.pg.log2_page];
-                    off = sl & (P - 1);
+                    pr.page[i] = own_pages[sl >> a.pg.log2_page];
+                    pr.off[i] = sl & (P - 1);
                 }
-                if (page >= 0) {
-                    const uint8_t *hb = a.pool + (uint64_t)page * a.pg.page_bytes + (uint64_t)g * a.pg.head_bytes;
-                    const uint8_t *src = isv ? hb + (uint64_t)P * DK * ES + (uint64_t)off * DV * ES
-                                             : hb + (uint64_t)off * DK * ES;
-                    sg.w[i] = __builtin_nontemporal_load(reinterpret_cast<const u32x4 *>(src) + ch);
-                    if (ES == 1 && ch == 0)
-                        sg.sc[i] = reinterpret_cast<const float *>(hb + (uint64_t)P * (DK + DV))[(isv ? P : 0) + off];
-                }
+            }
+        }
+    };
+    auto load_tile = [&](const PageRef &pr, Staged<T::CPT> &sg) {
+#pragma unroll
+        for (int i = 0; i < T::CPT; i++) {
+            const int c = tid + i * NTHR;
+            const bool isv = c >= PF_KT * T::KC;
+            const int cc = isv ? c - PF_KT * T::KC : c;
+            const int ch = isv ? cc % T::VC : cc % T::KC;
+            sg.w[i] = u32x4{0u, 0u, 0u, 0u};
+            sg.sc[i] = 0.0f;
+            if (pr.page[i] >= 0) {
+                const int off = pr.off[i];
+                const uint8_t *hb = a.pool + (uint64_t)pr.page[i] * a.pg.page_bytes + (uint64_t)g * a.pg.head_bytes;
+                const uint8_t *src = isv ? hb + (uint64_t)P * DK * ES + (uint64_t)off * DV * ES
+                                         : hb + (uint64_t)off * DK * ES;
+                sg.w[i] = __builtin_nontemporal_load(reinterpret_cast<const u32x4 *>(src) + ch);
+                if (ES == 1 && ch == 0)
+                    sg.sc[i] = reinterpret_cast<const float *>(hb + (uint64_t)P * (DK + DV))[(isv ? P : 0) + off];
             }
         }
     };
@@ -215,14 +230,18 @@ __global__ __launch_bounds__(64 * W) void prefill_kernel(PrefillArgs a)
     };
 
     Staged<T::CPT> sg;
-    load_tile(0, sg);
+    PageRef pr_next, pr_after;
+    fetch_pages(0, pr_next);
+    load_tile(pr_next, sg);
     store_tile(sg, 0);
+    fetch_pages(PF_KT, pr_next);
     __syncthreads();
     int cur = 0;
     for (int kt = 0; kt < kmax; kt += PF_KT, cur ^= 1) {
         const bool more = kt + PF_KT < kmax;
         if (more)
-            load_tile(kt + PF_KT, sg);      // in flight while this tile computes
+            load_tile(pr_next, sg);         // tile kt+32: in flight while this tile computes
+        fetch_pages(kt + 2 * PF_KT, pr_after);
         const _Float16 (*Ks)[T::KPAD] = Ks2[cur];
         const _Float16 (*Vt)[T::VPAD] = Vt2[cur];
         const float *Ksc = Ksc2[cur], *Vsc = Vsc2[cur];
@@ -235,26 +254,31 @@ __global__ __launch_bounds__(64 * W) void prefill_kernel(PrefillArgs a)
             st = mfma32(ka, qh[kb], st);
             st = mfma32(ka, ql[kb], st);
         }
-        // register i holds key 8*(i/4) + 4*jh + (i%4) of the tile, row ln
-        const bool need_mask = (kt + PF_KT > kfull) || !rvalid;
-        float mt = -FLT_MAX;
+        // register i holds key 8*(i/4) + 4*jh + (i%4) of the tile, row ln.
+        // Only tiles crossing the diagonal mask (a work-group-uniform branch);
+        // rows past the chunk compute on zero queries and are never written.
+        if constexpr (ES == 1) {
 #pragma unroll
-        for (int i = 0; i < 16; i++) {
-            const int kl = 8 * (i >> 2) + 4 * jh + (i & 3);
-            float s = st[i];
-            if constexpr (ES == 1)
-                s *= Ksc[kl];
-            if (need_mask && (!rvalid || kt + kl > qpos))
-                s = -INFINITY;
-            st[i] = s;
-            mt = fmaxf(mt, s);
+            for (int i = 0; i < 16; i++)
+                st[i] *= Ksc[8 * (i >> 2) + 4 * jh + (i & 3)];
         }
+        if (kt + PF_KT > kfull) {
+#pragma unroll
+            for (int i = 0; i < 16; i++) {
+                const int kl = 8 * (i >> 2) + 4 * jh + (i & 3);
+                st[i] = kt + kl > qpos ? -INFINITY : st[i];
+            }
+        }
+        float mt = st[0];
+#pragma unroll
+        for (int i = 1; i < 16; i++)
+            mt = fmaxf(mt, st[i]);
         mt = fmaxf(mt, __shfl_xor(mt, 32, 64));
         // Lazy max: keep the running max unless the tile exceeds it by more
         // than 2^8 (weights stay <= 256, exact range for fp16 and fp32), and
         // skip the rescale sweep when no row of the wave moved.
         const bool grow = mt > m + 8.0f;
-        if (__ballot(grow)) {
+        if (__builtin_expect(__ballot(grow) != 0, 0)) {
             const float mnew = grow ? mt : m;
             const float rs = fast_exp2(m - mnew);
             m = mnew;
@@ -306,6 +330,7 @@ __global__ __launch_bounds__(64 * W) void prefill_kernel(PrefillArgs a)
         }
         if (more)
             store_tile(sg, cur ^ 1);        // the other buffer: its readers finished last iteration
+        pr_next = pr_after;
         __syncthreads();
     }
 

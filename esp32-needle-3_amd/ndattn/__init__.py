@@ -29,7 +29,7 @@ ABI_SYMBOLS = [
     "nda_prefix_build", "nda_seq_attach", "nda_seq_rewind", "nda_prefix_free",
     "nda_kv_append", "nda_decode", "nda_step", "nda_prefill", "nda_sync",
     "nda_kv_read", "nda_kv_write", "nda_kv_fill_normal",
-    "nda_dev_alloc", "nda_dev_free", "nda_h2d", "nda_d2h", "nda_memset", "nda_fill_normal",
+    "nda_dev_alloc", "nda_dev_free", "nda_h2d", "nda_d2h", "nda_d2d", "nda_memset", "nda_fill_normal",
     "nda_stream_create", "nda_stream_destroy", "nda_device_sync", "nda_device_info",
     "nda_prof_enable", "nda_prof_read",
 ]
@@ -94,6 +94,7 @@ def lib():
             "nda_h2d": (C.c_int, [vp, vp, C.c_size_t]),
             "nda_d2h": (C.c_int, [vp, vp, C.c_size_t]),
             "nda_memset": (C.c_int, [vp, C.c_int, C.c_size_t]),
+            "nda_d2d": (C.c_int, [vp, vp, C.c_size_t, vp]),
             "nda_fill_normal": (C.c_int, [vp, u64, C.c_int, u64, C.c_float, vp]),
             "nda_stream_create": (C.c_int, [C.POINTER(vp)]),
             "nda_stream_destroy": (C.c_int, [vp]),

@@ -185,6 +185,9 @@ int nda_dev_free(void *ptr);
 int nda_h2d(void *dst, const void *src, size_t bytes);
 int nda_d2h(void *dst, const void *src, size_t bytes);
 int nda_memset(void *dst, int value, size_t bytes);
+/* Device-to-device copy on a stream (also the known-size copy used to
+ * calibrate memory-traffic counters). */
+int nda_d2d(void *dst, const void *src, size_t bytes, void *stream);
 /* dst[i] = N(0,1) * scale as fp32 (dtype 0) or fp16 (dtype 1), i < n;
  * counter-based (seed, i). */
 int nda_fill_normal(void *dst, uint64_t n, int dtype, uint64_t seed, float scale, void *stream);
