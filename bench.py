@@ -27,6 +27,19 @@ LMIN, LMAX = 213, 1024
 SEED = 20261201
 
 
+def committed_traffic():
+    """HBM bytes per decode launch measured with rocprofv3 FETCH_SIZE and
+    WRITE_SIZE on this same command, calibrated on a copy of known size, as
+    recorded in the committed profile summary (None when absent)."""
+    import re
+    path = os.path.join(REPO, "profiles", "attend_kernel_decode_b4096_f16.md")
+    try:
+        m = re.search(r"traffic_bytes_per_launch:\s*(\d+)", open(path).read())
+        return int(m.group(1)) if m else None
+    except OSError:
+        return None
+
+
 def log(*a):
     print(*a, file=sys.stderr, flush=True)
 
@@ -118,6 +131,83 @@ def prefill_leg(N, stream, nseq=256, lmin=8192, lmax=32768, chunk=512, reps=3):
             "flop_per_launch": flops, "append_ms": round(ms[N.K_APPEND] / max(1, launches[N.K_APPEND]), 4),
             "call_ms": round(el * 1e3 / reps, 3), "max_abs_delta_sampled": worst,
             "note": "unmasked causal FLOPs; the kernel issues 2x this on MFMA (fp16 hi+lo for Q and P)"}
+
+
+def shared_prefix_leg(N, stream, nseq=1024, npre=213, nmin=32, nmax=64, dsteps=64, layers=LAYERS):
+    """Config 4: nseq sequences share one npre-token prefix (stored once per
+    layer); each prefills n ~ U[nmin, nmax] new tokens causally, then decodes
+    dsteps tokens, through `layers` layers. Unique bytes count the prefix once
+    per layer; logical bytes count it once per sequence."""
+    rng = np.random.default_rng(SEED + 9)
+    n = rng.integers(nmin, nmax + 1, nseq)
+    window = 384                                   # the engine's KV window
+    ctx = N.Context(layers, H, H, D, D, window, kv_dtype=N.KV_F16, max_seqs=nseq + 1)
+    builder = nseq
+    T = max(npre, int(n.sum()))
+    q, k, v, out = (N.DevBuf(T * H * D * 4) for _ in range(4))
+    for i, buf in enumerate((q, k, v)):
+        buf.fill_normal(T * H * D, 0, SEED + 90 + i, stream=stream)
+    for li in range(layers):
+        ctx.prefill(li, [npre], q, k, v, out, seq_ids=[builder], stream=stream)
+    ctx.advance(1, [builder], npre, stream=stream)
+    pid = ctx.prefix_build(builder, stream=stream)
+    for b in range(nseq):
+        ctx.seq_attach(b, pid, stream=stream)
+    ctx.sync(stream)
+    ctx.prof_enable(True)
+    ctx.prof_read(reset=True)
+    t0 = time.perf_counter()
+    for li in range(layers):
+        ctx.prefill(li, n, q, k, v, out, stream=stream)
+    ctx.sync(stream)
+    t_pf = time.perf_counter() - t0
+    ms, launches = ctx.prof_read(reset=True)
+    pf_ms = ms[N.K_PREFILL] / max(1, launches[N.K_PREFILL])
+    for b in range(nseq):
+        ctx.advance(1, [b], int(n[b]), stream=stream)
+    ctx.sync(stream)
+    pf_flops = float(sum(H * 2 * (D + D) * (npre * int(x) + int(x) * (int(x) + 1) / 2) for x in n))
+    pf_unique = (npre + int(n.sum())) * 2048 + int(n.sum()) * H * D * 4 * 2   # K/V once + q, out
+    ctx.prof_read(reset=True)
+    t0 = time.perf_counter()
+    for _ in range(dsteps):
+        for li in range(layers):
+            ctx.step(li, nseq, q, k, v, out, stream=stream)
+        ctx.advance(nseq, None, 1, stream=stream)
+    ctx.sync(stream)
+    t_dec = time.perf_counter() - t0
+    ms2, launches2 = ctx.prof_read(reset=True)
+    ctx.prof_enable(False)
+    dec_ms = ms2[N.K_DECODE] / max(1, launches2[N.K_DECODE])
+    # per decode launch: the prefix once + every sequence's own positions
+    own = sum(int(x) + s + 1 for x in n for s in range(dsteps)) / dsteps
+    uniq = npre * 2048 + own * 2048 + nseq * H * D * 4 * 2
+    logical = nseq * npre * 2048 + own * 2048 + nseq * H * D * 4 * 2
+    import ndoracle as O
+    qh = q.to_array(np.float32, (nseq, H * D))
+    oh = out.to_array(np.float32, (nseq, H * D))
+    worst = 0.0
+    for b in (0, nseq - 1):
+        pos = ctx.seq_state(b)[0] - 1
+        kk, vv, _, _ = ctx.kv_read(layers - 1, b, 0, pos + 1)
+        kv = O.kv_view(kk, vv, None, None, H, pos + 1, 0, pos, O.KV_F16)
+        want = O.attend_runs(kv, np.arange(pos + 1), [npre, pos + 1 - npre], qh[b], None)
+        worst = max(worst, float(np.abs(want - oh[b]).max()))
+    for b in range(nseq + 1):
+        ctx.seq_reset(b)
+    ctx.prefix_free(pid)
+    ctx.close()
+    return {"workload": "shared prefix: %d sequences share one %d-token prefix (stored once per layer), "
+                        "causal prefill of n ~ U[%d,%d] tokens each, then %d decode steps; %d layers, "
+                        "8 heads x 64, fp16, window 384" % (nseq, npre, nmin, nmax, dsteps, layers),
+            "prefill_kernel_ms": round(pf_ms, 4), "prefill_tflops": round(pf_flops / (pf_ms * 1e-3) / 1e12, 1),
+            "prefill_unique_GBps": round(pf_unique / (pf_ms * 1e-3) / 1e9, 1),
+            "prefill_wall_ms": round(t_pf * 1e3, 2),
+            "decode_tokens_per_s": round(nseq * dsteps / t_dec, 1),
+            "decode_kernel_ms": round(dec_ms, 4),
+            "decode_unique_GBps": round(uniq / (dec_ms * 1e-3) / 1e9, 1),
+            "decode_logical_GBps": round(logical / (dec_ms * 1e-3) / 1e9, 1),
+            "max_abs_delta_sampled": worst}
 
 
 def main():
@@ -234,6 +324,13 @@ def main():
     for bufs in (q, kn, vn, out):
         for bb in bufs:
             bb.free()
+    shared = None
+    if not args.no_prefill:
+        shared = shared_prefix_leg(N, stream)
+        log("shared prefix: prefill %.1f TFLOP/s (%.1f GB/s unique), decode %.0f tok/s, %.0f GB/s unique / "
+            "%.0f GB/s logical, sampled max |delta| %.3g" % (
+                shared["prefill_tflops"], shared["prefill_unique_GBps"], shared["decode_tokens_per_s"],
+                shared["decode_unique_GBps"], shared["decode_logical_GBps"], shared["max_abs_delta_sampled"]))
     prefill = None
     if not args.no_prefill:
         prefill = prefill_leg(N, stream)
@@ -268,11 +365,12 @@ def main():
                    "step_GB": round(step_bytes / 1e9, 3),
                    "step_GBps": round(step_bytes / (ms_per_step * 1e-3) / 1e9, 1)},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
-                     "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
+                     "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": committed_traffic(),
                      "kernel": "attend_kernel<f16,64,64,rep1>", "kernel_ms": round(dec_ms, 4),
                      "bytes_per_launch": int(dec_bytes_per_launch)},
         "cpu_baseline": cpu,
         "prefill": prefill,
+        "shared_prefix": shared,
         "max_abs_delta_sampled": worst,
         "device": name,
     }

@@ -50,7 +50,8 @@ struct nda_ctx {
     Geo geo{};
     PageGeom pg{};
     uint64_t max_pages = 0;
-    uint32_t chunk = 0;
+    uint32_t chunk = 0;                 // fixed split size, 0 = chosen per launch
+    int cus = 256;
 
     uint8_t *pool = nullptr;            // n_layers * layer_bytes
     int32_t *d_pages = nullptr;         // [max_seqs][pps]
@@ -386,8 +387,28 @@ int upload_rows(nda_ctx *c, uint32_t rows, const uint32_t *row_seq, const uint32
     return NDA_OK;
 }
 
+// Split-KV size for a launch. With enough (row, kv-head) units to fill the
+// chip many times over, rows are not split (no partials, no merge); with few
+// units, rows are cut into chunks so that ~64 work items per CU balance the
+// ragged lengths. A fixed split_chunk in the config overrides this.
+uint32_t pick_chunk(const nda_ctx *c, uint64_t units, uint64_t sum_total, uint32_t max_total)
+{
+    if (c->chunk)
+        return c->chunk;
+    const uint64_t cus = (uint64_t)c->cus;
+    uint64_t ch;
+    if (units >= 16 * cus)
+        ch = std::max<uint64_t>(max_total, 64);
+    else
+        ch = std::max<uint64_t>(256, (sum_total * c->cfg.n_kv_heads / (64 * cus) + 63) / 64 * 64);
+    // grid.y bound
+    const uint64_t min_ch = ((uint64_t)max_total + 65534) / 65535;
+    ch = std::max(ch, min_ch);
+    return (uint32_t)std::min<uint64_t>(ch, 1u << 30);
+}
+
 AttnArgs attn_args(nda_ctx *c, uint32_t layer, uint32_t rows, const float *q, const float *gate,
-                   float *out, uint32_t max_total)
+                   float *out, uint32_t max_total, uint64_t sum_total)
 {
     AttnArgs a{};
     a.q = q;
@@ -401,9 +422,9 @@ AttnArgs attn_args(nda_ctx *c, uint32_t layer, uint32_t rows, const float *q, co
     a.pg = c->pg;
     a.rows = rows;
     a.nh = c->cfg.n_heads;
-    a.chunk = c->chunk;
+    a.chunk = pick_chunk(c, (uint64_t)rows * c->cfg.n_kv_heads, sum_total, max_total);
     // grid.y and the partial-buffer stride: chunks of the longest row.
-    a.max_chunks = std::max<uint32_t>(1, (max_total + c->chunk - 1) / c->chunk);
+    a.max_chunks = std::max<uint32_t>(1, (max_total + a.chunk - 1) / a.chunk);
     a.qscale = (float)(1.4426950408889634 / std::sqrt((double)c->cfg.qk_head_dim));
     return a;
 }
@@ -490,12 +511,19 @@ int nda_create(const nda_config *cfg_in, nda_ctx **out)
     // Split-KV: a sequence longer than `chunk` visible positions is split into
     // chunks merged by the combine kernel. Visible positions <= 2 * window
     // (shared sinks + own slots).
-    c->chunk = cfg.split_chunk ? cfg.split_chunk : 1024;
+    c->chunk = cfg.split_chunk;
     if (c->chunk % 64)
         c->chunk = (c->chunk + 63) / 64 * 64;
-    if ((2ull * cfg.window + c->chunk - 1) / c->chunk > 65535) {
+    if (c->chunk && (2ull * cfg.window + c->chunk - 1) / c->chunk > 65535) {
         delete c;
         return NDA_ERR_ARG;
+    }
+    {
+        int dev = 0;
+        hipDeviceProp_t prop;
+        if (hipGetDevice(&dev) == hipSuccess && hipGetDeviceProperties(&prop, dev) == hipSuccess &&
+            prop.multiProcessorCount > 0)
+            c->cus = prop.multiProcessorCount;
     }
 
     const uint64_t pool_bytes = c->pg.layer_bytes * cfg.n_layers;
@@ -862,11 +890,13 @@ int nda_decode(nda_ctx *c, uint32_t layer, uint32_t nseq, const uint32_t *ids, c
     // Every visible slot must be backed (written by an append, a write or an
     // attach); an unbacked one means the caller skipped the append.
     uint32_t max_total = 0;
+    uint64_t sum_total = 0;
     for (uint32_t b = 0; b < nseq; b++) {
         const uint32_t qq = sid(ids, b);
         const SeqHost &s = c->seqs[qq];
         const Vis v = visible(s, s.pos, c->cfg.window);
         max_total = std::max(max_total, v.n_sh + v.n_own);
+        sum_total += v.n_sh + v.n_own;
         if (v.n_own) {
             const int32_t *row = &c->pages[(size_t)qq * c->pg.pages_per_seq];
             if (row[(v.n_own - 1) >> c->pg.log2_page] < 0 || row[0] < 0)
@@ -878,7 +908,7 @@ int nda_decode(nda_ctx *c, uint32_t layer, uint32_t nseq, const uint32_t *ids, c
     const uint32_t *d_seq, *d_t;
     if (int rc = upload_rows(c, nseq, ids, nullptr, st, &d_seq, &d_t))
         return rc;
-    AttnArgs a = attn_args(c, layer, nseq, q, gate, out, max_total);
+    AttnArgs a = attn_args(c, layer, nseq, q, gate, out, max_total, sum_total);
     a.row_seq = d_seq;
     a.row_t = d_t;
     return run_attend(c, a, st);
@@ -905,6 +935,7 @@ int nda_prefill(nda_ctx *c, uint32_t layer, uint32_t nseq, const uint32_t *ids, 
     hipStream_t st = (hipStream_t)stream;
     uint64_t rows = 0;
     uint32_t max_total = 0;
+    uint64_t sum_total = 0;
     for (uint32_t b = 0; b < nseq; b++) {
         const uint32_t qq = sid(ids, b);
         const SeqHost &s = c->seqs[qq];
@@ -917,6 +948,7 @@ int nda_prefill(nda_ctx *c, uint32_t layer, uint32_t nseq, const uint32_t *ids, 
         if (n_tokens[b]) {
             const Vis v = visible(s, s.pos + n_tokens[b] - 1, c->cfg.window);
             max_total = std::max(max_total, v.n_sh + v.n_own);
+            sum_total += (uint64_t)n_tokens[b] * (v.n_sh + v.n_own);
         }
         rows += n_tokens[b];
     }
@@ -963,7 +995,7 @@ int nda_prefill(nda_ctx *c, uint32_t layer, uint32_t nseq, const uint32_t *ids, 
             return hip_fail(c, e, "append kernel launch");
     }
     if (c->cfg.flags & NDA_FLAG_PREFILL_VALU) {
-        AttnArgs a = attn_args(c, layer, (uint32_t)rows, q, gate, out, max_total);
+        AttnArgs a = attn_args(c, layer, (uint32_t)rows, q, gate, out, max_total, sum_total);
         a.row_seq = d_seq;
         a.row_t = d_t;
         return run_attend(c, a, st);

@@ -648,12 +648,30 @@ __global__ __launch_bounds__(256) void fill_kv_kernel(FillKvArgs a)
 
 // ------------------------------------------------------------- dispatch
 
-// Lanes per KV position: 16-byte slices of a 64-element row.
-template <int ES>
-constexpr int lanes_per_pos() { return ES == 2 ? 8 : 4; }
+// Lanes per KV position: 16-byte row slices (8 fp16 or 16 int8 elements);
+// 8-byte int8 slices for the widest GQA group, whose per-lane state would
+// not fit in registers otherwise.
+template <int ES, int DK, int REP>
+constexpr int lanes_per_pos() { return ES == 2 ? 8 : ((REP >= 8 && DK % 64 == 0) ? 8 : 4); }
 
-constexpr int ATT_NW = 4;
-constexpr int ATT_NP = 2;
+// Waves per decode work-group and positions per lane group per step
+// (build-time tuning knobs).
+#ifndef NDA_ATT_NW
+#define NDA_ATT_NW 8
+#endif
+constexpr int ATT_NW = NDA_ATT_NW;
+
+// Positions per lane group per step: as many loads in flight as registers
+// allow without spilling (the int8 and wide-GQA states are larger).
+template <int ES, int REP>
+constexpr int att_np()
+{
+#ifdef NDA_ATT_NP
+    return NDA_ATT_NP;
+#else
+    return (ES == 2 && REP <= 2) ? 4 : (REP <= 2 ? 2 : 1);
+#endif
+}
 
 #define NDA_FOR_GEOMETRIES(X) \
     X(2, 64, 64, 1) X(2, 64, 64, 2) X(2, 64, 64, 4) X(2, 64, 64, 6) X(2, 64, 64, 8) \
@@ -680,7 +698,7 @@ hipError_t launch_attend(const Geo &g, const AttnArgs &a, hipStream_t s)
     dim3 grid(a.rows * a.pg.nkv, a.max_chunks);
 #define X(ES, DK, DV, REP)                                                                      \
     if (es_of(g) == ES && g.dk == DK && g.dv == DV && g.rep == REP) {                          \
-        hipLaunchKernelGGL((attend_kernel<ES, DK, DV, REP, lanes_per_pos<ES>(), ATT_NP, ATT_NW>), \
+        hipLaunchKernelGGL((attend_kernel<ES, DK, DV, REP, lanes_per_pos<ES, DK, REP>(), att_np<ES, REP>(), ATT_NW>), \
                            grid, dim3(64 * ATT_NW), 0, s, a);                                   \
         return hipGetLastError();                                                               \
     }
