@@ -76,6 +76,49 @@ def cpu_baseline(lens_all, seconds, nthreads):
     return tok_s, "%d sequences (L mean %.0f) x %d layer-calls, %.1f s" % (S, lens.mean(), calls, el)
 
 
+def cpu_reference_int8(lens_all, seconds):
+    """The reference engine's own store + attn_heads (oracle/_ref, compiled
+    from its sources) on the same shapes in its own dtype (int8 KV + scales,
+    MHA 8 x 64), one session per sequence, serial as the host build runs it
+    (rows_serial). Caches hold random int8 codes; the timed call is one
+    decode token (store + attend) per (sequence, layer). Returns tokens/s."""
+    import ctypes as C
+    import ndoracle as O
+    if not O.have_ref():
+        return None
+    rng = np.random.default_rng(SEED + 2)
+    S = 32
+    lens = rng.choice(lens_all, S)
+    sess = []
+    for L in lens:
+        r = O.RefSession(1, H, H, D, D, int(L) + 1)
+        k, v, ks, vs = r.cache()
+        k[:] = rng.integers(-127, 128, k.shape, dtype=np.int8)
+        v[:] = rng.integers(-127, 128, v.shape, dtype=np.int8)
+        ks[:] = rng.uniform(0.01, 0.03, ks.shape).astype(np.float32)
+        vs[:] = rng.uniform(0.01, 0.03, vs.shape).astype(np.float32)
+        O.ref().ref_set_pos(r.m, int(L) - 1)
+        sess.append(r)
+    q = rng.standard_normal(H * D).astype(np.float32)
+    kn = rng.standard_normal(H * D).astype(np.float32)
+    vn = rng.standard_normal(H * D).astype(np.float32)
+    out = np.zeros(H * D, np.float32)
+    f = O.ref().ref_attention
+    calls, t0 = 0, time.perf_counter()
+    while True:
+        for r in sess:
+            f(r.m, 0, q.ctypes.data, kn.ctypes.data, vn.ctypes.data, None, out.ctypes.data)
+        calls += S
+        el = time.perf_counter() - t0
+        if el >= seconds:
+            break
+    for r in sess:
+        r.close()
+    return {"value": round(calls / el / LAYERS, 1), "unit": "tokens/s", "cores": 1, "kind": "reference",
+            "sample": "%d sequences (L mean %.0f), int8 KV (the engine's dtype), %d layer-calls, %.1f s"
+                      % (S, lens.mean(), calls, el)}
+
+
 def prefill_leg(N, stream, nseq=256, lmin=8192, lmax=32768, chunk=512, reps=3):
     """Config 5's prefill: nseq sequences with L ~ U[lmin, lmax] stored
     positions each take a `chunk`-token causal prefill (append + MFMA attention)
@@ -338,12 +381,16 @@ def main():
             (prefill["tflops"], prefill["frac"], prefill["kernel_ms"], prefill["max_abs_delta_sampled"]))
 
     cpu = None
+    cpu_ref = None
     if not args.no_cpu:
         ncores = min(16, os.cpu_count() or 1)
         c_tok, sample = cpu_baseline(lens, args.cpu_seconds, ncores)
         cpu = {"value": round(c_tok, 1), "unit": "tokens/s", "cores": ncores, "kind": "port",
                "sample": sample + ", fp16 KV, no gate, oracle attn_heads restatement"}
         log("cpu baseline: %.1f tok/s on %d threads" % (c_tok, ncores))
+        cpu_ref = cpu_reference_int8(lens, args.cpu_seconds / 2)
+        if cpu_ref:
+            log("cpu reference (int8, 1 thread): %.1f tok/s" % cpu_ref["value"])
 
     res = {
         "metric": "decode attn tokens/s + HBM GB/s (% peak) at B=4096; prefill TFLOP/s",
@@ -369,6 +416,7 @@ def main():
                      "kernel": "attend_kernel<f16,64,64,rep1>", "kernel_ms": round(dec_ms, 4),
                      "bytes_per_launch": int(dec_bytes_per_launch)},
         "cpu_baseline": cpu,
+        "cpu_reference_int8": cpu_ref,
         "prefill": prefill,
         "shared_prefix": shared,
         "max_abs_delta_sampled": worst,

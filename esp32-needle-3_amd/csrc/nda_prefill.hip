@@ -229,19 +229,24 @@ __global__ __launch_bounds__(64 * W) void prefill_kernel(PrefillArgs a)
         }
     };
 
-    Staged<T::CPT> sg;
-    PageRef pr_next, pr_after;
-    fetch_pages(0, pr_next);
-    load_tile(pr_next, sg);
-    store_tile(sg, 0);
-    fetch_pages(PF_KT, pr_next);
+    // Two tiles of registers in flight: tile kt+32 waits in sg1 for its LDS
+    // store while tile kt+64 loads into sg2, so each load has two tiles of
+    // compute to land; page ids run one tile further ahead.
+    Staged<T::CPT> sg1, sg2;
+    PageRef pr2, pr3;
+    fetch_pages(0, pr2);
+    load_tile(pr2, sg1);
+    store_tile(sg1, 0);
+    fetch_pages(PF_KT, pr2);
+    load_tile(pr2, sg1);
+    fetch_pages(2 * PF_KT, pr2);
     __syncthreads();
     int cur = 0;
     for (int kt = 0; kt < kmax; kt += PF_KT, cur ^= 1) {
         const bool more = kt + PF_KT < kmax;
-        if (more)
-            load_tile(pr_next, sg);         // tile kt+32: in flight while this tile computes
-        fetch_pages(kt + 2 * PF_KT, pr_after);
+        if (kt + 2 * PF_KT < kmax)
+            load_tile(pr2, sg2);            // tile kt+64
+        fetch_pages(kt + 3 * PF_KT, pr3);
         const _Float16 (*Ks)[T::KPAD] = Ks2[cur];
         const _Float16 (*Vt)[T::VPAD] = Vt2[cur];
         const float *Ksc = Ksc2[cur], *Vsc = Vsc2[cur];
@@ -329,8 +334,9 @@ __global__ __launch_bounds__(64 * W) void prefill_kernel(PrefillArgs a)
             }
         }
         if (more)
-            store_tile(sg, cur ^ 1);        // the other buffer: its readers finished last iteration
-        pr_next = pr_after;
+            store_tile(sg1, cur ^ 1);       // tile kt+32 into the other buffer (its readers are done)
+        sg1 = sg2;
+        pr2 = pr3;
         __syncthreads();
     }
 

@@ -561,3 +561,61 @@ def test_prefill_mfma_matches_valu_path():
     _, a = _prefill_case(O.KV_F16, 8, 8, 64, hist, ntok, seed=24)
     _, b = _prefill_case(O.KV_F16, 8, 8, 64, hist, ntok, seed=24, flags=1)
     assert maxdiff(a, b) <= 2e-6
+
+
+@pytest.mark.parametrize("page_size", [32, 64])
+def test_page_sizes_decode_and_prefill(page_size):
+    """The paged layout at 32 and 64 positions per page: ragged decode,
+    split-KV, shared-prefix prefill, against the oracle."""
+    say("page size", page_size)
+    N = nda()
+    rng = np.random.default_rng(30 + page_size)
+    nh = nkv = 8
+    d, W = 64, 512
+    for dt in (O.KV_F16, O.KV_INT8):
+        ctx = N.Context(1, nh, nkv, d, d, W, kv_dtype=dt, max_seqs=5, page_size=page_size, split_chunk=128)
+        # a 100-token prefix shared by 4 sequences, ragged suffixes, one decode step
+        npre = 100
+        q = rng.standard_normal((npre, nh, d)).astype(np.float32)
+        k = rng.standard_normal((npre, nkv, d)).astype(np.float32)
+        v = rng.standard_normal((npre, nkv, d)).astype(np.float32)
+        dout = N.DevBuf(npre * nh * d * 4)
+        ctx.prefill(0, [npre], N.DevBuf.from_array(q), N.DevBuf.from_array(k), N.DevBuf.from_array(v),
+                    dout, seq_ids=[4])
+        ctx.advance(1, [4], npre)
+        pid = ctx.prefix_build(4)
+        for b in range(4):
+            ctx.seq_attach(b, pid)
+        n = [1, 37, 64, 200]
+        T = sum(n)
+        q = rng.standard_normal((T, nh, d)).astype(np.float32)
+        k = rng.standard_normal((T, nkv, d)).astype(np.float32)
+        v = rng.standard_normal((T, nkv, d)).astype(np.float32)
+        dout = N.DevBuf(T * nh * d * 4)
+        ctx.prefill(0, n, N.DevBuf.from_array(q), N.DevBuf.from_array(k), N.DevBuf.from_array(v), dout,
+                    seq_ids=[0, 1, 2, 3])
+        ctx.sync()
+        got = dout.to_array(np.float32, (T, nh * d))
+        r, worst = 0, 0.0
+        for b in range(4):
+            view, keep = _views_for(ctx, 0, b, npre + n[b] - 1, nh, dt)
+            for t in range(n[b]):
+                pos = npre + t
+                want = O.attend_runs(view, np.arange(pos + 1), [npre, pos + 1 - npre], q[r], None)
+                worst = max(worst, maxdiff(got[r], want))
+                r += 1
+        for b in range(4):
+            ctx.advance(1, [b], n[b])
+        qd = rng.standard_normal((4, nh, d)).astype(np.float32)
+        kd = rng.standard_normal((4, nkv, d)).astype(np.float32)
+        vd = rng.standard_normal((4, nkv, d)).astype(np.float32)
+        dout = N.DevBuf(4 * nh * d * 4)
+        ctx.step(0, 4, N.DevBuf.from_array(qd), N.DevBuf.from_array(kd), N.DevBuf.from_array(vd), dout)
+        ctx.sync()
+        got = dout.to_array(np.float32, (4, nh * d))
+        for b in range(4):
+            pos = ctx.seq_state(b)[0]
+            view, keep = _views_for(ctx, 0, b, pos, nh, dt)
+            want = O.attend_runs(view, np.arange(pos + 1), [npre, pos + 1 - npre], qd[b], None)
+            worst = max(worst, maxdiff(got[b], want))
+        assert worst <= TOL, (dt, worst)
