@@ -1005,7 +1005,11 @@ int nda_prefill(nda_ctx *c, uint32_t layer, uint32_t nseq, const uint32_t *ids, 
     uint32_t max_rows = 0;
     for (uint32_t b = 0; b < nseq; b++)
         max_rows = std::max(max_rows, n_tokens[b] * rep);
-    const int waves = max_rows <= 64 ? 2 : 4;
+    // Work-group size by the longest chunk: 64-row groups for short
+    // suffixes, 256-row groups (K/V staged once for 8 waves) for long ones.
+    int waves = max_rows <= 64 ? 2 : (max_rows >= 256 ? 8 : 4);
+    if (waves == 8 && !(c->geo.kv_f16 && c->geo.rep == 1))
+        waves = 4;
     const uint32_t trows = 32u * waves;
     std::vector<uint32_t> host(3 * (size_t)nseq);
     std::vector<uint32_t> items;

@@ -74,7 +74,8 @@ __device__ __forceinline__ _Float16 code_at(uint32_t w, int i)
 }
 
 template <int ES, int DK, int DV, int REP, int W>
-__global__ __launch_bounds__(64 * W) void prefill_kernel(PrefillArgs a)
+__global__ __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(W >= 8 ? 4 : 1)))
+void prefill_kernel(PrefillArgs a)
 {
     using T = PfTile<ES, DK, DV, 64 * W>;
     static_assert(DK % 16 == 0 && DV == 64, "prefill tiles: dk multiple of 16, dv 64");
@@ -229,24 +230,37 @@ __global__ __launch_bounds__(64 * W) void prefill_kernel(PrefillArgs a)
         }
     };
 
-    // Two tiles of registers in flight: tile kt+32 waits in sg1 for its LDS
+    // Register prefetch: with PD = 2, tile kt+32 waits in sg1 for its LDS
     // store while tile kt+64 loads into sg2, so each load has two tiles of
-    // compute to land; page ids run one tile further ahead.
+    // compute to land; the 8-wave variant keeps one tile in flight to stay
+    // within the 128 registers of 4 waves per SIMD. Page ids run one tile
+    // further ahead than the data.
+    constexpr int PD = W >= 8 ? 1 : 2;
     Staged<T::CPT> sg1, sg2;
     PageRef pr2, pr3;
     fetch_pages(0, pr2);
     load_tile(pr2, sg1);
     store_tile(sg1, 0);
     fetch_pages(PF_KT, pr2);
-    load_tile(pr2, sg1);
-    fetch_pages(2 * PF_KT, pr2);
+    if constexpr (PD == 2) {
+        load_tile(pr2, sg1);
+        fetch_pages(2 * PF_KT, pr2);
+    }
     __syncthreads();
     int cur = 0;
-    for (int kt = 0; kt < kmax; kt += PF_KT, cur ^= 1) {
+    // One key tile; `masked` is a literal at both call sites, so the
+    // unmasked loop carries no diagonal-mask code at all.
+    auto tile = [&](const int kt, const bool masked) __attribute__((always_inline)) {
         const bool more = kt + PF_KT < kmax;
-        if (kt + 2 * PF_KT < kmax)
-            load_tile(pr2, sg2);            // tile kt+64
-        fetch_pages(kt + 3 * PF_KT, pr3);
+        if constexpr (PD == 2) {
+            if (kt + 2 * PF_KT < kmax)
+                load_tile(pr2, sg2);        // tile kt+64
+            fetch_pages(kt + 3 * PF_KT, pr3);
+        } else {
+            if (more)
+                load_tile(pr2, sg1);        // tile kt+32
+            fetch_pages(kt + 2 * PF_KT, pr3);
+        }
         const _Float16 (*Ks)[T::KPAD] = Ks2[cur];
         const _Float16 (*Vt)[T::VPAD] = Vt2[cur];
         const float *Ksc = Ksc2[cur], *Vsc = Vsc2[cur];
@@ -267,7 +281,7 @@ __global__ __launch_bounds__(64 * W) void prefill_kernel(PrefillArgs a)
             for (int i = 0; i < 16; i++)
                 st[i] *= Ksc[8 * (i >> 2) + 4 * jh + (i & 3)];
         }
-        if (kt + PF_KT > kfull) {
+        if (masked) {
 #pragma unroll
             for (int i = 0; i < 16; i++) {
                 const int kl = 8 * (i >> 2) + 4 * jh + (i & 3);
@@ -306,9 +320,14 @@ __global__ __launch_bounds__(64 * W) void prefill_kernel(PrefillArgs a)
                 p1 *= Vsc[8 * (i >> 2) + 4 * jh + ((i + 1) & 3)];
             }
             const fp16x2 h = __builtin_amdgcn_cvt_pkrtz(p0, p1);
-            const fp16x2 lo = __builtin_amdgcn_cvt_pkrtz(p0 - (float)h[0], p1 - (float)h[1]);
-            phw[i >> 3][(i & 7) >> 1] = __builtin_bit_cast(uint32_t, h);
-            plw[i >> 3][(i & 7) >> 1] = __builtin_bit_cast(uint32_t, lo);
+            const uint32_t hw = __builtin_bit_cast(uint32_t, h);
+            // lo = fp16(p - hi): one mixed-precision FMA per element, the fp16
+            // hi half widened inside the FMA, written into its half of lw.
+            uint32_t lw;
+            asm("v_fma_mixlo_f16 %0, %1, -1.0, %2 op_sel_hi:[1,0,0]" : "=v"(lw) : "v"(hw), "v"(p0));
+            asm("v_fma_mixhi_f16 %0, %1, -1.0, %2 op_sel:[1,0,0] op_sel_hi:[1,0,0]" : "+v"(lw) : "v"(hw), "v"(p1));
+            phw[i >> 3][(i & 7) >> 1] = hw;
+            plw[i >> 3][(i & 7) >> 1] = lw;
         }
         half8 ph[2], pl[2];
         ph[0] = __builtin_bit_cast(half8, phw[0]);
@@ -335,10 +354,19 @@ __global__ __launch_bounds__(64 * W) void prefill_kernel(PrefillArgs a)
         }
         if (more)
             store_tile(sg1, cur ^ 1);       // tile kt+32 into the other buffer (its readers are done)
-        sg1 = sg2;
+        if constexpr (PD == 2)
+            sg1 = sg2;
         pr2 = pr3;
         __syncthreads();
-    }
+        cur ^= 1;
+    };
+    // tiles [0, kfull_end) are visible to every row of the work-group
+    const int kfull_end = min((kfull / PF_KT) * PF_KT, kmax);
+    int kt = 0;
+    for (; kt < kfull_end; kt += PF_KT)
+        tile(kt, false);
+    for (; kt < kmax; kt += PF_KT)
+        tile(kt, true);
 
     // ---- emit: lane holds row ln, dims 32*dt + 8*(i/4) + 4*jh + (i%4)
     lsum += __shfl_xor(lsum, 32, 64);
@@ -375,16 +403,24 @@ __global__ __launch_bounds__(64 * W) void prefill_kernel(PrefillArgs a)
     X(1, 64, 64, 1) X(1, 64, 64, 2) X(1, 64, 64, 4) X(1, 64, 64, 6) X(1, 64, 64, 8) \
     X(1, 48, 64, 1) X(1, 48, 64, 2) X(1, 48, 64, 6)
 
+// Geometries whose 8-wave variant fits the 128-register budget of 4 waves per
+// SIMD; the others run 4-wave work-groups.
+static bool pf_w8_fits(const Geo &g) { return g.kv_f16 && g.rep == 1; }
+
 hipError_t launch_prefill(const Geo &g, const PrefillArgs &a, int waves, hipStream_t s)
 {
     if (a.n_items == 0)
         return hipSuccess;
+    if (waves == 8 && !pf_w8_fits(g))
+        waves = 4;
     const int es = g.kv_f16 ? 2 : 1;
     dim3 grid(a.n_items);     // n_items: a multiple of 8 (padded with empty items)
 #define X(ES, DK, DV, REP)                                                                      \
     if (es == ES && g.dk == DK && g.dv == DV && g.rep == REP) {                                 \
         if (waves == 2)                                                                          \
             hipLaunchKernelGGL((prefill_kernel<ES, DK, DV, REP, 2>), grid, dim3(128), 0, s, a);  \
+        else if (waves == 8)                                                                     \
+            hipLaunchKernelGGL((prefill_kernel<ES, DK, DV, REP, 8>), grid, dim3(512), 0, s, a);  \
         else                                                                                     \
             hipLaunchKernelGGL((prefill_kernel<ES, DK, DV, REP, 4>), grid, dim3(256), 0, s, a);  \
         return hipGetLastError();                                                                \
