@@ -3,9 +3,10 @@ MI355X (the headline workload: 4096 independent sequences, 8 heads x 64,
 fp16 K/V, ragged lengths uniform in [213, 1024], one new token per sequence
 through 8 layers).
 
-A step = for each of 8 layers: KV append of the new token (nda_kv_append) and
-single-token attention (nda_decode), then pos += 1 (nda_advance); inputs are
-resident in HBM before the timed region. Prints one JSON line.
+A step = for each of 8 layers: KV append of the new token and single-token
+attention (nda_step: the append kernel then the decode kernel at this batch
+size), then pos += 1 (nda_advance); inputs are resident in HBM before the
+timed region. Prints one JSON line.
 
     python bench.py [--steps K] [--warmup W] [--no-cpu]
 """
@@ -253,6 +254,48 @@ def shared_prefix_leg(N, stream, nseq=1024, npre=213, nmin=32, nmax=64, dsteps=6
             "max_abs_delta_sampled": worst}
 
 
+def engine_session_leg(N, steps=200):
+    """The engine drop-in: one session through the C shim (nd_gpu_attention,
+    host arrays in and out, as attention() would call it), MHA 8 x 64, int8
+    KV, 213 pinned prefix positions + decode; mean latency per layer call,
+    beside the reference's own store + attn_heads on the same session shape
+    (oracle/_ref, one host thread)."""
+    import ndoracle as O
+    rng = np.random.default_rng(SEED + 11)
+    geom = (1, H, H, D, D, 512)
+    g = N.GpuSession(*geom)
+    r = O.RefSession(*geom) if O.have_ref() else None
+    toks = [[rng.standard_normal(H * D).astype(np.float32) for _ in range(4)] for _ in range(8)]
+    for t in range(213):
+        g.attention(0, *toks[t % 8])
+        g.step_end()
+        if r:
+            r.attention(0, *toks[t % 8])
+            r.step_end()
+    g.snapshot()
+    if r:
+        r.snapshot()
+    t0 = time.perf_counter()
+    for t in range(steps):
+        g.attention(0, *toks[t % 8])
+        g.step_end()
+    gpu_us = (time.perf_counter() - t0) / steps * 1e6
+    ref_us = None
+    if r:
+        t0 = time.perf_counter()
+        for t in range(steps):
+            r.attention(0, *toks[t % 8])
+            r.step_end()
+        ref_us = (time.perf_counter() - t0) / steps * 1e6
+        r.close()
+    g.close()
+    return {"workload": "one engine session through nd_gpu_attention (host arrays): MHA 8 x 64, int8 KV, "
+                        "window 512, 213 pinned + %d decode positions" % steps,
+            "gpu_us_per_layer_call": round(gpu_us, 1),
+            "reference_cpu_us_per_layer_call": None if ref_us is None else round(ref_us, 1),
+            "note": "latency-bound (host<->device copies + 1 fused launch); throughput comes from batching"}
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -313,8 +356,7 @@ def main():
 
     def step():
         for li in range(LAYERS):
-            ctx.kv_append(li, B, kn[li], vn[li], stream=stream)
-            ctx.decode(li, B, q[li], out[li], stream=stream)
+            ctx.step(li, B, q[li], kn[li], vn[li], out[li], stream=stream)   # append + decode
         ctx.advance(B, None, 1, stream=stream)
 
     for _ in range(args.warmup):
@@ -367,6 +409,9 @@ def main():
     for bufs in (q, kn, vn, out):
         for bb in bufs:
             bb.free()
+    engine = engine_session_leg(N)
+    log("engine session: GPU %.1f us per layer call, reference CPU %s us" % (
+        engine["gpu_us_per_layer_call"], engine["reference_cpu_us_per_layer_call"]))
     shared = None
     if not args.no_prefill:
         shared = shared_prefix_leg(N, stream)
@@ -418,6 +463,7 @@ def main():
         "cpu_baseline": cpu,
         "cpu_reference_int8": cpu_ref,
         "prefill": prefill,
+        "engine_session": engine,
         "shared_prefix": shared,
         "max_abs_delta_sampled": worst,
         "device": name,

@@ -877,16 +877,30 @@ int nda_kv_append(nda_ctx *c, uint32_t layer, uint32_t nseq, const uint32_t *ids
     return NDA_OK;
 }
 
-int nda_decode(nda_ctx *c, uint32_t layer, uint32_t nseq, const uint32_t *ids, const float *q,
-               const float *gate, float *out, void *stream)
+// Decode, optionally with the append of this position fused in (k/v set).
+static int decode_impl(nda_ctx *c, uint32_t layer, uint32_t nseq, const uint32_t *ids, const float *q,
+                       const float *k, const float *v, const float *gate, float *out, void *stream)
 {
     if (!c || (nseq && (!q || !out)))
         return c ? fail(c, NDA_ERR_ARG, "null q/out") : NDA_ERR_ARG;
+    if (nseq && k && !v)
+        return fail(c, NDA_ERR_ARG, "null v");
     if (layer >= c->cfg.n_layers)
         return fail(c, NDA_ERR_ARG, "layer %u out of range", layer);
     if (int rc = check_ids(c, nseq, ids))
         return rc;
     hipStream_t st = (hipStream_t)stream;
+    if (k) {
+        for (uint32_t b = 0; b < nseq; b++) {
+            const uint32_t qq = sid(ids, b);
+            if (int rc = back_positions(c, qq, c->seqs[qq].pos, 1))
+                return rc;
+        }
+        for (uint32_t b = 0; b < nseq; b++) {
+            SeqHost &s = c->seqs[sid(ids, b)];
+            s.stored_end = std::max(s.stored_end, s.pos + 1);
+        }
+    }
     // Every visible slot must be backed (written by an append, a write or an
     // attach); an unbacked one means the caller skipped the append.
     uint32_t max_total = 0;
@@ -894,12 +908,12 @@ int nda_decode(nda_ctx *c, uint32_t layer, uint32_t nseq, const uint32_t *ids, c
     for (uint32_t b = 0; b < nseq; b++) {
         const uint32_t qq = sid(ids, b);
         const SeqHost &s = c->seqs[qq];
-        const Vis v = visible(s, s.pos, c->cfg.window);
-        max_total = std::max(max_total, v.n_sh + v.n_own);
-        sum_total += v.n_sh + v.n_own;
-        if (v.n_own) {
+        const Vis vv = visible(s, s.pos, c->cfg.window);
+        max_total = std::max(max_total, vv.n_sh + vv.n_own);
+        sum_total += vv.n_sh + vv.n_own;
+        if (vv.n_own) {
             const int32_t *row = &c->pages[(size_t)qq * c->pg.pages_per_seq];
-            if (row[(v.n_own - 1) >> c->pg.log2_page] < 0 || row[0] < 0)
+            if (row[(vv.n_own - 1) >> c->pg.log2_page] < 0 || row[0] < 0)
                 return fail(c, NDA_ERR_STATE, "sequence %u: slot of position %u never stored", qq, s.pos);
         }
     }
@@ -911,16 +925,33 @@ int nda_decode(nda_ctx *c, uint32_t layer, uint32_t nseq, const uint32_t *ids, c
     AttnArgs a = attn_args(c, layer, nseq, q, gate, out, max_total, sum_total);
     a.row_seq = d_seq;
     a.row_t = d_t;
+    a.k_new = k;
+    a.v_new = v;
     return run_attend(c, a, st);
 }
 
+int nda_decode(nda_ctx *c, uint32_t layer, uint32_t nseq, const uint32_t *ids, const float *q,
+               const float *gate, float *out, void *stream)
+{
+    return decode_impl(c, layer, nseq, ids, q, nullptr, nullptr, gate, out, stream);
+}
+
+// Store, then attend. Small batches (launch latency dominates, e.g. one
+// engine session) fuse both into one launch: the decode work-group owning
+// the new slot quantises and stores it before attending. Large batches keep
+// two launches: a store plus barrier at the head of every one of tens of
+// thousands of work-groups costs more than the separate append kernel.
 int nda_step(nda_ctx *c, uint32_t layer, uint32_t nseq, const uint32_t *ids, const float *q,
              const float *k, const float *v, const float *gate, float *out, void *stream)
 {
-    int rc = nda_kv_append(c, layer, nseq, ids, k, v, stream);
-    if (rc)
-        return rc;
-    return nda_decode(c, layer, nseq, ids, q, gate, out, stream);
+    if (c && nseq && (!k || !v))
+        return fail(c, NDA_ERR_ARG, "null k/v");
+    if (c && (uint64_t)nseq * c->cfg.n_kv_heads >= 16ull * (uint64_t)c->cus) {
+        if (int rc = nda_kv_append(c, layer, nseq, ids, k, v, stream))
+            return rc;
+        return decode_impl(c, layer, nseq, ids, q, nullptr, nullptr, gate, out, stream);
+    }
+    return decode_impl(c, layer, nseq, ids, q, k, v, gate, out, stream);
 }
 
 int nda_prefill(nda_ctx *c, uint32_t layer, uint32_t nseq, const uint32_t *ids, const uint32_t *n_tokens,

@@ -52,6 +52,8 @@ struct AttnArgs {
     uint32_t chunk;          /* positions per work item */
     uint32_t max_chunks;
     float qscale;            /* log2(e) / sqrt(dk) */
+    const float *k_new;      /* [rows][nkv][dk] fused append (decode), or null */
+    const float *v_new;      /* [rows][nkv][dv] */
 };
 
 /* One launch of the MFMA causal-prefill kernel. A work item is one tile of

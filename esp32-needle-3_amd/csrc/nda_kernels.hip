@@ -109,6 +109,58 @@ __device__ __forceinline__ float elem(const uint32_t *w, int e)
     }
 }
 
+// One wave per (row, kv-head), lane = element. INT8: absmax over the row,
+// scale = absmax/127 (1 for a zero row), then the engine's store
+// (engine/src/nd_model.c:2426-2449 and kv_store_int8 :1819-1866) step for
+// step: r = 1/scale, y = x*r, e = fma(-scale, y, x), q = fma(e, r, y) (a plain
+// divide for |x| >= 1e30), clamp +-127, round half-to-even; a NaN quotient
+// (scale below 2^-127, where 1/scale overflows) stores 0 as the host build
+// does. F16: round to nearest even.
+__device__ __forceinline__ int8_t quant_code(float x, float scale, float r)
+{
+    float q;
+    if (x > -1e30f && x < 1e30f) {
+        const float y = x * r;
+        const float e = __builtin_fmaf(-scale, y, x);
+        q = __builtin_fmaf(e, r, y);
+    } else {
+        q = __fdiv_rn(x, scale);
+    }
+    if (q != q)
+        return 0;
+    q = q > 127.0f ? 127.0f : q;
+    q = q < -127.0f ? -127.0f : q;
+    return (int8_t)(int)__builtin_rintf(q);
+}
+
+// Store one row of K and V (lane = element) for slot `off` of a page's
+// kv-head block at hb. Shared by the append kernel and the fused append of
+// the decode kernel.
+template <int ES, int DK, int DV>
+__device__ __forceinline__ void store_row(uint8_t *hb, int off, int P, float kx, float vx, int lane)
+{
+    if constexpr (ES == 2) {
+        if (lane < DK)
+            reinterpret_cast<_Float16 *>(hb + (uint64_t)off * DK * 2)[lane] = (_Float16)kx;
+        if (lane < DV)
+            reinterpret_cast<_Float16 *>(hb + (uint64_t)P * DK * 2 + (uint64_t)off * DV * 2)[lane] = (_Float16)vx;
+    } else {
+        const float ak = wave_max(fabsf(kx)), av = wave_max(fabsf(vx));
+        const float sk = ak > 0.0f ? __fdiv_rn(ak, 127.0f) : 1.0f;
+        const float sv = av > 0.0f ? __fdiv_rn(av, 127.0f) : 1.0f;
+        const float rk = __fdiv_rn(1.0f, sk), rv = __fdiv_rn(1.0f, sv);
+        if (lane < DK)
+            reinterpret_cast<int8_t *>(hb + (uint64_t)off * DK)[lane] = quant_code(kx, sk, rk);
+        if (lane < DV)
+            reinterpret_cast<int8_t *>(hb + (uint64_t)P * DK + (uint64_t)off * DV)[lane] = quant_code(vx, sv, rv);
+        if (lane == 0) {
+            float *sc = reinterpret_cast<float *>(hb + (uint64_t)P * (DK + DV));
+            sc[off] = sk;
+            sc[P + off] = sv;
+        }
+    }
+}
+
 // -------------------------------------------------------- decode / causal
 
 template <int ES, int DK, int DV, int REP, int G, int NP, int NW>
@@ -278,6 +330,32 @@ __global__ __launch_bounds__(64 * NW) void attend_kernel(AttnArgs a)
         return;
     const int c0 = (int)chunk * (int)a.chunk, c1 = min(total, c0 + (int)a.chunk);
 
+    // Fused KV append (decode step): the work-group whose chunk holds the new
+    // position's slot stores it first (the engine stores before it attends,
+    // engine/src/nd_model.c:2426-2454), then every wave reads it like any
+    // other slot.
+    if (a.k_new) {
+        const int nslot = own_slot(sd, p, (int)a.pg.window);
+        const int vi = vis.n_sh + nslot;
+        if (vi >= c0 && vi < c1) {
+            if (wave == 0) {
+                const int32_t page = a.page_table[(uint64_t)seq * a.pg.pages_per_seq + (nslot >> a.pg.log2_page)];
+                if (page >= 0) {
+                    const int P = 1 << a.pg.log2_page;
+                    uint8_t *hb = const_cast<uint8_t *>(a.pool) + (uint64_t)page * a.pg.page_bytes +
+                                  (uint64_t)g * a.pg.head_bytes;
+                    const float kx = lane < DK ? a.k_new[((uint64_t)row * nkv + g) * DK + lane] : 0.0f;
+                    const float vx = lane < DV ? a.v_new[((uint64_t)row * nkv + g) * DV + lane] : 0.0f;
+                    store_row<ES, DK, DV>(hb, nslot & (P - 1), P, kx, vx, lane);
+                }
+            }
+            // Workgroup-scope release/acquire + barrier: all waves of the group
+            // share the CU's L1, so this is all the visibility the store needs
+            // (an agent-scope fence would write back L2 from every group).
+            __syncthreads();
+        }
+    }
+
     AttnState<ES, DK, DV, REP, G, NP, NW> st;
 #pragma unroll
     for (int t = 0; t < REP; t++) {
@@ -410,30 +488,6 @@ __global__ __launch_bounds__(256) void combine_kernel(AttnArgs a)
 
 // ------------------------------------------------------------- KV append
 
-// One wave per (row, kv-head), lane = element. INT8: absmax over the row,
-// scale = absmax/127 (1 for a zero row), then the engine's store
-// (engine/src/nd_model.c:2426-2449 and kv_store_int8 :1819-1866) step for
-// step: r = 1/scale, y = x*r, e = fma(-scale, y, x), q = fma(e, r, y) (a plain
-// divide for |x| >= 1e30), clamp +-127, round half-to-even; a NaN quotient
-// (scale below 2^-127, where 1/scale overflows) stores 0 as the host build
-// does. F16: round to nearest even.
-__device__ __forceinline__ int8_t quant_code(float x, float scale, float r)
-{
-    float q;
-    if (x > -1e30f && x < 1e30f) {
-        const float y = x * r;
-        const float e = __builtin_fmaf(-scale, y, x);
-        q = __builtin_fmaf(e, r, y);
-    } else {
-        q = __fdiv_rn(x, scale);
-    }
-    if (q != q)
-        return 0;
-    q = q > 127.0f ? 127.0f : q;
-    q = q < -127.0f ? -127.0f : q;
-    return (int8_t)(int)__builtin_rintf(q);
-}
-
 template <int ES, int DK, int DV>
 __global__ __launch_bounds__(256) void append_kernel(AppendArgs a)
 {
@@ -457,26 +511,7 @@ __global__ __launch_bounds__(256) void append_kernel(AppendArgs a)
 
     const float kx = lane < DK ? a.k[((uint64_t)row * nkv + g) * DK + lane] : 0.0f;
     const float vx = lane < DV ? a.v[((uint64_t)row * nkv + g) * DV + lane] : 0.0f;
-    if constexpr (ES == 2) {
-        if (lane < DK)
-            reinterpret_cast<_Float16 *>(hb + (uint64_t)off * DK * 2)[lane] = (_Float16)kx;
-        if (lane < DV)
-            reinterpret_cast<_Float16 *>(hb + (uint64_t)P * DK * 2 + (uint64_t)off * DV * 2)[lane] = (_Float16)vx;
-    } else {
-        const float ak = wave_max(fabsf(kx)), av = wave_max(fabsf(vx));
-        const float sk = ak > 0.0f ? __fdiv_rn(ak, 127.0f) : 1.0f;
-        const float sv = av > 0.0f ? __fdiv_rn(av, 127.0f) : 1.0f;
-        const float rk = __fdiv_rn(1.0f, sk), rv = __fdiv_rn(1.0f, sv);
-        if (lane < DK)
-            reinterpret_cast<int8_t *>(hb + (uint64_t)off * DK)[lane] = quant_code(kx, sk, rk);
-        if (lane < DV)
-            reinterpret_cast<int8_t *>(hb + (uint64_t)P * DK + (uint64_t)off * DV)[lane] = quant_code(vx, sv, rv);
-        if (lane == 0) {
-            float *sc = reinterpret_cast<float *>(hb + (uint64_t)P * (DK + DV));
-            sc[off] = sk;
-            sc[P + off] = sv;
-        }
-    }
+    store_row<ES, DK, DV>(hb, off, P, kx, vx, lane);
 }
 
 // ------------------------------------------------------ copies and staging

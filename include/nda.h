@@ -137,8 +137,9 @@ int nda_kv_append(nda_ctx *ctx, uint32_t layer, uint32_t nseq, const uint32_t *s
 int nda_decode(nda_ctx *ctx, uint32_t layer, uint32_t nseq, const uint32_t *seq_ids,
                const float *q, const float *gate, float *out, void *stream);
 
-/* nda_kv_append + nda_decode in one launch sequence (the order attention()
- * runs them: store first, the current token is attended). */
+/* nda_kv_append + nda_decode, in the order attention() runs them (store
+ * first; the current token is attended). Small batches run it as one fused
+ * launch, large ones as the two kernels; the results are the same. */
 int nda_step(nda_ctx *ctx, uint32_t layer, uint32_t nseq, const uint32_t *seq_ids,
              const float *q, const float *k, const float *v, const float *gate,
              float *out, void *stream);
