@@ -41,6 +41,23 @@ def committed_traffic():
         return None
 
 
+def host_info():
+    """ROCm version, host CPU model and the cores the CPU legs could use."""
+    info = {"cpus": os.cpu_count()}
+    try:
+        info["rocm"] = open("/opt/rocm/.info/version").read().strip()
+    except OSError:
+        info["rocm"] = None
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                info["cpu_model"] = line.split(":", 1)[1].strip()
+                break
+    except OSError:
+        pass
+    return info
+
+
 def log(*a):
     print(*a, file=sys.stderr, flush=True)
 
@@ -121,10 +138,13 @@ def cpu_reference_int8(lens_all, seconds):
 
 
 def prefill_leg(N, stream, nseq=256, lmin=8192, lmax=32768, chunk=512, reps=3):
-    """Config 5's prefill: nseq sequences with L ~ U[lmin, lmax] stored
-    positions each take a `chunk`-token causal prefill (append + MFMA attention)
-    on one layer. FLOPs count the unmasked causal pairs only:
-    sum_s H * 2 * (dk + dv) * (chunk * L_s + chunk * (chunk + 1) / 2)."""
+    """Long-context leg: nseq sequences with L ~ U[lmin, lmax] stored positions
+    each take one decode token (append + split-KV attention over L+1
+    positions, HBM-bound), then a `chunk`-token causal prefill (append + MFMA
+    attention) on one layer. Prefill FLOPs count the unmasked causal pairs
+    only: sum_s H * 2 * (dk + dv) * (chunk * L_s + chunk * (chunk + 1) / 2).
+    Decode bytes: sum_s (L_s + 1) * H * (dk + dv) * 2 plus q, out and the
+    appended row."""
     rng = np.random.default_rng(SEED + 5)
     lens = rng.integers(lmin, lmax + 1, nseq)
     P = 16
@@ -138,6 +158,9 @@ def prefill_leg(N, stream, nseq=256, lmin=8192, lmax=32768, chunk=512, reps=3):
     q, k, v, out = (N.DevBuf(T * H * D * 4) for _ in range(4))
     for i, buf in enumerate((q, k, v)):
         buf.fill_normal(T * H * D, 0, SEED + 70 + i, stream=stream)
+    dec = decode_long(N, ctx, stream, lens, q, k, v, out, reps=10)
+    ctx.advance(nseq, stream=stream)             # the decoded token stays; the chunk follows it
+    lens = lens + 1
     ntok = np.full(nseq, chunk, np.uint32)
     ctx.prefill(0, ntok, q, k, v, out, stream=stream)       # warm-up
     ctx.sync(stream)
@@ -171,10 +194,53 @@ def prefill_leg(N, stream, nseq=256, lmin=8192, lmax=32768, chunk=512, reps=3):
                         % (nseq, chunk, lmin, lmax),
             "tflops": round(tflops, 1), "unit": "TFLOP/s", "bound": "mfma",
             "peak": 2500.0, "frac": round(tflops / 2500.0, 4),
-            "kernel": "prefill_kernel<f16,64,64,rep1,W4>", "kernel_ms": round(pf_ms, 3),
+            "kernel": "prefill_kernel<f16,64,64,rep1,W8>", "kernel_ms": round(pf_ms, 3),
             "flop_per_launch": flops, "append_ms": round(ms[N.K_APPEND] / max(1, launches[N.K_APPEND]), 4),
             "call_ms": round(el * 1e3 / reps, 3), "max_abs_delta_sampled": worst,
-            "note": "unmasked causal FLOPs; the kernel issues 2x this on MFMA (fp16 hi+lo for Q and P)"}
+            "note": "unmasked causal FLOPs; the kernel issues 2x this on MFMA (fp16 hi+lo for Q and P)",
+            "decode": dec}
+
+
+def decode_long(N, ctx, stream, lens, q, k, v, out, reps):
+    """One decode token per sequence at position L_s (append + attention over
+    [0, L_s], split-KV at this batch), repeated `reps` times at the same
+    position; timed per kernel with HIP events on `stream`."""
+    nseq = len(lens)
+    ctx.step(0, nseq, q, k, v, out, stream=stream)           # warm-up
+    ctx.sync(stream)
+    ctx.prof_enable(True)
+    ctx.prof_read(reset=True)
+    t0 = time.perf_counter()
+    for _ in range(reps):
+        ctx.step(0, nseq, q, k, v, out, stream=stream)
+    ctx.sync(stream)
+    el = time.perf_counter() - t0
+    ms, launches = ctx.prof_read(reset=True)
+    ctx.prof_enable(False)
+    # per step; at this batch nda_step fuses the append into the attention launch
+    att_ms, comb_ms, app_ms = (ms[kind] / reps for kind in (N.K_DECODE, N.K_COMBINE, N.K_APPEND))
+    kv_bytes = float(sum((int(L) + 1) * H * (D + D) * 2 for L in lens))
+    io_bytes = nseq * H * D * 4 * 2
+    app_bytes = nseq * H * (D + D) * (4 + 2)
+    import ndoracle as O
+    qh = q.to_array(np.float32, (nseq, H * D))
+    oh = out.to_array(np.float32, (nseq, H * D))
+    worst = 0.0
+    for b in (0, nseq - 1):
+        L = int(lens[b])
+        kk, vv, _, _ = ctx.kv_read(0, b, 0, L + 1)
+        kv = O.kv_view(kk, vv, None, None, H, L + 1, 0, L, O.KV_F16)
+        worst = max(worst, float(np.abs(O.attend_view(kv, qh[b], None) - oh[b]).max()))
+    return {"workload": "long-context decode: %d sequences, 1 token each over L ~ U[%d,%d] + 1 "
+                        "positions, 8 heads x 64, fp16 K/V, 1 layer (append + split-KV attention + merge)"
+                        % (nseq, int(lens.min()), int(lens.max())),
+            "attend_ms": round(att_ms, 4), "combine_ms": round(comb_ms, 4), "append_ms": round(app_ms, 4),
+            "call_ms": round(el * 1e3 / reps, 4),
+            "attend_GBps": round((kv_bytes + io_bytes) / (att_ms * 1e-3) / 1e9, 1),
+            "step_GBps": round((kv_bytes + io_bytes + app_bytes) / ((att_ms + comb_ms + app_ms) * 1e-3) / 1e9, 1),
+            "frac_attend": round((kv_bytes + io_bytes) / (att_ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+            "bytes_per_launch": kv_bytes + io_bytes,
+            "max_abs_delta_sampled": worst}
 
 
 def shared_prefix_leg(N, stream, nseq=1024, npre=213, nmin=32, nmax=64, dsteps=64, layers=LAYERS):
@@ -467,6 +533,7 @@ def main():
         "shared_prefix": shared,
         "max_abs_delta_sampled": worst,
         "device": name,
+        "host": host_info(),
     }
     print(json.dumps(res), flush=True)
 

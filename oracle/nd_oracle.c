@@ -452,7 +452,35 @@ int ndo_session_init(ndo_session *s, uint32_t n_layers, uint32_t nh, uint32_t nk
 void ndo_session_free(ndo_session *s)
 {
     free(s->k_cache); free(s->v_cache); free(s->k_scale); free(s->v_scale);
+    free(s->q_hist); free(s->k_hist); free(s->v_hist);
+    free(s->snap_q_hist); free(s->snap_k_hist); free(s->snap_v_hist);
+    free(s->rope_inv);
     memset(s, 0, sizeof *s);
+}
+
+/* Floats in one of the three history arrays over all layers. */
+static size_t hist_len(const ndo_session *s, int which)
+{
+    size_t dim = which == 0 ? (size_t)s->nh * s->qk_hd
+               : which == 1 ? (size_t)s->nkv * s->qk_hd : (size_t)s->nkv * s->v_hd;
+    return (size_t)s->n_layers * s->taps * dim;
+}
+
+/* The histories take part in reset / snapshot / rewind as in
+ * nd_model.c:1423-1425, :1451-1453, :1575-1580. */
+static void hist_move(ndo_session *s, int to_snap)
+{
+    float *live[3] = { s->q_hist, s->k_hist, s->v_hist };
+    float *snap[3] = { s->snap_q_hist, s->snap_k_hist, s->snap_v_hist };
+    int a;
+    if (!s->taps)
+        return;
+    for (a = 0; a < 3; a++) {
+        if (to_snap)
+            memcpy(snap[a], live[a], sizeof(float) * hist_len(s, a));
+        else
+            memcpy(live[a], snap[a], sizeof(float) * hist_len(s, a));
+    }
 }
 
 void ndo_reset(ndo_session *s)
@@ -460,6 +488,11 @@ void ndo_reset(ndo_session *s)
     s->pos = 0;
     s->n_sink = 0;
     s->has_snap = 0;
+    if (s->taps) {
+        memset(s->q_hist, 0, sizeof(float) * hist_len(s, 0));
+        memset(s->k_hist, 0, sizeof(float) * hist_len(s, 1));
+        memset(s->v_hist, 0, sizeof(float) * hist_len(s, 2));
+    }
 }
 
 void ndo_set_sink(ndo_session *s, uint32_t n)
@@ -471,6 +504,7 @@ int ndo_snapshot(ndo_session *s)
 {
     ndo_set_sink(s, s->pos);
     s->snap_pos = s->pos;
+    hist_move(s, 1);
     s->has_snap = 1;
     return 0;
 }
@@ -482,6 +516,7 @@ void ndo_rewind(ndo_session *s)
         return;
     }
     s->pos = s->snap_pos;
+    hist_move(s, 0);
 }
 
 struct ndo_prefix {
@@ -496,7 +531,7 @@ static size_t prefix_bytes(const ndo_session *s, uint32_t live)
 {
     size_t es = elem_size(s->kv_dtype), per_layer;
     per_layer = (size_t)live * s->nkv * ((s->qk_hd + s->v_hd) * es + 2u * sizeof(float));
-    return per_layer * s->n_layers;
+    return per_layer * s->n_layers + sizeof(float) * (hist_len(s, 0) + hist_len(s, 1) + hist_len(s, 2));
 }
 
 static void prefix_move(ndo_session *s, unsigned char *data, uint32_t live, int restore)
@@ -520,6 +555,18 @@ static void prefix_move(ndo_session *s, unsigned char *data, uint32_t live, int 
                 memcpy(r, data + off, n);
             else
                 memcpy(data + off, r, n);
+            off += n;
+        }
+    }
+    /* then the snapshot histories (prefix_copy, nd_model.c:1519-1521) */
+    {
+        float *snap[3] = { s->snap_q_hist, s->snap_k_hist, s->snap_v_hist };
+        for (a = 0; a < 3 && s->taps; a++) {
+            size_t n = sizeof(float) * hist_len(s, (int)a);
+            if (restore)
+                memcpy(snap[a], data + off, n);
+            else
+                memcpy(data + off, snap[a], n);
             off += n;
         }
     }
@@ -621,6 +668,92 @@ void ndo_prefill_tokens(ndo_session *s, uint32_t li, uint32_t n, const float *q,
                       out + (size_t)t * s->nh * s->v_hd);
     }
     s->pos = p0;
+}
+
+/* --------------------------------------------------------- attention front */
+
+void ndo_rope_inv(float theta, uint32_t qk_hd, float *inv)
+{
+    uint32_t i;
+    for (i = 0; i < qk_hd / 2; i++)
+        inv[i] = 1.0f / powf(theta, (float)(2 * i) / (float)qk_hd);
+}
+
+void ndo_rope_row(const float *inv, uint32_t qk_hd, uint32_t pos, float *cs, float *sn)
+{
+    uint32_t i;
+    for (i = 0; i < qk_hd / 2; i++) {
+        float angle = (float)pos * inv[i];
+        cs[i] = cosf(angle);
+        sn[i] = sinf(angle);
+    }
+}
+
+void ndo_tap_conv(float *proj, float *hist, const float *w, uint32_t taps, uint32_t pos,
+                  uint32_t dim)
+{
+    uint32_t nt = taps <= pos + 1u ? taps : pos + 1u, i, j;
+    memcpy(hist + (size_t)(pos % taps) * dim, proj, sizeof(float) * dim);
+    for (i = 0; i < dim; i++) {
+        float acc = 0.0f;
+        for (j = 0; j < nt; j++)
+            acc += w[(size_t)j * dim + i] * hist[(size_t)((pos - j) % taps) * dim + i];
+        proj[i] = acc;
+    }
+}
+
+void ndo_zcrms_heads(float *x, uint32_t nheads, uint32_t dim, const float *s, const float *cs,
+                     const float *sn)
+{
+    uint32_t h, i, half = dim / 2;
+    for (h = 0; h < nheads; h++) {
+        float *r = x + (size_t)h * dim;
+        float ss = 0.0f, inv;
+        for (i = 0; i < dim; i++)
+            ss += r[i] * r[i];
+        inv = 1.0f / sqrtf(ss / (float)dim + 1e-6f);      /* ND_EPS, nd_model.c:31 */
+        for (i = 0; i < half; i++) {
+            float a = (1.0f + s[i]) * r[i] * inv;
+            float b = (1.0f + s[i + half]) * r[i + half] * inv;
+            r[i] = a * cs[i] - b * sn[i];
+            r[i + half] = b * cs[i] + a * sn[i];
+        }
+        if (2u * half < dim)
+            r[dim - 1] = (1.0f + s[dim - 1]) * r[dim - 1] * inv;
+    }
+}
+
+int ndo_session_front(ndo_session *s, uint32_t taps, float rope_theta)
+{
+    int a;
+    float **live[3] = { &s->q_hist, &s->k_hist, &s->v_hist };
+    float **snap[3] = { &s->snap_q_hist, &s->snap_k_hist, &s->snap_v_hist };
+    if (!taps || s->taps)
+        return -1;
+    s->taps = taps;
+    for (a = 0; a < 3; a++) {
+        *live[a] = (float *)calloc(hist_len(s, a), sizeof(float));
+        *snap[a] = (float *)calloc(hist_len(s, a), sizeof(float));
+        if (!*live[a] || !*snap[a])
+            return -2;
+    }
+    s->rope_inv = (float *)malloc(sizeof(float) * (s->qk_hd / 2 + 1));
+    if (!s->rope_inv)
+        return -2;
+    ndo_rope_inv(rope_theta, s->qk_hd, s->rope_inv);
+    return 0;
+}
+
+void ndo_front(ndo_session *s, uint32_t li, const ndo_front_w *w, float *q, float *k, float *v)
+{
+    uint32_t dq = s->nh * s->qk_hd, dk = s->nkv * s->qk_hd, dv = s->nkv * s->v_hd;
+    float cs[NDO_HD_MAX / 2], sn[NDO_HD_MAX / 2];
+    ndo_rope_row(s->rope_inv, s->qk_hd, s->pos, cs, sn);
+    ndo_tap_conv(q, s->q_hist + (size_t)li * s->taps * dq, w->tap_q, s->taps, s->pos, dq);
+    ndo_tap_conv(k, s->k_hist + (size_t)li * s->taps * dk, w->tap_k, s->taps, s->pos, dk);
+    ndo_tap_conv(v, s->v_hist + (size_t)li * s->taps * dv, w->tap_v, s->taps, s->pos, dv);
+    ndo_zcrms_heads(q, s->nh, s->qk_hd, w->norm_q, cs, sn);
+    ndo_zcrms_heads(k, s->nkv, s->qk_hd, w->norm_k, cs, sn);
 }
 
 /* ------------------------------------------------------ threaded baseline */

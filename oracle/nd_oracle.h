@@ -20,6 +20,13 @@
  *   ndo_attend (fp16)                     - pinned: float64 textbook + special cases (the reference
  *                                           has no fp16 KV path)
  *   session/prefix functions              - pinned: reference harness session replay
+ *   ndo_tap_conv, ndo_zcrms_heads,
+ *   ndo_front (+ its session state)       - pinned: reference harness (bit-exact tap_projection,
+ *                                           zcrms_heads, snapshot/rewind/prefix of the histories)
+ *   ndo_rope_inv, ndo_rope_row            - pinned: float64 bound (<= 1 ulp of the exact value
+ *                                           of the rounded argument); the reference computes
+ *                                           them inline in nd_model_open / step_hidden, so no
+ *                                           harness can call them
  */
 #ifndef ND_ORACLE_H
 #define ND_ORACLE_H
@@ -88,6 +95,13 @@ typedef struct {
     uint32_t snap_pos;
     void    *k_cache, *v_cache;       /* [layer][window][nkv*hd] int8 or fp16 */
     float   *k_scale, *v_scale;       /* [layer][window][nkv] (int8 only)   */
+    /* attention front state (ndo_session_front): tap histories of the raw
+     * projections [layer][tap][dim] (nd_model.h:147,167) and the rotary
+     * inverse frequencies [qk_hd/2] (nd_model.h:170). taps = 0: no front. */
+    uint32_t taps;
+    float   *q_hist, *k_hist, *v_hist;
+    float   *snap_q_hist, *snap_k_hist, *snap_v_hist;
+    float   *rope_inv;
 } ndo_session;
 
 int  ndo_session_init(ndo_session *s, uint32_t n_layers, uint32_t nh, uint32_t nkv,
@@ -113,6 +127,45 @@ void ndo_attend_session(const ndo_session *s, uint32_t li, const float *q,
                         const float *gate, float *out);
 void ndo_step_end(ndo_session *s);                   /* pos++ (nd_model.c:3094) */
 void ndo_view(const ndo_session *s, uint32_t li, ndo_kv_view *kv);
+
+/* ---- attention front: qkv tap convolution, per-head ZC-RMSNorm + RoPE ----
+ *
+ * What attention() does to the raw q/k/v projections before the KV store
+ * (nd_model.c:2413-2424): a causal depthwise convolution over the last `taps`
+ * raw projections of each column, then for q and k a per-head RMS norm with a
+ * (1 + s) scale shared by all heads, fused with GPT-NeoX half-split rotary
+ * embedding at the current position. v gets the convolution only. */
+
+/* rope_inv[i] = 1 / theta^(2i/qk_hd), i < qk_hd/2 (nd_model.c:1233-1236). */
+void ndo_rope_inv(float theta, uint32_t qk_hd, float *inv);
+/* cos/sin of pos * rope_inv[i] for one position (nd_model.c:2949-2954). */
+void ndo_rope_row(const float *inv, uint32_t qk_hd, uint32_t pos, float *cs, float *sn);
+/* One projection's tap convolution at position pos (tap_projection + tap_rows,
+ * nd_model.c:2361-2379, :1748-1802): hist [taps][dim] of this layer receives
+ * proj in slot pos % taps, then proj[i] = sum over j < min(taps, pos+1), in
+ * ascending j from +0, of w[j][i] * hist[(pos - j) % taps][i]. */
+void ndo_tap_conv(float *proj, float *hist, const float *w, uint32_t taps, uint32_t pos,
+                  uint32_t dim);
+/* In-place per-head ZC-RMSNorm with the rotary emit folded in
+ * (zcrms_head_rows, nd_model.c:324-360): x [nheads][dim], s [dim],
+ * cs/sn [dim/2]. */
+void ndo_zcrms_heads(float *x, uint32_t nheads, uint32_t dim, const float *s, const float *cs,
+                     const float *sn);
+
+/* One layer's front weights: the staged fp32 tap weights [taps][dim] for q
+ * (dim nh*qk_hd), k (nkv*qk_hd), v (nkv*v_hd) and the q/k norm scales [qk_hd]
+ * (the engine's fp16_slot[li][4..8]). */
+typedef struct {
+    const float *tap_q, *tap_k, *tap_v;
+    const float *norm_q, *norm_k;
+} ndo_front_w;
+
+/* Give a session the front state: taps >= 1 histories (zeroed) and the
+ * rotary table for rope_theta. 0 ok, negative on bad arguments / no memory. */
+int  ndo_session_front(ndo_session *s, uint32_t taps, float rope_theta);
+/* The front for layer li at s->pos, in place on q [nh*qk_hd], k [nkv*qk_hd],
+ * v [nkv*v_hd] (raw projections in, store-ready rows out). */
+void ndo_front(ndo_session *s, uint32_t li, const ndo_front_w *w, float *q, float *k, float *v);
 
 /* ---- CPU baseline: batched fp16 decode, threaded over sequences ----
  *

@@ -35,7 +35,16 @@ class Session(C.Structure):
                 ("kv_dtype", C.c_int), ("pos", C.c_uint32), ("n_sink", C.c_uint32),
                 ("has_snap", C.c_int), ("snap_pos", C.c_uint32),
                 ("k_cache", C.c_void_p), ("v_cache", C.c_void_p),
-                ("k_scale", C.c_void_p), ("v_scale", C.c_void_p)]
+                ("k_scale", C.c_void_p), ("v_scale", C.c_void_p),
+                ("taps", C.c_uint32),
+                ("q_hist", C.c_void_p), ("k_hist", C.c_void_p), ("v_hist", C.c_void_p),
+                ("snap_q_hist", C.c_void_p), ("snap_k_hist", C.c_void_p), ("snap_v_hist", C.c_void_p),
+                ("rope_inv", C.c_void_p)]
+
+
+class FrontW(C.Structure):
+    _fields_ = [("tap_q", C.c_void_p), ("tap_k", C.c_void_p), ("tap_v", C.c_void_p),
+                ("norm_q", C.c_void_p), ("norm_k", C.c_void_p)]
 
 
 class BatchF16(C.Structure):
@@ -101,6 +110,14 @@ def lib():
         L.ndo_prefill_tokens.argtypes = [C.POINTER(Session), C.c_uint32, C.c_uint32] + [C.c_void_p] * 5
         L.ndo_decode_batch_f16.argtypes = [C.POINTER(BatchF16), C.c_int]
         L.ndo_decode_batch_f16.restype = C.c_int
+        L.ndo_rope_inv.argtypes = [C.c_float, C.c_uint32, C.c_void_p]
+        L.ndo_rope_row.argtypes = [C.c_void_p, C.c_uint32, C.c_uint32, C.c_void_p, C.c_void_p]
+        L.ndo_tap_conv.argtypes = [C.c_void_p, C.c_void_p, C.c_void_p, C.c_uint32, C.c_uint32, C.c_uint32]
+        L.ndo_zcrms_heads.argtypes = [C.c_void_p, C.c_uint32, C.c_uint32, C.c_void_p, C.c_void_p,
+                                      C.c_void_p]
+        L.ndo_session_front.argtypes = [C.POINTER(Session), C.c_uint32, C.c_float]
+        L.ndo_session_front.restype = C.c_int
+        L.ndo_front.argtypes = [C.POINTER(Session), C.c_uint32, C.POINTER(FrontW)] + [C.c_void_p] * 3
         _lib = L
     return _lib
 
@@ -147,6 +164,10 @@ def ref():
         R.ref_kv_store.argtypes = [C.c_void_p, C.c_uint32, C.c_void_p, C.c_void_p]
         R.ref_attend.argtypes = [C.c_void_p, C.c_uint32, C.c_void_p, C.c_void_p, C.c_void_p]
         R.ref_attention.argtypes = [C.c_void_p, C.c_uint32] + [C.c_void_p] * 5
+        R.ref_session_front.argtypes = [C.c_void_p, C.c_uint32, C.c_float]
+        R.ref_session_front.restype = C.c_int
+        R.ref_front.argtypes = [C.c_void_p, C.c_uint32] + [C.c_void_p] * 8
+        R.ref_hist.argtypes = [C.c_void_p, C.c_int] + [C.POINTER(C.c_void_p)] * 3
         _ref = R
     return _ref
 
@@ -232,6 +253,32 @@ class OracleSession:
         lib().ndo_attend_session(C.byref(self.s), li, _ptr(q), _ptr(g), _ptr(out))
         return out
 
+    def front_init(self, taps, rope_theta):
+        rc = lib().ndo_session_front(C.byref(self.s), taps, rope_theta)
+        if rc:
+            raise ValueError("ndo_session_front failed: %d" % rc)
+
+    def front(self, li, w, q, k, v):
+        """The attention front at the current position: returns (q, k, v)
+        after tap convolution, head norm and RoPE; w = FrontWeights."""
+        q = np.array(q, np.float32)
+        k = np.array(k, np.float32)
+        v = np.array(v, np.float32)
+        lib().ndo_front(C.byref(self.s), li, C.byref(w.struct(li)), _ptr(q), _ptr(k), _ptr(v))
+        return q, k, v
+
+    def hist(self, snap=False):
+        """(q, k, v) tap histories [layer][tap][dim] (copies)."""
+        L, nh, nkv, qk, vd, W = self.geom
+        T = self.s.taps
+        out = []
+        for ptr, dim in ((self.s.snap_q_hist if snap else self.s.q_hist, nh * qk),
+                         (self.s.snap_k_hist if snap else self.s.k_hist, nkv * qk),
+                         (self.s.snap_v_hist if snap else self.s.v_hist, nkv * vd)):
+            a = np.ctypeslib.as_array((C.c_float * (L * T * dim)).from_address(ptr))
+            out.append(a.reshape(L, T, dim).copy())
+        return tuple(out)
+
     def cache(self):
         """(k, v, k_scale, v_scale) numpy views [layer][window][nkv][hd]."""
         L, nh, nkv, qk, vd, W = self.geom
@@ -301,6 +348,33 @@ class RefSession:
         g = None if gate is None else np.ascontiguousarray(gate, np.float32)
         ref().ref_attention(self.m, li, _ptr(q), _ptr(k), _ptr(v), _ptr(g), _ptr(out))
         return out
+
+    def front_init(self, taps, rope_theta):
+        if ref().ref_session_front(self.m, taps, rope_theta):
+            raise ValueError("ref_session_front failed")
+        self.taps = taps
+
+    def front(self, li, w, q, k, v):
+        q = np.array(q, np.float32)
+        k = np.array(k, np.float32)
+        v = np.array(v, np.float32)
+        a = w.arrays(li)
+        ref().ref_front(self.m, li, *(_ptr(x) for x in a), _ptr(q), _ptr(k), _ptr(v))
+        return q, k, v
+
+    def hist(self, snap=False):
+        L, nh, nkv, qk, vd, W = self.geom
+        T = self.taps
+        ptrs = [C.c_void_p() for _ in range(3)]
+        ref().ref_hist(self.m, 1 if snap else 0, *(C.byref(p) for p in ptrs))
+        out = []
+        for p, dim in zip(ptrs, (nh * qk, nkv * qk, nkv * vd)):
+            if not p.value:     # no snapshot taken yet: the engine has not allocated it
+                out.append(np.zeros((L, T, dim), np.float32))
+                continue
+            a = np.ctypeslib.as_array((C.c_float * (L * T * dim)).from_address(p.value))
+            out.append(a.reshape(L, T, dim).copy())
+        return tuple(out)
 
     def cache(self):
         L, nh, nkv, qk, vd, W = self.geom
@@ -374,3 +448,55 @@ def decode_batch_f16(nh, nkv, qk_hd, v_hd, lens, kbase, vbase, koff, voff, q, k_
     rc = lib().ndo_decode_batch_f16(C.byref(b), nthreads)
     del keep
     return rc
+
+
+# ------------------------------------------------------------ attention front
+
+class FrontWeights:
+    """Per-layer front weights: tap_q/tap_k/tap_v [L][taps][dim] and
+    norm_q/norm_k [L][qk_hd] (float32, kept alive here)."""
+
+    def __init__(self, tap_q, tap_k, tap_v, norm_q, norm_k):
+        self.tap_q, self.tap_k, self.tap_v, self.norm_q, self.norm_k = (
+            np.ascontiguousarray(a, np.float32) for a in (tap_q, tap_k, tap_v, norm_q, norm_k))
+        self.taps = self.tap_q.shape[1]
+
+    def arrays(self, li):
+        return (self.tap_q[li], self.tap_k[li], self.tap_v[li], self.norm_q[li], self.norm_k[li])
+
+    def struct(self, li):
+        w = FrontW()
+        w.tap_q, w.tap_k, w.tap_v, w.norm_q, w.norm_k = (a.ctypes.data for a in self.arrays(li))
+        return w
+
+
+def rope_inv(theta, qk_hd):
+    inv = np.zeros(qk_hd // 2 + 1, np.float32)
+    lib().ndo_rope_inv(theta, qk_hd, _ptr(inv))
+    return inv[:qk_hd // 2]
+
+
+def rope_row(inv, qk_hd, pos):
+    inv = np.ascontiguousarray(inv, np.float32)
+    cs = np.zeros(qk_hd // 2 + 1, np.float32)
+    sn = np.zeros(qk_hd // 2 + 1, np.float32)
+    lib().ndo_rope_row(_ptr(inv), qk_hd, pos, _ptr(cs), _ptr(sn))
+    return cs[:qk_hd // 2], sn[:qk_hd // 2]
+
+
+def tap_conv(proj, hist, w, pos):
+    """One projection's tap convolution; returns (out, new_hist)."""
+    proj = np.array(proj, np.float32)
+    hist = np.array(hist, np.float32)
+    w = np.ascontiguousarray(w, np.float32)
+    taps, dim = hist.shape
+    lib().ndo_tap_conv(_ptr(proj), _ptr(hist), _ptr(w), taps, pos, dim)
+    return proj, hist
+
+
+def zcrms_heads(x, s, cs, sn):
+    """x [nheads][dim] -> normed + rotated copy."""
+    x = np.array(x, np.float32)
+    s, cs, sn = (np.ascontiguousarray(a, np.float32) for a in (s, cs, sn))
+    lib().ndo_zcrms_heads(_ptr(x), x.shape[0], x.shape[1], _ptr(s), _ptr(cs), _ptr(sn))
+    return x

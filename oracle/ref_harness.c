@@ -10,6 +10,7 @@
  *   nd_model_set_sink / snapshot / rewind / prefix_*   :1314-1555
  *   kv_store_int8    :1822-1866
  *   attn_heads       :2105-2359
+ *   tap_projection / tap_rows, zcrms_heads   :2361-2379, :1748-1802, :324-360
  * An nd_model is assembled by hand with only the KV geometry and buffers set
  * (no archive), and the store + dispatch steps of attention() (:2426-2483) are
  * replayed around those calls.
@@ -87,7 +88,76 @@ void ref_session_free(void *vm)
     free(m->k_cache); free(m->v_cache); free(m->k_scale); free(m->v_scale);
     free(m->q); free(m->gate); free(m->attn); free(m->kbuf); free(m->vbuf);
     free(m->snap_eg_hist); free(m->snap_q_hist); free(m->snap_k_hist); free(m->snap_v_hist);
+    free(m->q_hist); free(m->k_hist); free(m->v_hist);
+    free(m->rope_inv); free(m->rope_cos); free(m->rope_sin);
     free(m);
+}
+
+/* ------------------------------------------------------ attention front */
+
+/* Give the hand-built model the attention-front state nd_model_open sets up:
+ * qkv_conv_taps, the tap histories [layer][tap][dim] (nd_model.c:1178-1180)
+ * and the rotary inverse frequencies (:1233-1236, restated here because
+ * nd_model_open needs an archive). */
+int ref_session_front(void *vm, uint32_t taps, float theta)
+{
+    nd_model *m = (nd_model *)vm;
+    uint32_t i, half = m->qk_head_dim / 2;
+    m->c.h.qkv_conv_taps = taps;
+    m->c.h.rope_theta = theta;
+    m->q_hist = (float *)calloc((size_t)m->n_layers * taps * m->n_heads * m->qk_head_dim, sizeof(float));
+    m->k_hist = (float *)calloc((size_t)m->n_layers * taps * m->k_dim, sizeof(float));
+    m->v_hist = (float *)calloc((size_t)m->n_layers * taps * m->v_dim, sizeof(float));
+    m->rope_inv = (float *)calloc(half + 1, sizeof(float));
+    m->rope_cos = (float *)calloc(half + 1, sizeof(float));
+    m->rope_sin = (float *)calloc(half + 1, sizeof(float));
+    if (!m->q_hist || !m->k_hist || !m->v_hist || !m->rope_inv || !m->rope_cos || !m->rope_sin)
+        return -1;
+    for (i = 0; i < half; i++)
+        m->rope_inv[i] = 1.0f / powf(theta, (float)(2 * i) / (float)m->qk_head_dim);
+    return 0;
+}
+
+/* The front of attention() for layer li at the model's pos (nd_model.c:
+ * 2413-2424) on raw q/k/v, in place: the per-position rotary table of
+ * nd_model_step_hidden (:2949-2954, restated), then the reference's own
+ * tap_projection x3 and zcrms_heads x2 with the given per-layer weights in
+ * the engine's fp16_slot[li][4..8]. */
+void ref_front(void *vm, uint32_t li, const float *tap_q, const float *tap_k, const float *tap_v,
+               const float *norm_q, const float *norm_k, float *q, float *k, float *v)
+{
+    nd_model *m = (nd_model *)vm;
+    uint32_t i, nh = m->n_heads, qk = m->qk_head_dim;
+    for (i = 0; i < qk / 2; i++) {
+        float angle = (float)m->pos * m->rope_inv[i];
+        m->rope_cos[i] = cosf(angle);
+        m->rope_sin[i] = sinf(angle);
+    }
+    m->fp16_slot[li][4] = (float *)tap_q;
+    m->fp16_slot[li][5] = (float *)tap_k;
+    m->fp16_slot[li][6] = (float *)tap_v;
+    m->fp16_slot[li][7] = (float *)norm_q;
+    m->fp16_slot[li][8] = (float *)norm_k;
+    memcpy(m->q, q, sizeof(float) * nh * qk);
+    memcpy(m->kbuf, k, sizeof(float) * m->k_dim);
+    memcpy(m->vbuf, v, sizeof(float) * m->v_dim);
+    tap_projection(m, 4, m->q, m->q_hist, li, nh * qk);
+    tap_projection(m, 5, m->kbuf, m->k_hist, li, m->k_dim);
+    tap_projection(m, 6, m->vbuf, m->v_hist, li, m->v_dim);
+    zcrms_heads(m, m->fp16_slot[li][7], m->rope_cos, m->rope_sin, m->q, nh, qk);
+    zcrms_heads(m, m->fp16_slot[li][8], m->rope_cos, m->rope_sin, m->kbuf, m->n_kv_heads, qk);
+    memcpy(q, m->q, sizeof(float) * nh * qk);
+    memcpy(k, m->kbuf, sizeof(float) * m->k_dim);
+    memcpy(v, m->vbuf, sizeof(float) * m->v_dim);
+}
+
+/* The reference's own tap histories (live, or the snapshot's). */
+void ref_hist(void *vm, int snap, float **q, float **k, float **v)
+{
+    nd_model *m = (nd_model *)vm;
+    *q = snap ? m->snap_q_hist : m->q_hist;
+    *k = snap ? m->snap_k_hist : m->k_hist;
+    *v = snap ? m->snap_v_hist : m->v_hist;
 }
 
 void ref_reset(void *vm) { nd_model_reset((nd_model *)vm); }

@@ -6,7 +6,8 @@ import numpy as np
 import pytest
 
 REPO = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
-for p in (os.path.join(REPO, "oracle"), os.path.join(REPO, "esp32-needle-3_amd")):
+for p in (os.path.join(REPO, "oracle"), os.path.join(REPO, "esp32-needle-3_amd"),
+          os.path.join(REPO, "tests", "golden")):
     if p not in sys.path:
         sys.path.insert(0, p)
 

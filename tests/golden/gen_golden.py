@@ -28,7 +28,7 @@ REF = os.environ.get("REF", "/root/reference")
 
 # Session scripts. Each event: ("tok", gated) store+attend one token on every
 # layer then pos++, ("snap",), ("sink", n), ("save", slot), ("restore", slot),
-# ("reset",). Outputs are recorded for the token steps listed in `record`.
+# ("reset",), ("rewind",). Outputs are recorded for the token steps listed in `record`.
 SESSIONS = {
     # one layer, MHA 8x64, 213-token pinned prefix + 16 prompt tokens
     "cfg1": dict(geom=(1, 8, 8, 64, 64, 256), seed=101,
@@ -57,15 +57,46 @@ SESSIONS = {
     # config 2's shape on 2 layers: causal prefill of 256 tokens, window 256
     "prefill": dict(geom=(2, 8, 8, 64, 64, 256), seed=606,
                     script=[("tok", True)] * 256, record=list(range(0, 256, 17)) + [255]),
+    # with the attention front (tap convolution + head norm + RoPE on raw
+    # projections): the archive's shapes, 3 taps, snapshot / rewind / prefix
+    # switching, which must carry the tap histories along
+    "front_engine": dict(geom=(2, 12, 2, 48, 64, 384), seed=707, front=(3, 10000.0),
+                         script=[("tok", True)] * 30 + [("snap",), ("save", 0)] + [("tok", True)] * 5 +
+                                [("rewind",)] + [("tok", True)] * 3 +
+                                [("reset",)] + [("tok", True)] * 7 + [("snap",), ("save", 1)] +
+                                [("tok", True)] * 2 + [("restore", 0)] + [("tok", True)] * 2 +
+                                [("restore", 1)] + [("tok", True)] * 2,
+                         record="all"),
+    # MHA 8x64 with 4 taps and theta 1e6 past a ring wrap, at large positions
+    "front_cfg": dict(geom=(1, 8, 8, 64, 64, 128), seed=808, front=(4, 1000000.0),
+                      script=[("tok", True)] * 20 + [("sink", 20)] + [("tok", i % 4 != 0) for i in range(200)],
+                      record=list(range(0, 220, 7)) + [219]),
 }
 
 
+def front_weights(spec):
+    """Per-layer tap weights [L][taps][dim] and norm scales [L][qk_hd]."""
+    L, nh, nkv, qk, vd, W = spec["geom"]
+    taps = spec["front"][0]
+    st = Stream(spec["seed"] + 1)
+    shape = lambda dim: st.take(L * taps * dim).reshape(L, taps, dim) * np.float32(0.5)
+    return O.FrontWeights(shape(nh * qk), shape(nkv * qk), shape(nkv * vd),
+                          st.take(L * qk).reshape(L, qk) * np.float32(0.25),
+                          st.take(L * qk).reshape(L, qk) * np.float32(0.25))
+
+
 def run_session(S, spec):
+    """Replays a script on an OracleSession or a RefSession; with a `front`
+    entry the raw q/k/v go through the attention front first."""
     L, nh, nkv, qk, vd, W = spec["geom"]
     st = Stream(spec["seed"])
     outs, saved = [], {}
     ntok = 0
     rec = spec["record"]
+    fw = None
+    if "front" in spec:
+        S.front_init(*spec["front"])
+        fw = front_weights(spec)
     for ev in spec["script"]:
         if ev[0] == "tok":
             for li in range(L):
@@ -73,6 +104,8 @@ def run_session(S, spec):
                 k = st.take(nkv * qk)
                 v = st.take(nkv * vd)
                 g = st.take(nh * vd) if ev[1] else None
+                if fw is not None:
+                    q, k, v = S.front(li, fw, q, k, v)
                 o = S.attention(li, q, k, v, g)
                 if rec == "all" or ntok in rec:
                     outs.append(o.copy())
@@ -89,7 +122,14 @@ def run_session(S, spec):
             assert S.prefix_restore(saved[ev[1]]) == 0
         elif ev[0] == "reset":
             S.reset()
+        elif ev[0] == "rewind":
+            S.rewind()
     return np.stack(outs), saved
+
+
+def hist_blob(S):
+    """Live and snapshot tap histories, flattened (float32)."""
+    return np.concatenate([h.ravel() for h in S.hist(False) + S.hist(True)]).astype(np.float32)
 
 
 def exp_pairs_inputs():
@@ -147,6 +187,8 @@ def main():
         out["sess_" + name + "_kvsum"] = np.array(
             [int(k.astype(np.int64).sum()), int(v.astype(np.int64).sum()),
              int(np.abs(k.astype(np.int64)).sum()), int(np.abs(v.astype(np.int64)).sum())], np.int64)
+        if "front" in spec:
+            out["sess_" + name + "_hist"] = hist_blob(S)
         for p in saved.values():
             O.ref().ref_prefix_free(p)
         S.close()

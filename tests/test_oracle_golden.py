@@ -56,3 +56,6 @@ def test_session_bit_exact(name):
     kvsum = [int(k.astype(np.int64).sum()), int(v.astype(np.int64).sum()),
              int(np.abs(k.astype(np.int64)).sum()), int(np.abs(v.astype(np.int64)).sum())]
     assert kvsum == list(G["sess_" + name + "_kvsum"])
+    if "front" in spec:
+        from gen_golden import hist_blob
+        assert np.array_equal(bits(hist_blob(S)), bits(G["sess_" + name + "_hist"]))
