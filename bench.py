@@ -377,7 +377,7 @@ def main():
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py measures one GPU: this build has no multi-GPU path "
-              "(decode shards by sequence with no exchange; see DESIGN.md)", file=sys.stderr)
+              "(decode would shard by sequence with no exchange between GPUs)", file=sys.stderr)
         sys.exit(2)
 
     import ndattn as N

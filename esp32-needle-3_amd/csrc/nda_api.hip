@@ -15,6 +15,7 @@
 #include <cstring>
 #include <new>
 #include <string>
+#include <unordered_set>
 #include <vector>
 
 using namespace nda;
@@ -36,6 +37,7 @@ struct SeqHost {
     bool has_snap = false;
     uint32_t snap_pos = 0;
     uint32_t stored_end = 0;   // one past the highest position stored
+    uint32_t ring_lo = 0;      // ring positions in [n_sink, ring_lo) were overwritten before a rewind
 };
 
 struct ProfRec {
@@ -74,6 +76,25 @@ struct nda_ctx {
     bool seqs_dirty = true;
     uint32_t dirty_lo = UINT32_MAX, dirty_hi = 0;   // page-table rows to upload
     bool prefix_dirty = true;
+
+    // attention front (nda_front_init): tap histories, weights, rotary table
+    uint32_t taps = 0, max_pos = 0, dcol = 0;
+    uint64_t hist_block = 0;            // floats per sequence: n_layers * taps * dcol
+    float *d_hist = nullptr;            // [max_seqs] blocks, live
+    float *d_snap_hist = nullptr;       // [max_seqs] blocks, restored by rewind
+    float *d_prefix_hist = nullptr;     // [max_prefixes] blocks
+    float *d_front_w = nullptr;         // [n_layers][taps][dcol]
+    float *d_front_norm = nullptr;      // [n_layers][2][qk]
+    float2 *d_rope = nullptr;           // [max_pos][qk/2]
+    std::vector<uint8_t> front_w_set;   // per layer
+    float *d_qfront = nullptr;          // nda_attention's normalised q
+    size_t qfront_cap = 0;              // floats
+    uint32_t *d_front_rows = nullptr;   // row_seq | row_t | row_n
+    size_t front_rows_cap = 0;          // uint32 entries
+    HistOp *d_hist_ops = nullptr;
+    size_t hist_ops_cap = 0;
+    std::vector<HistOp> hist_pending;   // applied in order before the next front launch
+    std::vector<uint8_t> seen;          // duplicate-id scratch
 
     bool prof = false;
     std::vector<ProfRec> prof_pending;
@@ -242,8 +263,8 @@ int ensure_rows(nda_ctx *c, size_t rows)
     if (rows * 2 <= c->rows_cap)
         return NDA_OK;
     if (c->d_rows) {
-        hipDeviceSynchronize();   // launches still reading the old staging
-        hipFree(c->d_rows);
+        (void)hipDeviceSynchronize();   // launches still reading the old staging
+        (void)hipFree(c->d_rows);
         c->dev_bytes -= c->rows_cap * sizeof(uint32_t);
         c->d_rows = nullptr;
     }
@@ -259,8 +280,8 @@ int ensure_part(nda_ctx *c, size_t floats)
     if (floats <= c->part_cap)
         return NDA_OK;
     if (c->d_part) {
-        hipDeviceSynchronize();
-        hipFree(c->d_part);
+        (void)hipDeviceSynchronize();
+        (void)hipFree(c->d_part);
         c->dev_bytes -= c->part_cap * sizeof(float);
         c->d_part = nullptr;
     }
@@ -275,8 +296,8 @@ int ensure_pf(nda_ctx *c, size_t n)
     if (n <= c->pf_cap)
         return NDA_OK;
     if (c->d_pf) {
-        hipDeviceSynchronize();
-        hipFree(c->d_pf);
+        (void)hipDeviceSynchronize();
+        (void)hipFree(c->d_pf);
         c->dev_bytes -= c->pf_cap * sizeof(uint32_t);
         c->d_pf = nullptr;
     }
@@ -292,14 +313,35 @@ int ensure_stage(nda_ctx *c, size_t bytes)
     if (bytes <= c->stage_cap)
         return NDA_OK;
     if (c->d_stage) {
-        hipDeviceSynchronize();
-        hipFree(c->d_stage);
+        (void)hipDeviceSynchronize();
+        (void)hipFree(c->d_stage);
         c->dev_bytes -= c->stage_cap;
         c->d_stage = nullptr;
     }
     HIPC(c, hipMalloc(&c->d_stage, bytes));
     c->stage_cap = bytes;
     c->dev_bytes += bytes;
+    return NDA_OK;
+}
+
+// Grows a device staging buffer (elements of T); the old one may still be
+// read by queued launches, so the device is drained before it is freed.
+template <typename T>
+int ensure_buf(nda_ctx *c, T *&buf, size_t &cap, size_t need)
+{
+    if (need <= cap)
+        return NDA_OK;
+    if (buf) {
+        (void)hipDeviceSynchronize();
+        (void)hipFree(buf);
+        c->dev_bytes -= cap * sizeof(T);
+        buf = nullptr;
+        cap = 0;
+    }
+    const size_t n = std::max<size_t>(need, 4096);
+    HIPC(c, hipMalloc((void **)&buf, n * sizeof(T)));
+    cap = n;
+    c->dev_bytes += n * sizeof(T);
     return NDA_OK;
 }
 
@@ -327,13 +369,13 @@ struct ProfScope {
             a = take_event(c);
             b = take_event(c);
             if (a && b)
-                hipEventRecord(a, st);
+                (void)hipEventRecord(a, st);
         }
     }
     ~ProfScope()
     {
         if (a && b) {
-            hipEventRecord(b, st);
+            (void)hipEventRecord(b, st);
             c->prof_pending.push_back({kind, a, b});
         } else {
             if (a)
@@ -363,6 +405,71 @@ int check_ids(nda_ctx *c, uint32_t nseq, const uint32_t *ids)
 }
 
 inline uint32_t sid(const uint32_t *ids, uint32_t b) { return ids ? ids[b] : b; }
+
+// ---- tap histories of the attention front ----
+
+float *hist_live(nda_ctx *c, uint32_t seq) { return c->d_hist + (uint64_t)seq * c->hist_block; }
+float *hist_snap(nda_ctx *c, uint32_t seq) { return c->d_snap_hist + (uint64_t)seq * c->hist_block; }
+float *hist_prefix(nda_ctx *c, int32_t id) { return c->d_prefix_hist + (uint64_t)id * c->hist_block; }
+
+// Queue a whole-block copy (src null: clear). Calls without a stream
+// (reset, rewind) only queue; the queue is applied in order on the caller's
+// stream before the next front launch or history read.
+int hist_flush(nda_ctx *c, hipStream_t st);
+
+void hist_queue(nda_ctx *c, float *dst, const float *src)
+{
+    if (!c->taps)
+        return;
+    c->hist_pending.push_back({dst, src});
+    // A context that never runs the front again would only grow the queue:
+    // past this length it is applied on the null stream, which is ordered
+    // after the work already queued on the context's (blocking) stream.
+    if (c->hist_pending.size() >= (1u << 16))
+        (void)hist_flush(c, nullptr);
+}
+
+int hist_flush(nda_ctx *c, hipStream_t st)
+{
+    if (c->hist_pending.empty())
+        return NDA_OK;
+    const size_t n = c->hist_pending.size();
+    if (int rc = ensure_buf(c, c->d_hist_ops, c->hist_ops_cap, n))
+        return rc;
+    HIPC(c, hipMemcpyAsync(c->d_hist_ops, c->hist_pending.data(), n * sizeof(HistOp), hipMemcpyHostToDevice,
+                           st));
+    // Launch maximal runs of ops that touch disjoint blocks; a run ends where
+    // an op writes a block the run reads or writes, or reads one it writes.
+    std::unordered_set<const float *> dsts, srcs;
+    size_t b0 = 0;
+    auto launch = [&](size_t b1) -> int {
+        for (size_t o = b0; o < b1; o += 65535) {
+            hipError_t e = launch_hist_ops(c->d_hist_ops + o, (uint32_t)std::min<size_t>(65535, b1 - o),
+                                           c->hist_block, st);
+            if (e != hipSuccess)
+                return hip_fail(c, e, "history copy launch");
+        }
+        return NDA_OK;
+    };
+    for (size_t i = 0; i < n; i++) {
+        const HistOp &op = c->hist_pending[i];
+        const bool clash = dsts.count(op.dst) || srcs.count(op.dst) || (op.src && dsts.count(op.src));
+        if (clash) {
+            if (int rc = launch(i))
+                return rc;
+            b0 = i;
+            dsts.clear();
+            srcs.clear();
+        }
+        dsts.insert(op.dst);
+        if (op.src)
+            srcs.insert(op.src);
+    }
+    if (int rc = launch(n))
+        return rc;
+    c->hist_pending.clear();
+    return NDA_OK;
+}
 
 // Upload seq ids (and optional per-row offsets) for a launch; returns device
 // pointers, null when the identity mapping applies.
@@ -565,21 +672,20 @@ void nda_destroy(nda_ctx *c)
 {
     if (!c)
         return;
-    hipDeviceSynchronize();
+    (void)hipDeviceSynchronize();
     for (auto &r : c->prof_pending) {
-        hipEventDestroy(r.a);
-        hipEventDestroy(r.b);
+        (void)hipEventDestroy(r.a);
+        (void)hipEventDestroy(r.b);
     }
     for (auto e : c->ev_free)
-        hipEventDestroy(e);
-    hipFree(c->pool);
-    hipFree(c->d_pages);
-    hipFree(c->d_prefix_pages);
-    hipFree(c->d_seqs);
-    hipFree(c->d_rows);
-    hipFree(c->d_part);
-    hipFree(c->d_stage);
-    hipFree(c->d_pf);
+        (void)hipEventDestroy(e);
+    void *bufs[] = {c->pool, c->d_pages, c->d_prefix_pages, c->d_seqs, c->d_rows, c->d_part,
+                    c->d_stage, c->d_pf, c->d_hist, c->d_snap_hist, c->d_prefix_hist,
+                    c->d_front_w, c->d_front_norm, c->d_rope, c->d_qfront, c->d_front_rows,
+                    c->d_hist_ops};
+    for (void *b : bufs)
+        if (b)
+            (void)hipFree(b);
     delete c;
 }
 
@@ -599,6 +705,8 @@ int nda_seq_reset(nda_ctx *c, uint32_t seq)
     release_pages(c, seq);
     s = SeqHost();
     c->seqs_dirty = true;
+    if (c->taps)
+        hist_queue(c, hist_live(c, seq), nullptr);    // nd_model_reset, nd_model.c:1575-1580
     return NDA_OK;
 }
 
@@ -753,6 +861,14 @@ int nda_prefix_build(nda_ctx *c, uint32_t seq, int32_t *prefix_id, void *stream)
     s.snap_pos = len;
     c->seqs_dirty = true;
     *prefix_id = id;
+    // The tap histories go with the snapshot and the prefix
+    // (nd_model.c:1423-1425, :1519-1521).
+    if (c->taps) {
+        hist_queue(c, hist_prefix(c, id), hist_live(c, seq));
+        hist_queue(c, hist_snap(c, seq), hist_live(c, seq));
+        if (int rc = hist_flush(c, st))
+            return rc;
+    }
     return NDA_OK;
 }
 
@@ -779,6 +895,12 @@ int nda_seq_attach(nda_ctx *c, uint32_t seq, int32_t id, void *stream)
     s.stored_end = pf.len;
     c->prefixes[id].refs++;
     c->seqs_dirty = true;
+    if (c->taps) {   // nd_model_prefix_restore + rewind (nd_model.c:1543-1553, :1451-1453)
+        hist_queue(c, hist_live(c, seq), hist_prefix(c, id));
+        hist_queue(c, hist_snap(c, seq), hist_prefix(c, id));
+        if (int rc = hist_flush(c, st))
+            return rc;
+    }
     // Positions past the sink clamp live in the ring: copy them in, as the
     // engine's restore copies every live slot.
     if (pf.len > pf.n_sink) {
@@ -812,8 +934,17 @@ int nda_seq_rewind(nda_ctx *c, uint32_t seq)
     SeqHost &s = c->seqs[seq];
     if (!s.has_snap)
         return nda_seq_reset(c, seq);
+    // Positions from snap_pos on are stored again from here; ring slots the
+    // ring already overwrote stay lost (the inspection calls check both).
+    const uint32_t rcap = c->cfg.window - s.n_sink;
+    if (s.stored_end > rcap)
+        s.ring_lo = std::max(s.ring_lo, s.stored_end - rcap);
+    s.ring_lo = std::min(s.ring_lo, s.snap_pos);
+    s.stored_end = std::min(s.stored_end, s.snap_pos);
     s.pos = s.snap_pos;
     c->seqs_dirty = true;
+    if (c->taps)
+        hist_queue(c, hist_live(c, seq), hist_snap(c, seq));   // nd_model.c:1451-1453
     return NDA_OK;
 }
 
@@ -1089,6 +1220,298 @@ int nda_prefill(nda_ctx *c, uint32_t layer, uint32_t nseq, const uint32_t *ids, 
     return NDA_OK;
 }
 
+// ------------------------------------------------------- attention front
+
+int nda_front_init(nda_ctx *c, const nda_front_config *fc)
+{
+    if (!c || !fc)
+        return NDA_ERR_ARG;
+    if (c->taps)
+        return fail(c, NDA_ERR_STATE, "attention front already initialised");
+    if (fc->taps < 1 || fc->taps > 8)
+        return fail(c, NDA_ERR_ARG, "taps %u outside 1..8", fc->taps);
+    if (!(fc->rope_theta > 0.0f))
+        return fail(c, NDA_ERR_ARG, "rope_theta must be positive");
+    const nda_config &g = c->cfg;
+    const uint32_t max_pos = fc->max_pos ? fc->max_pos : 65536u;
+    if (max_pos > (1u << 24))
+        return fail(c, NDA_ERR_ARG, "max_pos %u above 2^24 (positions must be exact in fp32)", max_pos);
+    const uint32_t dcol = g.n_heads * g.qk_head_dim + g.n_kv_heads * (g.qk_head_dim + g.v_head_dim);
+    const uint32_t lds = ((g.n_heads + g.n_kv_heads) * (g.qk_head_dim + 2) + g.n_kv_heads * g.v_head_dim) * 4;
+    if (lds > 64 * 1024)
+        return fail(c, NDA_ERR_UNSUPPORTED, "front row of %u columns exceeds the work-group's LDS", dcol);
+    if (dcol % 4)
+        return fail(c, NDA_ERR_UNSUPPORTED, "front row of %u columns is not a multiple of 4", dcol);
+    const uint32_t half = g.qk_head_dim / 2;
+    const uint64_t block = (uint64_t)g.n_layers * fc->taps * dcol;
+    // Rotary table: the engine's inverse frequencies (nd_model.c:1233-1236)
+    // and per-position cos/sin (:2949-2954), with the same libm calls.
+    std::vector<float> inv(half);
+    for (uint32_t i = 0; i < half; i++)
+        inv[i] = 1.0f / powf(fc->rope_theta, (float)(2 * i) / (float)g.qk_head_dim);
+    std::vector<float2> rope((size_t)max_pos * half);
+    for (uint32_t p = 0; p < max_pos; p++)
+        for (uint32_t i = 0; i < half; i++) {
+            const float angle = (float)p * inv[i];
+            rope[(size_t)p * half + i] = make_float2(cosf(angle), sinf(angle));
+        }
+    auto alloc = [&](void **ptr, size_t bytes) -> int {
+        HIPC(c, hipMalloc(ptr, bytes));
+        c->dev_bytes += bytes;
+        return NDA_OK;
+    };
+    const size_t hist_bytes = block * sizeof(float);
+    if (int rc = alloc((void **)&c->d_hist, hist_bytes * g.max_seqs))
+        return rc;
+    if (int rc = alloc((void **)&c->d_snap_hist, hist_bytes * g.max_seqs))
+        return rc;
+    if (int rc = alloc((void **)&c->d_prefix_hist, hist_bytes * std::max(1u, g.max_prefixes)))
+        return rc;
+    if (int rc = alloc((void **)&c->d_front_w, (size_t)g.n_layers * fc->taps * dcol * sizeof(float)))
+        return rc;
+    if (int rc = alloc((void **)&c->d_front_norm, (size_t)g.n_layers * 2 * g.qk_head_dim * sizeof(float)))
+        return rc;
+    if (int rc = alloc((void **)&c->d_rope, rope.size() * sizeof(float2)))
+        return rc;
+    HIPC(c, hipMemset(c->d_hist, 0, hist_bytes * g.max_seqs));
+    HIPC(c, hipMemset(c->d_snap_hist, 0, hist_bytes * g.max_seqs));
+    HIPC(c, hipMemcpy(c->d_rope, rope.data(), rope.size() * sizeof(float2), hipMemcpyHostToDevice));
+    c->taps = fc->taps;
+    c->max_pos = max_pos;
+    c->dcol = dcol;
+    c->hist_block = block;
+    c->front_w_set.assign(g.n_layers, 0);
+    return NDA_OK;
+}
+
+int nda_front_weights(nda_ctx *c, uint32_t layer, const float *tap_q, const float *tap_k,
+                      const float *tap_v, const float *norm_q, const float *norm_k)
+{
+    if (!c)
+        return NDA_ERR_ARG;
+    if (!c->taps)
+        return fail(c, NDA_ERR_STATE, "attention front not initialised (nda_front_init)");
+    if (layer >= c->cfg.n_layers)
+        return fail(c, NDA_ERR_ARG, "layer %u out of range", layer);
+    if (!tap_q || !tap_k || !tap_v || !norm_q || !norm_k)
+        return fail(c, NDA_ERR_ARG, "null weight array");
+    const nda_config &g = c->cfg;
+    const uint32_t dq = g.n_heads * g.qk_head_dim, dk = g.n_kv_heads * g.qk_head_dim,
+                   dv = g.n_kv_heads * g.v_head_dim;
+    // Device rows are [tap][q | k | v] so one tap's weights for a column sit
+    // at the column's offset in every row.
+    std::vector<float> w((size_t)c->taps * c->dcol);
+    for (uint32_t j = 0; j < c->taps; j++) {
+        float *r = &w[(size_t)j * c->dcol];
+        std::memcpy(r, tap_q + (size_t)j * dq, dq * sizeof(float));
+        std::memcpy(r + dq, tap_k + (size_t)j * dk, dk * sizeof(float));
+        std::memcpy(r + dq + dk, tap_v + (size_t)j * dv, dv * sizeof(float));
+    }
+    std::vector<float> nrm(2 * (size_t)g.qk_head_dim);
+    std::memcpy(nrm.data(), norm_q, g.qk_head_dim * sizeof(float));
+    std::memcpy(nrm.data() + g.qk_head_dim, norm_k, g.qk_head_dim * sizeof(float));
+    HIPC(c, hipMemcpy(c->d_front_w + (size_t)layer * c->taps * c->dcol, w.data(), w.size() * sizeof(float),
+                      hipMemcpyHostToDevice));
+    HIPC(c, hipMemcpy(c->d_front_norm + (size_t)layer * 2 * g.qk_head_dim, nrm.data(),
+                      nrm.size() * sizeof(float), hipMemcpyHostToDevice));
+    c->front_w_set[layer] = 1;
+    return NDA_OK;
+}
+
+namespace {
+
+// Checks shared by the front entry points: initialised, weights present,
+// each sequence at most once, every position inside the rotary table.
+int front_check(nda_ctx *c, uint32_t layer, uint32_t nseq, const uint32_t *ids, const uint32_t *n_tokens)
+{
+    if (!c->taps)
+        return fail(c, NDA_ERR_STATE, "attention front not initialised (nda_front_init)");
+    if (layer >= c->cfg.n_layers)
+        return fail(c, NDA_ERR_ARG, "layer %u out of range", layer);
+    if (!c->front_w_set[layer])
+        return fail(c, NDA_ERR_STATE, "no front weights for layer %u (nda_front_weights)", layer);
+    if (int rc = check_ids(c, nseq, ids))
+        return rc;
+    c->seen.assign(c->cfg.max_seqs, 0);
+    for (uint32_t b = 0; b < nseq; b++) {
+        const uint32_t q = sid(ids, b);
+        if (c->seen[q]++)
+            return fail(c, NDA_ERR_ARG, "sequence %u listed twice", q);
+        const uint32_t n = n_tokens ? n_tokens[b] : 1u;
+        if (n && (uint64_t)c->seqs[q].pos + n > c->max_pos)
+            return fail(c, NDA_ERR_RANGE, "sequence %u: position %u beyond the rotary table (max_pos %u)", q,
+                        c->seqs[q].pos + n - 1, c->max_pos);
+    }
+    return NDA_OK;
+}
+
+FrontArgs front_args(nda_ctx *c, uint32_t layer)
+{
+    FrontArgs a{};
+    a.hist = c->d_hist;
+    a.w = c->d_front_w + (size_t)layer * c->taps * c->dcol;
+    a.norm = c->d_front_norm + (size_t)layer * 2 * c->cfg.qk_head_dim;
+    a.rope = c->d_rope;
+    a.seqs = c->d_seqs;
+    a.pg = c->pg;
+    a.layer = layer;
+    a.n_layers = c->cfg.n_layers;
+    a.taps = c->taps;
+    a.nh = c->cfg.n_heads;
+    a.nkv = c->cfg.n_kv_heads;
+    a.qk = c->cfg.qk_head_dim;
+    a.vd = c->cfg.v_head_dim;
+    return a;
+}
+
+} // namespace
+
+int nda_front(nda_ctx *c, uint32_t layer, uint32_t nseq, const uint32_t *ids, const uint32_t *n_tokens,
+              const float *q, const float *k, const float *v, float *q_out, float *k_out, float *v_out,
+              void *stream)
+{
+    if (!c)
+        return NDA_ERR_ARG;
+    if (nseq && (!q || !k || !v || !q_out || !k_out || !v_out))
+        return fail(c, NDA_ERR_ARG, "null q/k/v or output");
+    if (int rc = front_check(c, layer, nseq, ids, n_tokens))
+        return rc;
+    hipStream_t st = (hipStream_t)stream;
+    uint64_t rows = 0;
+    bool multi = false;
+    for (uint32_t b = 0; b < nseq; b++) {
+        const uint32_t n = n_tokens ? n_tokens[b] : 1u;
+        rows += n;
+        multi |= n > 1;
+    }
+    if (rows == 0)
+        return NDA_OK;
+    if (rows > (1u << 26))
+        return fail(c, NDA_ERR_ARG, "too many front rows (%llu)", (unsigned long long)rows);
+    if (int rc = sync_tables(c, st))
+        return rc;
+    if (int rc = hist_flush(c, st))
+        return rc;
+    if (int rc = ensure_buf(c, c->d_front_rows, c->front_rows_cap, 3 * rows))
+        return rc;
+    std::vector<uint32_t> host(3 * rows);
+    for (uint32_t b = 0, r = 0; b < nseq; b++) {
+        const uint32_t n = n_tokens ? n_tokens[b] : 1u;
+        for (uint32_t t = 0; t < n; t++, r++) {
+            host[r] = sid(ids, b);
+            host[rows + r] = t;
+            host[2 * rows + r] = n;
+        }
+    }
+    HIPC(c, hipMemcpyAsync(c->d_front_rows, host.data(), host.size() * 4, hipMemcpyHostToDevice, st));
+    FrontArgs a = front_args(c, layer);
+    a.q = q;
+    a.k = k;
+    a.v = v;
+    a.q_out = q_out;
+    a.k_out = k_out;
+    a.v_out = v_out;
+    a.row_seq = c->d_front_rows;
+    a.row_t = c->d_front_rows + rows;
+    a.rows = (uint32_t)rows;
+    a.hist_write = multi ? 0u : 1u;
+    {
+        ProfScope ps(c, NDA_K_FRONT, st);
+        hipError_t e = launch_front(c->geo, a, st);
+        if (e != hipSuccess)
+            return hip_fail(c, e, "front kernel launch");
+    }
+    if (multi) {
+        HistTailArgs h{};
+        h.q = q;
+        h.k = k;
+        h.v = v;
+        h.hist = c->d_hist;
+        h.seqs = c->d_seqs;
+        h.row_seq = a.row_seq;
+        h.row_t = a.row_t;
+        h.row_n = c->d_front_rows + 2 * rows;
+        h.rows = (uint32_t)rows;
+        h.layer = layer;
+        h.n_layers = c->cfg.n_layers;
+        h.taps = c->taps;
+        h.dq = c->cfg.n_heads * c->cfg.qk_head_dim;
+        h.dk = c->cfg.n_kv_heads * c->cfg.qk_head_dim;
+        h.dv = c->cfg.n_kv_heads * c->cfg.v_head_dim;
+        hipError_t e = launch_hist_tail(h, st);
+        if (e != hipSuccess)
+            return hip_fail(c, e, "history write-back launch");
+    }
+    return NDA_OK;
+}
+
+int nda_attention(nda_ctx *c, uint32_t layer, uint32_t nseq, const uint32_t *ids, const float *q,
+                  const float *k, const float *v, const float *gate, float *out, void *stream)
+{
+    if (!c)
+        return NDA_ERR_ARG;
+    if (nseq && (!q || !k || !v || !out))
+        return fail(c, NDA_ERR_ARG, "null q/k/v/out");
+    if (int rc = front_check(c, layer, nseq, ids, nullptr))
+        return rc;
+    if (nseq == 0)
+        return NDA_OK;
+    hipStream_t st = (hipStream_t)stream;
+    for (uint32_t b = 0; b < nseq; b++) {
+        const uint32_t qq = sid(ids, b);
+        if (int rc = back_positions(c, qq, c->seqs[qq].pos, 1))
+            return rc;
+    }
+    for (uint32_t b = 0; b < nseq; b++) {
+        SeqHost &s = c->seqs[sid(ids, b)];
+        s.stored_end = std::max(s.stored_end, s.pos + 1);
+    }
+    if (int rc = sync_tables(c, st))
+        return rc;
+    if (int rc = hist_flush(c, st))
+        return rc;
+    const size_t dq = (size_t)c->cfg.n_heads * c->cfg.qk_head_dim;
+    if (int rc = ensure_buf(c, c->d_qfront, c->qfront_cap, (size_t)nseq * dq))
+        return rc;
+    const uint32_t *d_seq, *d_t;
+    if (int rc = upload_rows(c, nseq, ids, nullptr, st, &d_seq, &d_t))
+        return rc;
+    FrontArgs a = front_args(c, layer);
+    a.q = q;
+    a.k = k;
+    a.v = v;
+    a.q_out = c->d_qfront;
+    a.row_seq = d_seq;
+    a.rows = nseq;
+    a.hist_write = 1;
+    a.pool = c->pool + (uint64_t)layer * c->pg.layer_bytes;
+    a.page_table = c->d_pages;
+    {
+        ProfScope ps(c, NDA_K_FRONT, st);
+        hipError_t e = launch_front(c->geo, a, st);
+        if (e != hipSuccess)
+            return hip_fail(c, e, "front kernel launch");
+    }
+    return decode_impl(c, layer, nseq, ids, c->d_qfront, nullptr, nullptr, gate, out, stream);
+}
+
+int nda_front_hist(nda_ctx *c, uint32_t seq, int snap, float *dst, void *stream)
+{
+    if (!c || !dst)
+        return c ? fail(c, NDA_ERR_ARG, "null destination") : NDA_ERR_ARG;
+    if (!c->taps)
+        return fail(c, NDA_ERR_STATE, "attention front not initialised (nda_front_init)");
+    if (int rc = check_seq(c, seq))
+        return rc;
+    hipStream_t st = (hipStream_t)stream;
+    if (int rc = hist_flush(c, st))
+        return rc;
+    const float *src = snap ? hist_snap(c, seq) : hist_live(c, seq);
+    HIPC(c, hipMemcpyAsync(dst, src, c->hist_block * sizeof(float), hipMemcpyDeviceToHost, st));
+    HIPC(c, hipStreamSynchronize(st));
+    return NDA_OK;
+}
+
 int nda_sync(nda_ctx *c, void *stream)
 {
     hipError_t e = hipStreamSynchronize((hipStream_t)stream);
@@ -1119,7 +1542,7 @@ static int locate(nda_ctx *c, uint32_t seq, uint32_t p0, uint32_t count, bool fo
             const uint32_t rcap = c->cfg.window - s.n_sink;
             if (p >= s.stored_end)
                 return fail(c, NDA_ERR_RANGE, "position %u was never stored", p);
-            if (p >= s.n_sink && s.stored_end - p > rcap)
+            if (p >= s.n_sink && (s.stored_end - p > rcap || p < s.ring_lo))
                 return fail(c, NDA_ERR_RANGE, "position %u has left the ring", p);
         }
         const uint32_t sl = own_slot(s, p, c->cfg.window);

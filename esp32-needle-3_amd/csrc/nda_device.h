@@ -40,4 +40,64 @@ __device__ __forceinline__ int own_slot(const SeqDev &s, int p, int window)
     return s.n_sink + (p - s.n_sink) % (window - s.n_sink);
 }
 
+__device__ __forceinline__ float wave_max(float x)
+{
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1)
+        x = fmaxf(x, __shfl_xor(x, o, 64));
+    return x;
+}
+
+// One wave per (row, kv-head), lane = element. INT8: absmax over the row,
+// scale = absmax/127 (1 for a zero row), then the engine's store
+// (engine/src/nd_model.c:2426-2449 and kv_store_int8 :1819-1866) step for
+// step: r = 1/scale, y = x*r, e = fma(-scale, y, x), q = fma(e, r, y) (a plain
+// divide for |x| >= 1e30), clamp +-127, round half-to-even; a NaN quotient
+// (scale below 2^-127, where 1/scale overflows) stores 0 as the host build
+// does. F16: round to nearest even.
+__device__ __forceinline__ int8_t quant_code(float x, float scale, float r)
+{
+    float q;
+    if (x > -1e30f && x < 1e30f) {
+        const float y = x * r;
+        const float e = __builtin_fmaf(-scale, y, x);
+        q = __builtin_fmaf(e, r, y);
+    } else {
+        q = __fdiv_rn(x, scale);
+    }
+    if (q != q)
+        return 0;
+    q = q > 127.0f ? 127.0f : q;
+    q = q < -127.0f ? -127.0f : q;
+    return (int8_t)(int)__builtin_rintf(q);
+}
+
+// Store one row of K and V (lane = element) for slot `off` of a page's
+// kv-head block at hb. Shared by the append kernel and the fused append of
+// the decode kernel.
+template <int ES, int DK, int DV>
+__device__ __forceinline__ void store_row(uint8_t *hb, int off, int P, float kx, float vx, int lane)
+{
+    if constexpr (ES == 2) {
+        if (lane < DK)
+            reinterpret_cast<_Float16 *>(hb + (uint64_t)off * DK * 2)[lane] = (_Float16)kx;
+        if (lane < DV)
+            reinterpret_cast<_Float16 *>(hb + (uint64_t)P * DK * 2 + (uint64_t)off * DV * 2)[lane] = (_Float16)vx;
+    } else {
+        const float ak = wave_max(fabsf(kx)), av = wave_max(fabsf(vx));
+        const float sk = ak > 0.0f ? __fdiv_rn(ak, 127.0f) : 1.0f;
+        const float sv = av > 0.0f ? __fdiv_rn(av, 127.0f) : 1.0f;
+        const float rk = __fdiv_rn(1.0f, sk), rv = __fdiv_rn(1.0f, sv);
+        if (lane < DK)
+            reinterpret_cast<int8_t *>(hb + (uint64_t)off * DK)[lane] = quant_code(kx, sk, rk);
+        if (lane < DV)
+            reinterpret_cast<int8_t *>(hb + (uint64_t)P * DK + (uint64_t)off * DV)[lane] = quant_code(vx, sv, rv);
+        if (lane == 0) {
+            float *sc = reinterpret_cast<float *>(hb + (uint64_t)P * (DK + DV));
+            sc[off] = sk;
+            sc[P + off] = sv;
+        }
+    }
+}
+
 } // namespace nda

@@ -119,6 +119,48 @@ struct FillKvArgs {
     PageGeom pg;
 };
 
+/* One launch of the attention front: the qkv tap convolution, per-head
+ * ZC-RMSNorm and RoPE on raw projections (engine/src/nd_model.c:2413-2424).
+ * A row is one token of one sequence; the rows of a sequence are contiguous
+ * and in token order, so token t reads raw rows row-j for j <= t and the tap
+ * history for older positions. */
+struct FrontArgs {
+    const float *q, *k, *v;        /* raw [rows][dq], [rows][dk], [rows][dv] */
+    float *q_out;                  /* [rows][dq] */
+    float *k_out, *v_out;          /* [rows][dk], [rows][dv]; null: store into the KV pages */
+    float *hist;                   /* [max_seqs][n_layers][taps][dcol] raw history */
+    const float *w;                /* this layer's tap weights [taps][dcol] (q | k | v columns) */
+    const float *norm;             /* this layer's norm scales [2][qk]: q, then k */
+    const float2 *rope;            /* [max_pos][qk/2] (cos, sin) */
+    const SeqDev *seqs;
+    const uint32_t *row_seq;       /* [rows] or null: identity */
+    const uint32_t *row_t;         /* [rows] token index within its sequence, or null: 0 */
+    uint8_t *pool;                 /* this layer's pool (store mode) */
+    const int32_t *page_table;
+    PageGeom pg;
+    uint32_t rows, layer, n_layers, taps;
+    uint32_t nh, nkv, qk, vd;
+    uint32_t hist_write;           /* 1: each row writes its raw projection into the history */
+};
+
+/* Tap-history maintenance: copies (or zeroes, src null) of whole per-
+ * sequence history blocks, applied in order by the host in batches whose
+ * blocks do not overlap. */
+struct HistOp {
+    float *dst;
+    const float *src;
+};
+
+/* History write-back after a multi-token front launch: the raw rows of the
+ * last `taps` tokens of every sequence go to their slots pos % taps. */
+struct HistTailArgs {
+    const float *q, *k, *v;
+    float *hist;
+    const SeqDev *seqs;
+    const uint32_t *row_seq, *row_t, *row_n;   /* row_n: tokens of the row's sequence */
+    uint32_t rows, layer, n_layers, taps, dq, dk, dv;
+};
+
 /* Kernel geometry key. */
 struct Geo {
     int kv_f16;
@@ -139,5 +181,11 @@ hipError_t launch_advance(SeqDev *seqs, const uint32_t *seq_list, uint32_t nseq,
 hipError_t launch_fill_normal(void *dst, uint64_t n, int dtype, uint64_t seed, float scale,
                               hipStream_t s);
 bool geometry_supported(const Geo &g);
+
+/* nda_front.hip */
+hipError_t launch_front(const Geo &g, const FrontArgs &a, hipStream_t s);
+hipError_t launch_hist_tail(const HistTailArgs &a, hipStream_t s);
+hipError_t launch_hist_ops(const HistOp *d_ops, uint32_t n_ops, uint64_t block_floats, hipStream_t s);
+size_t front_lds_bytes(const FrontArgs &a);
 
 } // namespace nda

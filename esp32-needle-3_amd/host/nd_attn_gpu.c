@@ -224,6 +224,41 @@ int nd_gpu_attention(nd_gpu_model *m, uint32_t li, const float *q, const float *
     return nda_d2h(out, m->d_out, sizeof(float) * m->nh * m->v_hd);
 }
 
+int nd_gpu_front_init(nd_gpu_model *m, uint32_t taps, float rope_theta, uint32_t max_pos)
+{
+    nda_front_config fc;
+    fc.taps = taps;
+    fc.rope_theta = rope_theta;
+    fc.max_pos = max_pos;
+    return nda_front_init(m->ctx, &fc);
+}
+
+int nd_gpu_front_weights(nd_gpu_model *m, uint32_t li, const float *tap_q, const float *tap_k,
+                         const float *tap_v, const float *norm_q, const float *norm_k)
+{
+    return nda_front_weights(m->ctx, li, tap_q, tap_k, tap_v, norm_q, norm_k);
+}
+
+int nd_gpu_attention_raw(nd_gpu_model *m, uint32_t li, const float *q, const float *k,
+                         const float *v, const float *gate, float *out)
+{
+    int rc;
+    if (nda_h2d(m->d_q, q, sizeof(float) * m->nh * m->qk_hd) ||
+        nda_h2d(m->d_k, k, sizeof(float) * m->nkv * m->qk_hd) ||
+        nda_h2d(m->d_v, v, sizeof(float) * m->nkv * m->v_hd))
+        return NDA_ERR_HIP;
+    if (gate && nda_h2d(m->d_gate, gate, sizeof(float) * m->nh * m->v_hd))
+        return NDA_ERR_HIP;
+    rc = nda_attention(m->ctx, li, 1, NULL, m->d_q, m->d_k, m->d_v, gate ? m->d_gate : NULL,
+                       m->d_out, NULL);
+    if (rc)
+        return rc;
+    rc = nda_sync(m->ctx, NULL);
+    if (rc)
+        return rc;
+    return nda_d2h(out, m->d_out, sizeof(float) * m->nh * m->v_hd);
+}
+
 void nd_gpu_step_end(nd_gpu_model *m)
 {
     nda_advance(m->ctx, 1, NULL, 1, NULL);

@@ -19,7 +19,8 @@ NDA_OK = 0
 ERRORS = {-1: "NDA_ERR_ARG", -2: "NDA_ERR_NOMEM", -3: "NDA_ERR_HIP", -4: "NDA_ERR_RANGE",
           -5: "NDA_ERR_STATE", -6: "NDA_ERR_UNSUPPORTED", -7: "NDA_ERR_NODEV"}
 KV_INT8, KV_F16 = 0, 1
-K_APPEND, K_DECODE, K_COMBINE, K_PREFILL = 0, 1, 2, 3
+K_APPEND, K_DECODE, K_COMBINE, K_PREFILL, K_FRONT = 0, 1, 2, 3, 4
+K_COUNT = 5
 FLAG_PREFILL_VALU = 1
 
 # Every symbol include/nda.h declares (checked by the CPU test suite).
@@ -33,11 +34,13 @@ ABI_SYMBOLS = [
     "nda_dev_alloc", "nda_dev_free", "nda_h2d", "nda_d2h", "nda_d2d", "nda_memset", "nda_fill_normal",
     "nda_stream_create", "nda_stream_destroy", "nda_device_sync", "nda_device_info",
     "nda_prof_enable", "nda_prof_read",
+    "nda_front_init", "nda_front_weights", "nda_front", "nda_attention", "nda_front_hist",
 ]
 HOST_SYMBOLS = [
     "nd_gpu_open", "nd_gpu_close", "nd_gpu_reset", "nd_gpu_set_sink", "nd_gpu_snapshot",
     "nd_gpu_rewind", "nd_gpu_prefix_save", "nd_gpu_prefix_restore", "nd_gpu_prefix_free",
     "nd_gpu_attention", "nd_gpu_step_end", "nd_gpu_pos", "nd_gpu_n_sink", "nd_gpu_ctx",
+    "nd_gpu_front_init", "nd_gpu_front_weights", "nd_gpu_attention_raw",
 ]
 
 
@@ -53,6 +56,10 @@ class Config(C.Structure):
                 ("page_size", C.c_uint32), ("kv_dtype", C.c_uint32), ("max_seqs", C.c_uint32),
                 ("max_prefixes", C.c_uint32), ("max_pages", C.c_uint64),
                 ("split_chunk", C.c_uint32), ("flags", C.c_uint32)]
+
+
+class FrontConfig(C.Structure):
+    _fields_ = [("taps", C.c_uint32), ("rope_theta", C.c_float), ("max_pos", C.c_uint32)]
 
 
 _lib = None
@@ -103,6 +110,11 @@ def lib():
             "nda_device_info": (C.c_int, [C.c_char_p, C.c_size_t, C.POINTER(C.c_int)]),
             "nda_prof_enable": (C.c_int, [vp, C.c_int]),
             "nda_prof_read": (C.c_int, [vp, C.POINTER(C.c_double), C.POINTER(u64), C.c_int]),
+            "nda_front_init": (C.c_int, [vp, C.POINTER(FrontConfig)]),
+            "nda_front_weights": (C.c_int, [vp, u32, vp, vp, vp, vp, vp]),
+            "nda_front": (C.c_int, [vp, u32, u32, vp, vp, vp, vp, vp, vp, vp, vp, vp]),
+            "nda_attention": (C.c_int, [vp, u32, u32, vp, vp, vp, vp, vp, vp, vp]),
+            "nda_front_hist": (C.c_int, [vp, u32, C.c_int, vp, vp]),
         }
         for name, (res, args) in sig.items():
             f = getattr(L, name)
@@ -140,6 +152,12 @@ def host_lib():
         H.nd_gpu_n_sink.argtypes = [vp]
         H.nd_gpu_ctx.restype = vp
         H.nd_gpu_ctx.argtypes = [vp]
+        H.nd_gpu_front_init.restype = C.c_int
+        H.nd_gpu_front_init.argtypes = [vp, u32, C.c_float, u32]
+        H.nd_gpu_front_weights.restype = C.c_int
+        H.nd_gpu_front_weights.argtypes = [vp, u32, vp, vp, vp, vp, vp]
+        H.nd_gpu_attention_raw.restype = C.c_int
+        H.nd_gpu_attention_raw.argtypes = [vp, u32, vp, vp, vp, vp, vp]
         _host = H
     return _host
 
@@ -236,6 +254,7 @@ class Context:
         self.owned = True
         _check(lib().nda_create(C.byref(cfg), C.byref(self.h)))
         self.cfg = cfg
+        self._taps = 0
 
     @classmethod
     def borrow(cls, handle, cfg):
@@ -244,6 +263,7 @@ class Context:
         c.h = vp(handle)
         c.owned = False
         c.cfg = cfg
+        c._taps = 0
         return c
 
     def close(self):
@@ -355,9 +375,38 @@ class Context:
     def prof_enable(self, on=True):
         self._c(lib().nda_prof_enable(self.h, 1 if on else 0))
 
+    def front_init(self, taps, rope_theta, max_pos=0):
+        fc = FrontConfig(taps, rope_theta, max_pos)
+        self._c(lib().nda_front_init(self.h, C.byref(fc)))
+        self._taps = taps
+
+    def front_weights(self, layer, tap_q, tap_k, tap_v, norm_q, norm_k):
+        """Host arrays: tap_* [taps][dim], norm_* [qk_head_dim]."""
+        arrs = [np.ascontiguousarray(a, np.float32) for a in (tap_q, tap_k, tap_v, norm_q, norm_k)]
+        self._c(lib().nda_front_weights(self.h, layer, *(a.ctypes.data for a in arrs)))
+
+    def front(self, layer, nseq, q, k, v, q_out, k_out, v_out, n_tokens=None, seq_ids=None, stream=None):
+        keep, p = _ids(seq_ids)
+        n = None if n_tokens is None else np.ascontiguousarray(n_tokens, np.uint32)
+        self._c(lib().nda_front(self.h, layer, nseq, p, None if n is None else n.ctypes.data,
+                                _dp(q), _dp(k), _dp(v), _dp(q_out), _dp(k_out), _dp(v_out), stream))
+
+    def attention(self, layer, nseq, q, k, v, out, gate=None, seq_ids=None, stream=None):
+        keep, p = _ids(seq_ids)
+        self._c(lib().nda_attention(self.h, layer, nseq, p, _dp(q), _dp(k), _dp(v), _dp(gate), _dp(out),
+                                    stream))
+
+    def front_hist(self, seq, snap=False, stream=None):
+        """One sequence's tap histories [n_layers][taps][dcol] (host copy)."""
+        c = self.cfg
+        dcol = c.n_heads * c.qk_head_dim + c.n_kv_heads * (c.qk_head_dim + c.v_head_dim)
+        out = np.zeros((c.n_layers, self._taps, dcol), np.float32)
+        self._c(lib().nda_front_hist(self.h, seq, 1 if snap else 0, out.ctypes.data, stream))
+        return out
+
     def prof_read(self, reset=True):
-        ms = (C.c_double * 4)()
-        n = (u64 * 4)()
+        ms = (C.c_double * K_COUNT)()
+        n = (u64 * K_COUNT)()
         self._c(lib().nda_prof_read(self.h, ms, n, 1 if reset else 0))
         return list(ms), list(n)
 
@@ -371,12 +420,16 @@ class GpuSession:
             raise NdaError(-1, "nd_gpu_open failed")
         self.geom = (n_layers, nh, nkv, qk_hd, v_hd, window)
         self.kv_dtype = kv_dtype
+        self.front_on = False
+        self.taps = 0
 
     def context(self):
         """The session's nda_ctx (sequence 0), borrowed."""
         L, nh, nkv, qk, vd, W = self.geom
-        return Context.borrow(host_lib().nd_gpu_ctx(self.m),
-                              Config(L, nh, nkv, qk, vd, W, 16, self.kv_dtype, 1, 0, 0, 0, 0))
+        c = Context.borrow(host_lib().nd_gpu_ctx(self.m),
+                           Config(L, nh, nkv, qk, vd, W, 16, self.kv_dtype, 1, 0, 0, 0, 0))
+        c._taps = self.taps
+        return c
 
     def close(self):
         if self.m:
@@ -428,7 +481,22 @@ class GpuSession:
         k = np.ascontiguousarray(k, np.float32)
         v = np.ascontiguousarray(v, np.float32)
         g = None if gate is None else np.ascontiguousarray(gate, np.float32)
-        rc = host_lib().nd_gpu_attention(self.m, li, q.ctypes.data, k.ctypes.data, v.ctypes.data,
-                                         None if g is None else g.ctypes.data, out.ctypes.data)
+        fn = host_lib().nd_gpu_attention_raw if self.front_on else host_lib().nd_gpu_attention
+        rc = fn(self.m, li, q.ctypes.data, k.ctypes.data, v.ctypes.data,
+                None if g is None else g.ctypes.data, out.ctypes.data)
         _check(rc)
         return out
+
+    def front_init(self, taps, rope_theta, weights, max_pos=0):
+        """Enable the attention front; weights.arrays(li) gives one layer's
+        (tap_q, tap_k, tap_v, norm_q, norm_k). attention() then takes raw
+        projections."""
+        _check(host_lib().nd_gpu_front_init(self.m, taps, rope_theta, max_pos))
+        L = self.geom[0]
+        self._front_keep = []
+        for li in range(L):
+            arrs = [np.ascontiguousarray(a, np.float32) for a in weights.arrays(li)]
+            self._front_keep.append(arrs)
+            _check(host_lib().nd_gpu_front_weights(self.m, li, *(a.ctypes.data for a in arrs)))
+        self.front_on = True
+        self.taps = taps

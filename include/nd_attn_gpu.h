@@ -15,9 +15,17 @@
  *   nd_gpu_attention      the KV store + attn_heads dispatch of attention()
  *                         :2426-2483 (m->q, m->kbuf, m->vbuf, m->gate -> m->attn)
  *   nd_gpu_step_end       pos++ at the end of nd_model_step_hidden :3094
+ *   nd_gpu_front_init     the tap histories (:1178-1180) and rotary
+ *                         frequencies (:1233-1236) that nd_model_open sets up
+ *   nd_gpu_front_weights  one layer's staged tap weights and q/k norm scales
+ *                         (fp16_slot[li][4..8])
+ *   nd_gpu_attention_raw  attention() after the projections :2413-2483: tap
+ *                         convolution, head norm + RoPE, KV store, attn_heads
+ *                         and the gate, from the raw m->q, m->kbuf, m->vbuf
  *
- * Only the KV part of the session state lives here; the non-KV prefix state
- * (conv taps, engram, confidence pool) stays with the engine.
+ * The KV part of the session state lives here, and with the front
+ * initialised the qkv tap histories too; the rest of the prefix state
+ * (engram, confidence pool) stays with the engine.
  */
 #ifndef ND_ATTN_GPU_H
 #define ND_ATTN_GPU_H
@@ -52,6 +60,16 @@ void nd_gpu_prefix_free(nd_gpu_prefix *p);
  * v [nkv*v_hd], gate [nh*v_hd] (NULL: no gate), out [nh*v_hd]. */
 int  nd_gpu_attention(nd_gpu_model *m, uint32_t li, const float *q, const float *k,
                       const float *v, const float *gate, float *out);
+/* The attention front: after nd_gpu_front_init (taps 1..8, max_pos 0 for
+ * 65536) and nd_gpu_front_weights for every layer, nd_gpu_attention_raw takes
+ * the RAW projections (before tap_projection / zcrms_heads) in the same
+ * layout as nd_gpu_attention. Snapshot, rewind, prefix save / restore and
+ * reset carry the tap histories as the engine does. */
+int  nd_gpu_front_init(nd_gpu_model *m, uint32_t taps, float rope_theta, uint32_t max_pos);
+int  nd_gpu_front_weights(nd_gpu_model *m, uint32_t li, const float *tap_q, const float *tap_k,
+                          const float *tap_v, const float *norm_q, const float *norm_k);
+int  nd_gpu_attention_raw(nd_gpu_model *m, uint32_t li, const float *q, const float *k,
+                          const float *v, const float *gate, float *out);
 void nd_gpu_step_end(nd_gpu_model *m);
 
 uint32_t nd_gpu_pos(const nd_gpu_model *m);

@@ -159,6 +159,53 @@ int nda_prefill(nda_ctx *ctx, uint32_t layer, uint32_t nseq, const uint32_t *seq
 
 int nda_sync(nda_ctx *ctx, void *stream);
 
+/* ---- attention front (engine/src/nd_model.c:2413-2424) ----
+ * What attention() does to the raw q/k/v projections before the store:
+ * tap_projection for q, k and v (:2361-2379, tap_rows :1748-1802), a causal
+ * depthwise convolution of every column over its last `taps` raw values,
+ * then zcrms_heads for q and k (:324-360), a per-head RMS norm with a
+ * (1 + s) scale shared by all heads, fused with half-split RoPE at the
+ * token's position. Results are bit-identical to the engine's host build.
+ * The raw projections of the last `taps` positions of each sequence and
+ * layer (the engine's q_hist/k_hist/v_hist, nd_model.h:167) live on the
+ * device and follow the sequence through nda_seq_reset (zeroed),
+ * nda_prefix_build / nda_seq_attach (saved with the prefix and restored,
+ * as nd_model_prefix_save / restore do, :1519-1521) and nda_seq_rewind. */
+typedef struct {
+    uint32_t taps;         /* the archive's qkv_conv_taps, 1..8 */
+    float    rope_theta;   /* the archive's rope_theta */
+    uint32_t max_pos;      /* the rotary table covers positions [0, max_pos); 0: 65536 */
+} nda_front_config;
+
+/* Allocates the tap histories and the rotary table (cos/sin of
+ * pos * theta^(-2i/qk_head_dim), as nd_model_open :1233-1236 and
+ * nd_model_step_hidden :2949-2954 compute them). Once per context. */
+int nda_front_init(nda_ctx *ctx, const nda_front_config *fc);
+/* One layer's weights from HOST arrays, the engine's staged fp32 slots
+ * (fp16_slot[li][4..8]): tap_q [taps][n_heads*qk_head_dim],
+ * tap_k [taps][n_kv_heads*qk_head_dim], tap_v [taps][n_kv_heads*v_head_dim],
+ * norm_q / norm_k [qk_head_dim]. */
+int nda_front_weights(nda_ctx *ctx, uint32_t layer, const float *tap_q, const float *tap_k,
+                      const float *tap_v, const float *norm_q, const float *norm_k);
+/* The front for n_tokens[b] tokens of each listed sequence at positions
+ * pos, pos+1, ... (n_tokens NULL: one token each), packed token-major as
+ * nda_prefill's inputs: raw q/k/v in, q_out/k_out/v_out (same shapes, device)
+ * out, ready for nda_step / nda_prefill. Updates the tap histories; does not
+ * advance pos. Each sequence at most once per call. */
+int nda_front(nda_ctx *ctx, uint32_t layer, uint32_t nseq, const uint32_t *seq_ids,
+              const uint32_t *n_tokens, const float *q, const float *k, const float *v,
+              float *q_out, float *k_out, float *v_out, void *stream);
+/* attention() from the raw projections on: the front, the KV store of this
+ * position and the decode, for one token of each listed sequence. q/k/v raw
+ * [nseq][...], gate/out as nda_decode. Does not advance pos. */
+int nda_attention(nda_ctx *ctx, uint32_t layer, uint32_t nseq, const uint32_t *seq_ids,
+                  const float *q, const float *k, const float *v, const float *gate,
+                  float *out, void *stream);
+/* Copies one sequence's tap histories (snap 0: live, 1: the snapshot that
+ * nda_seq_rewind restores) to a HOST buffer
+ * [n_layers][taps][n_heads*qk_head_dim + n_kv_heads*(qk_head_dim + v_head_dim)]. */
+int nda_front_hist(nda_ctx *ctx, uint32_t seq, int snap, float *dst, void *stream);
+
 /* ---- inspection (tests, tools) ---- */
 
 /* Copies the stored K/V of `count` consecutive positions starting at
@@ -205,7 +252,8 @@ int nda_device_info(char *name, size_t name_len, int *cu_count);
 #define NDA_K_DECODE  1   /* ND_P_ATTN */
 #define NDA_K_COMBINE 2   /* split-KV merge */
 #define NDA_K_PREFILL 3
-#define NDA_K_COUNT   4
+#define NDA_K_FRONT   4   /* ND_P_TAPS + ND_P_HNORM (+ the store in nda_attention) */
+#define NDA_K_COUNT   5
 int nda_prof_enable(nda_ctx *ctx, int on);
 /* Synchronises outstanding timed launches, then returns per kind the summed
  * milliseconds and launch counts; resets when reset != 0. */
