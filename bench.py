@@ -355,11 +355,122 @@ def engine_session_leg(N, steps=200):
         ref_us = (time.perf_counter() - t0) / steps * 1e6
         r.close()
     g.close()
+    front_gpu_us, front_ref_us = engine_front_timing(N, O, geom, toks, steps)
     return {"workload": "one engine session through nd_gpu_attention (host arrays): MHA 8 x 64, int8 KV, "
                         "window 512, 213 pinned + %d decode positions" % steps,
             "gpu_us_per_layer_call": round(gpu_us, 1),
             "reference_cpu_us_per_layer_call": None if ref_us is None else round(ref_us, 1),
-            "note": "latency-bound (host<->device copies + 1 fused launch); throughput comes from batching"}
+            "front_gpu_us_per_layer_call": round(front_gpu_us, 1),
+            "front_reference_cpu_us_per_layer_call": None if front_ref_us is None else round(front_ref_us, 1),
+            "note": "latency-bound (host<->device copies + 1 fused launch); throughput comes from batching. "
+                    "front_*: raw projections through nd_gpu_attention_raw (3-tap convolution, head norm, "
+                    "RoPE, store, attend) beside the reference's tap_projection + zcrms_heads + store + "
+                    "attn_heads"}
+
+
+def engine_front_timing(N, O, geom, toks, steps, taps=3, theta=10000.0):
+    """Per-layer-call latency of the shim with the attention front, and of
+    the reference engine's own front + attention on one host thread."""
+    rng = np.random.default_rng(SEED + 12)
+    L, nh, nkv, qk, vd, W = geom
+    t = lambda dim: (rng.standard_normal((L, taps, dim)) * 0.5).astype(np.float32)
+    fw = O.FrontWeights(t(nh * qk), t(nkv * qk), t(nkv * vd),
+                        (rng.standard_normal((L, qk)) * 0.25).astype(np.float32),
+                        (rng.standard_normal((L, qk)) * 0.25).astype(np.float32))
+    g = N.GpuSession(*geom)
+    g.front_init(taps, theta, fw)
+    for i in range(213):
+        g.attention(0, *toks[i % 8])
+        g.step_end()
+    g.snapshot()
+    t0 = time.perf_counter()
+    for i in range(steps):
+        g.attention(0, *toks[i % 8])
+        g.step_end()
+    gpu_us = (time.perf_counter() - t0) / steps * 1e6
+    g.close()
+    if not O.have_ref():
+        return gpu_us, None
+    r = O.RefSession(*geom)
+    r.front_init(taps, theta)
+    for i in range(213):
+        q, k, v = r.front(0, fw, *toks[i % 8][:3])
+        r.attention(0, q, k, v, toks[i % 8][3])
+        r.step_end()
+    r.snapshot()
+    t0 = time.perf_counter()
+    for i in range(steps):
+        q, k, v = r.front(0, fw, *toks[i % 8][:3])
+        r.attention(0, q, k, v, toks[i % 8][3])
+        r.step_end()
+    ref_us = (time.perf_counter() - t0) / steps * 1e6
+    r.close()
+    return gpu_us, ref_us
+
+
+def front_leg(N, stream, steps=5, warmup=2, taps=3, theta=10000.0):
+    """The headline decode with the attention front: per layer nda_attention
+    takes RAW q/k/v projections (tap convolution over 3 taps, per-head
+    ZC-RMSNorm + RoPE, KV store, decode), then pos += 1. The front kernel's
+    algorithmic HBM bytes per row: raw q/k/v in, taps-1 history rows read, one
+    written, normalised q out, the fp16 K/V row stored:
+    4*dcol*(taps+1) + 4*dq + 2*(dk+dv) with dcol = dq+dk+dv."""
+    rng = np.random.default_rng(SEED + 21)
+    lens = rng.integers(LMIN, LMAX + 1, B)
+    total = warmup + steps
+    P = 16
+    window = LMAX + total + 16
+    need = int(sum((int(L) + total + P - 1) // P for L in lens)) + 64
+    ctx = N.Context(LAYERS, H, H, D, D, window, kv_dtype=N.KV_F16, max_seqs=B, page_size=P, max_pages=need)
+    ctx.front_init(taps, theta)
+    for li in range(LAYERS):
+        ctx.front_weights(li, *(rng.standard_normal(shape).astype(np.float32) * np.float32(scale)
+                                for shape, scale in (((taps, H * D), 0.5), ((taps, H * D), 0.5),
+                                                     ((taps, H * D), 0.5), ((D,), 0.25), ((D,), 0.25))))
+    for b in range(B):
+        ctx.seq_set_pos(b, int(lens[b]) - 1)
+        ctx.seq_reserve(b, total + 1)
+    ctx.kv_fill_normal(B, seed=SEED + 22, stream=stream)
+    q, kn, vn, out = ([N.DevBuf(B * H * D * 4) for _ in range(LAYERS)] for _ in range(4))
+    for li in range(LAYERS):
+        for j, buf in enumerate((q[li], kn[li], vn[li])):
+            buf.fill_normal(B * H * D, 0, SEED + 100 * li + j, stream=stream)
+    ctx.sync(stream)
+
+    def step():
+        for li in range(LAYERS):
+            ctx.attention(li, B, q[li], kn[li], vn[li], out[li], stream=stream)
+        ctx.advance(B, None, 1, stream=stream)
+
+    for _ in range(warmup):
+        step()
+    ctx.sync(stream)
+    ctx.prof_enable(True)
+    ctx.prof_read(reset=True)
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        step()
+    ctx.sync(stream)
+    el = time.perf_counter() - t0
+    ms, launches = ctx.prof_read(reset=True)
+    ctx.prof_enable(False)
+    dq = H * D
+    dcol = 3 * dq
+    row_bytes = 4 * dcol * (taps + 1) + 4 * dq + 2 * (2 * dq)
+    front_ms = ms[N.K_FRONT] / max(1, launches[N.K_FRONT])
+    gbs = B * row_bytes / (front_ms * 1e-3) / 1e9
+    ctx.close()
+    for bufs in (q, kn, vn, out):
+        for bb in bufs:
+            bb.free()
+    return {"workload": "batched decode with the attention front: 4096 sequences, 8 heads x 64, fp16 K/V, "
+                        "L ~ U[213,1024], raw q/k/v -> %d-tap convolution + head norm + RoPE + store + "
+                        "attend, 8 layers" % taps,
+            "tokens_per_s": round(B * steps / el, 1), "ms_per_step": round(el * 1e3 / steps, 4),
+            "front_kernel_ms": round(front_ms, 4), "decode_kernel_ms": round(
+                ms[N.K_DECODE] / max(1, launches[N.K_DECODE]), 4),
+            "front_GBps": round(gbs, 1), "front_frac": round(gbs / HBM_PEAK_GBS, 4),
+            "front_bytes_per_launch": B * row_bytes}
 
 
 def main():
@@ -475,6 +586,9 @@ def main():
     for bufs in (q, kn, vn, out):
         for bb in bufs:
             bb.free()
+    front = front_leg(N, stream)
+    log("front: %.0f tok/s, step %.3f ms, front kernel %.4f ms (%.0f GB/s)" % (
+        front["tokens_per_s"], front["ms_per_step"], front["front_kernel_ms"], front["front_GBps"]))
     engine = engine_session_leg(N)
     log("engine session: GPU %.1f us per layer call, reference CPU %s us" % (
         engine["gpu_us_per_layer_call"], engine["reference_cpu_us_per_layer_call"]))
@@ -530,6 +644,7 @@ def main():
         "cpu_reference_int8": cpu_ref,
         "prefill": prefill,
         "engine_session": engine,
+        "front": front,
         "shared_prefix": shared,
         "max_abs_delta_sampled": worst,
         "device": name,

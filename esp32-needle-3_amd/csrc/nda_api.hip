@@ -1237,11 +1237,6 @@ int nda_front_init(nda_ctx *c, const nda_front_config *fc)
     if (max_pos > (1u << 24))
         return fail(c, NDA_ERR_ARG, "max_pos %u above 2^24 (positions must be exact in fp32)", max_pos);
     const uint32_t dcol = g.n_heads * g.qk_head_dim + g.n_kv_heads * (g.qk_head_dim + g.v_head_dim);
-    const uint32_t lds = ((g.n_heads + g.n_kv_heads) * (g.qk_head_dim + 2) + g.n_kv_heads * g.v_head_dim) * 4;
-    if (lds > 64 * 1024)
-        return fail(c, NDA_ERR_UNSUPPORTED, "front row of %u columns exceeds the work-group's LDS", dcol);
-    if (dcol % 4)
-        return fail(c, NDA_ERR_UNSUPPORTED, "front row of %u columns is not a multiple of 4", dcol);
     const uint32_t half = g.qk_head_dim / 2;
     const uint64_t block = (uint64_t)g.n_layers * fc->taps * dcol;
     // Rotary table: the engine's inverse frequencies (nd_model.c:1233-1236)
@@ -1320,6 +1315,8 @@ int nda_front_weights(nda_ctx *c, uint32_t layer, const float *tap_q, const floa
 
 namespace {
 
+inline bool aligned16(const void *p) { return ((uintptr_t)p & 15) == 0; }
+
 // Checks shared by the front entry points: initialised, weights present,
 // each sequence at most once, every position inside the rotary table.
 int front_check(nda_ctx *c, uint32_t layer, uint32_t nseq, const uint32_t *ids, const uint32_t *n_tokens)
@@ -1376,6 +1373,8 @@ int nda_front(nda_ctx *c, uint32_t layer, uint32_t nseq, const uint32_t *ids, co
         return fail(c, NDA_ERR_ARG, "null q/k/v or output");
     if (int rc = front_check(c, layer, nseq, ids, n_tokens))
         return rc;
+    if (!aligned16(q) || !aligned16(k) || !aligned16(v) || !aligned16(k_out) || !aligned16(v_out))
+        return fail(c, NDA_ERR_ARG, "q/k/v and k_out/v_out must be 16-byte aligned");
     hipStream_t st = (hipStream_t)stream;
     uint64_t rows = 0;
     bool multi = false;
@@ -1456,6 +1455,8 @@ int nda_attention(nda_ctx *c, uint32_t layer, uint32_t nseq, const uint32_t *ids
         return rc;
     if (nseq == 0)
         return NDA_OK;
+    if (!aligned16(q) || !aligned16(k) || !aligned16(v))
+        return fail(c, NDA_ERR_ARG, "q/k/v must be 16-byte aligned");
     hipStream_t st = (hipStream_t)stream;
     for (uint32_t b = 0; b < nseq; b++) {
         const uint32_t qq = sid(ids, b);

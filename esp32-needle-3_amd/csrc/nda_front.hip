@@ -10,153 +10,181 @@
 //                       shared by all heads, fused with GPT-NeoX half-split
 //                       RoPE at the row's position (:324-360)
 //
-// One work-group per row (one token of one sequence) covers every column of
-// q, k and v: the convolution is one column per thread, the per-head sums of
-// squares one head per thread (a sequential walk, the reference's order),
-// the emit one (head, rotary pair) per thread. Store mode then writes the k/v
-// rows into the KV pages exactly as the append kernel does (int8 with the
-// engine's Markstein store, or fp16), so the decode launch that follows reads
-// them from the cache.
+// One work-group per (row, kv-head group): a row is one token of one
+// sequence, a group the rep query heads sharing one kv-head plus that k and v
+// head, so every normalised head lies inside one work-group. Each thread owns
+// four consecutive columns and issues all its loads (the raw row, the older
+// raw rows of the taps, the tap weights) before using any, so a wave keeps
+// its whole working set in flight. The per-head sum of squares is a
+// sequential walk by one thread per head (the reference's order); the emit is
+// one (head, rotary pair) per thread. Store mode then writes the k/v rows
+// into the KV pages exactly as the append kernel does (int8 with the engine's
+// Markstein store, or fp16), so the decode launch that follows reads them
+// from the cache.
 //
 // Every multiply and add rounds on its own (no contraction) and divide / sqrt
 // are correctly rounded, so the results are bit-identical to the engine's
 // host build, and so are the int8 codes computed from them.
 #include "nda_device.h"
 
+#include <algorithm>
+
 namespace nda {
 
-namespace {
-
-// LDS layout: the q and k heads' convolution outputs, one row of qk+1 floats
-// per head (the pad keeps the one-head-per-thread column walk free of bank
-// conflicts), then v, then one inverse RMS per q/k head.
-struct FrontLds {
-    uint32_t stride, nqk, v_off, inv_off, total;
+template <int DK, int DV, int REP>
+struct FrontShape {
+    static constexpr int NC = REP * DK + DK + DV;   // columns of one kv group
+    static constexpr int NG = NC / 4;               // four-column groups, one per thread
+    static constexpr int W = (NG + 63) / 64;        // waves per work-group
+    static constexpr int NH = REP + 1;              // normalised heads: REP q + 1 k
+    static constexpr int STRIDE = DK + 4;           // LDS row: 16-byte aligned, banks spread
+    static constexpr int HALF = DK / 2;
+    static constexpr int TREG = 4;                  // taps held in registers; more are streamed
+    static_assert(DK % 4 == 0 && DV % 4 == 0, "four-column groups");
+    static_assert(W <= 4, "one group per thread");
 };
 
-__host__ __device__ inline FrontLds front_lds(uint32_t nh, uint32_t nkv, uint32_t qk, uint32_t vd)
-{
-    FrontLds l;
-    l.stride = qk + 1;
-    l.nqk = nh + nkv;
-    l.v_off = l.nqk * l.stride;
-    l.inv_off = l.v_off + nkv * vd;
-    l.total = l.inv_off + l.nqk;
-    return l;
-}
+__device__ __forceinline__ float4 ld4(const float *p) { return *reinterpret_cast<const float4 *>(p); }
 
-} // namespace
-
-template <int ES, int DK, int DV>
-__global__ __launch_bounds__(256) void front_kernel(FrontArgs a)
+__device__ __forceinline__ void acc4(float4 &a, const float4 &w, const float4 &x)
 {
 #pragma clang fp contract(off)
-    extern __shared__ float lds[];
-    const uint32_t row = blockIdx.x;
-    const uint32_t tid = threadIdx.x;
+    a.x = a.x + w.x * x.x;
+    a.y = a.y + w.y * x.y;
+    a.z = a.z + w.z * x.z;
+    a.w = a.w + w.w * x.w;
+}
+
+template <int ES, int DK, int DV, int REP>
+__global__ __launch_bounds__((64 * FrontShape<DK, DV, REP>::W)) void front_kernel(FrontArgs a)
+{
+#pragma clang fp contract(off)
+    using S = FrontShape<DK, DV, REP>;
+    __shared__ __align__(16) float ylds[S::NH * S::STRIDE];   // conv outputs of the q/k heads
+    __shared__ __align__(16) float sqlds[S::NH * S::STRIDE];  // their squares
+    __shared__ __align__(16) float vlds[DV];
+    __shared__ float invlds[S::NH];
+
+    const uint32_t nkv = a.nkv;
+    const uint32_t row = blockIdx.x / nkv, g = blockIdx.x % nkv;
+    const int tid = threadIdx.x;
     const uint32_t seq = a.row_seq ? a.row_seq[row] : row;
     const uint32_t t = a.row_t ? a.row_t[row] : 0u;
     const SeqDev sd = a.seqs[seq];
     const uint32_t pos = (uint32_t)sd.pos + t;
     const uint32_t taps = a.taps;
     const uint32_t nt = min(taps, pos + 1u);
-    const uint32_t nh = a.nh, nkv = a.nkv;
-    const uint32_t dq = nh * DK, dk = nkv * DK, dv = nkv * DV, dcol = dq + dk + dv;
-    const FrontLds L = front_lds(nh, nkv, DK, DV);
+    const uint32_t dq = nkv * REP * DK, dk = nkv * DK, dv = nkv * DV, dcol = dq + dk + dv;
     float *hist = a.hist + ((uint64_t)seq * a.n_layers + a.layer) * taps * dcol;
     const bool store = a.k_out == nullptr;
 
-    // 1. tap convolution, one column per thread
-    for (uint32_t c = tid; c < dcol; c += 256) {
-        const float *src;
-        uint32_t cc, ld;
-        if (c < dq) {
-            src = a.q; cc = c; ld = dq;
-        } else if (c < dq + dk) {
-            src = a.k; cc = c - dq; ld = dk;
-        } else {
-            src = a.v; cc = c - dq - dk; ld = dv;
+    // 1. tap convolution of this thread's four columns
+    const bool active = tid < S::NG;
+    const int lc = tid * 4;                      // column within the group
+    const float *src;
+    uint32_t ld, cc, gc;                         // source row length, column in it, column in dcol
+    if (lc < REP * DK) {
+        src = a.q; ld = dq; cc = g * REP * DK + lc; gc = cc;
+    } else if (lc < REP * DK + DK) {
+        src = a.k; ld = dk; cc = g * DK + (lc - REP * DK); gc = dq + cc;
+    } else {
+        src = a.v; ld = dv; cc = g * DV + (lc - REP * DK - DK); gc = dq + dk + cc;
+    }
+    float4 acc = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    float4 raw = acc;
+    if (active) {
+        float4 x[S::TREG], w[S::TREG];
+        raw = ld4(src + (uint64_t)row * ld + cc);
+#pragma unroll
+        for (int j = 0; j < S::TREG; j++) {
+            if ((uint32_t)j < nt) {
+                w[j] = ld4(a.w + (uint64_t)j * dcol + gc);
+                if (j == 0)
+                    x[j] = raw;
+                else if ((uint32_t)j <= t)
+                    x[j] = ld4(src + (uint64_t)(row - j) * ld + cc);
+                else
+                    x[j] = ld4(hist + (uint64_t)((pos - j) % taps) * dcol + gc);
+            }
         }
-        const float raw = src[(uint64_t)row * ld + cc];
-        float acc = 0.0f;
-        for (uint32_t j = 0; j < nt; j++) {
-            float x;
-            if (j == 0)
-                x = raw;
-            else if (j <= t)
-                x = src[(uint64_t)(row - j) * ld + cc];
-            else
-                x = hist[(uint64_t)((pos - j) % taps) * dcol + c];
-            acc = acc + a.w[(uint64_t)j * dcol + c] * x;
+#pragma unroll
+        for (int j = 0; j < S::TREG; j++)
+            if ((uint32_t)j < nt)
+                acc4(acc, w[j], x[j]);
+        for (uint32_t j = S::TREG; j < nt; j++) {
+            const float4 wj = ld4(a.w + (uint64_t)j * dcol + gc);
+            const float4 xj = j <= t ? ld4(src + (uint64_t)(row - j) * ld + cc)
+                                     : ld4(hist + (uint64_t)((pos - j) % taps) * dcol + gc);
+            acc4(acc, wj, xj);
         }
         if (a.hist_write)
-            hist[(uint64_t)(pos % taps) * dcol + c] = raw;
-        if (c < dq + dk) {
-            lds[(c / DK) * L.stride + (c % DK)] = acc;
+            *reinterpret_cast<float4 *>(hist + (uint64_t)(pos % taps) * dcol + gc) = raw;
+        if (lc < (REP + 1) * DK) {
+            const int o = (lc / DK) * S::STRIDE + lc % DK;
+            *reinterpret_cast<float4 *>(ylds + o) = acc;
+            *reinterpret_cast<float4 *>(sqlds + o) =
+                make_float4(acc.x * acc.x, acc.y * acc.y, acc.z * acc.z, acc.w * acc.w);
         } else if (store) {
-            lds[L.v_off + cc] = acc;
+            *reinterpret_cast<float4 *>(vlds + (lc - (REP + 1) * DK)) = acc;
         } else {
-            a.v_out[(uint64_t)row * dv + cc] = acc;
+            *reinterpret_cast<float4 *>(a.v_out + (uint64_t)row * dv + cc) = acc;
         }
     }
     __syncthreads();
 
     // 2. per-head sum of squares in index order, inverse RMS
-    for (uint32_t h = tid; h < L.nqk; h += 256) {
-        const float *r = lds + h * L.stride;
+    if (tid < S::NH) {
+        const float *r = sqlds + tid * S::STRIDE;
         float ss = 0.0f;
-#pragma unroll 8
-        for (uint32_t i = 0; i < DK; i++)
-            ss = ss + r[i] * r[i];
-        lds[L.inv_off + h] = 1.0f / __builtin_sqrtf(ss / (float)DK + 1e-6f);
+#pragma unroll
+        for (int i = 0; i < DK; i++)
+            ss = ss + r[i];
+        invlds[tid] = 1.0f / __builtin_sqrtf(ss / (float)DK + 1e-6f);
     }
     __syncthreads();
 
     // 3. (1 + s) * x * inv, rotated by the position's (cos, sin)
-    constexpr uint32_t HALF = DK / 2;
-    const float2 *rope = a.rope + (uint64_t)pos * HALF;
-    for (uint32_t e = tid; e < L.nqk * HALF; e += 256) {
-        const uint32_t h = e / HALF, i = e % HALF;
-        const bool is_q = h < nh;
+    const float2 *rope = a.rope + (uint64_t)pos * S::HALF;
+    for (int e = tid; e < S::NH * S::HALF; e += 64 * S::W) {
+        const int h = e / S::HALF, i = e % S::HALF;
+        const bool is_q = h < REP;
         const float *s = a.norm + (is_q ? 0 : DK);
-        float *r = lds + h * L.stride;
-        const float iv = lds[L.inv_off + h];
+        float *r = ylds + h * S::STRIDE;
+        const float iv = invlds[h];
         const float x1 = (1.0f + s[i]) * r[i] * iv;
-        const float x2 = (1.0f + s[i + HALF]) * r[i + HALF] * iv;
+        const float x2 = (1.0f + s[i + S::HALF]) * r[i + S::HALF] * iv;
         const float2 cs = rope[i];
         const float o1 = x1 * cs.x - x2 * cs.y;
         const float o2 = x2 * cs.x + x1 * cs.y;
         if (is_q) {
-            float *qo = a.q_out + (uint64_t)row * dq + h * DK;
+            float *qo = a.q_out + (uint64_t)row * dq + (g * REP + h) * DK;
             qo[i] = o1;
-            qo[i + HALF] = o2;
+            qo[i + S::HALF] = o2;
         } else if (store) {
             r[i] = o1;
-            r[i + HALF] = o2;
+            r[i + S::HALF] = o2;
         } else {
-            float *ko = a.k_out + (uint64_t)row * dk + (h - nh) * DK;
+            float *ko = a.k_out + (uint64_t)row * dk + g * DK;
             ko[i] = o1;
-            ko[i + HALF] = o2;
+            ko[i + S::HALF] = o2;
         }
     }
     if (!store)
         return;
     __syncthreads();
 
-    // 4. store this position's k/v rows (one wave per kv-head)
+    // 4. store this position's k/v rows of kv-head g (wave 0, lane = element)
+    if (tid >= 64)
+        return;
     const int slot = own_slot(sd, (int)pos, (int)a.pg.window);
     const int P = 1 << a.pg.log2_page;
     const int32_t page = a.page_table[(uint64_t)seq * a.pg.pages_per_seq + (slot >> a.pg.log2_page)];
     if (page < 0)
         return;   // the host backs every stored slot; never taken
-    const int off = slot & (P - 1);
-    const int lane = tid & 63;
-    for (uint32_t g = tid >> 6; g < nkv; g += 4) {
-        uint8_t *hb = a.pool + (uint64_t)page * a.pg.page_bytes + (uint64_t)g * a.pg.head_bytes;
-        const float kx = lane < DK ? lds[(nh + g) * L.stride + lane] : 0.0f;
-        const float vx = lane < DV ? lds[L.v_off + g * DV + lane] : 0.0f;
-        store_row<ES, DK, DV>(hb, off, P, kx, vx, lane);
-    }
+    uint8_t *hb = a.pool + (uint64_t)page * a.pg.page_bytes + (uint64_t)g * a.pg.head_bytes;
+    const float kx = tid < DK ? ylds[REP * S::STRIDE + tid] : 0.0f;
+    const float vx = tid < DV ? vlds[tid] : 0.0f;
+    store_row<ES, DK, DV>(hb, slot & (P - 1), P, kx, vx, tid);
 }
 
 // Raw rows of each sequence's last `taps` tokens into their history slots,
@@ -194,24 +222,18 @@ __global__ __launch_bounds__(256) void hist_ops_kernel(const HistOp *ops, uint64
         d[i] = s ? s[i] : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
 }
 
-size_t front_lds_bytes(const FrontArgs &a)
-{
-    return (size_t)front_lds(a.nh, a.nkv, a.qk, a.vd).total * sizeof(float);
-}
-
-#define NDA_FRONT_SHAPES(X) X(2, 64, 64) X(2, 48, 64) X(1, 64, 64) X(1, 48, 64)
-
 hipError_t launch_front(const Geo &g, const FrontArgs &a, hipStream_t s)
 {
     if (a.rows == 0)
         return hipSuccess;
-    const size_t lds = front_lds_bytes(a);
-#define X(ES, DK, DV)                                                                          \
-    if ((g.kv_f16 ? 2 : 1) == ES && g.dk == DK && g.dv == DV) {                               \
-        hipLaunchKernelGGL((front_kernel<ES, DK, DV>), dim3(a.rows), dim3(256), lds, s, a);    \
-        return hipGetLastError();                                                              \
+    const dim3 grid(a.rows * a.nkv);
+#define X(ES, DK, DV, REP)                                                                      \
+    if ((g.kv_f16 ? 2 : 1) == ES && g.dk == DK && g.dv == DV && g.rep == REP) {                \
+        hipLaunchKernelGGL((front_kernel<ES, DK, DV, REP>), grid, dim3((64 * FrontShape<DK, DV, REP>::W)), \
+                           0, s, a);                                                            \
+        return hipGetLastError();                                                               \
     }
-    NDA_FRONT_SHAPES(X)
+    NDA_FOR_GEOMETRIES(X)
 #undef X
     return hipErrorNotSupported;
 }

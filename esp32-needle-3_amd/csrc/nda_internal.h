@@ -161,6 +161,13 @@ struct HistTailArgs {
     uint32_t rows, layer, n_layers, taps, dq, dk, dv;
 };
 
+/* Compiled geometries: (KV element bytes, qk_head_dim, v_head_dim, GQA rep). */
+#define NDA_FOR_GEOMETRIES(X) \
+    X(2, 64, 64, 1) X(2, 64, 64, 2) X(2, 64, 64, 4) X(2, 64, 64, 6) X(2, 64, 64, 8) \
+    X(2, 48, 64, 1) X(2, 48, 64, 2) X(2, 48, 64, 6) \
+    X(1, 64, 64, 1) X(1, 64, 64, 2) X(1, 64, 64, 4) X(1, 64, 64, 6) X(1, 64, 64, 8) \
+    X(1, 48, 64, 1) X(1, 48, 64, 2) X(1, 48, 64, 6)
+
 /* Kernel geometry key. */
 struct Geo {
     int kv_f16;
@@ -186,6 +193,5 @@ bool geometry_supported(const Geo &g);
 hipError_t launch_front(const Geo &g, const FrontArgs &a, hipStream_t s);
 hipError_t launch_hist_tail(const HistTailArgs &a, hipStream_t s);
 hipError_t launch_hist_ops(const HistOp *d_ops, uint32_t n_ops, uint64_t block_floats, hipStream_t s);
-size_t front_lds_bytes(const FrontArgs &a);
 
 } // namespace nda

@@ -648,12 +648,6 @@ constexpr int att_np()
 #endif
 }
 
-#define NDA_FOR_GEOMETRIES(X) \
-    X(2, 64, 64, 1) X(2, 64, 64, 2) X(2, 64, 64, 4) X(2, 64, 64, 6) X(2, 64, 64, 8) \
-    X(2, 48, 64, 1) X(2, 48, 64, 2) X(2, 48, 64, 6) \
-    X(1, 64, 64, 1) X(1, 64, 64, 2) X(1, 64, 64, 4) X(1, 64, 64, 6) X(1, 64, 64, 8) \
-    X(1, 48, 64, 1) X(1, 48, 64, 2) X(1, 48, 64, 6)
-
 static inline int es_of(const Geo &g) { return g.kv_f16 ? 2 : 1; }
 
 bool geometry_supported(const Geo &g)
