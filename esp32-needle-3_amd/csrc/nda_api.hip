@@ -497,7 +497,10 @@ int upload_rows(nda_ctx *c, uint32_t rows, const uint32_t *row_seq, const uint32
 // Split-KV size for a launch. With enough (row, kv-head) units to fill the
 // chip many times over, rows are not split (no partials, no merge); with few
 // units, rows are cut into chunks so that ~64 work items per CU balance the
-// ragged lengths. A fixed split_chunk in the config overrides this.
+// ragged lengths, but never below 1024 positions, where the merge launch
+// would cost more than the split saves (one engine session at a few hundred
+// positions runs as one launch). A fixed split_chunk in the config overrides
+// this.
 uint32_t pick_chunk(const nda_ctx *c, uint64_t units, uint64_t sum_total, uint32_t max_total)
 {
     if (c->chunk)
@@ -507,7 +510,7 @@ uint32_t pick_chunk(const nda_ctx *c, uint64_t units, uint64_t sum_total, uint32
     if (units >= 16 * cus)
         ch = std::max<uint64_t>(max_total, 64);
     else
-        ch = std::max<uint64_t>(256, (sum_total * c->cfg.n_kv_heads / (64 * cus) + 63) / 64 * 64);
+        ch = std::max<uint64_t>(1024, (sum_total * c->cfg.n_kv_heads / (64 * cus) + 63) / 64 * 64);
     // grid.y bound
     const uint64_t min_ch = ((uint64_t)max_total + 65534) / 65535;
     ch = std::max(ch, min_ch);
@@ -1700,6 +1703,30 @@ int nda_h2d(void *dst, const void *src, size_t bytes)
 int nda_d2h(void *dst, const void *src, size_t bytes)
 {
     return hipMemcpy(dst, src, bytes, hipMemcpyDeviceToHost) == hipSuccess ? NDA_OK : NDA_ERR_HIP;
+}
+
+int nda_host_alloc(void **ptr, size_t bytes)
+{
+    if (!ptr)
+        return NDA_ERR_ARG;
+    hipError_t e = hipHostMalloc(ptr, bytes ? bytes : 1, hipHostMallocDefault);
+    return e == hipSuccess ? NDA_OK : (e == hipErrorOutOfMemory ? NDA_ERR_NOMEM : NDA_ERR_HIP);
+}
+
+int nda_host_free(void *ptr) { return hipHostFree(ptr) == hipSuccess ? NDA_OK : NDA_ERR_HIP; }
+
+int nda_h2d_async(void *dst, const void *src, size_t bytes, void *stream)
+{
+    return hipMemcpyAsync(dst, src, bytes, hipMemcpyHostToDevice, (hipStream_t)stream) == hipSuccess
+               ? NDA_OK
+               : NDA_ERR_HIP;
+}
+
+int nda_d2h_async(void *dst, const void *src, size_t bytes, void *stream)
+{
+    return hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToHost, (hipStream_t)stream) == hipSuccess
+               ? NDA_OK
+               : NDA_ERR_HIP;
 }
 
 int nda_d2d(void *dst, const void *src, size_t bytes, void *stream)

@@ -21,8 +21,12 @@ struct nd_gpu_model {
      * them; released once the session detaches. */
     int32_t orphan[64];
     uint32_t n_orphan;
-    /* device staging for one token */
-    float *d_q, *d_k, *d_v, *d_gate, *d_out;
+    /* One token's q | k | v | gate, staged through page-locked host memory
+     * in one copy each way; d_q.. point into d_in. */
+    float *d_in, *d_q, *d_k, *d_v, *d_gate, *d_out;
+    float *h_in, *h_out;
+    size_t nq, nk, nv, ng;       /* floats */
+    void *stream;
 };
 
 struct nd_gpu_prefix {
@@ -60,14 +64,23 @@ nd_gpu_model *nd_gpu_open(uint32_t n_layers, uint32_t n_heads, uint32_t n_kv_hea
     m->v_hd = v_head_dim;
     m->window = window;
     m->snap_prefix = -1;
-    if (nda_dev_alloc((void **)&m->d_q, sizeof(float) * n_heads * qk_head_dim) ||
-        nda_dev_alloc((void **)&m->d_k, sizeof(float) * n_kv_heads * qk_head_dim) ||
-        nda_dev_alloc((void **)&m->d_v, sizeof(float) * n_kv_heads * v_head_dim) ||
-        nda_dev_alloc((void **)&m->d_gate, sizeof(float) * n_heads * v_head_dim) ||
-        nda_dev_alloc((void **)&m->d_out, sizeof(float) * n_heads * v_head_dim)) {
+    /* each part rounded to 4 floats keeps every part 16-byte aligned */
+    m->nq = ((size_t)n_heads * qk_head_dim + 3) & ~(size_t)3;
+    m->nk = ((size_t)n_kv_heads * qk_head_dim + 3) & ~(size_t)3;
+    m->nv = ((size_t)n_kv_heads * v_head_dim + 3) & ~(size_t)3;
+    m->ng = ((size_t)n_heads * v_head_dim + 3) & ~(size_t)3;
+    if (nda_stream_create(&m->stream) ||
+        nda_dev_alloc((void **)&m->d_in, sizeof(float) * (m->nq + m->nk + m->nv + m->ng)) ||
+        nda_dev_alloc((void **)&m->d_out, sizeof(float) * m->ng) ||
+        nda_host_alloc((void **)&m->h_in, sizeof(float) * (m->nq + m->nk + m->nv + m->ng)) ||
+        nda_host_alloc((void **)&m->h_out, sizeof(float) * m->ng)) {
         nd_gpu_close(m);
         return NULL;
     }
+    m->d_q = m->d_in;
+    m->d_k = m->d_q + m->nq;
+    m->d_v = m->d_k + m->nk;
+    m->d_gate = m->d_v + m->nv;
     return m;
 }
 
@@ -75,12 +88,17 @@ void nd_gpu_close(nd_gpu_model *m)
 {
     if (!m)
         return;
-    nda_dev_free(m->d_q);
-    nda_dev_free(m->d_k);
-    nda_dev_free(m->d_v);
-    nda_dev_free(m->d_gate);
-    nda_dev_free(m->d_out);
+    if (m->d_in)
+        nda_dev_free(m->d_in);
+    if (m->d_out)
+        nda_dev_free(m->d_out);
+    if (m->h_in)
+        nda_host_free(m->h_in);
+    if (m->h_out)
+        nda_host_free(m->h_out);
     nda_destroy(m->ctx);
+    if (m->stream)
+        nda_stream_destroy(m->stream);
     free(m);
 }
 
@@ -140,9 +158,9 @@ int nd_gpu_snapshot(nd_gpu_model *m)
 {
     int32_t id = -1;
     int32_t old = m->snap_prefix;
-    if (nda_prefix_build(m->ctx, 0, &id, NULL) != NDA_OK)
+    if (nda_prefix_build(m->ctx, 0, &id, m->stream) != NDA_OK)
         return -1;
-    if (nda_seq_attach(m->ctx, 0, id, NULL) != NDA_OK) {
+    if (nda_seq_attach(m->ctx, 0, id, m->stream) != NDA_OK) {
         nda_prefix_free(m->ctx, id);
         return -1;
     }
@@ -184,7 +202,7 @@ int nd_gpu_prefix_restore(nd_gpu_model *m, const nd_gpu_prefix *p)
     if (!p || p->owner != m)
         return -1;
     old = m->snap_prefix;
-    if (nda_seq_attach(m->ctx, 0, p->segment, NULL) != NDA_OK)
+    if (nda_seq_attach(m->ctx, 0, p->segment, m->stream) != NDA_OK)
         return -1;
     if (old != p->segment)
         orphan(m, old);
@@ -204,24 +222,45 @@ void nd_gpu_prefix_free(nd_gpu_prefix *p)
     free(p);
 }
 
+/* One layer call on host arrays: stage q | k | v | gate into page-locked
+ * memory, one copy in, the launches, one copy out, one wait. raw selects the
+ * front (raw projections) or the post-front entry. */
+static int attend_host(nd_gpu_model *m, int raw, uint32_t li, const float *q, const float *k,
+                       const float *v, const float *gate, float *out)
+{
+    size_t n = m->nq + m->nk + m->nv + (gate ? m->ng : 0);
+    size_t vh = (size_t)m->nh * m->v_hd;
+    int rc;
+    memcpy(m->h_in, q, sizeof(float) * m->nh * m->qk_hd);
+    memcpy(m->h_in + m->nq, k, sizeof(float) * m->nkv * m->qk_hd);
+    memcpy(m->h_in + m->nq + m->nk, v, sizeof(float) * m->nkv * m->v_hd);
+    if (gate)
+        memcpy(m->h_in + m->nq + m->nk + m->nv, gate, sizeof(float) * vh);
+    rc = nda_h2d_async(m->d_in, m->h_in, sizeof(float) * n, m->stream);
+    if (rc)
+        return rc;
+    if (raw)
+        rc = nda_attention(m->ctx, li, 1, NULL, m->d_q, m->d_k, m->d_v, gate ? m->d_gate : NULL,
+                           m->d_out, m->stream);
+    else
+        rc = nda_step(m->ctx, li, 1, NULL, m->d_q, m->d_k, m->d_v, gate ? m->d_gate : NULL,
+                      m->d_out, m->stream);
+    if (rc)
+        return rc;
+    rc = nda_d2h_async(m->h_out, m->d_out, sizeof(float) * vh, m->stream);
+    if (rc)
+        return rc;
+    rc = nda_sync(m->ctx, m->stream);
+    if (rc)
+        return rc;
+    memcpy(out, m->h_out, sizeof(float) * vh);
+    return 0;
+}
+
 int nd_gpu_attention(nd_gpu_model *m, uint32_t li, const float *q, const float *k,
                      const float *v, const float *gate, float *out)
 {
-    int rc;
-    if (nda_h2d(m->d_q, q, sizeof(float) * m->nh * m->qk_hd) ||
-        nda_h2d(m->d_k, k, sizeof(float) * m->nkv * m->qk_hd) ||
-        nda_h2d(m->d_v, v, sizeof(float) * m->nkv * m->v_hd))
-        return NDA_ERR_HIP;
-    if (gate && nda_h2d(m->d_gate, gate, sizeof(float) * m->nh * m->v_hd))
-        return NDA_ERR_HIP;
-    rc = nda_step(m->ctx, li, 1, NULL, m->d_q, m->d_k, m->d_v, gate ? m->d_gate : NULL,
-                  m->d_out, NULL);
-    if (rc)
-        return rc;
-    rc = nda_sync(m->ctx, NULL);
-    if (rc)
-        return rc;
-    return nda_d2h(out, m->d_out, sizeof(float) * m->nh * m->v_hd);
+    return attend_host(m, 0, li, q, k, v, gate, out);
 }
 
 int nd_gpu_front_init(nd_gpu_model *m, uint32_t taps, float rope_theta, uint32_t max_pos)
@@ -242,24 +281,10 @@ int nd_gpu_front_weights(nd_gpu_model *m, uint32_t li, const float *tap_q, const
 int nd_gpu_attention_raw(nd_gpu_model *m, uint32_t li, const float *q, const float *k,
                          const float *v, const float *gate, float *out)
 {
-    int rc;
-    if (nda_h2d(m->d_q, q, sizeof(float) * m->nh * m->qk_hd) ||
-        nda_h2d(m->d_k, k, sizeof(float) * m->nkv * m->qk_hd) ||
-        nda_h2d(m->d_v, v, sizeof(float) * m->nkv * m->v_hd))
-        return NDA_ERR_HIP;
-    if (gate && nda_h2d(m->d_gate, gate, sizeof(float) * m->nh * m->v_hd))
-        return NDA_ERR_HIP;
-    rc = nda_attention(m->ctx, li, 1, NULL, m->d_q, m->d_k, m->d_v, gate ? m->d_gate : NULL,
-                       m->d_out, NULL);
-    if (rc)
-        return rc;
-    rc = nda_sync(m->ctx, NULL);
-    if (rc)
-        return rc;
-    return nda_d2h(out, m->d_out, sizeof(float) * m->nh * m->v_hd);
+    return attend_host(m, 1, li, q, k, v, gate, out);
 }
 
 void nd_gpu_step_end(nd_gpu_model *m)
 {
-    nda_advance(m->ctx, 1, NULL, 1, NULL);
+    nda_advance(m->ctx, 1, NULL, 1, m->stream);
 }

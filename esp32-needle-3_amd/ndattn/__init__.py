@@ -32,6 +32,7 @@ ABI_SYMBOLS = [
     "nda_kv_append", "nda_decode", "nda_step", "nda_prefill", "nda_sync",
     "nda_kv_read", "nda_kv_write", "nda_kv_fill_normal",
     "nda_dev_alloc", "nda_dev_free", "nda_h2d", "nda_d2h", "nda_d2d", "nda_memset", "nda_fill_normal",
+    "nda_host_alloc", "nda_host_free", "nda_h2d_async", "nda_d2h_async",
     "nda_stream_create", "nda_stream_destroy", "nda_device_sync", "nda_device_info",
     "nda_prof_enable", "nda_prof_read",
     "nda_front_init", "nda_front_weights", "nda_front", "nda_attention", "nda_front_hist",
@@ -103,6 +104,10 @@ def lib():
             "nda_d2h": (C.c_int, [vp, vp, C.c_size_t]),
             "nda_memset": (C.c_int, [vp, C.c_int, C.c_size_t]),
             "nda_d2d": (C.c_int, [vp, vp, C.c_size_t, vp]),
+            "nda_host_alloc": (C.c_int, [C.POINTER(vp), C.c_size_t]),
+            "nda_host_free": (C.c_int, [vp]),
+            "nda_h2d_async": (C.c_int, [vp, vp, C.c_size_t, vp]),
+            "nda_d2h_async": (C.c_int, [vp, vp, C.c_size_t, vp]),
             "nda_fill_normal": (C.c_int, [vp, u64, C.c_int, u64, C.c_float, vp]),
             "nda_stream_create": (C.c_int, [C.POINTER(vp)]),
             "nda_stream_destroy": (C.c_int, [vp]),

@@ -233,6 +233,12 @@ int nda_dev_free(void *ptr);
 int nda_h2d(void *dst, const void *src, size_t bytes);
 int nda_d2h(void *dst, const void *src, size_t bytes);
 int nda_memset(void *dst, int value, size_t bytes);
+/* Page-locked host memory, and stream-ordered copies to / from it (from
+ * pageable memory they complete before returning). */
+int nda_host_alloc(void **ptr, size_t bytes);
+int nda_host_free(void *ptr);
+int nda_h2d_async(void *dst, const void *src, size_t bytes, void *stream);
+int nda_d2h_async(void *dst, const void *src, size_t bytes, void *stream);
 /* Device-to-device copy on a stream (also the known-size copy used to
  * calibrate memory-traffic counters). */
 int nda_d2d(void *dst, const void *src, size_t bytes, void *stream);
