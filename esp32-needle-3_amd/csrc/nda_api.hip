@@ -406,6 +406,8 @@ int check_ids(nda_ctx *c, uint32_t nseq, const uint32_t *ids)
 
 inline uint32_t sid(const uint32_t *ids, uint32_t b) { return ids ? ids[b] : b; }
 
+inline bool aligned16(const void *p) { return ((uintptr_t)p & 15) == 0; }
+
 // ---- tap histories of the attention front ----
 
 float *hist_live(nda_ctx *c, uint32_t seq) { return c->d_hist + (uint64_t)seq * c->hist_block; }
@@ -1093,6 +1095,8 @@ int nda_prefill(nda_ctx *c, uint32_t layer, uint32_t nseq, const uint32_t *ids, 
 {
     if (!c || (nseq && (!n_tokens || !q || !k || !v || !out)))
         return c ? fail(c, NDA_ERR_ARG, "null argument") : NDA_ERR_ARG;
+    if (!aligned16(q) || !aligned16(out))
+        return fail(c, NDA_ERR_ARG, "q and out must be 16-byte aligned");
     if (layer >= c->cfg.n_layers)
         return fail(c, NDA_ERR_ARG, "layer %u out of range", layer);
     if (int rc = check_ids(c, nseq, ids))
@@ -1317,8 +1321,6 @@ int nda_front_weights(nda_ctx *c, uint32_t layer, const float *tap_q, const floa
 }
 
 namespace {
-
-inline bool aligned16(const void *p) { return ((uintptr_t)p & 15) == 0; }
 
 // Checks shared by the front entry points: initialised, weights present,
 // each sequence at most once, every position inside the rotary table.

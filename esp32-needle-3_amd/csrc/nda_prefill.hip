@@ -117,16 +117,35 @@ void prefill_kernel(PrefillArgs a)
     const int qpos = pos + tok;                 // keys [0, qpos] visible
     const uint64_t qrow = (uint64_t)(a.btok0[b] + tok) * a.nh + h;
 
-    // Q^T operand, hi and lo halves, slots = dims 16*kb + 8*jh + s
+    // Q^T operand, hi and lo halves, slots = dims 16*kb + 8*jh + s: eight
+    // consecutive floats per k-block, loaded as two float4 (all issued
+    // before any is used; rows past the chunk read row 0 and are zeroed).
     half8 qh[NKB], ql[NKB];
+    {
+        const float *qr = a.q + (rvalid ? qrow : (uint64_t)a.btok0[b] * a.nh + (int)g * REP) * DK + 8 * jh;
+        float4 qv[NKB][2];
 #pragma unroll
-    for (int kb = 0; kb < NKB; kb++) {
+        for (int kb = 0; kb < NKB; kb++) {
+            qv[kb][0] = *reinterpret_cast<const float4 *>(qr + 16 * kb);
+            qv[kb][1] = *reinterpret_cast<const float4 *>(qr + 16 * kb + 4);
+        }
+        const float qs = rvalid ? a.qscale : 0.0f;
 #pragma unroll
-        for (int s = 0; s < 8; s++) {
-            const float x = rvalid ? a.q[qrow * DK + 16 * kb + 8 * jh + s] * a.qscale : 0.0f;
-            const _Float16 hi = (_Float16)x;
-            qh[kb][s] = hi;
-            ql[kb][s] = (_Float16)(x - (float)hi);
+        for (int kb = 0; kb < NKB; kb++) {
+            const float xs[8] = {qv[kb][0].x, qv[kb][0].y, qv[kb][0].z, qv[kb][0].w,
+                                 qv[kb][1].x, qv[kb][1].y, qv[kb][1].z, qv[kb][1].w};
+#pragma unroll
+            for (int s = 0; s < 8; s++) {
+                // hi and lo must both derive from the one rounded fp32 x;
+                // the empty asm keeps the compiler from rounding the exact
+                // product straight to fp16 for one of them (fused
+                // multiply-convert), which would pair lo with another hi
+                float x = xs[s] * qs;
+                asm volatile("" : "+v"(x));
+                const _Float16 hi = (_Float16)x;
+                qh[kb][s] = hi;
+                ql[kb][s] = (_Float16)(x - (float)hi);
+            }
         }
     }
 
@@ -252,13 +271,15 @@ void prefill_kernel(PrefillArgs a)
     // unmasked loop carries no diagonal-mask code at all.
     auto tile = [&](const int kt, const bool masked) __attribute__((always_inline)) {
         const bool more = kt + PF_KT < kmax;
+        // No `more` guard on the loads: page ids past kmax are -1, so such a
+        // tile loads nothing, and every path waits for the page ids at the
+        // same point (a guarded load left a path on which the wait moved
+        // behind the just-issued tile load).
         if constexpr (PD == 2) {
-            if (kt + 2 * PF_KT < kmax)
-                load_tile(pr2, sg2);        // tile kt+64
+            load_tile(pr2, sg2);            // tile kt+64
             fetch_pages(kt + 3 * PF_KT, pr3);
         } else {
-            if (more)
-                load_tile(pr2, sg1);        // tile kt+32
+            load_tile(pr2, sg1);            // tile kt+32
             fetch_pages(kt + 2 * PF_KT, pr3);
         }
         const _Float16 (*Ks)[T::KPAD] = Ks2[cur];

@@ -152,7 +152,7 @@ int nda_step(nda_ctx *ctx, uint32_t layer, uint32_t nseq, const uint32_t *seq_id
  * sum(n_tokens[0..b)): q [T][n_heads][qk_head_dim], k [T][n_kv_heads][qk_head_dim],
  * v [T][n_kv_heads][v_head_dim], gate/out [T][n_heads][v_head_dim].
  * Requires pos + n <= window (no ring wrap inside the chunk): NDA_ERR_RANGE
- * otherwise. Does not advance pos. */
+ * otherwise; q and out 16-byte aligned (NDA_ERR_ARG). Does not advance pos. */
 int nda_prefill(nda_ctx *ctx, uint32_t layer, uint32_t nseq, const uint32_t *seq_ids,
                 const uint32_t *n_tokens, const float *q, const float *k, const float *v,
                 const float *gate, float *out, void *stream);
