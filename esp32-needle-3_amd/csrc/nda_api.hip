@@ -1179,6 +1179,9 @@ int nda_prefill(nda_ctx *c, uint32_t layer, uint32_t nseq, const uint32_t *ids, 
     int waves = max_rows <= 64 ? 2 : (max_rows >= 256 ? 8 : 4);
     if (waves == 8 && !(c->geo.kv_f16 && c->geo.rep == 1))
         waves = 4;
+#ifdef NDA_PF_FORCE_W     // build-time tuning knob: one work-group size for every chunk
+    waves = NDA_PF_FORCE_W;
+#endif
     const uint32_t trows = 32u * waves;
     std::vector<uint32_t> host(3 * (size_t)nseq);
     std::vector<uint32_t> items;
