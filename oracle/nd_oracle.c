@@ -756,6 +756,140 @@ void ndo_front(ndo_session *s, uint32_t li, const ndo_front_w *w, float *q, floa
     ndo_zcrms_heads(k, s->nkv, s->qk_hd, w->norm_k, cs, sn);
 }
 
+/* --------------------------------------------------------- CQ projections */
+
+uint32_t ndo_cq_in_pad(uint32_t in, uint32_t group) { return (in + group - 1) / group * group; }
+
+void ndo_fwht(float *x, uint32_t n)
+{
+    uint32_t len, i, j;
+    for (len = 1; len < n; len <<= 1)
+        for (i = 0; i < n; i += len << 1)
+            for (j = i; j < i + len; j++) {
+                float a = x[j], b = x[j + len];
+                x[j] = a + b;
+                x[j + len] = a - b;
+            }
+}
+
+void ndo_cq_prepare(uint32_t in, uint32_t group, const float *x, float *xh)
+{
+    uint32_t in_pad = ndo_cq_in_pad(in, group), gi, j;
+    float scale = 1.0f / sqrtf((float)group);
+    memcpy(xh, x, sizeof(float) * in);
+    memset(xh + in, 0, sizeof(float) * (in_pad - in));
+    for (gi = 0; gi < in_pad / group; gi++) {
+        float *blk = xh + (size_t)gi * group;
+        ndo_fwht(blk, group);
+        for (j = 0; j < group; j++)
+            blk[j] = blk[j] * scale;
+    }
+}
+
+static uint32_t load_u32le(const uint8_t *p)
+{
+    return (uint32_t)p[0] | ((uint32_t)p[1] << 8) | ((uint32_t)p[2] << 16) | ((uint32_t)p[3] << 24);
+}
+
+/* One group's sum of cb[idx] * xh: four interleaved accumulators for the
+ * byte-aligned 2- and 4-bit packings, one running sum otherwise. */
+static float cq_dot_group(const uint8_t *p, uint32_t bit_off, uint32_t bits, uint32_t g,
+                          const float *cb, const float *xh)
+{
+    float s = 0.0f, s0 = 0.0f, s1 = 0.0f, s2 = 0.0f, s3 = 0.0f;
+    uint32_t j, k;
+    if ((bits == 2 || bits == 4) && (bit_off & 7u) == 0) {
+        const uint8_t *q = p + (bit_off >> 3);
+        const uint32_t per = 32 / bits, mask = (1u << bits) - 1u;   /* weights per word */
+        for (j = 0; j < g; j += per) {
+            uint32_t w = load_u32le(q);
+            q += 4;
+            for (k = 0; k < per; k++) {
+                float t = cb[(w >> (k * bits)) & mask] * xh[j + k];
+                switch (k & 3u) {
+                case 0: s0 += t; break;
+                case 1: s1 += t; break;
+                case 2: s2 += t; break;
+                default: s3 += t; break;
+                }
+            }
+        }
+        return (s0 + s1) + (s2 + s3);
+    }
+    for (j = 0; j < g; j++) {
+        uint32_t b = bit_off + j * bits, byt = b >> 3, sh = b & 7u, w = p[byt];
+        if (sh + bits > 8)
+            w |= (uint32_t)p[byt + 1] << 8;
+        s += cb[(w >> sh) & ((1u << bits) - 1u)] * xh[j];
+    }
+    return s;
+}
+
+void ndo_cq_gemv(uint32_t out, uint32_t in, uint32_t group, uint32_t bits, const void *blob,
+                 const float *cb, const float *xh, float *y)
+{
+    uint32_t in_pad = ndo_cq_in_pad(in, group), ngroup = in_pad / group;
+    size_t rowbytes = (size_t)in_pad * bits / 8;
+    const uint8_t *packed = (const uint8_t *)blob;
+    const uint8_t *nb = packed + (size_t)out * rowbytes;     /* fp16 norms [out][ngroup] */
+    uint32_t r, gi;
+    for (r = 0; r < out; r++) {
+        float acc = 0.0f;
+        for (gi = 0; gi < ngroup; gi++) {
+            size_t o = ((size_t)r * ngroup + gi) * 2;
+            float nf = ndo_f16_to_f32((uint16_t)(nb[o] | (nb[o + 1] << 8)));
+            acc += nf * cq_dot_group(packed + (size_t)r * rowbytes, gi * group * bits, bits, group, cb,
+                                     xh + (size_t)gi * group);
+        }
+        y[r] = acc;
+    }
+}
+
+void ndo_cq_lut_build(const float *cb, const float *xh, uint32_t in_pad, float *lut)
+{
+    uint32_t p, i0, i1;
+    for (p = 0; p < in_pad / 2; p++) {
+        float a[4], b[4];
+        for (i0 = 0; i0 < 4; i0++) {
+            a[i0] = cb[i0] * xh[2 * p];
+            b[i0] = cb[i0] * xh[2 * p + 1];
+        }
+        for (i1 = 0; i1 < 4; i1++)
+            for (i0 = 0; i0 < 4; i0++)
+                lut[(size_t)p * 16 + i0 + 4 * i1] = a[i0] + b[i1];
+    }
+}
+
+void ndo_cq_gemv_lut2(uint32_t out, uint32_t in, uint32_t group, const void *blob,
+                      const float *lut, float *y)
+{
+    uint32_t in_pad = ndo_cq_in_pad(in, group), ngroup = in_pad / group;
+    size_t rowbytes = (size_t)in_pad / 4;
+    const uint8_t *packed = (const uint8_t *)blob;
+    const uint8_t *nb = packed + (size_t)out * rowbytes;
+    uint32_t r, gi, j, k;
+    for (r = 0; r < out; r++) {
+        float acc = 0.0f;
+        for (gi = 0; gi < ngroup; gi++) {
+            size_t o = ((size_t)r * ngroup + gi) * 2;
+            float nf = ndo_f16_to_f32((uint16_t)(nb[o] | (nb[o + 1] << 8)));
+            float s[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+            const uint8_t *q = packed + (size_t)r * rowbytes + (size_t)gi * group / 4;
+            const float *T = lut + (size_t)gi * (group / 2) * 16;
+            /* one word = 8 pairs; pair k of the word indexes table block k */
+            for (j = 0; j < group; j += 16) {
+                uint32_t w = load_u32le(q);
+                q += 4;
+                for (k = 0; k < 8; k++)
+                    s[k & 3u] += T[16 * k + ((w >> (4 * k)) & 15u)];
+                T += 128;
+            }
+            acc += nf * ((s[0] + s[1]) + (s[2] + s[3]));
+        }
+        y[r] = acc;
+    }
+}
+
 /* ------------------------------------------------------ threaded baseline */
 
 typedef struct {

@@ -23,6 +23,10 @@
  *   ndo_tap_conv, ndo_zcrms_heads,
  *   ndo_front (+ its session state)       - pinned: reference harness (bit-exact tap_projection,
  *                                           zcrms_heads, snapshot/rewind/prefix of the histories)
+ *   ndo_fwht, ndo_cq_prepare, ndo_cq_gemv,
+ *   ndo_cq_lut_build, ndo_cq_gemv_lut2    - pinned: reference harness (bit-exact nd_fwht,
+ *                                           nd_cq_prepare, nd_cq_gemv_prepared, nd_cq_lut_build,
+ *                                           nd_cq_gemv_lut2) + float64 dequantised matvec
  *   ndo_rope_inv, ndo_rope_row            - pinned: float64 bound (<= 1 ulp of the exact value
  *                                           of the rounded argument); the reference computes
  *                                           them inline in nd_model_open / step_hidden, so no
@@ -166,6 +170,36 @@ int  ndo_session_front(ndo_session *s, uint32_t taps, float rope_theta);
 /* The front for layer li at s->pos, in place on q [nh*qk_hd], k [nkv*qk_hd],
  * v [nkv*v_hd] (raw projections in, store-ready rows out). */
 void ndo_front(ndo_session *s, uint32_t li, const ndo_front_w *w, float *q, float *k, float *v);
+
+/* ---- CQ projections (engine/src/nd_quant.c, engine/include/nd_quant.h) ----
+ *
+ * A CQ tensor [out][in] stores per group of `group` weights a `bits`-wide
+ * codebook index per weight (an LSB-first bitstream per row, rows of
+ * in_pad*bits/8 bytes, in_pad = in rounded up to group) and one fp16 norm
+ * per (row, group), the norms [out][in_pad/group] following the packed rows
+ * in the same blob. w_group = (cb[idx] * norm) @ H with H the orthonormal
+ * Walsh-Hadamard matrix, so a matvec transforms the activation instead:
+ * xh = H x per group, y[o] = sum_g norm[o][g] * sum_i cb[idx[o][i]] * xh[i].
+ * cb is the archive's codebook slice for the width (2^bits entries, already
+ * scaled by 1/sqrt(group)). */
+uint32_t ndo_cq_in_pad(uint32_t in, uint32_t group);
+/* In-place unnormalised fast Walsh-Hadamard transform, n a power of two
+ * (nd_fwht, nd_quant.c:36-65). */
+void ndo_fwht(float *x, uint32_t n);
+/* xh[in_pad] = x zero-padded, then per group H scaled by 1/sqrt(group)
+ * (nd_cq_prepare, nd_quant.c:354-387; fwht_rows / fw_scale :99-116, :303-352). */
+void ndo_cq_prepare(uint32_t in, uint32_t group, const float *x, float *xh);
+/* y[out] = W . x for a prepared xh: the generic row walker and its group dot
+ * (gemv_rows_generic :616-632, dot_group :389-462). */
+void ndo_cq_gemv(uint32_t out, uint32_t in, uint32_t group, uint32_t bits, const void *blob,
+                 const float *cb, const float *xh, float *y);
+/* The 2-bit pair table: lut[p*16 + i0 + 4*i1] = cb[i0]*xh[2p] + cb[i1]*xh[2p+1]
+ * (nd_cq_lut_build / lutb_rows, :75-97, :800-807). */
+void ndo_cq_lut_build(const float *cb2, const float *xh, uint32_t in_pad, float *lut);
+/* y[out] = W . x for a 2-bit tensor through the pair table (nd_cq_gemv_lut2 /
+ * nd_lut2_rows_c, :734-773, :809-839). */
+void ndo_cq_gemv_lut2(uint32_t out, uint32_t in, uint32_t group, const void *blob,
+                      const float *lut, float *y);
 
 /* ---- CPU baseline: batched fp16 decode, threaded over sequences ----
  *

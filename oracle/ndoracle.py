@@ -118,6 +118,13 @@ def lib():
         L.ndo_session_front.argtypes = [C.POINTER(Session), C.c_uint32, C.c_float]
         L.ndo_session_front.restype = C.c_int
         L.ndo_front.argtypes = [C.POINTER(Session), C.c_uint32, C.POINTER(FrontW)] + [C.c_void_p] * 3
+        L.ndo_cq_in_pad.restype = C.c_uint32
+        L.ndo_cq_in_pad.argtypes = [C.c_uint32, C.c_uint32]
+        L.ndo_fwht.argtypes = [C.c_void_p, C.c_uint32]
+        L.ndo_cq_prepare.argtypes = [C.c_uint32, C.c_uint32, C.c_void_p, C.c_void_p]
+        L.ndo_cq_gemv.argtypes = [C.c_uint32] * 4 + [C.c_void_p] * 4
+        L.ndo_cq_lut_build.argtypes = [C.c_void_p, C.c_void_p, C.c_uint32, C.c_void_p]
+        L.ndo_cq_gemv_lut2.argtypes = [C.c_uint32] * 3 + [C.c_void_p] * 3
         _lib = L
     return _lib
 
@@ -168,6 +175,10 @@ def ref():
         R.ref_session_front.restype = C.c_int
         R.ref_front.argtypes = [C.c_void_p, C.c_uint32] + [C.c_void_p] * 8
         R.ref_hist.argtypes = [C.c_void_p, C.c_int] + [C.POINTER(C.c_void_p)] * 3
+        R.ref_fwht.argtypes = [C.c_void_p, C.c_uint32]
+        R.ref_cq_prepare.argtypes = [C.c_uint32, C.c_uint32, C.c_void_p, C.c_void_p]
+        R.ref_cq_gemv.argtypes = [C.c_uint32] * 4 + [C.c_void_p] * 4
+        R.ref_cq_lut2.argtypes = [C.c_uint32] * 3 + [C.c_void_p] * 5
         _ref = R
     return _ref
 
@@ -500,3 +511,58 @@ def zcrms_heads(x, s, cs, sn):
     s, cs, sn = (np.ascontiguousarray(a, np.float32) for a in (s, cs, sn))
     lib().ndo_zcrms_heads(_ptr(x), x.shape[0], x.shape[1], _ptr(s), _ptr(cs), _ptr(sn))
     return x
+
+
+# ----------------------------------------------------------- CQ projections
+
+class CQTensor:
+    """A CQ tensor as the archive stores it: blob = packed rows
+    [out][in_pad*bits/8] then fp16 norms [out][in_pad/group] (little-endian);
+    codebook = the archive's 28 floats cb2 | cb3 | cb4."""
+
+    def __init__(self, out, inp, group, bits, blob, codebook):
+        self.out, self.inp, self.group, self.bits = out, inp, group, bits
+        self.blob = np.ascontiguousarray(blob, np.uint8)
+        self.codebook = np.ascontiguousarray(codebook, np.float32)
+        self.in_pad = (inp + group - 1) // group * group
+        self.rowbytes = self.in_pad * bits // 8
+        assert self.blob.size == out * self.rowbytes + out * (self.in_pad // group) * 2
+
+    def cb(self):
+        off = {2: 0, 3: 4, 4: 12}[self.bits]
+        return self.codebook[off:off + (1 << self.bits)]
+
+    def codes(self):
+        """Index matrix [out][in_pad] decoded from the LSB-first bitstream."""
+        rows = self.blob[: self.out * self.rowbytes].reshape(self.out, self.rowbytes)
+        bitsarr = np.unpackbits(rows, axis=1, bitorder="little").reshape(self.out, self.in_pad, self.bits)
+        return (bitsarr * (1 << np.arange(self.bits))).sum(axis=2)
+
+    def norms(self):
+        nb = self.blob[self.out * self.rowbytes:]
+        return nb.view(np.float16).astype(np.float32).reshape(self.out, self.in_pad // self.group)
+
+
+def cq_prepare(t, x):
+    x = np.ascontiguousarray(x, np.float32)
+    xh = np.zeros(t.in_pad, np.float32)
+    lib().ndo_cq_prepare(t.inp, t.group, _ptr(x), _ptr(xh))
+    return xh
+
+
+def cq_gemv(t, xh):
+    xh = np.ascontiguousarray(xh, np.float32)
+    y = np.zeros(t.out, np.float32)
+    cb = np.ascontiguousarray(t.cb())
+    lib().ndo_cq_gemv(t.out, t.inp, t.group, t.bits, _ptr(t.blob), _ptr(cb), _ptr(xh), _ptr(y))
+    return y
+
+
+def cq_gemv_lut2(t, xh):
+    xh = np.ascontiguousarray(xh, np.float32)
+    lut = np.zeros(t.in_pad // 2 * 16, np.float32)
+    y = np.zeros(t.out, np.float32)
+    cb = np.ascontiguousarray(t.cb())
+    lib().ndo_cq_lut_build(_ptr(cb), _ptr(xh), t.in_pad, _ptr(lut))
+    lib().ndo_cq_gemv_lut2(t.out, t.inp, t.group, _ptr(t.blob), _ptr(lut), _ptr(y))
+    return y

@@ -11,6 +11,9 @@
  *   kv_store_int8    :1822-1866
  *   attn_heads       :2105-2359
  *   tap_projection / tap_rows, zcrms_heads   :2361-2379, :1748-1802, :324-360
+ * and the CQ kernels of engine/src/nd_quant.c (nd_fwht, nd_cq_prepare,
+ * nd_cq_gemv_prepared, nd_cq_lut_build, nd_cq_gemv_lut2), driven with
+ * hand-built nd_tensor / nd_cact records.
  * An nd_model is assembled by hand with only the KV geometry and buffers set
  * (no archive), and the store + dispatch steps of attention() (:2426-2483) are
  * replayed around those calls.
@@ -251,4 +254,49 @@ void ref_attention(void *vm, uint32_t li, const float *q, const float *k, const 
 {
     ref_kv_store(vm, li, k, v);
     ref_attend(vm, li, q, gate, out);
+}
+
+/* ------------------------------------------------------- CQ projections */
+
+void ref_fwht(float *x, uint32_t n) { nd_fwht(x, n); }
+
+static void cq_tensor(nd_tensor *t, uint32_t out, uint32_t in, uint32_t group, uint32_t bits)
+{
+    memset(t, 0, sizeof *t);
+    t->ndim = 2;
+    t->shape[0] = out;
+    t->shape[1] = in;
+    t->group = group;
+    t->bits = bits;
+}
+
+void ref_cq_prepare(uint32_t in, uint32_t group, const float *x, float *xh)
+{
+    nd_tensor t;
+    cq_tensor(&t, 1, in, group, 2);
+    nd_cq_prepare(&t, x, xh);
+}
+
+/* codebook: the archive's 28 floats cb2 | cb3 | cb4 (nd_cact_codebook). */
+void ref_cq_gemv(uint32_t out, uint32_t in, uint32_t group, uint32_t bits, const void *blob,
+                 const float *codebook, const float *xh, float *y)
+{
+    nd_tensor t;
+    nd_cact c;
+    memset(&c, 0, sizeof c);
+    c.codebook = codebook;
+    cq_tensor(&t, out, in, group, bits);
+    nd_cq_gemv_prepared(&c, &t, blob, xh, y);
+}
+
+void ref_cq_lut2(uint32_t out, uint32_t in, uint32_t group, const void *blob, const float *codebook,
+                 const float *xh, float *lut, float *y)
+{
+    nd_tensor t;
+    nd_cact c;
+    memset(&c, 0, sizeof c);
+    c.codebook = codebook;
+    cq_tensor(&t, out, in, group, 2);
+    nd_cq_lut_build(&c, xh, nd_cq_in_pad(&t), lut);
+    nd_cq_gemv_lut2(&t, blob, lut, y);
 }

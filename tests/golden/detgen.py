@@ -38,3 +38,22 @@ class Stream:
     def take(self, n):
         self.k += 1
         return det_normal(self.seed * 1000003 + self.k, n)
+
+
+def make_cq_tensor(seed, out, inp, group, bits_, special_norms=False):
+    """A synthetic CQ tensor in the archive's blob layout."""
+    rng = np.random.default_rng(seed)
+    in_pad = (inp + group - 1) // group * group
+    rowbytes = in_pad * bits_ // 8
+    packed = rng.integers(0, 256, out * rowbytes, dtype=np.uint8)
+    norms = rng.uniform(0.25, 2.0, (out, in_pad // group)).astype(np.float16)
+    if special_norms:
+        norms.flat[::7] = np.float16(-0.75)          # negative
+        norms.flat[3::11] = np.float16(3e-6)         # subnormal in fp16
+        norms.flat[5::13] = np.float16(0.0)
+    cb = np.concatenate([np.sort(det_normal(seed + 1, 4)), np.sort(det_normal(seed + 2, 8)),
+                         np.sort(det_normal(seed + 3, 16))]).astype(np.float32)
+    cb = (cb / np.sqrt(np.float32(group))).astype(np.float32)
+    blob = np.concatenate([packed, norms.view(np.uint8).ravel()])
+    import ndoracle as O
+    return O.CQTensor(out, inp, group, bits_, blob, cb)

@@ -192,6 +192,25 @@ def main():
         for p in saved.values():
             O.ref().ref_prefix_free(p)
         S.close()
+    # CQ projections: the reference's prepare, generic matvec and 2-bit table path
+    from detgen import make_cq_tensor
+    cq_shapes = [(24, 256, 128, 2), (9, 300, 128, 4), (13, 96, 32, 3)]
+    out["cq_shapes"] = np.array(cq_shapes, np.int32)
+    for i, (o, n, g, b) in enumerate(cq_shapes):
+        t = make_cq_tensor(100 + i, o, n, g, b, special_norms=True)
+        x = det_normal(200 + i, n)
+        xh = np.zeros(t.in_pad, np.float32)
+        R.ref_cq_prepare(n, g, x.ctypes.data, xh.ctypes.data)
+        y = np.zeros(o, np.float32)
+        R.ref_cq_gemv(o, n, g, b, t.blob.ctypes.data, t.codebook.ctypes.data, xh.ctypes.data, y.ctypes.data)
+        out["cq_blob_%d" % i], out["cq_cb_%d" % i], out["cq_x_%d" % i] = t.blob, t.codebook, x
+        out["cq_xh_%d" % i], out["cq_y_%d" % i] = xh, y
+        if b == 2:
+            lut = np.zeros(t.in_pad // 2 * 16, np.float32)
+            y2 = np.zeros(o, np.float32)
+            R.ref_cq_lut2(o, n, g, t.blob.ctypes.data, t.codebook.ctypes.data, xh.ctypes.data,
+                          lut.ctypes.data, y2.ctypes.data)
+            out["cq_y2_%d" % i] = y2
     np.savez_compressed(os.path.join(HERE, "golden.npz"), **out)
     print("wrote", os.path.join(HERE, "golden.npz"), {k: v.shape for k, v in out.items()})
 
