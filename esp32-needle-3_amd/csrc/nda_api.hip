@@ -1710,6 +1710,129 @@ int nda_d2h(void *dst, const void *src, size_t bytes)
     return hipMemcpy(dst, src, bytes, hipMemcpyDeviceToHost) == hipSuccess ? NDA_OK : NDA_ERR_HIP;
 }
 
+// ------------------------------------------------------- CQ projections
+
+struct nda_cq {
+    uint32_t out, in, in_pad, group, ngroup, bits, rowbytes;
+    uint8_t *packed = nullptr;     // [out][rowbytes]
+    uint16_t *norms = nullptr;     // [out][ngroup], 2-byte aligned copy
+    float *cb = nullptr;           // [1 << bits]
+};
+
+int nda_cq_create(uint32_t out, uint32_t in, uint32_t group, uint32_t bits, const void *blob,
+                  const float *codebook, nda_cq **tp)
+{
+    if (!tp || !blob || !codebook || out == 0 || in == 0)
+        return NDA_ERR_ARG;
+    *tp = nullptr;
+    if (bits < 2 || bits > 4 || group < 8 || group > 4096 || (group & (group - 1)))
+        return NDA_ERR_UNSUPPORTED;
+    nda_cq *t = new (std::nothrow) nda_cq();
+    if (!t)
+        return NDA_ERR_NOMEM;
+    t->out = out;
+    t->in = in;
+    t->group = group;
+    t->bits = bits;
+    t->in_pad = (in + group - 1) / group * group;
+    t->ngroup = t->in_pad / group;
+    t->rowbytes = t->in_pad * bits / 8;
+    if (t->in_pad > 16384) {
+        delete t;
+        return NDA_ERR_UNSUPPORTED;
+    }
+    const size_t pb = (size_t)out * t->rowbytes, nb = (size_t)out * t->ngroup * 2;
+    // +4 bytes: the bitstream reader may touch the byte after a straddling field
+    if (hipMalloc(&t->packed, pb + 4) != hipSuccess || hipMalloc(&t->norms, nb) != hipSuccess ||
+        hipMalloc(&t->cb, sizeof(float) << bits) != hipSuccess ||
+        hipMemcpy(t->packed, blob, pb, hipMemcpyHostToDevice) != hipSuccess ||
+        hipMemset(t->packed + pb, 0, 4) != hipSuccess ||
+        hipMemcpy(t->norms, (const uint8_t *)blob + pb, nb, hipMemcpyHostToDevice) != hipSuccess ||
+        hipMemcpy(t->cb, codebook, sizeof(float) << bits, hipMemcpyHostToDevice) != hipSuccess) {
+        nda_cq_destroy(t);
+        return NDA_ERR_HIP;
+    }
+    *tp = t;
+    return NDA_OK;
+}
+
+int nda_cq_destroy(nda_cq *t)
+{
+    if (!t)
+        return NDA_OK;
+    for (void *b : {(void *)t->packed, (void *)t->norms, (void *)t->cb})
+        if (b)
+            (void)hipFree(b);
+    delete t;
+    return NDA_OK;
+}
+
+uint32_t nda_cq_in_pad(const nda_cq *t) { return t ? t->in_pad : 0; }
+
+int nda_cq_prepare(const nda_cq *t, uint32_t rows, const float *x, float *xh, void *stream)
+{
+    if (!t || (rows && (!x || !xh)))
+        return NDA_ERR_ARG;
+    if (((uintptr_t)x & 15) || ((uintptr_t)xh & 15))
+        return NDA_ERR_ARG;
+    CqPrepArgs a{};
+    a.x = x;
+    a.xh = xh;
+    a.rows = rows;
+    a.in = t->in;
+    a.in_pad = t->in_pad;
+    a.group = t->group;
+    a.scale = 1.0f / sqrtf((float)t->group);      // nd_cq_prepare's scale
+    return launch_cq_prepare(a, (hipStream_t)stream) == hipSuccess ? NDA_OK : NDA_ERR_HIP;
+}
+
+int nda_cq_gemm(const nda_cq *t, uint32_t rows, const float *xh, float *y, void *stream)
+{
+    if (!t || (rows && (!xh || !y)))
+        return NDA_ERR_ARG;
+    if ((uintptr_t)xh & 15)
+        return NDA_ERR_ARG;
+    if ((uint64_t)rows > 65535ull * 64)
+        return NDA_ERR_ARG;
+    CqGemmArgs a{};
+    a.xh = xh;
+    a.y = y;
+    a.packed = t->packed;
+    a.norms = t->norms;
+    a.cb = t->cb;
+    a.rows = rows;
+    a.out = t->out;
+    a.in_pad = t->in_pad;
+    a.group = t->group;
+    a.ngroup = t->ngroup;
+    a.bits = t->bits;
+    a.rowbytes = t->rowbytes;
+    return launch_cq_gemm(a, (hipStream_t)stream) == hipSuccess ? NDA_OK : NDA_ERR_HIP;
+}
+
+int nda_event_create(void **ev)
+{
+    if (!ev)
+        return NDA_ERR_ARG;
+    return hipEventCreate((hipEvent_t *)ev) == hipSuccess ? NDA_OK : NDA_ERR_HIP;
+}
+
+int nda_event_destroy(void *ev) { return hipEventDestroy((hipEvent_t)ev) == hipSuccess ? NDA_OK : NDA_ERR_HIP; }
+
+int nda_event_record(void *ev, void *stream)
+{
+    return hipEventRecord((hipEvent_t)ev, (hipStream_t)stream) == hipSuccess ? NDA_OK : NDA_ERR_HIP;
+}
+
+int nda_event_elapsed(void *start, void *stop, float *ms)
+{
+    if (!ms)
+        return NDA_ERR_ARG;
+    if (hipEventSynchronize((hipEvent_t)stop) != hipSuccess)
+        return NDA_ERR_HIP;
+    return hipEventElapsedTime(ms, (hipEvent_t)start, (hipEvent_t)stop) == hipSuccess ? NDA_OK : NDA_ERR_HIP;
+}
+
 int nda_host_alloc(void **ptr, size_t bytes)
 {
     if (!ptr)

@@ -161,6 +161,26 @@ struct HistTailArgs {
     uint32_t rows, layer, n_layers, taps, dq, dk, dv;
 };
 
+/* CQ projections (nda_cq.hip). */
+struct CqPrepArgs {
+    const float *x;          /* [rows][in] */
+    float *xh;               /* [rows][in_pad] */
+    uint32_t rows, in, in_pad, group;
+    float scale;             /* 1 / sqrt(group) */
+};
+
+struct CqGemmArgs {
+    const float *xh;         /* [rows][in_pad] prepared activations */
+    float *y;                /* [rows][out] */
+    const uint8_t *packed;   /* [out][rowbytes] LSB-first index bitstream */
+    const uint16_t *norms;   /* [out][ngroup] fp16 bits */
+    const float *cb;         /* [1 << bits] codebook (scaled by 1/sqrt(group)) */
+    uint32_t rows, out, in_pad, group, ngroup, bits, rowbytes;
+};
+
+hipError_t launch_cq_prepare(const CqPrepArgs &a, hipStream_t s);
+hipError_t launch_cq_gemm(const CqGemmArgs &a, hipStream_t s);
+
 /* Compiled geometries: (KV element bytes, qk_head_dim, v_head_dim, GQA rep). */
 #define NDA_FOR_GEOMETRIES(X) \
     X(2, 64, 64, 1) X(2, 64, 64, 2) X(2, 64, 64, 4) X(2, 64, 64, 6) X(2, 64, 64, 8) \

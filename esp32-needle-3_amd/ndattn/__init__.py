@@ -36,6 +36,8 @@ ABI_SYMBOLS = [
     "nda_stream_create", "nda_stream_destroy", "nda_device_sync", "nda_device_info",
     "nda_prof_enable", "nda_prof_read",
     "nda_front_init", "nda_front_weights", "nda_front", "nda_attention", "nda_front_hist",
+    "nda_cq_create", "nda_cq_destroy", "nda_cq_in_pad", "nda_cq_prepare", "nda_cq_gemm",
+    "nda_event_create", "nda_event_destroy", "nda_event_record", "nda_event_elapsed",
 ]
 HOST_SYMBOLS = [
     "nd_gpu_open", "nd_gpu_close", "nd_gpu_reset", "nd_gpu_set_sink", "nd_gpu_snapshot",
@@ -120,6 +122,15 @@ def lib():
             "nda_front": (C.c_int, [vp, u32, u32, vp, vp, vp, vp, vp, vp, vp, vp, vp]),
             "nda_attention": (C.c_int, [vp, u32, u32, vp, vp, vp, vp, vp, vp, vp]),
             "nda_front_hist": (C.c_int, [vp, u32, C.c_int, vp, vp]),
+            "nda_cq_create": (C.c_int, [u32, u32, u32, u32, vp, vp, C.POINTER(vp)]),
+            "nda_cq_destroy": (C.c_int, [vp]),
+            "nda_cq_in_pad": (u32, [vp]),
+            "nda_cq_prepare": (C.c_int, [vp, u32, vp, vp, vp]),
+            "nda_cq_gemm": (C.c_int, [vp, u32, vp, vp, vp]),
+            "nda_event_create": (C.c_int, [C.POINTER(vp)]),
+            "nda_event_destroy": (C.c_int, [vp]),
+            "nda_event_record": (C.c_int, [vp, vp]),
+            "nda_event_elapsed": (C.c_int, [vp, vp, C.POINTER(C.c_float)]),
         }
         for name, (res, args) in sig.items():
             f = getattr(L, name)
@@ -505,3 +516,53 @@ class GpuSession:
             _check(host_lib().nd_gpu_front_weights(self.m, li, *(a.ctypes.data for a in arrs)))
         self.front_on = True
         self.taps = taps
+
+
+class CQ:
+    """A CQ tensor on the device (nda_cq): the archive's blob + the codebook
+    slice for its width (host arrays)."""
+
+    def __init__(self, out, inp, group, bits, blob, codebook):
+        blob = np.ascontiguousarray(blob, np.uint8)
+        cb = np.ascontiguousarray(codebook, np.float32)
+        self.h = vp()
+        _check(lib().nda_cq_create(out, inp, group, bits, blob.ctypes.data, cb.ctypes.data, C.byref(self.h)))
+        self.out, self.inp, self.group, self.bits = out, inp, group, bits
+        self.in_pad = lib().nda_cq_in_pad(self.h)
+
+    def prepare(self, rows, x, xh, stream=None):
+        _check(lib().nda_cq_prepare(self.h, rows, _dp(x), _dp(xh), stream))
+
+    def gemm(self, rows, xh, y, stream=None):
+        _check(lib().nda_cq_gemm(self.h, rows, _dp(xh), _dp(y), stream))
+
+    def close(self):
+        if self.h and self.h.value:
+            lib().nda_cq_destroy(self.h)
+        self.h = vp()
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
+class Timer:
+    """Two HIP events on a stream: start(), stop(), ms()."""
+
+    def __init__(self):
+        self.a, self.b = vp(), vp()
+        _check(lib().nda_event_create(C.byref(self.a)))
+        _check(lib().nda_event_create(C.byref(self.b)))
+
+    def start(self, stream=None):
+        _check(lib().nda_event_record(self.a, stream))
+
+    def stop(self, stream=None):
+        _check(lib().nda_event_record(self.b, stream))
+
+    def ms(self):
+        f = C.c_float()
+        _check(lib().nda_event_elapsed(self.a, self.b, C.byref(f)))
+        return f.value

@@ -206,6 +206,41 @@ int nda_attention(nda_ctx *ctx, uint32_t layer, uint32_t nseq, const uint32_t *s
  * [n_layers][taps][n_heads*qk_head_dim + n_kv_heads*(qk_head_dim + v_head_dim)]. */
 int nda_front_hist(nda_ctx *ctx, uint32_t seq, int snap, float *dst, void *stream);
 
+/* ---- CQ projections (engine/src/nd_quant.c, engine/include/nd_quant.h) ----
+ * The engine's codebook-quantised matvecs for a batch of rows. A CQ tensor
+ * [out][in] is the archive's blob: per row an LSB-first bitstream of `bits`
+ * -wide codebook indices over in_pad = in rounded up to `group`, then the
+ * fp16 norms [out][in_pad/group]; the weights are
+ * w_group = (codebook[idx] * norm) @ H, H the orthonormal Walsh-Hadamard
+ * matrix of size group. As in the engine, the activation is transformed
+ * (nda_cq_prepare, nd_cq_prepare) and the transformed rows are multiplied
+ * against the codes (nda_cq_gemm: nd_cq_gemv_prepared / nd_cq_gemv_lut2,
+ * for every row of the batch). q/k/v/gate and out_proj of attention()
+ * (nd_model.c:2402-2411, :2495-2501) are such tensors at 2 bits. */
+typedef struct nda_cq nda_cq;
+
+/* Copies one tensor to the device. blob: host, the tensor payload (packed
+ * rows then norms); codebook: host, the 2^bits entries for this width
+ * (nd_cact_codebook). group a power of two in 8..4096, bits 2..4. */
+int nda_cq_create(uint32_t out, uint32_t in, uint32_t group, uint32_t bits, const void *blob,
+                  const float *codebook, nda_cq **t);
+int nda_cq_destroy(nda_cq *t);
+/* in_pad of the tensor (the prepared row length). */
+uint32_t nda_cq_in_pad(const nda_cq *t);
+/* xh[rows][in_pad] = per-group H of x[rows][in] zero-padded (device
+ * pointers, 16-byte aligned). Bit-identical to nd_cq_prepare. Reusable by
+ * every tensor with the same (in, group). */
+int nda_cq_prepare(const nda_cq *t, uint32_t rows, const float *x, float *xh, void *stream);
+/* y[rows][out] = W . x for each row, from its prepared xh (device pointers). */
+int nda_cq_gemm(const nda_cq *t, uint32_t rows, const float *xh, float *y, void *stream);
+
+/* ---- stream-ordered timing ---- */
+int nda_event_create(void **ev);
+int nda_event_destroy(void *ev);
+int nda_event_record(void *ev, void *stream);
+/* Milliseconds between two recorded events (waits for the second). */
+int nda_event_elapsed(void *start, void *stop, float *ms);
+
 /* ---- inspection (tests, tools) ---- */
 
 /* Copies the stored K/V of `count` consecutive positions starting at

@@ -1,0 +1,120 @@
+"""GPU parity of the CQ projections (nda_cq_prepare / nda_cq_gemm) against
+the oracle (itself bit-exact to the reference's nd_cq_prepare and
+nd_cq_gemv_prepared / nd_cq_gemv_lut2): the prepared rows bit-exact, the
+matvec outputs within fp32 reassociation of the engine's, bounded as
+|y - y_ref| <= 1e-5 * sum|w x| + 1e-6 per output; and the reference's own
+golden outputs."""
+import os
+import sys
+
+import numpy as np
+import pytest
+
+import ndoracle as O
+from detgen import det_normal, make_cq_tensor
+
+pytestmark = pytest.mark.gpu
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+
+
+def nda():
+    import ndattn
+    return ndattn
+
+
+def say(*a):
+    print("[gpu-case]", *a, flush=True)
+    sys.stdout.flush()
+
+
+def bits(a):
+    return np.asarray(a, np.float32).view(np.uint32)
+
+
+def abs_scale(t, x):
+    """sum_k |w[o][k]| |x[k]| per output, float64: the reassociation bound."""
+    from scipy.linalg import hadamard
+    H = hadamard(t.group) / np.sqrt(float(t.group))
+    cb = t.cb().astype(np.float64)
+    codes, nrm = t.codes(), t.norms().astype(np.float64)
+    W = np.zeros((t.out, t.in_pad))
+    for g in range(t.in_pad // t.group):
+        sl = slice(g * t.group, (g + 1) * t.group)
+        W[:, sl] = (cb[codes[:, sl]] * nrm[:, g:g + 1]) @ H
+    return np.abs(W[:, :t.inp]) @ np.abs(x.astype(np.float64)).T
+
+
+def run(t, x):
+    N = nda()
+    rows = x.shape[0]
+    q = N.CQ(t.out, t.inp, t.group, t.bits, t.blob, t.cb())
+    dx = N.DevBuf.from_array(x)
+    dxh = N.DevBuf(max(1, rows) * q.in_pad * 4)
+    dy = N.DevBuf(max(1, rows) * t.out * 4)
+    q.prepare(rows, dx, dxh)
+    q.gemm(rows, dxh, dy)
+    N.device_sync()
+    xh = dxh.to_array(np.float32, (rows, q.in_pad))
+    y = dy.to_array(np.float32, (rows, t.out))
+    q.close()
+    return xh, y
+
+
+@pytest.mark.parametrize("shape,rows", [
+    ((64, 512, 128, 2), 64),      # one full tile
+    ((576, 768, 128, 2), 70),     # the archive's q_proj shape (12 x 48 from d_model 768), ragged rows
+    ((100, 200, 64, 4), 33),      # padding, partial output tile
+    ((13, 96, 32, 3), 5),         # 3-bit straddling fields, group below the tile width
+    ((130, 1024, 256, 2), 129),
+    ((768, 576, 128, 2), 3),      # out_proj shape, few rows
+])
+def test_cq_prepare_and_gemm(shape, rows):
+    out, inp, group, b = shape
+    say("cq", shape, rows)
+    t = make_cq_tensor(out + inp + group + b, out, inp, group, b, special_norms=True)
+    x = np.stack([det_normal(1000 + r, inp) for r in range(rows)]) * np.float32(3.0)
+    xh, y = run(t, x)
+    sc = abs_scale(t, x)
+    worst = 0.0
+    for r in range(rows):
+        want_xh = O.cq_prepare(t, x[r])
+        assert np.array_equal(bits(xh[r]), bits(want_xh)), r
+        want = O.cq_gemv_lut2(t, want_xh) if b == 2 else O.cq_gemv(t, want_xh)
+        err = np.abs(y[r].astype(np.float64) - want)
+        assert np.all(err <= 1e-5 * sc[:, r] + 1e-6), (r, float(err.max()))
+        worst = max(worst, float(err.max()))
+    say("cq worst", worst)
+
+
+def test_cq_golden_reference_outputs():
+    """The reference's own outputs for the committed CQ vectors."""
+    G = np.load(os.path.join(HERE, "golden", "golden.npz"))
+    say("cq golden")
+    for i, shape in enumerate(G["cq_shapes"]):
+        out, inp, group, b = (int(v) for v in shape)
+        t = O.CQTensor(out, inp, group, b, G["cq_blob_%d" % i], G["cq_cb_%d" % i])
+        x = G["cq_x_%d" % i][None, :]
+        xh, y = run(t, x)
+        assert np.array_equal(bits(xh[0]), bits(G["cq_xh_%d" % i]))
+        ref = G["cq_y2_%d" % i] if b == 2 else G["cq_y_%d" % i]
+        sc = abs_scale(t, x)[:, 0]
+        assert np.all(np.abs(y[0].astype(np.float64) - ref) <= 1e-5 * sc + 1e-6)
+
+
+def test_cq_error_paths():
+    N = nda()
+    say("cq errors")
+    t = make_cq_tensor(5, 8, 64, 32, 2)
+    with pytest.raises(N.NdaError) as e:
+        N.CQ(8, 64, 48, 2, t.blob, t.cb())           # group not a power of two
+    assert e.value.code == -6
+    with pytest.raises(N.NdaError) as e:
+        N.CQ(8, 64, 32, 5, t.blob, t.cb())           # bits
+    assert e.value.code == -6
+    q = N.CQ(8, 64, 32, 2, t.blob, t.cb())
+    buf = N.DevBuf(4096)
+    with pytest.raises(N.NdaError) as e:
+        q.prepare(1, buf.value + 4, buf)             # misaligned
+    assert e.value.code == -1
+    q.close()
