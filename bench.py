@@ -408,6 +408,99 @@ def engine_front_timing(N, O, geom, toks, steps, taps=3, theta=10000.0):
     return gpu_us, ref_us
 
 
+def cq_tensor_synth(rng, out, inp, group=128, bits=2):
+    """A synthetic CQ tensor in the archive's blob layout: random codes,
+    positive fp16 norms, a sorted codebook scaled by 1/sqrt(group)."""
+    in_pad = (inp + group - 1) // group * group
+    packed = rng.integers(0, 256, out * in_pad * bits // 8, dtype=np.uint8)
+    norms = rng.uniform(0.25, 2.0, (out, in_pad // group)).astype(np.float16)
+    cb = (np.sort(rng.standard_normal(1 << bits)) / np.sqrt(group)).astype(np.float32)
+    return np.concatenate([packed, norms.view(np.uint8).ravel()]), cb
+
+
+def cq_leg(N, stream, rows=B, d_model=768, reps=20):
+    """The attention block's CQ projections for a batch of rows, at the
+    archive's shapes (12 q / 2 kv heads, qk 48, v 64, d_model 768, 2-bit,
+    group 128): prepare x, then q/k/v/gate from it; prepare attn, then
+    out_proj. FLOPs = 2 * rows * in * out per projection."""
+    rng = np.random.default_rng(SEED + 31)
+    shapes = {"q": (576, d_model), "k": (96, d_model), "v": (128, d_model), "gate": (768, d_model),
+              "out": (d_model, 768)}
+    ts, hosts = {}, {}
+    for name, (o, i) in shapes.items():
+        blob, cb = cq_tensor_synth(rng, o, i)
+        ts[name] = N.CQ(o, i, 128, 2, blob, cb)
+        hosts[name] = (o, i, blob, cb)
+    x = N.DevBuf(rows * d_model * 4)
+    x.fill_normal(rows * d_model, 0, SEED + 32, stream=stream)
+    att = N.DevBuf(rows * 768 * 4)
+    att.fill_normal(rows * 768, 0, SEED + 33, stream=stream)
+    xh = N.DevBuf(rows * ts["q"].in_pad * 4)
+    ah = N.DevBuf(rows * ts["out"].in_pad * 4)
+    ys = {name: N.DevBuf(rows * o * 4) for name, (o, _) in shapes.items()}
+
+    def block():
+        ts["q"].prepare(rows, x, xh, stream)
+        N.cq_gemm_many([ts[n] for n in ("q", "k", "v", "gate")], rows, xh,
+                       [ys[n] for n in ("q", "k", "v", "gate")], stream)
+        ts["out"].prepare(rows, att, ah, stream)
+        ts["out"].gemm(rows, ah, ys["out"], stream)
+
+    block()
+    tm, tq = N.Timer(), N.Timer()
+    tm.start(stream)
+    for _ in range(reps):
+        block()
+    tm.stop(stream)
+    block_ms = tm.ms() / reps
+    tq.start(stream)
+    for _ in range(reps):
+        ts["gate"].gemm(rows, xh, ys["gate"], stream)
+    tq.stop(stream)
+    gate_ms = tq.ms() / reps
+    flops = sum(2.0 * rows * o * i for o, i in shapes.values())
+    gate_flops = 2.0 * rows * 768 * d_model
+    # sampled parity: two rows of the gate projection against the oracle
+    import ndoracle as O
+    N.device_sync()
+    xr = x.to_array(np.float32, (rows, d_model))
+    yr = ys["gate"].to_array(np.float32, (rows, 768))
+    o_, i_, blob, cb = hosts["gate"]
+    t = O.CQTensor(o_, i_, 128, 2, blob, np.concatenate([cb, np.zeros(24, np.float32)]))
+    worst = 0.0
+    for r in (0, rows - 1):
+        want = O.cq_gemv_lut2(t, O.cq_prepare(t, xr[r]))
+        worst = max(worst, float(np.abs(want - yr[r]).max() / (np.abs(want).max() + 1e-30)))
+    ref_us = None
+    if O.have_ref():
+        R = O.ref()
+        cb28 = np.concatenate([cb, np.zeros(24, np.float32)])
+        xhr = O.cq_prepare(t, xr[0])
+        lut = np.zeros(t.in_pad // 2 * 16, np.float32)
+        yv = np.zeros(o_, np.float32)
+        t0 = time.perf_counter()
+        n = 0
+        while time.perf_counter() - t0 < 1.0:
+            R.ref_cq_lut2(o_, i_, 128, t.blob.ctypes.data, cb28.ctypes.data, xhr.ctypes.data,
+                          lut.ctypes.data, yv.ctypes.data)
+            n += 1
+        ref_us = (time.perf_counter() - t0) / n * 1e6
+    for q in ts.values():
+        q.close()
+    return {"workload": "CQ projections of one attention block for %d rows: 2-bit, group 128, d_model %d; "
+                        "q 576, k 96, v 128, gate 768 from one prepared x in one launch, out_proj 768 "
+                        "from 768" % (rows, d_model),
+            "block_ms": round(block_ms, 4), "block_tflops": round(flops / (block_ms * 1e-3) / 1e12, 1),
+            "gate_gemm_ms": round(gate_ms, 4),
+            "gate_gemm_tflops": round(gate_flops / (gate_ms * 1e-3) / 1e12, 1),
+            "peak_fp32_mfma_tflops": 157.3,
+            "frac_gate": round(gate_flops / (gate_ms * 1e-3) / 1e12 / 157.3, 4),
+            "rows_per_s": round(rows / (block_ms * 1e-3), 1),
+            "max_rel_delta_sampled": worst,
+            "reference_cpu_us_per_row_gate": None if ref_us is None else round(ref_us, 1),
+            "note": "fp32 MFMA (v_mfma_f32_32x32x2_f32); weights decoded from the 2-bit codes in LDS"}
+
+
 def front_leg(N, stream, steps=5, warmup=2, taps=3, theta=10000.0):
     """The headline decode with the attention front: per layer nda_attention
     takes RAW q/k/v projections (tap convolution over 3 taps, per-head
@@ -589,6 +682,9 @@ def main():
     front = front_leg(N, stream)
     log("front: %.0f tok/s, step %.3f ms, front kernel %.4f ms (%.0f GB/s)" % (
         front["tokens_per_s"], front["ms_per_step"], front["front_kernel_ms"], front["front_GBps"]))
+    cq = cq_leg(N, stream)
+    log("cq: block %.4f ms (%.1f TFLOP/s), gate gemm %.4f ms (%.1f TFLOP/s fp32 MFMA), sampled rel delta %.3g" % (
+        cq["block_ms"], cq["block_tflops"], cq["gate_gemm_ms"], cq["gate_gemm_tflops"], cq["max_rel_delta_sampled"]))
     engine = engine_session_leg(N)
     log("engine session: GPU %.1f us per layer call, reference CPU %s us" % (
         engine["gpu_us_per_layer_call"], engine["reference_cpu_us_per_layer_call"]))
@@ -645,6 +741,7 @@ def main():
         "prefill": prefill,
         "engine_session": engine,
         "front": front,
+        "cq_projections": cq,
         "shared_prefix": shared,
         "max_abs_delta_sampled": worst,
         "device": name,

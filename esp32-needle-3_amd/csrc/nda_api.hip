@@ -1725,7 +1725,7 @@ int nda_cq_create(uint32_t out, uint32_t in, uint32_t group, uint32_t bits, cons
     if (!tp || !blob || !codebook || out == 0 || in == 0)
         return NDA_ERR_ARG;
     *tp = nullptr;
-    if (bits < 2 || bits > 4 || group < 8 || group > 4096 || (group & (group - 1)))
+    if (bits < 2 || bits > 4 || group < 16 || group > 4096 || (group & (group - 1)))
         return NDA_ERR_UNSUPPORTED;
     nda_cq *t = new (std::nothrow) nda_cq();
     if (!t)
@@ -1786,28 +1786,51 @@ int nda_cq_prepare(const nda_cq *t, uint32_t rows, const float *x, float *xh, vo
     return launch_cq_prepare(a, (hipStream_t)stream) == hipSuccess ? NDA_OK : NDA_ERR_HIP;
 }
 
-int nda_cq_gemm(const nda_cq *t, uint32_t rows, const float *xh, float *y, void *stream)
+int nda_cq_gemm_many(const nda_cq *const *ts, uint32_t n, uint32_t rows, const float *xh, float *const *ys,
+                     void *stream)
 {
-    if (!t || (rows && (!xh || !y)))
+    if (!ts || !ys || n == 0 || n > (uint32_t)CQ_MAX_T || (rows && !xh))
         return NDA_ERR_ARG;
     if ((uintptr_t)xh & 15)
         return NDA_ERR_ARG;
-    if ((uint64_t)rows > 65535ull * 64)
+    if ((uint64_t)rows > 0x7FFFFFFFull)
+        return NDA_ERR_ARG;
+    const nda_cq *t0 = ts[0];
+    if (!t0)
         return NDA_ERR_ARG;
     CqGemmArgs a{};
     a.xh = xh;
-    a.y = y;
-    a.packed = t->packed;
-    a.norms = t->norms;
-    a.cb = t->cb;
     a.rows = rows;
-    a.out = t->out;
-    a.in_pad = t->in_pad;
-    a.group = t->group;
-    a.ngroup = t->ngroup;
-    a.bits = t->bits;
-    a.rowbytes = t->rowbytes;
+    a.in_pad = t0->in_pad;
+    a.group = t0->group;
+    a.ngroup = t0->ngroup;
+    a.bits = t0->bits;
+    a.rowbytes = t0->rowbytes;
+    a.nt = n;
+    uint32_t tiles = 0;
+    for (uint32_t i = 0; i < n; i++) {
+        const nda_cq *t = ts[i];
+        if (!t || (rows && !ys[i]))
+            return NDA_ERR_ARG;
+        if (t->in != t0->in || t->group != t0->group || t->bits != t0->bits)
+            return NDA_ERR_ARG;     // one prepared activation serves them all
+        a.y[i] = ys[i];
+        a.packed[i] = t->packed;
+        a.norms[i] = t->norms;
+        a.cb[i] = t->cb;
+        a.out[i] = t->out;
+        a.tile0[i] = tiles;
+        tiles += (t->out + 63) / 64;
+    }
+    a.tile0[n] = tiles;
+    if (tiles > 65535)
+        return NDA_ERR_ARG;
     return launch_cq_gemm(a, (hipStream_t)stream) == hipSuccess ? NDA_OK : NDA_ERR_HIP;
+}
+
+int nda_cq_gemm(const nda_cq *t, uint32_t rows, const float *xh, float *y, void *stream)
+{
+    return nda_cq_gemm_many(&t, 1, rows, xh, &y, stream);
 }
 
 int nda_event_create(void **ev)

@@ -16,10 +16,11 @@
 //
 // The engine runs one row against the weights (a GEMV that streams the
 // compressed weights); a batch of rows makes it a GEMM in which every weight
-// is reused by all rows. The GEMM decodes each 64-output x group tile of
-// codes once per work-group into LDS as fp32 cb * norm, stages the matching
-// 64-row xh tile beside it, and accumulates on v_mfma_f32_32x32x2_f32 (fp32
-// products and sums: the result is the engine's up to fp32 reassociation).
+// is reused by all rows. Per 64-column step a work-group decodes a 64-output
+// tile of codes into LDS as fp32 cb * norm, stages the matching 64-row xh
+// tile beside it (the next step's loads in flight during this step's MFMAs),
+// and accumulates on v_mfma_f32_32x32x2_f32 (fp32 products and sums: the
+// result is the engine's up to fp32 reassociation).
 #include "nda_device.h"
 
 #include <algorithm>
@@ -60,14 +61,8 @@ typedef float float4v __attribute__((ext_vector_type(4)));
 
 constexpr int CQ_MT = 64;     // rows per work-group
 constexpr int CQ_NT = 64;     // outputs per work-group
-constexpr int CQ_KT = 64;     // reduction columns per LDS tile (divides every group size used)
-
-// LDS row of one tile, k-permuted so that MFMA step s of lane half h reads
-// column 2s + h at [h*KT/2 + s]: four steps are one 16-byte read. +4 floats
-// of pad per row keep rows 16-byte aligned and spread over the banks.
-constexpr int CQ_KS = CQ_KT + 4;
-
-__device__ __forceinline__ int cq_perm(int k) { return (k & 1) * (CQ_KT / 2) + (k >> 1); }
+constexpr int CQ_KT = 64;     // reduction columns per LDS tile
+constexpr int CQ_KS = CQ_KT + 4;   // LDS row: +4 floats keep rows 16-byte aligned, banks spread
 
 // Index k of one row's bitstream (bits 2, 3 or 4): at most two bytes.
 __device__ __forceinline__ uint32_t cq_code(const uint8_t *row, uint32_t k, uint32_t bits)
@@ -81,6 +76,19 @@ __device__ __forceinline__ uint32_t cq_code(const uint8_t *row, uint32_t k, uint
 
 __device__ __forceinline__ float half_bits_to_float(uint16_t h) { return (float)__builtin_bit_cast(_Float16, h); }
 
+// One thread's share of a tile in flight: 4 float4 of xh (rows tid/16 + 16 i,
+// columns 4 (tid%16)..) and the 16 codes of one (output, 16-column) slice
+// with its group norm.
+struct CqStage {
+    float4 x[4];
+    uint32_t code[2];     // 16 codes: one word at 2 bits, two at 4 bits
+    uint16_t norm;
+};
+
+// WORDS: the 16 codes of a slice are one (2-bit) or two (4-bit) aligned
+// 32-bit words; otherwise (3 bits, or rows not 4-byte aligned) they are
+// read field by field at decode time.
+template <bool WORDS>
 __global__ __launch_bounds__(256) void cq_gemm_kernel(CqGemmArgs a)
 {
     __shared__ __attribute__((aligned(16))) float Xs[CQ_MT][CQ_KS];
@@ -89,61 +97,100 @@ __global__ __launch_bounds__(256) void cq_gemm_kernel(CqGemmArgs a)
 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int ln = lane & 31, lh = lane >> 5;
-    const uint32_t r0 = blockIdx.x * CQ_MT, o0 = blockIdx.y * CQ_NT;
+    // which tensor this output tile belongs to
+    uint32_t ti = 0;
+    while (ti + 1 < a.nt && blockIdx.y >= a.tile0[ti + 1])
+        ti++;
+    const uint32_t out = a.out[ti];
+    const uint8_t *packed = a.packed[ti];
+    const uint16_t *norms = a.norms[ti];
+    float *y = a.y[ti];
+    const uint32_t r0 = blockIdx.x * CQ_MT, o0 = (blockIdx.y - a.tile0[ti]) * CQ_NT;
     const int wr = (wave & 1) * 32, wo = (wave >> 1) * 32;     // this wave's 32 x 32 block
+    const int xr = tid >> 4, xc = (tid & 15) * 4;               // xh: rows xr + 16 i, columns xc..xc+3
+    const int wrow = tid >> 2, wc = (tid & 3) * 16;             // weights: output wrow, columns wc..wc+15
+    const bool wvalid = o0 + wrow < out;
+    const uint8_t *wrp = packed + (uint64_t)(o0 + wrow) * a.rowbytes;
 
     if (tid < (1 << a.bits))
-        cbs[tid] = a.cb[tid];
+        cbs[tid] = a.cb[ti][tid];
+
+    auto load = [&](uint32_t k0, CqStage &sg) {
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const uint32_t r = r0 + xr + 16 * i;
+            sg.x[i] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+            if (r < a.rows && k0 + xc < a.in_pad)          // in_pad is a multiple of 8
+                sg.x[i] = *reinterpret_cast<const float4 *>(a.xh + (uint64_t)r * a.in_pad + k0 + xc);
+        }
+        const uint32_t k = k0 + wc;
+        sg.code[0] = sg.code[1] = 0;
+        sg.norm = 0;
+        if (wvalid && k < a.in_pad) {
+            sg.norm = norms[(uint64_t)(o0 + wrow) * a.ngroup + k / a.group];
+            if constexpr (WORDS) {
+                const uint32_t *wp = reinterpret_cast<const uint32_t *>(wrp + (k * a.bits >> 3));
+                sg.code[0] = wp[0];
+                if (a.bits == 4)
+                    sg.code[1] = wp[1];
+            }
+        }
+    };
+    auto store = [&](uint32_t k0, const CqStage &sg) {
+#pragma unroll
+        for (int i = 0; i < 4; i++)
+            *reinterpret_cast<float4 *>(&Xs[xr + 16 * i][xc]) = sg.x[i];
+        const float nf = half_bits_to_float(sg.norm);
+        float w[16];
+        const uint32_t k = k0 + wc;
+        const uint32_t lim = a.in_pad - min(k, a.in_pad);   // columns of this slice inside the row
+#pragma unroll
+        for (int e = 0; e < 16; e++) {
+            uint32_t c;
+            if constexpr (WORDS)
+                c = a.bits == 2 ? (sg.code[0] >> (2 * e)) & 3u : (sg.code[e >> 3] >> (4 * (e & 7))) & 15u;
+            else
+                c = wvalid && (uint32_t)e < lim ? cq_code(wrp, k + e, a.bits) : 0u;
+            w[e] = cbs[c] * nf;
+        }
+#pragma unroll
+        for (int e = 0; e < 16; e += 4)
+            *reinterpret_cast<float4 *>(&Ws[wrow][wc + e]) = make_float4(w[e], w[e + 1], w[e + 2], w[e + 3]);
+    };
 
     float16v acc = {};
+    CqStage sg;
+    load(0, sg);
+    __syncthreads();          // cbs visible
     for (uint32_t k0 = 0; k0 < a.in_pad; k0 += CQ_KT) {
-        __syncthreads();      // previous tile's readers done (and cbs visible on the first pass)
-        // xh tile: 64 rows x 64 columns, float4 per thread per step
-        for (int c = tid; c < CQ_MT * CQ_KT / 4; c += 256) {
-            const int rr = c / (CQ_KT / 4), kk = (c % (CQ_KT / 4)) * 4;
-            float4 v = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-            if (r0 + rr < a.rows && k0 + kk < a.in_pad)       // in_pad is a multiple of 4
-                v = *reinterpret_cast<const float4 *>(a.xh + (uint64_t)(r0 + rr) * a.in_pad + k0 + kk);
-            Xs[rr][cq_perm(kk + 0)] = v.x;
-            Xs[rr][cq_perm(kk + 1)] = v.y;
-            Xs[rr][cq_perm(kk + 2)] = v.z;
-            Xs[rr][cq_perm(kk + 3)] = v.w;
-        }
-        // weight tile: decode codes, * the group norm
-        for (int c = tid; c < CQ_NT * CQ_KT; c += 256) {
-            const int oo = c / CQ_KT, kk = c % CQ_KT;
-            float w = 0.0f;
-            const uint32_t k = k0 + kk;
-            if (o0 + oo < a.out && k < a.in_pad) {
-                const uint8_t *row = a.packed + (uint64_t)(o0 + oo) * a.rowbytes;
-                const uint16_t nb = a.norms[(uint64_t)(o0 + oo) * a.ngroup + k / a.group];
-                w = cbs[cq_code(row, k, a.bits)] * half_bits_to_float(nb);
-            }
-            Ws[oo][cq_perm(kk)] = w;
-        }
+        store(k0, sg);
         __syncthreads();
-        // 32 MFMA steps of K = 2: A = xh rows (lane: row ln, column 2s + lh),
-        // B = W^T (lane: output ln, column 2s + lh)
-        const float *xa = &Xs[wr + ln][lh * (CQ_KT / 2)];
-        const float *wb = &Ws[wo + ln][lh * (CQ_KT / 2)];
+        if (k0 + CQ_KT < a.in_pad)
+            load(k0 + CQ_KT, sg);       // lands during this tile's MFMAs
+        // 32 MFMA steps of K = 2. Step 4j+e takes column 8j+e in lane half 0
+        // and 8j+4+e in lane half 1, for A (xh rows) and B (W^T) alike, so a
+        // lane reads four steps' operands as one 16-byte word.
+        const float *xa = &Xs[wr + ln][4 * lh];
+        const float *wb = &Ws[wo + ln][4 * lh];
 #pragma unroll
-        for (int s4 = 0; s4 < CQ_KT / 2; s4 += 4) {
-            const float4v xv = *reinterpret_cast<const float4v *>(xa + s4);
-            const float4v wv = *reinterpret_cast<const float4v *>(wb + s4);
+        for (int j = 0; j < CQ_KT / 8; j++) {
+            const float4v xv = *reinterpret_cast<const float4v *>(xa + 8 * j);
+            const float4v wv = *reinterpret_cast<const float4v *>(wb + 8 * j);
 #pragma unroll
             for (int e = 0; e < 4; e++)
                 acc = __builtin_amdgcn_mfma_f32_32x32x2f32(xv[e], wv[e], acc, 0, 0, 0);
         }
+        __syncthreads();      // readers done before the next store
     }
     // C layout: lane holds output column ln, rows 8*(i/4) + 4*lh + (i%4)
     const uint32_t oc = o0 + wo + ln;
-    if (oc >= a.out)
+    if (oc >= out)
         return;
 #pragma unroll
     for (int i = 0; i < 16; i++) {
         const uint32_t rr = r0 + wr + 8 * (i >> 2) + 4 * lh + (i & 3);
         if (rr < a.rows)
-            a.y[(uint64_t)rr * a.out + oc] = acc[i];
+            y[(uint64_t)rr * out + oc] = acc[i];
     }
 }
 
@@ -157,10 +204,14 @@ hipError_t launch_cq_prepare(const CqPrepArgs &a, hipStream_t s)
 
 hipError_t launch_cq_gemm(const CqGemmArgs &a, hipStream_t s)
 {
-    if (a.rows == 0 || a.out == 0)
+    if (a.rows == 0 || a.nt == 0 || a.tile0[a.nt] == 0)
         return hipSuccess;
-    const dim3 grid((a.rows + CQ_MT - 1) / CQ_MT, (a.out + CQ_NT - 1) / CQ_NT);
-    hipLaunchKernelGGL(cq_gemm_kernel, grid, dim3(256), 0, s, a);
+    const dim3 grid((a.rows + CQ_MT - 1) / CQ_MT, a.tile0[a.nt]);
+    const bool words = (a.bits == 2 || a.bits == 4) && a.rowbytes % 4 == 0;
+    if (words)
+        hipLaunchKernelGGL(cq_gemm_kernel<true>, grid, dim3(256), 0, s, a);
+    else
+        hipLaunchKernelGGL(cq_gemm_kernel<false>, grid, dim3(256), 0, s, a);
     return hipGetLastError();
 }
 

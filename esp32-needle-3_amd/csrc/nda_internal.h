@@ -169,13 +169,19 @@ struct CqPrepArgs {
     float scale;             /* 1 / sqrt(group) */
 };
 
+/* Up to CQ_MAX_T tensors sharing one prepared activation (same in, group,
+ * bits) in one launch: grid.y walks their 64-output tiles in order. */
+constexpr int CQ_MAX_T = 8;
 struct CqGemmArgs {
-    const float *xh;         /* [rows][in_pad] prepared activations */
-    float *y;                /* [rows][out] */
-    const uint8_t *packed;   /* [out][rowbytes] LSB-first index bitstream */
-    const uint16_t *norms;   /* [out][ngroup] fp16 bits */
-    const float *cb;         /* [1 << bits] codebook (scaled by 1/sqrt(group)) */
-    uint32_t rows, out, in_pad, group, ngroup, bits, rowbytes;
+    const float *xh;                    /* [rows][in_pad] prepared activations */
+    float *y[CQ_MAX_T];                 /* [rows][out[t]] */
+    const uint8_t *packed[CQ_MAX_T];    /* [out][rowbytes] LSB-first index bitstream */
+    const uint16_t *norms[CQ_MAX_T];    /* [out][ngroup] fp16 bits */
+    const float *cb[CQ_MAX_T];          /* [1 << bits] codebook (scaled by 1/sqrt(group)) */
+    uint32_t out[CQ_MAX_T];
+    uint32_t tile0[CQ_MAX_T + 1];       /* first grid.y tile of each tensor; tile0[nt] = total */
+    uint32_t nt;
+    uint32_t rows, in_pad, group, ngroup, bits, rowbytes;
 };
 
 hipError_t launch_cq_prepare(const CqPrepArgs &a, hipStream_t s);

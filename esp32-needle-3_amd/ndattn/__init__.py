@@ -36,7 +36,7 @@ ABI_SYMBOLS = [
     "nda_stream_create", "nda_stream_destroy", "nda_device_sync", "nda_device_info",
     "nda_prof_enable", "nda_prof_read",
     "nda_front_init", "nda_front_weights", "nda_front", "nda_attention", "nda_front_hist",
-    "nda_cq_create", "nda_cq_destroy", "nda_cq_in_pad", "nda_cq_prepare", "nda_cq_gemm",
+    "nda_cq_create", "nda_cq_destroy", "nda_cq_in_pad", "nda_cq_prepare", "nda_cq_gemm", "nda_cq_gemm_many",
     "nda_event_create", "nda_event_destroy", "nda_event_record", "nda_event_elapsed",
 ]
 HOST_SYMBOLS = [
@@ -127,6 +127,7 @@ def lib():
             "nda_cq_in_pad": (u32, [vp]),
             "nda_cq_prepare": (C.c_int, [vp, u32, vp, vp, vp]),
             "nda_cq_gemm": (C.c_int, [vp, u32, vp, vp, vp]),
+            "nda_cq_gemm_many": (C.c_int, [vp, u32, u32, vp, vp, vp]),
             "nda_event_create": (C.c_int, [C.POINTER(vp)]),
             "nda_event_destroy": (C.c_int, [vp]),
             "nda_event_record": (C.c_int, [vp, vp]),
@@ -546,6 +547,14 @@ class CQ:
             self.close()
         except Exception:
             pass
+
+
+def cq_gemm_many(tensors, rows, xh, ys, stream=None):
+    """One launch for tensors sharing a prepared activation: ys[i] = W_i . x."""
+    n = len(tensors)
+    th = (vp * n)(*[t.h for t in tensors])
+    yp = (vp * n)(*[_dp(y) for y in ys])
+    _check(lib().nda_cq_gemm_many(th, n, rows, _dp(xh), yp, stream))
 
 
 class Timer:

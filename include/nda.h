@@ -221,7 +221,7 @@ typedef struct nda_cq nda_cq;
 
 /* Copies one tensor to the device. blob: host, the tensor payload (packed
  * rows then norms); codebook: host, the 2^bits entries for this width
- * (nd_cact_codebook). group a power of two in 8..4096, bits 2..4. */
+ * (nd_cact_codebook). group a power of two in 16..4096, bits 2..4. */
 int nda_cq_create(uint32_t out, uint32_t in, uint32_t group, uint32_t bits, const void *blob,
                   const float *codebook, nda_cq **t);
 int nda_cq_destroy(nda_cq *t);
@@ -233,6 +233,11 @@ uint32_t nda_cq_in_pad(const nda_cq *t);
 int nda_cq_prepare(const nda_cq *t, uint32_t rows, const float *x, float *xh, void *stream);
 /* y[rows][out] = W . x for each row, from its prepared xh (device pointers). */
 int nda_cq_gemm(const nda_cq *t, uint32_t rows, const float *xh, float *y, void *stream);
+/* The same for n <= 8 tensors that share the prepared activation (same in,
+ * group and bits: q/k/v/gate of one layer), in one launch: y_i = W_i . x
+ * into ys[i][rows][out_i]. */
+int nda_cq_gemm_many(const nda_cq *const *ts, uint32_t n, uint32_t rows, const float *xh, float *const *ys,
+                     void *stream);
 
 /* ---- stream-ordered timing ---- */
 int nda_event_create(void **ev);

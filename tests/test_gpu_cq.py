@@ -87,6 +87,34 @@ def test_cq_prepare_and_gemm(shape, rows):
     say("cq worst", worst)
 
 
+def test_cq_gemm_many_matches_single_launches():
+    """q/k/v/gate of the archive's shapes in one launch equal four launches
+    bit for bit (the same tiles, the same order of operations)."""
+    N = nda()
+    say("cq gemm many")
+    shapes = [576, 96, 128, 768]
+    rows, inp = 70, 768
+    ts = [make_cq_tensor(700 + i, o, inp, 128, 2) for i, o in enumerate(shapes)]
+    qs = [N.CQ(o, inp, 128, 2, t.blob, t.cb()) for o, t in zip(shapes, ts)]
+    x = np.stack([det_normal(50 + r, inp) for r in range(rows)])
+    dx = N.DevBuf.from_array(x)
+    dxh = N.DevBuf(rows * qs[0].in_pad * 4)
+    qs[0].prepare(rows, dx, dxh)
+    one = [N.DevBuf(rows * o * 4) for o in shapes]
+    many = [N.DevBuf(rows * o * 4) for o in shapes]
+    for q, y in zip(qs, one):
+        q.gemm(rows, dxh, y)
+    N.cq_gemm_many(qs, rows, dxh, many)
+    N.device_sync()
+    for o, a, b in zip(shapes, one, many):
+        assert np.array_equal(a.to_array(np.uint32, (rows, o)), b.to_array(np.uint32, (rows, o)))
+    bad = N.CQ(64, 512, 128, 2, make_cq_tensor(9, 64, 512, 128, 2).blob, ts[0].cb())
+    with pytest.raises(N.NdaError):
+        N.cq_gemm_many([qs[0], bad], rows, dxh, many[:2])     # another reduction length
+    for q in qs + [bad]:
+        q.close()
+
+
 def test_cq_golden_reference_outputs():
     """The reference's own outputs for the committed CQ vectors."""
     G = np.load(os.path.join(HERE, "golden", "golden.npz"))
