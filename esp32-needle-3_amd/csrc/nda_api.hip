@@ -9,6 +9,7 @@
 #include "nda_internal.h"
 
 #include <algorithm>
+#include <array>
 #include <cmath>
 #include <cstdarg>
 #include <cstdio>
@@ -95,6 +96,12 @@ struct nda_ctx {
     size_t hist_ops_cap = 0;
     std::vector<HistOp> hist_pending;   // applied in order before the next front launch
     std::vector<uint8_t> seen;          // duplicate-id scratch
+
+    // attention block (nda_block_weights): per layer q, k, v, gate, out_proj
+    std::vector<std::array<const nda_cq *, 5>> blk;
+    uint32_t d_model = 0;
+    float *d_bscr = nullptr;            // xh | q | k | v | gate | attn | attn xh, per row
+    size_t bscr_cap = 0;                // floats
 
     bool prof = false;
     std::vector<ProfRec> prof_pending;
@@ -687,7 +694,7 @@ void nda_destroy(nda_ctx *c)
     void *bufs[] = {c->pool, c->d_pages, c->d_prefix_pages, c->d_seqs, c->d_rows, c->d_part,
                     c->d_stage, c->d_pf, c->d_hist, c->d_snap_hist, c->d_prefix_hist,
                     c->d_front_w, c->d_front_norm, c->d_rope, c->d_qfront, c->d_front_rows,
-                    c->d_hist_ops};
+                    c->d_hist_ops, c->d_bscr};
     for (void *b : bufs)
         if (b)
             (void)hipFree(b);
@@ -1831,6 +1838,81 @@ int nda_cq_gemm_many(const nda_cq *const *ts, uint32_t n, uint32_t rows, const f
 int nda_cq_gemm(const nda_cq *t, uint32_t rows, const float *xh, float *y, void *stream)
 {
     return nda_cq_gemm_many(&t, 1, rows, xh, &y, stream);
+}
+
+int nda_block_weights(nda_ctx *c, uint32_t layer, const nda_cq *q, const nda_cq *k, const nda_cq *v,
+                      const nda_cq *gate, const nda_cq *out_proj)
+{
+    if (!c)
+        return NDA_ERR_ARG;
+    if (layer >= c->cfg.n_layers)
+        return fail(c, NDA_ERR_ARG, "layer %u out of range", layer);
+    if (!q || !k || !v || !gate || !out_proj)
+        return fail(c, NDA_ERR_ARG, "null tensor");
+    const nda_config &g = c->cfg;
+    const uint32_t dq = g.n_heads * g.qk_head_dim, dk = g.n_kv_heads * g.qk_head_dim,
+                   dv = g.n_kv_heads * g.v_head_dim, da = g.n_heads * g.v_head_dim;
+    if (q->out != dq || k->out != dk || v->out != dv || gate->out != da || out_proj->in != da)
+        return fail(c, NDA_ERR_ARG, "projection shapes do not match the attention geometry");
+    const uint32_t dm = q->in;
+    for (const nda_cq *t : {k, v, gate})
+        if (t->in != dm || t->group != q->group || t->bits != q->bits)
+            return fail(c, NDA_ERR_ARG, "q/k/v/gate must share d_model, group and width");
+    if (out_proj->out != dm)
+        return fail(c, NDA_ERR_ARG, "out_proj must map back to d_model (%u)", dm);
+    if (c->d_model && c->d_model != dm)
+        return fail(c, NDA_ERR_ARG, "d_model %u differs from an earlier layer's %u", dm, c->d_model);
+    if (c->blk.empty())
+        c->blk.assign(g.n_layers, {nullptr, nullptr, nullptr, nullptr, nullptr});
+    c->d_model = dm;
+    c->blk[layer] = {q, k, v, gate, out_proj};
+    return NDA_OK;
+}
+
+int nda_attention_block(nda_ctx *c, uint32_t layer, uint32_t nseq, const uint32_t *ids, const float *x,
+                        float *out, void *stream)
+{
+    if (!c)
+        return NDA_ERR_ARG;
+    if (layer >= c->cfg.n_layers || c->blk.empty() || !c->blk[layer][0])
+        return fail(c, NDA_ERR_STATE, "no projection weights for layer %u (nda_block_weights)", layer);
+    if (nseq == 0)
+        return NDA_OK;
+    if (!x || !out || !aligned16(x) || !aligned16(out))
+        return fail(c, NDA_ERR_ARG, "x / out null or not 16-byte aligned");
+    hipStream_t st = (hipStream_t)stream;
+    const auto &w = c->blk[layer];
+    const nda_config &g = c->cfg;
+    // per-row scratch, each part a multiple of 4 floats (16-byte aligned)
+    auto r4 = [](size_t n) { return (n + 3) & ~(size_t)3; };
+    const size_t nxh = r4(w[0]->in_pad), nq = r4(w[0]->out), nk = r4(w[1]->out), nv = r4(w[2]->out),
+                 ng = r4(w[3]->out), na = r4((size_t)g.n_heads * g.v_head_dim), nah = r4(w[4]->in_pad);
+    const size_t per = nxh + nq + nk + nv + ng + na + nah;
+    if (int rc = ensure_buf(c, c->d_bscr, c->bscr_cap, per * nseq))
+        return rc;
+    float *xh = c->d_bscr, *yq = xh + nxh * nseq, *yk = yq + nq * nseq, *yv = yk + nk * nseq,
+          *yg = yv + nv * nseq, *att = yg + ng * nseq, *ah = att + na * nseq;
+    // the parts are laid out [part][row] with row strides equal to the
+    // tensors' own widths, as the kernels expect
+    {
+        ProfScope ps(c, NDA_K_PROJ, st);
+        if (int rc = nda_cq_prepare(w[0], nseq, x, xh, st))
+            return fail(c, rc, "q/k/v/gate prepare");
+        const nda_cq *ts[4] = {w[0], w[1], w[2], w[3]};
+        float *ys[4] = {yq, yk, yv, yg};
+        if (int rc = nda_cq_gemm_many(ts, 4, nseq, xh, ys, st))
+            return fail(c, rc, "q/k/v/gate projections");
+    }
+    int rc = c->taps ? nda_attention(c, layer, nseq, ids, yq, yk, yv, yg, att, stream)
+                     : nda_step(c, layer, nseq, ids, yq, yk, yv, yg, att, stream);
+    if (rc)
+        return rc;
+    ProfScope ps(c, NDA_K_PROJ, st);
+    if (int rc2 = nda_cq_prepare(w[4], nseq, att, ah, st))
+        return fail(c, rc2, "out_proj prepare");
+    if (int rc2 = nda_cq_gemm(w[4], nseq, ah, out, st))
+        return fail(c, rc2, "out_proj");
+    return NDA_OK;
 }
 
 int nda_event_create(void **ev)

@@ -27,6 +27,9 @@ struct nd_gpu_model {
     float *h_in, *h_out;
     size_t nq, nk, nv, ng;       /* floats */
     void *stream;
+    /* the whole block (nd_gpu_block_weights): d_model-sized staging */
+    uint32_t dm;
+    float *d_x, *d_y, *h_x, *h_y;
 };
 
 struct nd_gpu_prefix {
@@ -96,6 +99,14 @@ void nd_gpu_close(nd_gpu_model *m)
         nda_host_free(m->h_in);
     if (m->h_out)
         nda_host_free(m->h_out);
+    if (m->d_x)
+        nda_dev_free(m->d_x);
+    if (m->d_y)
+        nda_dev_free(m->d_y);
+    if (m->h_x)
+        nda_host_free(m->h_x);
+    if (m->h_y)
+        nda_host_free(m->h_y);
     nda_destroy(m->ctx);
     if (m->stream)
         nda_stream_destroy(m->stream);
@@ -282,6 +293,52 @@ int nd_gpu_attention_raw(nd_gpu_model *m, uint32_t li, const float *q, const flo
                          const float *v, const float *gate, float *out)
 {
     return attend_host(m, 1, li, q, k, v, gate, out);
+}
+
+int nd_gpu_block_weights(nd_gpu_model *m, uint32_t li, const nda_cq *q, const nda_cq *k, const nda_cq *v,
+                         const nda_cq *gate, const nda_cq *out_proj)
+{
+    int rc = nda_block_weights(m->ctx, li, q, k, v, gate, out_proj);
+    uint32_t dm = 0;
+    if (rc)
+        return rc;
+    dm = nda_cq_in_pad(q);     /* >= d_model; the staging holds either */
+    if (m->dm >= dm)
+        return 0;
+    if (m->d_x) { nda_dev_free(m->d_x); m->d_x = NULL; }
+    if (m->d_y) { nda_dev_free(m->d_y); m->d_y = NULL; }
+    if (m->h_x) { nda_host_free(m->h_x); m->h_x = NULL; }
+    if (m->h_y) { nda_host_free(m->h_y); m->h_y = NULL; }
+    m->dm = 0;
+    if (nda_dev_alloc((void **)&m->d_x, sizeof(float) * dm) ||
+        nda_dev_alloc((void **)&m->d_y, sizeof(float) * dm) ||
+        nda_host_alloc((void **)&m->h_x, sizeof(float) * dm) ||
+        nda_host_alloc((void **)&m->h_y, sizeof(float) * dm))
+        return NDA_ERR_NOMEM;
+    m->dm = dm;
+    return 0;
+}
+
+int nd_gpu_attention_block(nd_gpu_model *m, uint32_t li, const float *xin, uint32_t d_model, float *out)
+{
+    int rc;
+    if (!m->dm || d_model > m->dm)
+        return NDA_ERR_STATE;
+    memcpy(m->h_x, xin, sizeof(float) * d_model);
+    rc = nda_h2d_async(m->d_x, m->h_x, sizeof(float) * d_model, m->stream);
+    if (rc)
+        return rc;
+    rc = nda_attention_block(m->ctx, li, 1, NULL, m->d_x, m->d_y, m->stream);
+    if (rc)
+        return rc;
+    rc = nda_d2h_async(m->h_y, m->d_y, sizeof(float) * d_model, m->stream);
+    if (rc)
+        return rc;
+    rc = nda_sync(m->ctx, m->stream);
+    if (rc)
+        return rc;
+    memcpy(out, m->h_y, sizeof(float) * d_model);
+    return 0;
 }
 
 void nd_gpu_step_end(nd_gpu_model *m)

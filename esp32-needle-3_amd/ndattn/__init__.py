@@ -19,8 +19,8 @@ NDA_OK = 0
 ERRORS = {-1: "NDA_ERR_ARG", -2: "NDA_ERR_NOMEM", -3: "NDA_ERR_HIP", -4: "NDA_ERR_RANGE",
           -5: "NDA_ERR_STATE", -6: "NDA_ERR_UNSUPPORTED", -7: "NDA_ERR_NODEV"}
 KV_INT8, KV_F16 = 0, 1
-K_APPEND, K_DECODE, K_COMBINE, K_PREFILL, K_FRONT = 0, 1, 2, 3, 4
-K_COUNT = 5
+K_APPEND, K_DECODE, K_COMBINE, K_PREFILL, K_FRONT, K_PROJ = 0, 1, 2, 3, 4, 5
+K_COUNT = 6
 FLAG_PREFILL_VALU = 1
 
 # Every symbol include/nda.h declares (checked by the CPU test suite).
@@ -38,12 +38,14 @@ ABI_SYMBOLS = [
     "nda_front_init", "nda_front_weights", "nda_front", "nda_attention", "nda_front_hist",
     "nda_cq_create", "nda_cq_destroy", "nda_cq_in_pad", "nda_cq_prepare", "nda_cq_gemm", "nda_cq_gemm_many",
     "nda_event_create", "nda_event_destroy", "nda_event_record", "nda_event_elapsed",
+    "nda_block_weights", "nda_attention_block",
 ]
 HOST_SYMBOLS = [
     "nd_gpu_open", "nd_gpu_close", "nd_gpu_reset", "nd_gpu_set_sink", "nd_gpu_snapshot",
     "nd_gpu_rewind", "nd_gpu_prefix_save", "nd_gpu_prefix_restore", "nd_gpu_prefix_free",
     "nd_gpu_attention", "nd_gpu_step_end", "nd_gpu_pos", "nd_gpu_n_sink", "nd_gpu_ctx",
     "nd_gpu_front_init", "nd_gpu_front_weights", "nd_gpu_attention_raw",
+    "nd_gpu_block_weights", "nd_gpu_attention_block",
 ]
 
 
@@ -132,6 +134,8 @@ def lib():
             "nda_event_destroy": (C.c_int, [vp]),
             "nda_event_record": (C.c_int, [vp, vp]),
             "nda_event_elapsed": (C.c_int, [vp, vp, C.POINTER(C.c_float)]),
+            "nda_block_weights": (C.c_int, [vp, u32, vp, vp, vp, vp, vp]),
+            "nda_attention_block": (C.c_int, [vp, u32, u32, vp, vp, vp, vp]),
         }
         for name, (res, args) in sig.items():
             f = getattr(L, name)
@@ -175,6 +179,10 @@ def host_lib():
         H.nd_gpu_front_weights.argtypes = [vp, u32, vp, vp, vp, vp, vp]
         H.nd_gpu_attention_raw.restype = C.c_int
         H.nd_gpu_attention_raw.argtypes = [vp, u32, vp, vp, vp, vp, vp]
+        H.nd_gpu_block_weights.restype = C.c_int
+        H.nd_gpu_block_weights.argtypes = [vp, u32, vp, vp, vp, vp, vp]
+        H.nd_gpu_attention_block.restype = C.c_int
+        H.nd_gpu_attention_block.argtypes = [vp, u32, vp, u32, vp]
         _host = H
     return _host
 
@@ -413,6 +421,14 @@ class Context:
         self._c(lib().nda_attention(self.h, layer, nseq, p, _dp(q), _dp(k), _dp(v), _dp(gate), _dp(out),
                                     stream))
 
+    def block_weights(self, layer, q, k, v, gate, out_proj):
+        """CQ objects for one layer (kept alive by the caller)."""
+        self._c(lib().nda_block_weights(self.h, layer, q.h, k.h, v.h, gate.h, out_proj.h))
+
+    def attention_block(self, layer, nseq, x, out, seq_ids=None, stream=None):
+        keep, p = _ids(seq_ids)
+        self._c(lib().nda_attention_block(self.h, layer, nseq, p, _dp(x), _dp(out), stream))
+
     def front_hist(self, seq, snap=False, stream=None):
         """One sequence's tap histories [n_layers][taps][dcol] (host copy)."""
         c = self.cfg
@@ -502,6 +518,15 @@ class GpuSession:
         rc = fn(self.m, li, q.ctypes.data, k.ctypes.data, v.ctypes.data,
                 None if g is None else g.ctypes.data, out.ctypes.data)
         _check(rc)
+        return out
+
+    def block_weights(self, li, q, k, v, gate, out_proj):
+        _check(host_lib().nd_gpu_block_weights(self.m, li, q.h, k.h, v.h, gate.h, out_proj.h))
+
+    def attention_block(self, li, xin):
+        xin = np.ascontiguousarray(xin, np.float32)
+        out = np.zeros(xin.size, np.float32)
+        _check(host_lib().nd_gpu_attention_block(self.m, li, xin.ctypes.data, xin.size, out.ctypes.data))
         return out
 
     def front_init(self, taps, rope_theta, weights, max_pos=0):

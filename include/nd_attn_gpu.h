@@ -22,6 +22,10 @@
  *   nd_gpu_attention_raw  attention() after the projections :2413-2483: tap
  *                         convolution, head norm + RoPE, KV store, attn_heads
  *                         and the gate, from the raw m->q, m->kbuf, m->vbuf
+ *   nd_gpu_block_weights  one layer's q/k/v/gate/out_proj CQ tensors
+ *   nd_gpu_attention_block  the whole attention(m, li, xin, out) :2382-2502:
+ *                         CQ projections, the front (if initialised), store,
+ *                         attention, gate, out_proj
  *
  * The KV part of the session state lives here, and with the front
  * initialised the qkv tap histories too; the rest of the prefix state
@@ -70,6 +74,14 @@ int  nd_gpu_front_weights(nd_gpu_model *m, uint32_t li, const float *tap_q, cons
                           const float *tap_v, const float *norm_q, const float *norm_k);
 int  nd_gpu_attention_raw(nd_gpu_model *m, uint32_t li, const float *q, const float *k,
                           const float *v, const float *gate, float *out);
+/* The whole block: register each layer's CQ tensors (nda_cq_create from the
+ * archive's q_proj, k_proj, v_proj, gate_proj, out_proj; borrowed), then
+ * nd_gpu_attention_block takes the layer's normalised input xin [d_model]
+ * and writes attention()'s output out [d_model] (host arrays). */
+int  nd_gpu_block_weights(nd_gpu_model *m, uint32_t li, const nda_cq *q, const nda_cq *k,
+                          const nda_cq *v, const nda_cq *gate, const nda_cq *out_proj);
+int  nd_gpu_attention_block(nd_gpu_model *m, uint32_t li, const float *xin, uint32_t d_model,
+                            float *out);
 void nd_gpu_step_end(nd_gpu_model *m);
 
 uint32_t nd_gpu_pos(const nd_gpu_model *m);

@@ -239,6 +239,21 @@ int nda_cq_gemm(const nda_cq *t, uint32_t rows, const float *xh, float *y, void 
 int nda_cq_gemm_many(const nda_cq *const *ts, uint32_t n, uint32_t rows, const float *xh, float *const *ys,
                      void *stream);
 
+/* ---- the whole attention block (attention(), engine/src/nd_model.c:2382-2502) ----
+ * Register one layer's five CQ tensors (borrowed: they must outlive the
+ * context's use of them): q [nh*qk][d_model], k [nkv*qk][d_model],
+ * v [nkv*v][d_model], gate [nh*v][d_model], out_proj [d_model][nh*v], all
+ * with one group and width. */
+int nda_block_weights(nda_ctx *ctx, uint32_t layer, const nda_cq *q, const nda_cq *k, const nda_cq *v,
+                      const nda_cq *gate, const nda_cq *out_proj);
+/* attention() for one token of each listed sequence: x [nseq][d_model] (the
+ * layer's normalised input) -> q/k/v/gate projections -> the front (when
+ * initialised; raw projections otherwise go straight to the store) -> KV
+ * store + decode with the gate -> out_proj -> out [nseq][d_model]. Device
+ * pointers, 16-byte aligned. Does not advance pos. */
+int nda_attention_block(nda_ctx *ctx, uint32_t layer, uint32_t nseq, const uint32_t *seq_ids,
+                        const float *x, float *out, void *stream);
+
 /* ---- stream-ordered timing ---- */
 int nda_event_create(void **ev);
 int nda_event_destroy(void *ev);
@@ -299,7 +314,8 @@ int nda_device_info(char *name, size_t name_len, int *cu_count);
 #define NDA_K_COMBINE 2   /* split-KV merge */
 #define NDA_K_PREFILL 3
 #define NDA_K_FRONT   4   /* ND_P_TAPS + ND_P_HNORM (+ the store in nda_attention) */
-#define NDA_K_COUNT   5
+#define NDA_K_PROJ    5   /* ND_P_PREP + ND_P_PROJ: CQ prepare and matvec launches of nda_attention_block */
+#define NDA_K_COUNT   6
 int nda_prof_enable(nda_ctx *ctx, int on);
 /* Synchronises outstanding timed launches, then returns per kind the summed
  * milliseconds and launch counts; resets when reset != 0. */

@@ -890,6 +890,40 @@ void ndo_cq_gemv_lut2(uint32_t out, uint32_t in, uint32_t group, const void *blo
     }
 }
 
+/* ------------------------------------------------ the whole attention block */
+
+int ndo_attention_block(ndo_session *s, uint32_t li, const ndo_front_w *fw, const ndo_block_w *bw,
+                        const float *xin, float *out)
+{
+    uint32_t dq = s->nh * s->qk_hd, dk = s->nkv * s->qk_hd, dv = s->nkv * s->v_hd, da = s->nh * s->v_hd;
+    uint32_t pin = ndo_cq_in_pad(bw->d_model, bw->group), pat = ndo_cq_in_pad(da, bw->group);
+    uint32_t pmax = pin > pat ? pin : pat;
+    float *xh = (float *)malloc(sizeof(float) * pmax);
+    float *lut = (float *)malloc(sizeof(float) * (pmax / 2) * 16);
+    float *q = (float *)malloc(sizeof(float) * dq), *k = (float *)malloc(sizeof(float) * dk);
+    float *v = (float *)malloc(sizeof(float) * dv), *g = (float *)malloc(sizeof(float) * da);
+    float *att = (float *)malloc(sizeof(float) * da);
+    int rc = -2;
+    if (!s->taps)
+        rc = -1;
+    else if (xh && lut && q && k && v && g && att) {
+        ndo_cq_prepare(bw->d_model, bw->group, xin, xh);
+        ndo_cq_lut_build(bw->cb2, xh, pin, lut);
+        ndo_cq_gemv_lut2(dq, bw->d_model, bw->group, bw->blob[0], lut, q);
+        ndo_cq_gemv_lut2(dk, bw->d_model, bw->group, bw->blob[1], lut, k);
+        ndo_cq_gemv_lut2(dv, bw->d_model, bw->group, bw->blob[2], lut, v);
+        ndo_cq_gemv_lut2(da, bw->d_model, bw->group, bw->blob[3], lut, g);
+        ndo_front(s, li, fw, q, k, v);
+        ndo_attention(s, li, q, k, v, g, att);
+        ndo_cq_prepare(da, bw->group, att, xh);
+        ndo_cq_lut_build(bw->cb2, xh, pat, lut);
+        ndo_cq_gemv_lut2(bw->d_model, da, bw->group, bw->blob[4], lut, out);
+        rc = 0;
+    }
+    free(xh); free(lut); free(q); free(k); free(v); free(g); free(att);
+    return rc;
+}
+
 /* ------------------------------------------------------ threaded baseline */
 
 typedef struct {

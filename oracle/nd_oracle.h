@@ -27,6 +27,8 @@
  *   ndo_cq_lut_build, ndo_cq_gemv_lut2    - pinned: reference harness (bit-exact nd_fwht,
  *                                           nd_cq_prepare, nd_cq_gemv_prepared, nd_cq_lut_build,
  *                                           nd_cq_gemv_lut2) + float64 dequantised matvec
+ *   ndo_attention_block                   - pinned: reference harness (bit-exact against the
+ *                                           engine's own attention() over sessions)
  *   ndo_rope_inv, ndo_rope_row            - pinned: float64 bound (<= 1 ulp of the exact value
  *                                           of the rounded argument); the reference computes
  *                                           them inline in nd_model_open / step_hidden, so no
@@ -200,6 +202,22 @@ void ndo_cq_lut_build(const float *cb2, const float *xh, uint32_t in_pad, float 
  * nd_lut2_rows_c, :734-773, :809-839). */
 void ndo_cq_gemv_lut2(uint32_t out, uint32_t in, uint32_t group, const void *blob,
                       const float *lut, float *y);
+
+/* ---- the whole attention block (attention(), nd_model.c:2382-2502) ----
+ * One layer's five 2-bit CQ projections (blob[0..4]: q, k, v, gate, out_proj,
+ * the archive's payloads), the 2-bit codebook slice, d_model and the group. */
+typedef struct {
+    const void *blob[5];
+    const float *cb2;
+    uint32_t d_model, group;
+} ndo_block_w;
+
+/* attention(m, li, xin, out) at s->pos: prepare + pair table + q/k/v/gate
+ * (nd_model.c:2397-2411), the front (:2413-2424), the store and attn_heads
+ * with the gate (:2426-2483), prepare + out_proj (:2495-2501).
+ * xin [d_model] -> out [d_model]. Needs ndo_session_front. */
+int ndo_attention_block(ndo_session *s, uint32_t li, const ndo_front_w *fw, const ndo_block_w *bw,
+                        const float *xin, float *out);
 
 /* ---- CPU baseline: batched fp16 decode, threaded over sequences ----
  *

@@ -47,6 +47,11 @@ class FrontW(C.Structure):
                 ("norm_q", C.c_void_p), ("norm_k", C.c_void_p)]
 
 
+class BlockW(C.Structure):
+    _fields_ = [("blob", C.c_void_p * 5), ("cb2", C.c_void_p), ("d_model", C.c_uint32),
+                ("group", C.c_uint32)]
+
+
 class BatchF16(C.Structure):
     _fields_ = [("nseq", C.c_uint32), ("nh", C.c_uint32), ("nkv", C.c_uint32),
                 ("qk_hd", C.c_uint32), ("v_hd", C.c_uint32),
@@ -118,6 +123,9 @@ def lib():
         L.ndo_session_front.argtypes = [C.POINTER(Session), C.c_uint32, C.c_float]
         L.ndo_session_front.restype = C.c_int
         L.ndo_front.argtypes = [C.POINTER(Session), C.c_uint32, C.POINTER(FrontW)] + [C.c_void_p] * 3
+        L.ndo_attention_block.restype = C.c_int
+        L.ndo_attention_block.argtypes = [C.POINTER(Session), C.c_uint32, C.POINTER(FrontW),
+                                          C.POINTER(BlockW), C.c_void_p, C.c_void_p]
         L.ndo_cq_in_pad.restype = C.c_uint32
         L.ndo_cq_in_pad.argtypes = [C.c_uint32, C.c_uint32]
         L.ndo_fwht.argtypes = [C.c_void_p, C.c_uint32]
@@ -179,6 +187,9 @@ def ref():
         R.ref_cq_prepare.argtypes = [C.c_uint32, C.c_uint32, C.c_void_p, C.c_void_p]
         R.ref_cq_gemv.argtypes = [C.c_uint32] * 4 + [C.c_void_p] * 4
         R.ref_cq_lut2.argtypes = [C.c_uint32] * 3 + [C.c_void_p] * 5
+        R.ref_block_setup.argtypes = [C.c_void_p, C.c_uint32, C.c_uint32, C.c_void_p, C.c_void_p]
+        R.ref_block_setup.restype = C.c_int
+        R.ref_attention_block.argtypes = [C.c_void_p, C.c_uint32] + [C.c_void_p] * 7
         _ref = R
     return _ref
 
@@ -566,3 +577,55 @@ def cq_gemv_lut2(t, xh):
     lib().ndo_cq_lut_build(_ptr(cb), _ptr(xh), t.in_pad, _ptr(lut))
     lib().ndo_cq_gemv_lut2(t.out, t.inp, t.group, _ptr(t.blob), _ptr(lut), _ptr(y))
     return y
+
+
+# ----------------------------------------------------- the whole attention block
+
+class BlockWeights:
+    """Per layer the five 2-bit CQ blobs (q, k, v, gate, out_proj) and the
+    codebook (28 floats, cb2 first)."""
+
+    def __init__(self, blobs, codebook, d_model, group):
+        self.blobs = [[np.ascontiguousarray(b, np.uint8) for b in layer] for layer in blobs]
+        self.codebook = np.ascontiguousarray(codebook, np.float32)
+        self.d_model, self.group = d_model, group
+
+    def struct(self, li):
+        w = BlockW()
+        for t in range(5):
+            w.blob[t] = self.blobs[li][t].ctypes.data
+        w.cb2 = self.codebook.ctypes.data
+        w.d_model, w.group = self.d_model, self.group
+        return w
+
+
+def _block_oracle(self, li, fw, bw, xin):
+    out = np.zeros(bw.d_model, np.float32)
+    xin = np.ascontiguousarray(xin, np.float32)
+    rc = lib().ndo_attention_block(C.byref(self.s), li, C.byref(fw.struct(li)), C.byref(bw.struct(li)),
+                                   _ptr(xin), _ptr(out))
+    if rc:
+        raise ValueError("ndo_attention_block: %d" % rc)
+    return out
+
+
+OracleSession.attention_block = _block_oracle
+
+
+def _block_setup_ref(self, bw):
+    flat = [b for layer in bw.blobs for b in layer]
+    arr = (C.c_void_p * len(flat))(*[b.ctypes.data for b in flat])
+    self._bw = bw
+    if ref().ref_block_setup(self.m, bw.d_model, bw.group, arr, bw.codebook.ctypes.data):
+        raise ValueError("ref_block_setup failed")
+
+
+def _block_ref(self, li, fw, bw, xin):
+    out = np.zeros(bw.d_model, np.float32)
+    xin = np.ascontiguousarray(xin, np.float32)
+    ref().ref_attention_block(self.m, li, *(_ptr(x) for x in fw.arrays(li)), _ptr(xin), _ptr(out))
+    return out
+
+
+RefSession.block_setup = _block_setup_ref
+RefSession.attention_block = _block_ref

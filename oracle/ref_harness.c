@@ -93,6 +93,7 @@ void ref_session_free(void *vm)
     free(m->snap_eg_hist); free(m->snap_q_hist); free(m->snap_k_hist); free(m->snap_v_hist);
     free(m->q_hist); free(m->k_hist); free(m->v_hist);
     free(m->rope_inv); free(m->rope_cos); free(m->rope_sin);
+    free(m->xh); free(m->lut); free(m->layer); free((void *)m->c.base);
     free(m);
 }
 
@@ -299,4 +300,78 @@ void ref_cq_lut2(uint32_t out, uint32_t in, uint32_t group, const void *blob, co
     cq_tensor(&t, out, in, group, 2);
     nd_cq_lut_build(&c, xh, nd_cq_in_pad(&t), lut);
     nd_cq_gemv_lut2(&t, blob, lut, y);
+}
+
+/* ------------------------------------------------- the whole attention() */
+
+/* Give the hand-built model its CQ projections: per layer q, k, v, gate,
+ * out_proj (2-bit, one group) as archive blobs, laid into one buffer as
+ * nd_cact tensors so nd_tier_ptr / nd_cact_data resolve them, plus the gemv
+ * scratch (xh, the pair table). blobs[layer*5 + t]; d_model the projections'
+ * input width. Call once, after ref_session_front. */
+int ref_block_setup(void *vm, uint32_t d_model, uint32_t group, const void *const *blobs,
+                    const float *codebook)
+{
+    nd_model *m = (nd_model *)vm;
+    uint32_t outs[5] = { m->n_heads * m->qk_head_dim, m->k_dim, m->v_dim, m->attn_dim, d_model };
+    uint32_t ins[5] = { d_model, d_model, d_model, d_model, m->attn_dim };
+    size_t total = 0, off = 0, sizes[5];
+    uint32_t li, t, maxpad = 0;
+    uint8_t *base;
+    for (t = 0; t < 5; t++) {
+        uint32_t pad = (ins[t] + group - 1) / group * group;
+        sizes[t] = (size_t)outs[t] * pad / 4 + (size_t)outs[t] * (pad / group) * 2;
+        if (pad > maxpad)
+            maxpad = pad;
+    }
+    for (t = 0; t < 5; t++)
+        total += sizes[t];
+    total *= m->n_layers;
+    base = (uint8_t *)malloc(total + 64);
+    m->layer = (nd_layer *)calloc(m->n_layers, sizeof(nd_layer));
+    m->xh = (float *)calloc(maxpad, sizeof(float));
+    m->lut = (float *)calloc((size_t)maxpad / 2 * 16, sizeof(float));
+    if (!base || !m->layer || !m->xh || !m->lut)
+        return -1;
+    m->c.base = base;
+    m->c.size = total;
+    m->c.codebook = codebook;
+    for (li = 0; li < m->n_layers; li++) {
+        nd_tensor *ts[5] = { &m->layer[li].q_proj, &m->layer[li].k_proj, &m->layer[li].v_proj,
+                             &m->layer[li].gate_proj, &m->layer[li].out_proj };
+        for (t = 0; t < 5; t++) {
+            memset(ts[t], 0, sizeof *ts[t]);
+            ts[t]->ndim = 2;
+            ts[t]->shape[0] = outs[t];
+            ts[t]->shape[1] = ins[t];
+            ts[t]->group = group;
+            ts[t]->bits = 2;
+            ts[t]->offset = off;
+            ts[t]->nbytes = sizes[t];
+            memcpy(base + off, blobs[li * 5 + t], sizes[t]);
+            off += sizes[t];
+        }
+    }
+    return 0;
+}
+
+/* The engine's attention(m, li, xin, out) itself at the model's pos (the
+ * rotary table of nd_model_step_hidden :2949-2954 filled first, restated),
+ * with the front weights in fp16_slot[li][4..8]. */
+void ref_attention_block(void *vm, uint32_t li, const float *tap_q, const float *tap_k, const float *tap_v,
+                         const float *norm_q, const float *norm_k, const float *xin, float *out)
+{
+    nd_model *m = (nd_model *)vm;
+    uint32_t i;
+    for (i = 0; i < m->qk_head_dim / 2; i++) {
+        float angle = (float)m->pos * m->rope_inv[i];
+        m->rope_cos[i] = cosf(angle);
+        m->rope_sin[i] = sinf(angle);
+    }
+    m->fp16_slot[li][4] = (float *)tap_q;
+    m->fp16_slot[li][5] = (float *)tap_k;
+    m->fp16_slot[li][6] = (float *)tap_v;
+    m->fp16_slot[li][7] = (float *)norm_q;
+    m->fp16_slot[li][8] = (float *)norm_k;
+    attention(m, li, xin, out);
 }

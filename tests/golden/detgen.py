@@ -57,3 +57,22 @@ def make_cq_tensor(seed, out, inp, group, bits_, special_norms=False):
     blob = np.concatenate([packed, norms.view(np.uint8).ravel()])
     import ndoracle as O
     return O.CQTensor(out, inp, group, bits_, blob, cb)
+
+
+def make_block_weights(seed, n_layers, nh, nkv, qk, vd, d_model, group=128):
+    """Per layer five synthetic 2-bit CQ tensors: q [nh*qk][d_model],
+    k [nkv*qk][d_model], v [nkv*vd][d_model], gate [nh*vd][d_model],
+    out_proj [d_model][nh*vd]; one shared 28-float codebook."""
+    import ndoracle as O
+    outs = [nh * qk, nkv * qk, nkv * vd, nh * vd, d_model]
+    ins = [d_model] * 4 + [nh * vd]
+    blobs = []
+    cb = None
+    for li in range(n_layers):
+        layer = []
+        for t in range(5):
+            ct = make_cq_tensor(seed + 10 * li + t, outs[t], ins[t], group, 2)
+            layer.append(ct.blob)
+            cb = ct.codebook if cb is None else cb
+        blobs.append(layer)
+    return O.BlockWeights(blobs, cb, d_model, group)

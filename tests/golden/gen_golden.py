@@ -211,6 +211,14 @@ def main():
             R.ref_cq_lut2(o, n, g, t.blob.ctypes.data, t.codebook.ctypes.data, xh.ctypes.data,
                           lut.ctypes.data, y2.ctypes.data)
             out["cq_y2_%d" % i] = y2
+    # the engine's whole attention() over a session (tests/test_oracle_block.py)
+    sys.path.insert(0, os.path.dirname(HERE))
+    from test_oracle_block import BLOCK, replay_block
+    rs = O.RefSession(*BLOCK["geom"])
+    bo, bsaved = replay_block(rs, BLOCK)
+    out["block_out"] = bo.astype(np.float32)
+    for p in bsaved.values():
+        O.ref().ref_prefix_free(p)
     np.savez_compressed(os.path.join(HERE, "golden.npz"), **out)
     print("wrote", os.path.join(HERE, "golden.npz"), {k: v.shape for k, v in out.items()})
 
