@@ -501,6 +501,72 @@ def cq_leg(N, stream, rows=B, d_model=768, reps=20):
             "note": "fp32 MFMA (v_mfma_f32_32x32x2_f32); weights decoded from the 2-bit codes in LDS"}
 
 
+def block_leg(N, stream, nseq=B, steps=5, warmup=2, taps=3, theta=10000.0):
+    """The engine's whole attention() per layer for a batch of sequences at
+    the archive's shapes: 12 q / 2 kv heads, qk 48, v 64, d_model 768,
+    window 384, int8 KV (the engine's format), 2-bit CQ projections, 3 qkv
+    taps; L ~ U[213, 383] stored positions; 8 layers. A step is 8 x
+    nda_attention_block (prepare + q/k/v/gate, front + store, decode with
+    the gate, prepare + out_proj), then pos += 1."""
+    nh, nkv, qk, vd, dm, W = 12, 2, 48, 64, 768, 384
+    rng = np.random.default_rng(SEED + 41)
+    lens = rng.integers(213, 384, nseq)
+    ctx = N.Context(LAYERS, nh, nkv, qk, vd, W, kv_dtype=N.KV_INT8, max_seqs=nseq)
+    ctx.front_init(taps, theta)
+    cqs = []
+    shapes = [(nh * qk, dm), (nkv * qk, dm), (nkv * vd, dm), (nh * vd, dm), (dm, nh * vd)]
+    for li in range(LAYERS):
+        t = lambda dim: (rng.standard_normal((taps, dim)) * 0.5).astype(np.float32)
+        ctx.front_weights(li, t(nh * qk), t(nkv * qk), t(nkv * vd),
+                          (rng.standard_normal(qk) * 0.25).astype(np.float32),
+                          (rng.standard_normal(qk) * 0.25).astype(np.float32))
+        layer = []
+        for o, i in shapes:
+            blob, cb = cq_tensor_synth(rng, o, i)
+            layer.append(N.CQ(o, i, 128, 2, blob, cb))
+        ctx.block_weights(li, *layer)
+        cqs.append(layer)
+    for b in range(nseq):
+        ctx.seq_set_pos(b, int(lens[b]))
+        ctx.seq_reserve(b, W)
+    ctx.kv_fill_normal(nseq, seed=SEED + 42, stream=stream)
+    x = [N.DevBuf(nseq * dm * 4) for _ in range(LAYERS)]
+    y = [N.DevBuf(nseq * dm * 4) for _ in range(LAYERS)]
+    for li in range(LAYERS):
+        x[li].fill_normal(nseq * dm, 0, SEED + 43 + li, stream=stream)
+
+    def step():
+        for li in range(LAYERS):
+            ctx.attention_block(li, nseq, x[li], y[li], stream=stream)
+        ctx.advance(nseq, None, 1, stream=stream)
+
+    for _ in range(warmup):
+        step()
+    ctx.sync(stream)
+    ctx.prof_enable(True)
+    ctx.prof_read(reset=True)
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        step()
+    ctx.sync(stream)
+    el = time.perf_counter() - t0
+    ms, launches = ctx.prof_read(reset=True)
+    ctx.prof_enable(False)
+    per_step = {name: round(ms[k] / steps, 4) for name, k in
+                (("projections_ms", N.K_PROJ), ("front_store_ms", N.K_FRONT), ("decode_ms", N.K_DECODE),
+                 ("combine_ms", N.K_COMBINE))}
+    ctx.close()
+    for layer in cqs:
+        for c in layer:
+            c.close()
+    return {"workload": "the engine's attention() per layer for %d sequences: 12/2 heads, qk 48, v 64, d_model 768, "
+                        "window 384, int8 KV, 2-bit CQ projections, 3 qkv taps, L ~ U[213,383], 8 layers" % nseq,
+            "tokens_per_s": round(nseq * steps / el, 1), "ms_per_step": round(el * 1e3 / steps, 4),
+            "kernel_ms_per_step": per_step,
+            "note": "parity of the same path is held by tests/test_gpu_block.py (the engine's own attention() "
+                    "golden session replayed within 5e-6)"}
+
+
 def front_leg(N, stream, steps=5, warmup=2, taps=3, theta=10000.0):
     """The headline decode with the attention front: per layer nda_attention
     takes RAW q/k/v projections (tap convolution over 3 taps, per-head
@@ -682,6 +748,9 @@ def main():
     front = front_leg(N, stream)
     log("front: %.0f tok/s, step %.3f ms, front kernel %.4f ms (%.0f GB/s)" % (
         front["tokens_per_s"], front["ms_per_step"], front["front_kernel_ms"], front["front_GBps"]))
+    block = block_leg(N, stream)
+    log("block: %.0f tok/s, step %.3f ms, per step %s" % (block["tokens_per_s"], block["ms_per_step"],
+                                                          block["kernel_ms_per_step"]))
     cq = cq_leg(N, stream)
     log("cq: block %.4f ms (%.1f TFLOP/s), gate gemm %.4f ms (%.1f TFLOP/s fp32 MFMA), sampled rel delta %.3g" % (
         cq["block_ms"], cq["block_tflops"], cq["gate_gemm_ms"], cq["gate_gemm_tflops"], cq["max_rel_delta_sampled"]))
@@ -742,6 +811,7 @@ def main():
         "engine_session": engine,
         "front": front,
         "cq_projections": cq,
+        "attention_block": block,
         "shared_prefix": shared,
         "max_abs_delta_sampled": worst,
         "device": name,

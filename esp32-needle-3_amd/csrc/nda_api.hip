@@ -1658,8 +1658,6 @@ int nda_kv_fill_normal(nda_ctx *c, uint32_t nseq, const uint32_t *ids, uint64_t 
 {
     if (!c)
         return NDA_ERR_ARG;
-    if (c->cfg.kv_dtype != NDA_KV_F16)
-        return fail(c, NDA_ERR_UNSUPPORTED, "synthetic fill is fp16 only");
     if (int rc = check_ids(c, nseq, ids))
         return rc;
     hipStream_t st = (hipStream_t)stream;

@@ -201,15 +201,24 @@ __device__ __forceinline__ void attn_step(AttnState<ES, DK, DV, REP, G, NP, NW> 
 #pragma unroll
         for (int j = 0; j < NP; j++)
             mx = fmaxf(mx, sc[j]);
-        const float r = fast_exp2(st.m[t] - mx);
-        st.m[t] = mx;
-        st.l[t] *= r;
+        // Lazy running max: move it (and rescale the state) only when a score
+        // exceeds it by more than 2^8, so the weights stay <= 256; otherwise
+        // the rescale sweep over the accumulators is skipped for the whole
+        // wave. The state (m, l, acc) is the same softmax up to rounding.
+        const bool grow = mx > st.m[t] + 8.0f;
+        if (__builtin_expect(__ballot(grow) != 0, 0)) {
+            const float mnew = grow ? mx : st.m[t];
+            const float r = fast_exp2(st.m[t] - mnew);
+            st.m[t] = mnew;
+            st.l[t] *= r;
 #pragma unroll
-        for (int e = 0; e < C::EV; e++)
-            st.acc[t][e] *= r;
+            for (int e = 0; e < C::EV; e++)
+                st.acc[t][e] *= r;
+        }
+        const float mref = st.m[t];
 #pragma unroll
         for (int j = 0; j < NP; j++) {
-            const float p = fast_exp2(sc[j] - mx);
+            const float p = fast_exp2(sc[j] - mref);
             st.l[t] += p;
             float pv = ES == 1 ? p * vs[j] : p;
             if constexpr (MASK)
@@ -584,9 +593,11 @@ __global__ __launch_bounds__(256) void fill_normal_kernel(void *dst, uint64_t n,
     }
 }
 
-// Fill own slots [0, n_own) of every listed sequence (fp16). The value of
-// (layer, seq, slot, head, element) depends on those indices only.
-template <int DK, int DV>
+// Fill own slots [0, n_own) of every listed sequence. The value of
+// (layer, seq, slot, head, element) depends on those indices only. ES 1:
+// int8 codes round(32 x) clamped to +-127 with scales 1/32, so the
+// dequantised values are N(0,1) to within the code step.
+template <int ES, int DK, int DV>
 __global__ __launch_bounds__(256) void fill_kv_kernel(FillKvArgs a)
 {
     const uint32_t bi = blockIdx.x, l = blockIdx.y;
@@ -613,11 +624,25 @@ __global__ __launch_bounds__(256) void fill_kv_kernel(FillKvArgs a)
             continue;
         uint8_t *hb = lp + (uint64_t)pg * a.pg.page_bytes + g * a.pg.head_bytes;
         const int off = slot & (P - 1);
-        const _Float16 x = (_Float16)normal_from(splitmix64(key + i));
-        if (e < DK)
-            reinterpret_cast<_Float16 *>(hb + (uint64_t)off * DK * 2)[e] = x;
-        else
-            reinterpret_cast<_Float16 *>(hb + (uint64_t)P * DK * 2 + (uint64_t)off * DV * 2)[e - DK] = x;
+        const float z = normal_from(splitmix64(key + i));
+        if constexpr (ES == 2) {
+            const _Float16 x = (_Float16)z;
+            if (e < DK)
+                reinterpret_cast<_Float16 *>(hb + (uint64_t)off * DK * 2)[e] = x;
+            else
+                reinterpret_cast<_Float16 *>(hb + (uint64_t)P * DK * 2 + (uint64_t)off * DV * 2)[e - DK] = x;
+        } else {
+            const int8_t c = (int8_t)(int)fminf(fmaxf(__builtin_rintf(z * 32.0f), -127.0f), 127.0f);
+            if (e < DK)
+                reinterpret_cast<int8_t *>(hb + (uint64_t)off * DK)[e] = c;
+            else
+                reinterpret_cast<int8_t *>(hb + (uint64_t)P * DK + (uint64_t)off * DV)[e - DK] = c;
+            float *sc = reinterpret_cast<float *>(hb + (uint64_t)P * (DK + DV));
+            if (e == 0)
+                sc[off] = 1.0f / 32.0f;
+            else if (e == DK)
+                sc[P + off] = 1.0f / 32.0f;
+        }
     }
 }
 
@@ -629,12 +654,21 @@ __global__ __launch_bounds__(256) void fill_kv_kernel(FillKvArgs a)
 template <int ES, int DK, int REP>
 constexpr int lanes_per_pos() { return ES == 2 ? 8 : ((REP >= 8 && DK % 64 == 0) ? 8 : 4); }
 
-// Waves per decode work-group and positions per lane group per step
-// (build-time tuning knobs).
-#ifndef NDA_ATT_NW
-#define NDA_ATT_NW 8
+// Waves per decode work-group: 8 for MHA and narrow GQA, whose per-lane
+// state merges cheaply and whose rows are split across many waves; one wave
+// for wide GQA (rep >= 4), where each lane carries rep heads of state and the
+// cross-wave merge would cost more than it parallelises (rows of a few
+// hundred positions: 4.4x faster at 12 q / 2 kv heads, int8). NDA_ATT_NW
+// fixes one value for every geometry (a build-time tuning knob).
+template <int REP>
+constexpr int att_nw()
+{
+#ifdef NDA_ATT_NW
+    return NDA_ATT_NW;
+#else
+    return REP >= 4 ? 1 : 8;
 #endif
-constexpr int ATT_NW = NDA_ATT_NW;
+}
 
 // Positions per lane group per step: as many loads in flight as registers
 // allow without spilling (the int8 and wide-GQA states are larger).
@@ -667,8 +701,8 @@ hipError_t launch_attend(const Geo &g, const AttnArgs &a, hipStream_t s)
     dim3 grid(a.rows * a.pg.nkv, a.max_chunks);
 #define X(ES, DK, DV, REP)                                                                      \
     if (es_of(g) == ES && g.dk == DK && g.dv == DV && g.rep == REP) {                          \
-        hipLaunchKernelGGL((attend_kernel<ES, DK, DV, REP, lanes_per_pos<ES, DK, REP>(), att_np<ES, REP>(), ATT_NW>), \
-                           grid, dim3(64 * ATT_NW), 0, s, a);                                   \
+        hipLaunchKernelGGL((attend_kernel<ES, DK, DV, REP, lanes_per_pos<ES, DK, REP>(), att_np<ES, REP>(), att_nw<REP>()>), \
+                           grid, dim3(64 * att_nw<REP>()), 0, s, a);                            \
         return hipGetLastError();                                                               \
     }
     NDA_FOR_GEOMETRIES(X)
@@ -739,18 +773,17 @@ hipError_t launch_scatter(const Geo &g, const StageArgs &a, hipStream_t s) { ret
 
 hipError_t launch_fill_kv(const Geo &g, const FillKvArgs &a, hipStream_t s)
 {
-    if (!g.kv_f16)
-        return hipErrorNotSupported;
     if (a.nseq == 0 || a.n_layers == 0)
         return hipSuccess;
     dim3 grid(a.nseq, a.n_layers);
-    if (g.dk == 64 && g.dv == 64)
-        hipLaunchKernelGGL((fill_kv_kernel<64, 64>), grid, dim3(256), 0, s, a);
-    else if (g.dk == 48 && g.dv == 64)
-        hipLaunchKernelGGL((fill_kv_kernel<48, 64>), grid, dim3(256), 0, s, a);
-    else
-        return hipErrorNotSupported;
-    return hipGetLastError();
+#define X(ES, DK, DV)                                                                          \
+    if ((g.kv_f16 ? 2 : 1) == ES && g.dk == DK && g.dv == DV) {                               \
+        hipLaunchKernelGGL((fill_kv_kernel<ES, DK, DV>), grid, dim3(256), 0, s, a);           \
+        return hipGetLastError();                                                              \
+    }
+    NDA_FOR_SHAPES(X)
+#undef X
+    return hipErrorNotSupported;
 }
 
 hipError_t launch_advance(SeqDev *seqs, const uint32_t *seq_list, uint32_t nseq, uint32_t n, hipStream_t s)

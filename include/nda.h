@@ -278,7 +278,8 @@ int nda_kv_write(nda_ctx *ctx, uint32_t layer, uint32_t seq, uint32_t p0, uint32
 /* Fills the stored K/V of positions [0, pos) of every listed sequence, every
  * layer, with N(0,1) values from a counter-based generator keyed by (seed,
  * layer, sequence, position, head, element) - independent of page placement.
- * F16 only (INT8: NDA_ERR_UNSUPPORTED). Synthetic benchmark data. */
+ * INT8: codes round(32 x) clamped to +-127, scales 1/32. Synthetic benchmark
+ * data. */
 int nda_kv_fill_normal(nda_ctx *ctx, uint32_t nseq, const uint32_t *seq_ids, uint64_t seed,
                        void *stream);
 
