@@ -501,17 +501,16 @@ def cq_leg(N, stream, rows=B, d_model=768, reps=20):
             "note": "fp32 MFMA (v_mfma_f32_32x32x2_f32); weights decoded from the 2-bit codes in LDS"}
 
 
-def block_leg(N, stream, nseq=B, steps=5, warmup=2, taps=3, theta=10000.0):
-    """The engine's whole attention() per layer for a batch of sequences at
-    the archive's shapes: 12 q / 2 kv heads, qk 48, v 64, d_model 768,
-    window 384, int8 KV (the engine's format), 2-bit CQ projections, 3 qkv
-    taps; L ~ U[213, 383] stored positions; 8 layers. A step is 8 x
-    nda_attention_block (prepare + q/k/v/gate, front + store, decode with
-    the gate, prepare + out_proj), then pos += 1."""
-    nh, nkv, qk, vd, dm, W = 12, 2, 48, 64, 768, 384
-    rng = np.random.default_rng(SEED + 41)
-    lens = rng.integers(213, 384, nseq)
-    ctx = N.Context(LAYERS, nh, nkv, qk, vd, W, kv_dtype=N.KV_INT8, max_seqs=nseq)
+ENGINE_GEOM = (12, 2, 48, 64)      # q heads, kv heads, qk and v head dims of the archive
+ENGINE_D_MODEL, ENGINE_WINDOW = 768, 384
+
+
+def engine_block_ctx(N, rng, nseq, taps, theta):
+    """A context at the archive's attention shapes with synthetic front
+    weights and 2-bit CQ projections (group 128) registered for every layer."""
+    nh, nkv, qk, vd = ENGINE_GEOM
+    dm = ENGINE_D_MODEL
+    ctx = N.Context(LAYERS, nh, nkv, qk, vd, ENGINE_WINDOW, kv_dtype=N.KV_INT8, max_seqs=nseq)
     ctx.front_init(taps, theta)
     cqs = []
     shapes = [(nh * qk, dm), (nkv * qk, dm), (nkv * vd, dm), (nh * vd, dm), (dm, nh * vd)]
@@ -526,6 +525,81 @@ def block_leg(N, stream, nseq=B, steps=5, warmup=2, taps=3, theta=10000.0):
             layer.append(N.CQ(o, i, 128, 2, blob, cb))
         ctx.block_weights(li, *layer)
         cqs.append(layer)
+    return ctx, cqs
+
+
+def block_prefill_leg(N, stream, nseq=1024, npre=213, nmin=32, nmax=64, reps=3, taps=3, theta=10000.0):
+    """The engine's request flow through whole attention blocks, layer-batched:
+    one sequence primes the 213-token schema prefix (nda_prefill_block per
+    layer), it is shared (nda_prefix_build), then nseq requests attach to it
+    and each prefills n ~ U[nmin, nmax] prompt tokens: per layer ONE
+    nda_prefill_block over all sum(n) tokens (projections over every row,
+    the front per sequence chunk, store + causal attention with the gate,
+    out_proj). Archive shapes, int8 KV, 8 layers. Timed: the 8 layer calls
+    of one pass; the attach before each pass is not."""
+    rng = np.random.default_rng(SEED + 61)
+    n = rng.integers(nmin, nmax + 1, nseq)
+    ctx, cqs = engine_block_ctx(N, rng, nseq + 1, taps, theta)
+    dm, builder = ENGINE_D_MODEL, nseq
+    T = int(n.sum())
+    x = [N.DevBuf(max(T, npre) * dm * 4) for _ in range(LAYERS)]
+    y = N.DevBuf(max(T, npre) * dm * 4)
+    for li in range(LAYERS):
+        x[li].fill_normal(max(T, npre) * dm, 0, SEED + 62 + li, stream=stream)
+    for li in range(LAYERS):
+        ctx.prefill_block(li, 1, [npre], x[li], y, seq_ids=[builder], stream=stream)
+    ctx.advance(1, [builder], npre, stream=stream)
+    pid = ctx.prefix_build(builder, stream=stream)
+    best, kms = None, None
+    for _ in range(reps):
+        for b in range(nseq):
+            ctx.seq_attach(b, pid, stream=stream)
+        ctx.sync(stream)
+        ctx.prof_enable(True)
+        ctx.prof_read(reset=True)
+        t0 = time.perf_counter()
+        for li in range(LAYERS):
+            ctx.prefill_block(li, nseq, n, x[li], y, stream=stream)
+        ctx.sync(stream)
+        el = time.perf_counter() - t0
+        ms, _ = ctx.prof_read(reset=True)
+        ctx.prof_enable(False)
+        if best is None or el < best:
+            best, kms = el, ms
+    per_pass = {name: round(kms[k], 4) for name, k in
+                (("projections_ms", N.K_PROJ), ("front_ms", N.K_FRONT), ("append_ms", N.K_APPEND),
+                 ("prefill_ms", N.K_PREFILL))}
+    nh, nkv, qk, vd = ENGINE_GEOM
+    flops = float(sum(nh * 2 * (qk + vd) * (npre * int(t) + int(t) * (int(t) + 1) / 2) for t in n)) * LAYERS
+    for b in range(nseq + 1):
+        ctx.seq_reset(b)
+    ctx.prefix_free(pid)
+    ctx.close()
+    for layer in cqs:
+        for c in layer:
+            c.close()
+    return {"workload": "layer-batched prefill of the engine's attention() blocks: %d requests on one shared "
+                        "%d-token prefix, n ~ U[%d,%d] prompt tokens each (%d rows per layer call), 12/2 heads, "
+                        "qk 48, v 64, d_model 768, int8 KV, 2-bit CQ projections, 3 qkv taps, 8 layers"
+                        % (nseq, npre, nmin, nmax, T),
+            "prompt_tokens_per_s": round(T / best, 1), "ms_per_pass": round(best * 1e3, 3),
+            "kernel_ms_per_pass": per_pass,
+            "attention_tflops": round(flops / (kms[N.K_PREFILL] * 1e-3) / 1e12, 1),
+            "note": "parity of the same path is held by tests/test_gpu_prefill_block.py (against the engine's "
+                    "attention() stepped one token at a time)"}
+
+
+def block_leg(N, stream, nseq=B, steps=5, warmup=2, taps=3, theta=10000.0):
+    """The engine's whole attention() per layer for a batch of sequences at
+    the archive's shapes: 12 q / 2 kv heads, qk 48, v 64, d_model 768,
+    window 384, int8 KV (the engine's format), 2-bit CQ projections, 3 qkv
+    taps; L ~ U[213, 383] stored positions; 8 layers. A step is 8 x
+    nda_attention_block (prepare + q/k/v/gate, front + store, decode with
+    the gate, prepare + out_proj), then pos += 1."""
+    rng = np.random.default_rng(SEED + 41)
+    lens = rng.integers(213, 384, nseq)
+    ctx, cqs = engine_block_ctx(N, rng, nseq, taps, theta)
+    dm, W = ENGINE_D_MODEL, ENGINE_WINDOW
     for b in range(nseq):
         ctx.seq_set_pos(b, int(lens[b]))
         ctx.seq_reserve(b, W)
@@ -751,6 +825,11 @@ def main():
     block = block_leg(N, stream)
     log("block: %.0f tok/s, step %.3f ms, per step %s" % (block["tokens_per_s"], block["ms_per_step"],
                                                           block["kernel_ms_per_step"]))
+    block_pf = None
+    if not args.no_prefill:
+        block_pf = block_prefill_leg(N, stream)
+        log("block prefill: %.0f prompt tok/s, pass %.3f ms, per pass %s" % (
+            block_pf["prompt_tokens_per_s"], block_pf["ms_per_pass"], block_pf["kernel_ms_per_pass"]))
     cq = cq_leg(N, stream)
     log("cq: block %.4f ms (%.1f TFLOP/s), gate gemm %.4f ms (%.1f TFLOP/s fp32 MFMA), sampled rel delta %.3g" % (
         cq["block_ms"], cq["block_tflops"], cq["gate_gemm_ms"], cq["gate_gemm_tflops"], cq["max_rel_delta_sampled"]))
@@ -812,6 +891,7 @@ def main():
         "front": front,
         "cq_projections": cq,
         "attention_block": block,
+        "attention_block_prefill": block_pf,
         "shared_prefix": shared,
         "max_abs_delta_sampled": worst,
         "device": name,

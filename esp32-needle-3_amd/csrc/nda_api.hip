@@ -1097,6 +1097,23 @@ int nda_step(nda_ctx *c, uint32_t layer, uint32_t nseq, const uint32_t *ids, con
     return decode_impl(c, layer, nseq, ids, q, k, v, gate, out, stream);
 }
 
+// What a chunk must satisfy before nda_prefill changes anything: no ring
+// wrap inside it, and an attached sequence positioned past its prefix.
+static int prefill_check(nda_ctx *c, uint32_t nseq, const uint32_t *ids, const uint32_t *n_tokens)
+{
+    for (uint32_t b = 0; b < nseq; b++) {
+        const uint32_t qq = sid(ids, b);
+        const SeqHost &s = c->seqs[qq];
+        if ((uint64_t)s.pos + n_tokens[b] > c->cfg.window)
+            return fail(c, NDA_ERR_RANGE,
+                        "sequence %u: prefill of %u tokens at position %u would wrap the ring (window %u)",
+                        qq, n_tokens[b], s.pos, c->cfg.window);
+        if (s.prefix >= 0 && s.pos < s.n_sink)
+            return fail(c, NDA_ERR_STATE, "sequence %u positioned inside its shared prefix", qq);
+    }
+    return NDA_OK;
+}
+
 int nda_prefill(nda_ctx *c, uint32_t layer, uint32_t nseq, const uint32_t *ids, const uint32_t *n_tokens,
                 const float *q, const float *k, const float *v, const float *gate, float *out, void *stream)
 {
@@ -1108,19 +1125,14 @@ int nda_prefill(nda_ctx *c, uint32_t layer, uint32_t nseq, const uint32_t *ids, 
         return fail(c, NDA_ERR_ARG, "layer %u out of range", layer);
     if (int rc = check_ids(c, nseq, ids))
         return rc;
+    if (int rc = prefill_check(c, nseq, ids, n_tokens))
+        return rc;
     hipStream_t st = (hipStream_t)stream;
     uint64_t rows = 0;
     uint32_t max_total = 0;
     uint64_t sum_total = 0;
     for (uint32_t b = 0; b < nseq; b++) {
-        const uint32_t qq = sid(ids, b);
-        const SeqHost &s = c->seqs[qq];
-        if ((uint64_t)s.pos + n_tokens[b] > c->cfg.window)
-            return fail(c, NDA_ERR_RANGE,
-                        "sequence %u: prefill of %u tokens at position %u would wrap the ring (window %u)",
-                        qq, n_tokens[b], s.pos, c->cfg.window);
-        if (s.prefix >= 0 && s.pos < s.n_sink)
-            return fail(c, NDA_ERR_STATE, "sequence %u positioned inside its shared prefix", qq);
+        const SeqHost &s = c->seqs[sid(ids, b)];
         if (n_tokens[b]) {
             const Vis v = visible(s, s.pos + n_tokens[b] - 1, c->cfg.window);
             max_total = std::max(max_total, v.n_sh + v.n_own);
@@ -1910,6 +1922,78 @@ int nda_attention_block(nda_ctx *c, uint32_t layer, uint32_t nseq, const uint32_
         return fail(c, rc2, "out_proj prepare");
     if (int rc2 = nda_cq_gemm(w[4], nseq, ah, out, st))
         return fail(c, rc2, "out_proj");
+    return NDA_OK;
+}
+
+int nda_prefill_block(nda_ctx *c, uint32_t layer, uint32_t nseq, const uint32_t *ids, const uint32_t *n_tokens,
+                      const float *x, float *out, void *stream)
+{
+    if (!c)
+        return NDA_ERR_ARG;
+    if (layer >= c->cfg.n_layers || c->blk.empty() || !c->blk[layer][0])
+        return fail(c, NDA_ERR_STATE, "no projection weights for layer %u (nda_block_weights)", layer);
+    if (nseq == 0)
+        return NDA_OK;
+    if (!n_tokens || !x || !out || !aligned16(x) || !aligned16(out))
+        return fail(c, NDA_ERR_ARG, "n_tokens / x / out null, or x / out not 16-byte aligned");
+    if (int rc = check_ids(c, nseq, ids))
+        return rc;
+    if (int rc = prefill_check(c, nseq, ids, n_tokens))
+        return rc;
+    if (c->taps)
+        if (int rc = front_check(c, layer, nseq, ids, n_tokens))
+            return rc;
+    // Pages first: a full pool is reported before anything (tap histories
+    // included) has changed.
+    uint64_t rows = 0;
+    for (uint32_t b = 0; b < nseq; b++) {
+        const uint32_t qq = sid(ids, b);
+        if (n_tokens[b])
+            if (int rc = back_positions(c, qq, c->seqs[qq].pos, n_tokens[b]))
+                return rc;
+        rows += n_tokens[b];
+    }
+    if (rows == 0)
+        return NDA_OK;
+    if (rows > (1u << 26))
+        return fail(c, NDA_ERR_ARG, "too many prefill tokens (%llu)", (unsigned long long)rows);
+    hipStream_t st = (hipStream_t)stream;
+    const auto &w = c->blk[layer];
+    const nda_config &g = c->cfg;
+    auto r4 = [](size_t n) { return (n + 3) & ~(size_t)3; };
+    const size_t nxh = r4(w[0]->in_pad), nq = r4(w[0]->out), nk = r4(w[1]->out), nv = r4(w[2]->out),
+                 ng = r4(w[3]->out), na = r4((size_t)g.n_heads * g.v_head_dim), nah = r4(w[4]->in_pad);
+    const size_t nf = c->taps ? nq + nk + nv : 0;    // the front's outputs
+    const size_t per = nxh + nq + nk + nv + ng + nf + na + nah;
+    if (int rc = ensure_buf(c, c->d_bscr, c->bscr_cap, per * rows))
+        return rc;
+    // [part][row], each part at its tensor's own row width
+    float *xh = c->d_bscr, *yq = xh + nxh * rows, *yk = yq + nq * rows, *yv = yk + nk * rows,
+          *yg = yv + nv * rows, *fq = yg + ng * rows, *fk = fq + nq * rows, *fv = fk + nk * rows,
+          *att = yg + (ng + nf) * rows, *ah = att + na * rows;
+    const uint32_t nr = (uint32_t)rows;
+    {
+        ProfScope ps(c, NDA_K_PROJ, st);
+        if (int rc = nda_cq_prepare(w[0], nr, x, xh, st))
+            return fail(c, rc, "q/k/v/gate prepare");
+        const nda_cq *ts[4] = {w[0], w[1], w[2], w[3]};
+        float *ys[4] = {yq, yk, yv, yg};
+        if (int rc = nda_cq_gemm_many(ts, 4, nr, xh, ys, st))
+            return fail(c, rc, "q/k/v/gate projections");
+    }
+    if (c->taps) {
+        if (int rc = nda_front(c, layer, nseq, ids, n_tokens, yq, yk, yv, fq, fk, fv, stream))
+            return rc;
+        if (int rc = nda_prefill(c, layer, nseq, ids, n_tokens, fq, fk, fv, yg, att, stream))
+            return rc;
+    } else if (int rc = nda_prefill(c, layer, nseq, ids, n_tokens, yq, yk, yv, yg, att, stream)) {
+        return rc;
+    }
+    ProfScope ps(c, NDA_K_PROJ, st);
+    if (int rc = nda_cq_prepare(w[4], nr, att, ah, st))
+        return fail(c, rc, "out_proj prepare");
+    if (int rc = nda_cq_gemm(w[4], nr, ah, out, st))
+        return fail(c, rc, "out_proj");
     return NDA_OK;
 }
 

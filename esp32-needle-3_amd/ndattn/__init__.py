@@ -38,7 +38,7 @@ ABI_SYMBOLS = [
     "nda_front_init", "nda_front_weights", "nda_front", "nda_attention", "nda_front_hist",
     "nda_cq_create", "nda_cq_destroy", "nda_cq_in_pad", "nda_cq_prepare", "nda_cq_gemm", "nda_cq_gemm_many",
     "nda_event_create", "nda_event_destroy", "nda_event_record", "nda_event_elapsed",
-    "nda_block_weights", "nda_attention_block",
+    "nda_block_weights", "nda_attention_block", "nda_prefill_block",
 ]
 HOST_SYMBOLS = [
     "nd_gpu_open", "nd_gpu_close", "nd_gpu_reset", "nd_gpu_set_sink", "nd_gpu_snapshot",
@@ -136,6 +136,7 @@ def lib():
             "nda_event_elapsed": (C.c_int, [vp, vp, C.POINTER(C.c_float)]),
             "nda_block_weights": (C.c_int, [vp, u32, vp, vp, vp, vp, vp]),
             "nda_attention_block": (C.c_int, [vp, u32, u32, vp, vp, vp, vp]),
+            "nda_prefill_block": (C.c_int, [vp, u32, u32, vp, vp, vp, vp, vp]),
         }
         for name, (res, args) in sig.items():
             f = getattr(L, name)
@@ -428,6 +429,12 @@ class Context:
     def attention_block(self, layer, nseq, x, out, seq_ids=None, stream=None):
         keep, p = _ids(seq_ids)
         self._c(lib().nda_attention_block(self.h, layer, nseq, p, _dp(x), _dp(out), stream))
+
+    def prefill_block(self, layer, nseq, n_tokens, x, out, seq_ids=None, stream=None):
+        """x / out [sum(n_tokens)][d_model] device, packed token-major per sequence."""
+        keep, p = _ids(seq_ids)
+        n = np.ascontiguousarray(n_tokens, np.uint32)
+        self._c(lib().nda_prefill_block(self.h, layer, nseq, p, n.ctypes.data, _dp(x), _dp(out), stream))
 
     def front_hist(self, seq, snap=False, stream=None):
         """One sequence's tap histories [n_layers][taps][dcol] (host copy)."""

@@ -253,6 +253,19 @@ int nda_block_weights(nda_ctx *ctx, uint32_t layer, const nda_cq *q, const nda_c
  * pointers, 16-byte aligned. Does not advance pos. */
 int nda_attention_block(nda_ctx *ctx, uint32_t layer, uint32_t nseq, const uint32_t *seq_ids,
                         const float *x, float *out, void *stream);
+/* The same block for a chunk of n_tokens[b] tokens of each listed sequence
+ * at positions pos, pos+1, ..., all tokens of the layer at once: what
+ * n_tokens[b] successive attention() calls of this layer compute (the engine
+ * prefills one token at a time: esp32/main/main.c:233-234, :312-315; taps
+ * and the KV store depend only on earlier tokens, so a layer can take the
+ * chunk in one pass). x / out [T][d_model], packed token-major per sequence
+ * as nda_prefill's inputs, device, 16-byte aligned. The projections run
+ * over all T rows, the front over each sequence's chunk, then nda_prefill
+ * (store + causal attention with the gate) and out_proj. Requires
+ * pos + n <= window (NDA_ERR_RANGE); rejected chunks, and a full page pool,
+ * change nothing. Does not advance pos. */
+int nda_prefill_block(nda_ctx *ctx, uint32_t layer, uint32_t nseq, const uint32_t *seq_ids,
+                      const uint32_t *n_tokens, const float *x, float *out, void *stream);
 
 /* ---- stream-ordered timing ---- */
 int nda_event_create(void **ev);
