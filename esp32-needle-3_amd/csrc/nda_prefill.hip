@@ -36,6 +36,13 @@ typedef float float16v __attribute__((ext_vector_type(16)));
 
 constexpr int PF_KT = 32;   // keys per tile
 
+__device__ __forceinline__ float max3(float a, float b, float c)
+{
+    float r;
+    asm("v_max3_f32 %0, %1, %2, %3" : "=v"(r) : "v"(a), "v"(b), "v"(c));
+    return r;
+}
+
 __device__ __forceinline__ float16v mfma32(half8 a, half8 b, float16v c)
 {
     return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
@@ -288,12 +295,19 @@ void prefill_kernel(PrefillArgs a)
 
         // ---- S^T = K . Q^T (keys x rows), accumulate hi then lo
         float16v st = {};
+        // Wave priority: normal while this wave issues its S MFMAs, raised
+        // from the softmax through the P.V MFMAs, so a wave with softmax
+        // work wins issue over waves still in their S chains (4% on a
+        // 512-token chunk over 8K-32K keys; a ping-pong of half the waves one
+        // phase behind, tried against it, lost 8-15%).
+        __builtin_amdgcn_s_setprio(0);
 #pragma unroll
         for (int kb = 0; kb < NKB; kb++) {
             const half8 ka = *reinterpret_cast<const half8 *>(&Ks[ln][16 * kb + 8 * jh]);
             st = mfma32(ka, qh[kb], st);
             st = mfma32(ka, ql[kb], st);
         }
+        __builtin_amdgcn_s_setprio(1);
         // register i holds key 8*(i/4) + 4*jh + (i%4) of the tile, row ln.
         // Only tiles crossing the diagonal mask (a work-group-uniform branch);
         // rows past the chunk compute on zero queries and are never written.
@@ -309,11 +323,15 @@ void prefill_kernel(PrefillArgs a)
                 st[i] = kt + kl > qpos ? -INFINITY : st[i];
             }
         }
+        // tile max over the 16 scores and the partner lane's, on 3-input
+        // maxes (fmaxf would first make NaN-quieting copies of its inputs;
+        // scores are never NaN)
         float mt = st[0];
 #pragma unroll
-        for (int i = 1; i < 16; i++)
-            mt = fmaxf(mt, st[i]);
-        mt = fmaxf(mt, __shfl_xor(mt, 32, 64));
+        for (int i = 1; i < 15; i += 2)
+            mt = max3(mt, st[i], st[i + 1]);
+        mt = max3(mt, st[15], st[15]);
+        mt = max3(mt, __shfl_xor(mt, 32, 64), mt);
         // Lazy max: keep the running max unless the tile exceeds it by more
         // than 2^8 (weights stay <= 256, exact range for fp16 and fp32), and
         // skip the rescale sweep when no row of the wave moved.
@@ -373,6 +391,7 @@ void prefill_kernel(PrefillArgs a)
                 }
             }
         }
+        __builtin_amdgcn_s_setprio(0);
         if (more)
             store_tile(sg1, cur ^ 1);       // tile kt+32 into the other buffer (its readers are done)
         if constexpr (PD == 2)
