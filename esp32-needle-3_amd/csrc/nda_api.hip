@@ -1850,6 +1850,103 @@ int nda_cq_gemm(const nda_cq *t, uint32_t rows, const float *xh, float *y, void 
     return nda_cq_gemm_many(&t, 1, rows, xh, &y, stream);
 }
 
+static bool cq_split_ok(const nda_cq *t) { return t->bits == 2 && t->group >= 32; }
+
+// rows rounded up to a block of 32: operand blocks (4 bytes per element), then the exponents
+static size_t split_rows(uint32_t rows) { return ((size_t)rows + 31) & ~(size_t)31; }
+
+size_t nda_cq_split_bytes(const nda_cq *t, uint32_t rows)
+{
+    return t ? split_rows(rows) * t->in_pad * 4 + (size_t)rows * 4 : 0;
+}
+
+int nda_cq_prepare_split(const nda_cq *t, uint32_t rows, const float *x, void *xs, void *stream)
+{
+    if (!t || (rows && (!x || !xs)))
+        return NDA_ERR_ARG;
+    if (((uintptr_t)x & 15) || ((uintptr_t)xs & 15))
+        return NDA_ERR_ARG;
+    if (t->group < 32)
+        return NDA_ERR_UNSUPPORTED;
+    CqPrepSplitArgs a{};
+    a.x = x;
+    a.xs = (_Float16 *)xs;
+    a.rexp = (int32_t *)(a.xs + split_rows(rows) * t->in_pad * 2);
+    a.rows = rows;
+    a.in = t->in;
+    a.in_pad = t->in_pad;
+    a.group = t->group;
+    a.scale = 1.0f / sqrtf((float)t->group);
+    return launch_cq_prepare_split(a, (hipStream_t)stream) == hipSuccess ? NDA_OK : NDA_ERR_HIP;
+}
+
+int nda_cq_gemm_split_many(const nda_cq *const *ts, uint32_t n, uint32_t rows, const void *xs, float *const *ys,
+                           void *stream)
+{
+    if (!ts || !ys || n == 0 || n > (uint32_t)CQ_MAX_T || (rows && !xs))
+        return NDA_ERR_ARG;
+    if (((uintptr_t)xs & 15) || (uint64_t)rows > 0x7FFFFFFFull)
+        return NDA_ERR_ARG;
+    const nda_cq *t0 = ts[0];
+    if (!t0)
+        return NDA_ERR_ARG;
+    CqSplitArgs a{};
+    a.xs = (const _Float16 *)xs;
+    a.rexp = (const int32_t *)(a.xs + split_rows(rows) * t0->in_pad * 2);
+    a.rows = rows;
+    a.in_pad = t0->in_pad;
+    a.group = t0->group;
+    a.ngroup = t0->ngroup;
+    a.rowbytes = t0->rowbytes;
+    a.log2_group = (uint32_t)__builtin_ctz(t0->group);
+    a.nt = n;
+    uint32_t tiles = 0;
+    for (uint32_t i = 0; i < n; i++) {
+        const nda_cq *t = ts[i];
+        if (!t || (rows && !ys[i]))
+            return NDA_ERR_ARG;
+        if (t->in != t0->in || t->group != t0->group || t->bits != t0->bits)
+            return NDA_ERR_ARG;
+        if (!cq_split_ok(t))
+            return NDA_ERR_UNSUPPORTED;
+        a.y[i] = ys[i];
+        a.packed[i] = t->packed;
+        a.norms[i] = t->norms;
+        a.cb[i] = t->cb;
+        a.out[i] = t->out;
+        a.tile0[i] = tiles;
+        tiles += (t->out + CQ_SPLIT_NT - 1) / CQ_SPLIT_NT;
+    }
+    a.tile0[n] = tiles;
+    if (tiles > 65535)
+        return NDA_ERR_ARG;
+    return launch_cq_gemm_split(a, (hipStream_t)stream) == hipSuccess ? NDA_OK : NDA_ERR_HIP;
+}
+
+int nda_cq_gemm_split(const nda_cq *t, uint32_t rows, const void *xs, float *y, void *stream)
+{
+    return nda_cq_gemm_split_many(&t, 1, rows, xs, &y, stream);
+}
+
+// n tensors sharing one input (q/k/v/gate, or out_proj alone) for the block
+// paths: the split-precision kernels where every tensor allows them, the
+// fp32 ones otherwise. xs holds nda_cq_split_bytes(ts[0], rows).
+static int cq_project(const nda_cq *const *ts, uint32_t n, uint32_t rows, const float *x, void *xs,
+                      float *const *ys, hipStream_t st)
+{
+    bool split = true;
+    for (uint32_t i = 0; i < n; i++)
+        split = split && cq_split_ok(ts[i]);
+    if (split) {
+        if (int rc = nda_cq_prepare_split(ts[0], rows, x, xs, st))
+            return rc;
+        return nda_cq_gemm_split_many(ts, n, rows, xs, ys, st);
+    }
+    if (int rc = nda_cq_prepare(ts[0], rows, x, (float *)xs, st))
+        return rc;
+    return nda_cq_gemm_many(ts, n, rows, (const float *)xs, ys, st);
+}
+
 int nda_block_weights(nda_ctx *c, uint32_t layer, const nda_cq *q, const nda_cq *k, const nda_cq *v,
                       const nda_cq *gate, const nda_cq *out_proj)
 {
@@ -1893,24 +1990,24 @@ int nda_attention_block(nda_ctx *c, uint32_t layer, uint32_t nseq, const uint32_
     hipStream_t st = (hipStream_t)stream;
     const auto &w = c->blk[layer];
     const nda_config &g = c->cfg;
-    // per-row scratch, each part a multiple of 4 floats (16-byte aligned)
+    // scratch parts, each a multiple of 4 floats (16-byte aligned): the two
+    // prepared inputs in either form (the split one pads rows to 32 and adds
+    // the row exponents), the projections at rows x their widths
     auto r4 = [](size_t n) { return (n + 3) & ~(size_t)3; };
-    const size_t nxh = r4(w[0]->in_pad), nq = r4(w[0]->out), nk = r4(w[1]->out), nv = r4(w[2]->out),
-                 ng = r4(w[3]->out), na = r4((size_t)g.n_heads * g.v_head_dim), nah = r4(w[4]->in_pad);
-    const size_t per = nxh + nq + nk + nv + ng + na + nah;
-    if (int rc = ensure_buf(c, c->d_bscr, c->bscr_cap, per * nseq))
+    const size_t pxh = r4(nda_cq_split_bytes(w[0], nseq) / 4), pah = r4(nda_cq_split_bytes(w[4], nseq) / 4);
+    const size_t nq = r4(w[0]->out), nk = r4(w[1]->out), nv = r4(w[2]->out), ng = r4(w[3]->out),
+                 na = r4((size_t)g.n_heads * g.v_head_dim);
+    if (int rc = ensure_buf(c, c->d_bscr, c->bscr_cap, pxh + (nq + nk + nv + ng + na) * nseq + pah))
         return rc;
-    float *xh = c->d_bscr, *yq = xh + nxh * nseq, *yk = yq + nq * nseq, *yv = yk + nk * nseq,
+    float *xh = c->d_bscr, *yq = xh + pxh, *yk = yq + nq * nseq, *yv = yk + nk * nseq,
           *yg = yv + nv * nseq, *att = yg + ng * nseq, *ah = att + na * nseq;
     // the parts are laid out [part][row] with row strides equal to the
     // tensors' own widths, as the kernels expect
     {
         ProfScope ps(c, NDA_K_PROJ, st);
-        if (int rc = nda_cq_prepare(w[0], nseq, x, xh, st))
-            return fail(c, rc, "q/k/v/gate prepare");
         const nda_cq *ts[4] = {w[0], w[1], w[2], w[3]};
         float *ys[4] = {yq, yk, yv, yg};
-        if (int rc = nda_cq_gemm_many(ts, 4, nseq, xh, ys, st))
+        if (int rc = cq_project(ts, 4, nseq, x, xh, ys, st))
             return fail(c, rc, "q/k/v/gate projections");
     }
     int rc = c->taps ? nda_attention(c, layer, nseq, ids, yq, yk, yv, yg, att, stream)
@@ -1918,9 +2015,7 @@ int nda_attention_block(nda_ctx *c, uint32_t layer, uint32_t nseq, const uint32_
     if (rc)
         return rc;
     ProfScope ps(c, NDA_K_PROJ, st);
-    if (int rc2 = nda_cq_prepare(w[4], nseq, att, ah, st))
-        return fail(c, rc2, "out_proj prepare");
-    if (int rc2 = nda_cq_gemm(w[4], nseq, ah, out, st))
+    if (int rc2 = cq_project(&w[4], 1, nseq, att, ah, &out, st))
         return fail(c, rc2, "out_proj");
     return NDA_OK;
 }
@@ -1960,25 +2055,25 @@ int nda_prefill_block(nda_ctx *c, uint32_t layer, uint32_t nseq, const uint32_t 
     hipStream_t st = (hipStream_t)stream;
     const auto &w = c->blk[layer];
     const nda_config &g = c->cfg;
+    // scratch parts as in nda_attention_block, plus the front's outputs
     auto r4 = [](size_t n) { return (n + 3) & ~(size_t)3; };
-    const size_t nxh = r4(w[0]->in_pad), nq = r4(w[0]->out), nk = r4(w[1]->out), nv = r4(w[2]->out),
-                 ng = r4(w[3]->out), na = r4((size_t)g.n_heads * g.v_head_dim), nah = r4(w[4]->in_pad);
+    const size_t pxh = r4(nda_cq_split_bytes(w[0], (uint32_t)rows) / 4),
+                 pah = r4(nda_cq_split_bytes(w[4], (uint32_t)rows) / 4);
+    const size_t nq = r4(w[0]->out), nk = r4(w[1]->out), nv = r4(w[2]->out), ng = r4(w[3]->out),
+                 na = r4((size_t)g.n_heads * g.v_head_dim);
     const size_t nf = c->taps ? nq + nk + nv : 0;    // the front's outputs
-    const size_t per = nxh + nq + nk + nv + ng + nf + na + nah;
-    if (int rc = ensure_buf(c, c->d_bscr, c->bscr_cap, per * rows))
+    if (int rc = ensure_buf(c, c->d_bscr, c->bscr_cap, pxh + (nq + nk + nv + ng + nf + na) * rows + pah))
         return rc;
     // [part][row], each part at its tensor's own row width
-    float *xh = c->d_bscr, *yq = xh + nxh * rows, *yk = yq + nq * rows, *yv = yk + nk * rows,
+    float *xh = c->d_bscr, *yq = xh + pxh, *yk = yq + nq * rows, *yv = yk + nk * rows,
           *yg = yv + nv * rows, *fq = yg + ng * rows, *fk = fq + nq * rows, *fv = fk + nk * rows,
           *att = yg + (ng + nf) * rows, *ah = att + na * rows;
     const uint32_t nr = (uint32_t)rows;
     {
         ProfScope ps(c, NDA_K_PROJ, st);
-        if (int rc = nda_cq_prepare(w[0], nr, x, xh, st))
-            return fail(c, rc, "q/k/v/gate prepare");
         const nda_cq *ts[4] = {w[0], w[1], w[2], w[3]};
         float *ys[4] = {yq, yk, yv, yg};
-        if (int rc = nda_cq_gemm_many(ts, 4, nr, xh, ys, st))
+        if (int rc = cq_project(ts, 4, nr, x, xh, ys, st))
             return fail(c, rc, "q/k/v/gate projections");
     }
     if (c->taps) {
@@ -1990,9 +2085,7 @@ int nda_prefill_block(nda_ctx *c, uint32_t layer, uint32_t nseq, const uint32_t 
         return rc;
     }
     ProfScope ps(c, NDA_K_PROJ, st);
-    if (int rc = nda_cq_prepare(w[4], nr, att, ah, st))
-        return fail(c, rc, "out_proj prepare");
-    if (int rc = nda_cq_gemm(w[4], nr, ah, out, st))
+    if (int rc = cq_project(&w[4], 1, nr, att, ah, &out, st))
         return fail(c, rc, "out_proj");
     return NDA_OK;
 }

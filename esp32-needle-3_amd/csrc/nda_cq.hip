@@ -24,6 +24,7 @@
 #include "nda_device.h"
 
 #include <algorithm>
+#include <float.h>
 
 namespace nda {
 
@@ -58,6 +59,8 @@ __global__ __launch_bounds__(256) void cq_prepare_kernel(CqPrepArgs a)
 
 typedef float float16v __attribute__((ext_vector_type(16)));
 typedef float float4v __attribute__((ext_vector_type(4)));
+typedef _Float16 half8 __attribute__((ext_vector_type(8)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 
 constexpr int CQ_MT = 64;     // rows per work-group
 constexpr int CQ_NT = 64;     // outputs per work-group
@@ -192,6 +195,324 @@ __global__ __launch_bounds__(256) void cq_gemm_kernel(CqGemmArgs a)
         if (rr < a.rows)
             y[(uint64_t)rr * out + oc] = acc[i];
     }
+}
+
+// ------------------------------------------------ split-precision path
+//
+// For 2-bit tensors with group >= 32 the GEMM runs on fp16 MFMA
+// (v_mfma_f32_32x32x16_f16, 16x the fp32 rate) with each fp32 operand
+// carried as a pair of fp16 values:
+//   xh * 2^rexp[r]  = xa + xb     per row, from the split prepare
+//   cb[c] * 2^ecb   = ca + cb'    per tensor, its four codebook entries
+//   sum_k w x  ~  sum_k (ca xa + ca xb + cb' xa)   (cb' xb, 2^-22 relative, dropped)
+// Products and sums are fp32 inside the MFMA. A group's sum is scaled by
+// its norm into the running total, and the total by 2^-(rexp + ecb) at the
+// end. The powers of two put each row's and the codebook's largest |value|
+// in [2^14, 2^15), so every fp16 part is a normal number with its full 11
+// bits: the pairs hold 22 significant bits, and the result stays within
+// fp32 reassociation of the engine's matvec (a few 2^-22 of sum |w x|).
+//
+// The split rows are stored in the order the MFMA reads them: per block of
+// 32 rows and 16 columns, per plane (a, b), the 64 lanes' 16-byte operands
+// (lane = row % 32 + 32 * (column % 16 / 8), 8 consecutive columns), so one
+// wave loads an operand as one contiguous 1 KiB.
+
+__device__ __forceinline__ uint64_t split_index(uint32_t row, uint32_t col, uint32_t nkb, int plane)
+{
+    const uint32_t rb = row >> 5, kb = col >> 4, lane = (row & 31) + ((col >> 3) & 1) * 32;
+    return ((((uint64_t)rb * nkb + kb) * 2 + plane) * 64 + lane) * 8 + (col & 7);
+}
+
+// One wave per row, up to four rows per work-group (as many as fit 64 KiB
+// of LDS): the wave's row in LDS, the butterfly stages of cq_prepare_kernel
+// (same pairs, same order, so the values are the engine's bit for bit)
+// separated by wave-level barriers only, the row maximum by shuffles.
+
+__global__ __launch_bounds__(256) void cq_prepare_split_kernel(CqPrepSplitArgs a)
+{
+    extern __shared__ float xsh[];      // CQ_PREP_ROWS rows of in_pad values
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const uint32_t row = blockIdx.x * a.rpw + wave;
+    if ((uint32_t)wave >= a.rpw || row >= a.rows)
+        return;                         // no block barrier below: the other waves go on
+    float *xs = xsh + (size_t)wave * a.in_pad;
+    const float *x = a.x + (uint64_t)row * a.in;
+    for (uint32_t i = lane; i < a.in_pad; i += 64)
+        xs[i] = i < a.in ? x[i] : 0.0f;
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    for (uint32_t len = 1; len < a.group; len <<= 1) {
+        for (uint32_t p = lane; p < a.in_pad / 2; p += 64) {
+            const uint32_t j = (p / len) * (2 * len) + p % len;
+            const float u = xs[j], v = xs[j + len];
+            xs[j] = u + v;
+            xs[j + len] = u - v;
+        }
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    }
+    float m = 0.0f;
+    for (uint32_t i = lane; i < a.in_pad; i += 64) {
+        const float v = xs[i] * a.scale;        // the engine's prepared value
+        xs[i] = v;
+        m = fmaxf(m, fabsf(v));
+    }
+    m = wave_max(m);
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    int e = 0, sh = 0;
+    if (m > 0.0f && m <= FLT_MAX) {
+        (void)frexpf(m, &e);
+        sh = 15 - e;                            // m * 2^sh in [2^14, 2^15)
+    }
+    // eight consecutive columns per lane: one 16-byte store per plane
+    const uint32_t nkb = a.in_pad / 16;
+    for (uint32_t c0 = 8 * lane; c0 < a.in_pad; c0 += 8 * 64) {
+        _Float16 h8[8], l8[8];
+#pragma unroll
+        for (int s = 0; s < 8; s++) {
+            float v = ldexpf(xs[c0 + s], sh);
+            asm volatile("" : "+v"(v));         // both halves from this one value
+            h8[s] = (_Float16)v;
+            l8[s] = (_Float16)(v - (float)h8[s]);
+        }
+        *reinterpret_cast<half8 *>(a.xs + split_index(row, c0, nkb, 0)) =
+            half8{h8[0], h8[1], h8[2], h8[3], h8[4], h8[5], h8[6], h8[7]};
+        *reinterpret_cast<half8 *>(a.xs + split_index(row, c0, nkb, 1)) =
+            half8{l8[0], l8[1], l8[2], l8[3], l8[4], l8[5], l8[6], l8[7]};
+    }
+    if (lane == 0)
+        a.rexp[row] = sh;
+}
+
+constexpr int CS_KT = 32;           // reduction columns per step: two MFMA k-blocks
+
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+
+// Work-group = 128 rows x 128 outputs of one tensor, 4 waves of 64 x 64
+// (2 x 2 blocks of 32 x 32) that share only the code tables: each wave loads
+// its X operands straight from the split rows (one step ahead, in two
+// register sets used in turn) and decodes its W operands from the codes
+// through two 256-entry tables (one byte = four 2-bit codes -> their four
+// fp16 a parts, and their four b parts). No barrier inside the loop. Loads
+// for rows or outputs past the end read row 0 instead (in bounds); what
+// they feed lands only in rows or columns that are never stored.
+template <int OB>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(OB >= 2 ? 2 : 3)))
+void cq_gemm_split_kernel(CqSplitArgs a)
+{
+    __shared__ u32x2 luta[256], lutb[256];
+
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int ln = lane & 31, jh = lane >> 5;
+    // XCD-aware order: work-group w runs on XCD w % 8; consecutive work
+    // items are the output tiles of one row tile, which read the same X
+    // rows, so they go to one XCD and share its L2. The grid is padded to a
+    // multiple of 8.
+    const uint32_t nwg = gridDim.x, item = (blockIdx.x % 8u) * (nwg / 8u) + blockIdx.x / 8u;
+    const uint32_t ntiles = a.tile0[a.nt];
+    const uint32_t rtile = item / ntiles, otile = item % ntiles;
+    if (rtile * CQ_SPLIT_MT >= a.rows)
+        return;                         // padding
+    uint32_t ti = 0;
+    while (ti + 1 < a.nt && otile >= a.tile0[ti + 1])
+        ti++;
+    const uint32_t out = a.out[ti];
+    float *y = a.y[ti];
+    const uint32_t r0 = rtile * CQ_SPLIT_MT, o0 = (otile - a.tile0[ti]) * (64 * OB);
+    const int wr = (wave & 1) * 64, wo = (wave >> 1) * 32 * OB;
+
+    // the codebook as fp16 pairs, scaled so its largest |entry| is in [2^14, 2^15)
+    const float *cbp = a.cb[ti];
+    const float cbv[4] = {cbp[0], cbp[1], cbp[2], cbp[3]};
+    const float cm = fmaxf(fmaxf(fabsf(cbv[0]), fabsf(cbv[1])), fmaxf(fabsf(cbv[2]), fabsf(cbv[3])));
+    int ecb = 0;
+    if (cm > 0.0f && cm <= FLT_MAX) {
+        int e;
+        (void)frexpf(cm, &e);
+        ecb = 15 - e;
+    }
+    {
+        uint32_t hw[2] = {0u, 0u}, lw[2] = {0u, 0u};
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            const int c = (tid >> (2 * j)) & 3;
+            float v = ldexpf(c == 0 ? cbv[0] : c == 1 ? cbv[1] : c == 2 ? cbv[2] : cbv[3], ecb);
+            asm volatile("" : "+v"(v));
+            const _Float16 h = (_Float16)v, l = (_Float16)(v - (float)h);
+            hw[j >> 1] |= (uint32_t)__builtin_bit_cast(uint16_t, h) << (16 * (j & 1));
+            lw[j >> 1] |= (uint32_t)__builtin_bit_cast(uint16_t, l) << (16 * (j & 1));
+        }
+        luta[tid] = u32x2{hw[0], hw[1]};
+        lutb[tid] = u32x2{lw[0], lw[1]};
+    }
+
+    // X operands of this wave: row blocks RB0 + rb, per k-block both planes
+    const uint32_t nkb = a.in_pad / 16;
+    const uint32_t RB0 = (r0 + wr) >> 5;
+    const half8 *xrow[2];
+#pragma unroll
+    for (int rb = 0; rb < 2; rb++) {
+        const bool ok = r0 + wr + 32 * rb < a.rows;
+        xrow[rb] = reinterpret_cast<const half8 *>(a.xs) + (uint64_t)(ok ? RB0 + rb : 0) * nkb * 128 + lane;
+    }
+    // this lane's two output columns, o0 + wo + 32 ob + ln: 32 codes per step
+    // each (two words); lane half jh uses the 16-bit half jh of word ks
+    const uint8_t *crow[OB];
+    const uint16_t *nrow[OB];
+#pragma unroll
+    for (int ob = 0; ob < OB; ob++) {
+        const uint32_t o = o0 + wo + 32 * ob + ln, oc = o < out ? o : 0;
+        crow[ob] = a.packed[ti] + (uint64_t)oc * a.rowbytes;
+        nrow[ob] = a.norms[ti] + (uint64_t)oc * a.ngroup;
+    }
+    struct Step {
+        half8 x[2][2][2];               // [ks][rb][plane]
+        uint2 c[OB];                    // [ob] codes
+        uint16_t nb[OB];                // [ob] the norm of the step's group
+    };
+    auto load = [&](uint32_t k0, Step &st) {
+#pragma unroll
+        for (int ks = 0; ks < 2; ks++)
+#pragma unroll
+            for (int rb = 0; rb < 2; rb++)
+#pragma unroll
+                for (int p = 0; p < 2; p++)
+                    st.x[ks][rb][p] = xrow[rb][((k0 >> 4) + ks) * 128 + 64 * p];
+#pragma unroll
+        for (int ob = 0; ob < OB; ob++) {
+            st.c[ob] = *reinterpret_cast<const uint2 *>(crow[ob] + k0 / 4);
+            st.nb[ob] = nrow[ob][k0 >> a.log2_group];
+        }
+    };
+
+    float16v acc[2][OB], ysum[2][OB];
+#pragma unroll
+    for (int rb = 0; rb < 2; rb++)
+#pragma unroll
+        for (int ob = 0; ob < OB; ob++)
+            ysum[rb][ob] = float16v{};
+    // One step: 24 MFMAs; `first` starts the group's sums from zero (a literal
+    // at each call site, so each variant carries no branch).
+    auto compute = [&](const Step &st, const bool first) __attribute__((always_inline)) {
+#pragma unroll
+        for (int ks = 0; ks < 2; ks++) {
+            half8 wa[OB], wb[OB];
+#pragma unroll
+            for (int ob = 0; ob < OB; ob++) {
+                const uint32_t c16 = ((ks ? st.c[ob].y : st.c[ob].x) >> (16 * jh)) & 0xFFFFu;
+                // separate index registers for the two tables: merged into
+                // one read per byte, the a and b parts would land in the
+                // wrong registers and need moves into operand order
+                uint32_t i0 = c16 & 0xFFu, i1 = c16 >> 8, j0 = i0, j1 = i1;
+                asm volatile("" : "+v"(j0), "+v"(j1));
+                const u32x2 a0 = luta[i0], a1 = luta[i1];
+                const u32x2 b0 = lutb[j0], b1 = lutb[j1];
+                wa[ob] = __builtin_bit_cast(half8, u32x4{a0.x, a0.y, a1.x, a1.y});
+                wb[ob] = __builtin_bit_cast(half8, u32x4{b0.x, b0.y, b1.x, b1.y});
+            }
+            // the three products of each block in turn over the four blocks,
+            // so consecutive MFMAs never wait on each other's results
+#pragma unroll
+            for (int rb = 0; rb < 2; rb++)
+#pragma unroll
+                for (int ob = 0; ob < OB; ob++)
+                    acc[rb][ob] = __builtin_amdgcn_mfma_f32_32x32x16_f16(
+                        st.x[ks][rb][0], wa[ob], (first && ks == 0) ? float16v{} : acc[rb][ob], 0, 0, 0);
+#pragma unroll
+            for (int rb = 0; rb < 2; rb++)
+#pragma unroll
+                for (int ob = 0; ob < OB; ob++)
+                    acc[rb][ob] = __builtin_amdgcn_mfma_f32_32x32x16_f16(st.x[ks][rb][1], wa[ob], acc[rb][ob], 0, 0, 0);
+#pragma unroll
+            for (int rb = 0; rb < 2; rb++)
+#pragma unroll
+                for (int ob = 0; ob < OB; ob++)
+                    acc[rb][ob] = __builtin_amdgcn_mfma_f32_32x32x16_f16(st.x[ks][rb][0], wb[ob], acc[rb][ob], 0, 0, 0);
+        }
+    };
+    // A group's end folds its sums into the totals with its norms, which
+    // every step of the group loads beside its operands (so their wait is
+    // that of the step's own data).
+    auto fold = [&](const Step &st) {
+#pragma unroll
+        for (int rb = 0; rb < 2; rb++)
+#pragma unroll
+            for (int ob = 0; ob < OB; ob++) {
+                const float nrm = half_bits_to_float(st.nb[ob]);
+#pragma unroll
+                for (int i = 0; i < 16; i++)
+                    ysum[rb][ob][i] = fmaf(nrm, acc[rb][ob][i], ysum[rb][ob][i]);
+            }
+    };
+    const uint32_t nsteps = a.in_pad / CS_KT, gmask = (a.group / CS_KT) - 1;   // steps per group: a power of two
+    auto step = [&](const Step &st, uint32_t s) __attribute__((always_inline)) {
+        if ((s & gmask) == 0)
+            compute(st, true);
+        else
+            compute(st, false);
+        if (((s + 1) & gmask) == 0)
+            fold(st);
+    };
+
+    // Steps in pairs, so the two register sets alternate without copies.
+    // Every load is unconditional (a pair's last one re-reads a valid step
+    // when nothing is left), so each wait covers exactly the step it feeds
+    // and the next step's loads stay in flight. in_pad is a multiple of the
+    // group, itself a multiple of one step.
+    Step s0, s1;
+    load(0, s0);
+    __syncthreads();                    // the tables are written
+    uint32_t s = 0;
+    for (; s + 2 <= nsteps; s += 2) {
+        load((s + 1) * CS_KT, s1);
+        step(s0, s);
+        load(min(s + 2, nsteps - 1) * CS_KT, s0);
+        step(s1, s + 1);
+    }
+    if (s < nsteps)
+        step(s0, s);
+    // D layout: lane holds output column ln of each block, rows 8 (i/4) + 4 jh + (i%4)
+#pragma unroll
+    for (int ob = 0; ob < OB; ob++) {
+        const uint32_t o = o0 + wo + 32 * ob + ln;
+        if (o >= out)
+            continue;
+#pragma unroll
+        for (int rb = 0; rb < 2; rb++)
+#pragma unroll
+            for (int i = 0; i < 16; i++) {
+                const uint32_t row = r0 + wr + 32 * rb + 8 * (i >> 2) + 4 * jh + (i & 3);
+                if (row < a.rows)
+                    y[(uint64_t)row * out + o] = ldexpf(ysum[rb][ob][i], -(a.rexp[row] + ecb));
+            }
+    }
+}
+
+hipError_t launch_cq_prepare_split(const CqPrepSplitArgs &a, hipStream_t s)
+{
+    if (a.rows == 0)
+        return hipSuccess;
+    CqPrepSplitArgs b = a;
+    b.rpw = std::max(1u, std::min(4u, 16384u / a.in_pad));
+    hipLaunchKernelGGL(cq_prepare_split_kernel, dim3((a.rows + b.rpw - 1) / b.rpw), dim3(256),
+                       b.rpw * a.in_pad * sizeof(float), s, b);
+    return hipGetLastError();
+}
+
+hipError_t launch_cq_gemm_split(const CqSplitArgs &a, hipStream_t s)
+{
+    if (a.rows == 0 || a.nt == 0 || a.tile0[a.nt] == 0)
+        return hipSuccess;
+    const uint64_t items = (uint64_t)((a.rows + CQ_SPLIT_MT - 1) / CQ_SPLIT_MT) * a.tile0[a.nt];
+    const uint64_t grid = (items + 7) / 8 * 8;
+    if (grid > 0x7FFFFFFFull)
+        return hipErrorInvalidValue;
+    hipLaunchKernelGGL(cq_gemm_split_kernel<CQ_SPLIT_OB>, dim3((uint32_t)grid), dim3(256), 0, s, a);
+    return hipGetLastError();
 }
 
 hipError_t launch_cq_prepare(const CqPrepArgs &a, hipStream_t s)

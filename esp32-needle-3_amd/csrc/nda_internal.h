@@ -184,8 +184,44 @@ struct CqGemmArgs {
     uint32_t rows, in_pad, group, ngroup, bits, rowbytes;
 };
 
+/* The split-precision form of a prepared activation: xh * 2^rexp[r] as an
+ * fp16 pair (a, b) per element, rexp chosen per row so the row's largest
+ * |value| lands in [2^14, 2^15), in MFMA operand order: [row / 32][col / 16]
+ * [plane a, b][lane (row % 32) + 32 (col % 16 / 8)][col % 8] over rows
+ * rounded up to 32. */
+struct CqPrepSplitArgs {
+    const float *x;          /* [rows][in] */
+    _Float16 *xs;            /* the operand blocks */
+    int32_t *rexp;           /* [rows] */
+    uint32_t rows, in, in_pad, group;
+    float scale;             /* 1 / sqrt(group) */
+    uint32_t rpw;            /* rows per work-group (set by the launcher) */
+};
+
+/* 2-bit tensors, group >= 32: the GEMM on fp16 MFMA from split operands. */
+struct CqSplitArgs {
+    const _Float16 *xs;
+    const int32_t *rexp;
+    float *y[CQ_MAX_T];
+    const uint8_t *packed[CQ_MAX_T];
+    const uint16_t *norms[CQ_MAX_T];
+    const float *cb[CQ_MAX_T];
+    uint32_t out[CQ_MAX_T];
+    uint32_t tile0[CQ_MAX_T + 1];       /* first grid.y tile (of CQ_SPLIT_NT outputs) per tensor */
+    uint32_t nt;
+    uint32_t rows, in_pad, group, ngroup, rowbytes, log2_group;
+};
+#ifndef NDA_CQ_OB
+#define NDA_CQ_OB 2
+#endif
+constexpr int CQ_SPLIT_MT = 128;        /* rows per work-group */
+constexpr int CQ_SPLIT_OB = NDA_CQ_OB;  /* 32-output blocks per wave */
+constexpr int CQ_SPLIT_NT = 64 * CQ_SPLIT_OB;   /* outputs per work-group */
+
 hipError_t launch_cq_prepare(const CqPrepArgs &a, hipStream_t s);
 hipError_t launch_cq_gemm(const CqGemmArgs &a, hipStream_t s);
+hipError_t launch_cq_prepare_split(const CqPrepSplitArgs &a, hipStream_t s);
+hipError_t launch_cq_gemm_split(const CqSplitArgs &a, hipStream_t s);
 
 /* Compiled geometries: (KV element bytes, qk_head_dim, v_head_dim, GQA rep). */
 #define NDA_FOR_GEOMETRIES(X) \

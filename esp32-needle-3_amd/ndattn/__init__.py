@@ -37,6 +37,7 @@ ABI_SYMBOLS = [
     "nda_prof_enable", "nda_prof_read",
     "nda_front_init", "nda_front_weights", "nda_front", "nda_attention", "nda_front_hist",
     "nda_cq_create", "nda_cq_destroy", "nda_cq_in_pad", "nda_cq_prepare", "nda_cq_gemm", "nda_cq_gemm_many",
+    "nda_cq_split_bytes", "nda_cq_prepare_split", "nda_cq_gemm_split", "nda_cq_gemm_split_many",
     "nda_event_create", "nda_event_destroy", "nda_event_record", "nda_event_elapsed",
     "nda_block_weights", "nda_attention_block", "nda_prefill_block",
 ]
@@ -130,6 +131,10 @@ def lib():
             "nda_cq_prepare": (C.c_int, [vp, u32, vp, vp, vp]),
             "nda_cq_gemm": (C.c_int, [vp, u32, vp, vp, vp]),
             "nda_cq_gemm_many": (C.c_int, [vp, u32, u32, vp, vp, vp]),
+            "nda_cq_split_bytes": (C.c_size_t, [vp, u32]),
+            "nda_cq_prepare_split": (C.c_int, [vp, u32, vp, vp, vp]),
+            "nda_cq_gemm_split": (C.c_int, [vp, u32, vp, vp, vp]),
+            "nda_cq_gemm_split_many": (C.c_int, [vp, u32, u32, vp, vp, vp]),
             "nda_event_create": (C.c_int, [C.POINTER(vp)]),
             "nda_event_destroy": (C.c_int, [vp]),
             "nda_event_record": (C.c_int, [vp, vp]),
@@ -569,6 +574,15 @@ class CQ:
     def gemm(self, rows, xh, y, stream=None):
         _check(lib().nda_cq_gemm(self.h, rows, _dp(xh), _dp(y), stream))
 
+    def split_bytes(self, rows):
+        return lib().nda_cq_split_bytes(self.h, rows)
+
+    def prepare_split(self, rows, x, xs, stream=None):
+        _check(lib().nda_cq_prepare_split(self.h, rows, _dp(x), _dp(xs), stream))
+
+    def gemm_split(self, rows, xs, y, stream=None):
+        _check(lib().nda_cq_gemm_split(self.h, rows, _dp(xs), _dp(y), stream))
+
     def close(self):
         if self.h and self.h.value:
             lib().nda_cq_destroy(self.h)
@@ -587,6 +601,14 @@ def cq_gemm_many(tensors, rows, xh, ys, stream=None):
     th = (vp * n)(*[t.h for t in tensors])
     yp = (vp * n)(*[_dp(y) for y in ys])
     _check(lib().nda_cq_gemm_many(th, n, rows, _dp(xh), yp, stream))
+
+
+def cq_gemm_split_many(tensors, rows, xs, ys, stream=None):
+    """cq_gemm_many from the split-precision prepared form."""
+    n = len(tensors)
+    th = (vp * n)(*[t.h for t in tensors])
+    yp = (vp * n)(*[_dp(y) for y in ys])
+    _check(lib().nda_cq_gemm_split_many(th, n, rows, _dp(xs), yp, stream))
 
 
 class Timer:

@@ -238,6 +238,20 @@ int nda_cq_gemm(const nda_cq *t, uint32_t rows, const float *xh, float *y, void 
  * into ys[i][rows][out_i]. */
 int nda_cq_gemm_many(const nda_cq *const *ts, uint32_t n, uint32_t rows, const float *xh, float *const *ys,
                      void *stream);
+/* The same matvecs (nd_cq_prepare + nd_cq_gemv_lut2, for every row) on fp16
+ * MFMA with split operands, for 2-bit tensors with group >= 32 (otherwise
+ * NDA_ERR_UNSUPPORTED). The prepared form xs (device, 16-byte aligned,
+ * nda_cq_split_bytes) holds per row the engine's prepared values times a
+ * power of two 2^e as an fp16 pair hi + lo: plane hi [rows][in_pad], plane
+ * lo [rows][in_pad], then e [rows] (int32). Codebook entries are split the
+ * same way; the fourth product (lo x lo, 2^-22 relative) is dropped, so the
+ * result is within a few 2^-22 of sum |w x| of the engine's. The attention
+ * block calls take this path when all five tensors allow it. */
+size_t nda_cq_split_bytes(const nda_cq *t, uint32_t rows);
+int nda_cq_prepare_split(const nda_cq *t, uint32_t rows, const float *x, void *xs, void *stream);
+int nda_cq_gemm_split(const nda_cq *t, uint32_t rows, const void *xs, float *y, void *stream);
+int nda_cq_gemm_split_many(const nda_cq *const *ts, uint32_t n, uint32_t rows, const void *xs,
+                           float *const *ys, void *stream);
 
 /* ---- the whole attention block (attention(), engine/src/nd_model.c:2382-2502) ----
  * Register one layer's five CQ tensors (borrowed: they must outlive the

@@ -146,3 +146,101 @@ def test_cq_error_paths():
         q.prepare(1, buf.value + 4, buf)             # misaligned
     assert e.value.code == -1
     q.close()
+
+
+# ------------------------------------------------ split-precision path
+
+def run_split(t, x):
+    N = nda()
+    rows = x.shape[0]
+    q = N.CQ(t.out, t.inp, t.group, t.bits, t.blob, t.cb())
+    dx = N.DevBuf.from_array(x)
+    dxs = N.DevBuf(max(16, q.split_bytes(rows)))
+    dy = N.DevBuf(max(1, rows) * t.out * 4)
+    q.prepare_split(rows, dx, dxs)
+    q.gemm_split(rows, dxs, dy)
+    N.device_sync()
+    P = q.in_pad
+    rp = (rows + 31) // 32 * 32
+    raw = dxs.to_array(np.uint8, (q.split_bytes(rows),))
+    blk = raw[:rp * P * 4].view(np.float16)
+    # operand order: [row/32][col/16][plane][lane = row%32 + 32 (col%16/8)][col%8]
+    r, c = np.meshgrid(np.arange(rows), np.arange(P), indexing="ij")
+    lane = r % 32 + 32 * ((c % 16) // 8)
+    base = ((r // 32) * (P // 16) + c // 16) * 2
+    hi = blk[((base + 0) * 64 + lane) * 8 + c % 8]
+    lo = blk[((base + 1) * 64 + lane) * 8 + c % 8]
+    e = raw[rp * P * 4:].view(np.int32)
+    y = dy.to_array(np.float32, (rows, t.out))
+    q.close()
+    return hi, lo, e, y
+
+
+@pytest.mark.parametrize("shape,rows,scale", [
+    ((576, 768, 128, 2), 70, 3.0),     # q_proj of the archive, ragged rows
+    ((768, 768, 128, 2), 300, 1.0),    # gate / out_proj, several row tiles
+    ((100, 200, 64, 2), 33, 1e-4),     # padding, partial tiles, small activations
+    ((130, 1024, 256, 2), 129, 5e3),   # large activations
+    ((40, 96, 32, 2), 5, 1.0),         # the smallest group the path takes
+])
+def test_cq_split_prepare_and_gemm(shape, rows, scale):
+    """The split form holds the engine's prepared row times 2^e exactly to
+    2^-22, the row's largest |value| in [2^14, 2^15); the GEMM is within the
+    fp32 reassociation bound of the engine's matvec."""
+    out, inp, group, b = shape
+    say("cq split", shape, rows, scale)
+    t = make_cq_tensor(out + inp + group + 7, out, inp, group, b, special_norms=True)
+    x = np.stack([det_normal(2000 + r, inp) for r in range(rows)]) * np.float32(scale)
+    x[rows // 2] = 0.0                                   # a zero row: exponent 0, zero output
+    hi, lo, e, y = run_split(t, x)
+    sc = abs_scale(t, x)
+    worst = 0.0
+    for r in range(rows):
+        want_xh = O.cq_prepare(t, x[r]).astype(np.float64)
+        v = want_xh * 2.0 ** int(e[r])
+        pair = hi[r].astype(np.float64) + lo[r].astype(np.float64)
+        assert np.all(np.abs(pair - v) <= 2.0 ** -22 * np.abs(v).max() + 1e-30), r
+        m = np.abs(v).max()
+        assert (m == 0 and e[r] == 0) or 2 ** 14 <= m < 2 ** 15, (r, m, e[r])
+        want = O.cq_gemv_lut2(t, O.cq_prepare(t, x[r]))
+        err = np.abs(y[r].astype(np.float64) - want)
+        assert np.all(err <= 1e-5 * sc[:, r] + 1e-6 * max(1.0, scale)), (r, float(err.max()))
+        worst = max(worst, float((err / (sc[:, r] + 1e-30)).max()))
+    assert np.all(y[rows // 2] == 0.0)
+    say("cq split worst relative to sum|w x|", worst)
+
+
+def test_cq_split_many_matches_single_and_rejects():
+    """q/k/v/gate in one launch equal four launches bit for bit; widths and
+    groups the path does not take are refused."""
+    N = nda()
+    say("cq split many")
+    shapes = [576, 96, 128, 768]
+    rows, inp = 150, 768
+    ts = [make_cq_tensor(800 + i, o, inp, 128, 2) for i, o in enumerate(shapes)]
+    qs = [N.CQ(o, inp, 128, 2, t.blob, t.cb()) for o, t in zip(shapes, ts)]
+    x = np.stack([det_normal(60 + r, inp) for r in range(rows)])
+    dx = N.DevBuf.from_array(x)
+    dxs = N.DevBuf(qs[0].split_bytes(rows))
+    qs[0].prepare_split(rows, dx, dxs)
+    one = [N.DevBuf(rows * o * 4) for o in shapes]
+    many = [N.DevBuf(rows * o * 4) for o in shapes]
+    for q, y in zip(qs, one):
+        q.gemm_split(rows, dxs, y)
+    N.cq_gemm_split_many(qs, rows, dxs, many)
+    N.device_sync()
+    for o, a, b in zip(shapes, one, many):
+        assert np.array_equal(a.to_array(np.uint32, (rows, o)), b.to_array(np.uint32, (rows, o)))
+    t4 = make_cq_tensor(9, 64, 512, 128, 4)
+    q4 = N.CQ(64, 512, 128, 4, t4.blob, t4.cb())
+    buf = N.DevBuf(q4.split_bytes(4) + 64)
+    with pytest.raises(N.NdaError) as e:
+        q4.gemm_split(4, buf, buf)                   # 4-bit: not this path
+    assert e.value.code == -6
+    t16 = make_cq_tensor(10, 8, 64, 16, 2)
+    q16 = N.CQ(8, 64, 16, 2, t16.blob, t16.cb())
+    with pytest.raises(N.NdaError) as e:
+        q16.prepare_split(1, buf, buf)               # group 16
+    assert e.value.code == -6
+    for q in qs + [q4, q16]:
+        q.close()
