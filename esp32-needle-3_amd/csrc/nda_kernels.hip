@@ -258,7 +258,11 @@ __device__ __forceinline__ void merge_state(float &m, float &l, float *acc, int 
     m = M;
 }
 
-template <int ES, int DK, int DV, int REP, int G, int NP, int NW>
+// A work-group is one (row, kv-head) unit, or with HS > 1 one of HS units
+// that split the kv-head's query heads between them (REP each, REP * HS in
+// the group): each reads the kv-head's K/V, so the per-lane state of a wide
+// GQA group (heads x head dim) divides by HS and more units fit a CU.
+template <int ES, int DK, int DV, int REP, int G, int NP, int NW, int HS>
 __global__ __launch_bounds__(64 * NW) void attend_kernel(AttnArgs a)
 {
     using C = AttnCfg<ES, DK, DV, REP, G, NP, NW>;
@@ -266,7 +270,7 @@ __global__ __launch_bounds__(64 * NW) void attend_kernel(AttnArgs a)
     const int grp = lane / G, li = lane % G;
     const uint32_t nkv = a.pg.nkv;
     const uint32_t unit = blockIdx.x;
-    const uint32_t row = unit / nkv, g = unit % nkv;
+    const uint32_t row = unit / (nkv * HS), gv = unit % (nkv * HS), g = gv / HS;   // heads gv*REP..+REP
     const uint32_t chunk = blockIdx.y;
 
     const uint32_t seq = a.row_seq ? a.row_seq[row] : row;
@@ -283,7 +287,7 @@ __global__ __launch_bounds__(64 * NW) void attend_kernel(AttnArgs a)
     // position's slot stores it first (the engine stores before it attends,
     // engine/src/nd_model.c:2426-2454), then every wave reads it like any
     // other slot.
-    if (a.k_new) {
+    if (HS == 1 && a.k_new) {      // (the host never fuses the store into a split launch)
         const int nslot = own_slot(sd, p, (int)a.pg.window);
         const int vi = vis.n_sh + nslot;
         if (vi >= c0 && vi < c1) {
@@ -308,7 +312,7 @@ __global__ __launch_bounds__(64 * NW) void attend_kernel(AttnArgs a)
     AttnState<ES, DK, DV, REP, G, NP, NW> st;
 #pragma unroll
     for (int t = 0; t < REP; t++) {
-        const float *qh = a.q + ((uint64_t)row * a.nh + g * REP + t) * DK + li * C::EK;
+        const float *qh = a.q + ((uint64_t)row * a.nh + gv * REP + t) * DK + li * C::EK;
 #pragma unroll
         for (int e = 0; e < C::EK; e++)
             st.qr[t][e] = qh[e] * a.qscale;
@@ -374,7 +378,7 @@ __global__ __launch_bounds__(64 * NW) void attend_kernel(AttnArgs a)
 
 #pragma unroll
     for (int t = 0; t < REP; t++) {
-        const uint32_t h = g * REP + t;
+        const uint32_t h = gv * REP + t;
         if (nchunks == 1) {
             const float inv = 1.0f / st.l[t];
             float *o = a.out + ((uint64_t)row * a.nh + h) * DV + li * C::EV;
@@ -694,15 +698,50 @@ bool geometry_supported(const Geo &g)
 
 static inline unsigned blocks_for(uint64_t waves) { return (unsigned)((waves + 3) / 4); }
 
+// Query heads per work-group for a GQA group of REP: the widest groups
+// (rep >= 6) split in two, except when the launch also stores the new row
+// (one work-group per kv-head must own that store).
+template <int REP>
+constexpr int att_hs()
+{
+#ifdef NDA_ATT_HS
+    return REP % NDA_ATT_HS == 0 ? NDA_ATT_HS : 1;
+#else
+    return REP >= 6 ? 2 : 1;
+#endif
+}
+
+int attend_split(const Geo &g, const AttnArgs &a)
+{
+    if (a.k_new)
+        return 1;
+#define X(ES, DK, DV, REP) if (es_of(g) == ES && g.dk == DK && g.dv == DV && g.rep == REP) return att_hs<REP>();
+    NDA_FOR_GEOMETRIES(X)
+#undef X
+    return 1;
+}
+
+template <int ES, int DK, int DV, int REP, int HS>
+static void launch_attend_hs(const AttnArgs &a, hipStream_t s)
+{
+    constexpr int R = REP / HS;
+    constexpr int NW = HS > 1 ? 1 : att_nw<REP>();
+    const dim3 grid(a.rows * a.pg.nkv * HS, a.max_chunks);
+    hipLaunchKernelGGL((attend_kernel<ES, DK, DV, R, lanes_per_pos<ES, DK, R>(), att_np<ES, R>(), NW, HS>), grid,
+                       dim3(64 * NW), 0, s, a);
+}
+
 hipError_t launch_attend(const Geo &g, const AttnArgs &a, hipStream_t s)
 {
     if (a.rows == 0)
         return hipSuccess;
-    dim3 grid(a.rows * a.pg.nkv, a.max_chunks);
+    const int hs = attend_split(g, a);
 #define X(ES, DK, DV, REP)                                                                      \
     if (es_of(g) == ES && g.dk == DK && g.dv == DV && g.rep == REP) {                          \
-        hipLaunchKernelGGL((attend_kernel<ES, DK, DV, REP, lanes_per_pos<ES, DK, REP>(), att_np<ES, REP>(), att_nw<REP>()>), \
-                           grid, dim3(64 * att_nw<REP>()), 0, s, a);                            \
+        if (hs > 1)                                                                             \
+            launch_attend_hs<ES, DK, DV, REP, att_hs<REP>()>(a, s);                             \
+        else                                                                                    \
+            launch_attend_hs<ES, DK, DV, REP, 1>(a, s);                                         \
         return hipGetLastError();                                                               \
     }
     NDA_FOR_GEOMETRIES(X)
