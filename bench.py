@@ -422,7 +422,9 @@ def cq_leg(N, stream, rows=B, d_model=768, reps=20):
     """The attention block's CQ projections for a batch of rows, at the
     archive's shapes (12 q / 2 kv heads, qk 48, v 64, d_model 768, 2-bit,
     group 128): prepare x, then q/k/v/gate from it; prepare attn, then
-    out_proj. FLOPs = 2 * rows * in * out per projection."""
+    out_proj. FLOPs = 2 * rows * in * out per projection. Timed on both
+    paths: the split-precision one (fp16 MFMA, three products per block:
+    what the attention block calls use) and the fp32-MFMA one."""
     rng = np.random.default_rng(SEED + 31)
     shapes = {"q": (576, d_model), "k": (96, d_model), "v": (128, d_model), "gate": (768, d_model),
               "out": (d_model, 768)}
@@ -435,47 +437,61 @@ def cq_leg(N, stream, rows=B, d_model=768, reps=20):
     x.fill_normal(rows * d_model, 0, SEED + 32, stream=stream)
     att = N.DevBuf(rows * 768 * 4)
     att.fill_normal(rows * 768, 0, SEED + 33, stream=stream)
-    xh = N.DevBuf(rows * ts["q"].in_pad * 4)
-    ah = N.DevBuf(rows * ts["out"].in_pad * 4)
+    xh = N.DevBuf(max(rows * ts["q"].in_pad * 4, ts["q"].split_bytes(rows)))
+    ah = N.DevBuf(max(rows * ts["out"].in_pad * 4, ts["out"].split_bytes(rows)))
     ys = {name: N.DevBuf(rows * o * 4) for name, (o, _) in shapes.items()}
+    qkvg = [ts[n] for n in ("q", "k", "v", "gate")]
+    yq = [ys[n] for n in ("q", "k", "v", "gate")]
 
-    def block():
+    def block_fp32():
         ts["q"].prepare(rows, x, xh, stream)
-        N.cq_gemm_many([ts[n] for n in ("q", "k", "v", "gate")], rows, xh,
-                       [ys[n] for n in ("q", "k", "v", "gate")], stream)
+        N.cq_gemm_many(qkvg, rows, xh, yq, stream)
         ts["out"].prepare(rows, att, ah, stream)
         ts["out"].gemm(rows, ah, ys["out"], stream)
 
-    block()
-    tm, tq = N.Timer(), N.Timer()
-    tm.start(stream)
-    for _ in range(reps):
-        block()
-    tm.stop(stream)
-    block_ms = tm.ms() / reps
-    tq.start(stream)
-    for _ in range(reps):
-        ts["gate"].gemm(rows, xh, ys["gate"], stream)
-    tq.stop(stream)
-    gate_ms = tq.ms() / reps
-    flops = sum(2.0 * rows * o * i for o, i in shapes.values())
-    gate_flops = 2.0 * rows * 768 * d_model
-    # sampled parity: two rows of the gate projection against the oracle
+    def block_split():
+        ts["q"].prepare_split(rows, x, xh, stream)
+        N.cq_gemm_split_many(qkvg, rows, xh, yq, stream)
+        ts["out"].prepare_split(rows, att, ah, stream)
+        ts["out"].gemm_split(rows, ah, ys["out"], stream)
+
+    def timed(fn):
+        fn()
+        tm = N.Timer()
+        tm.start(stream)
+        for _ in range(reps):
+            fn()
+        tm.stop(stream)
+        return tm.ms() / reps
+
     import ndoracle as O
-    N.device_sync()
-    xr = x.to_array(np.float32, (rows, d_model))
-    yr = ys["gate"].to_array(np.float32, (rows, 768))
     o_, i_, blob, cb = hosts["gate"]
     t = O.CQTensor(o_, i_, 128, 2, blob, np.concatenate([cb, np.zeros(24, np.float32)]))
-    worst = 0.0
-    for r in (0, rows - 1):
-        want = O.cq_gemv_lut2(t, O.cq_prepare(t, xr[r]))
-        worst = max(worst, float(np.abs(want - yr[r]).max() / (np.abs(want).max() + 1e-30)))
+
+    def sampled():
+        N.device_sync()
+        xr = x.to_array(np.float32, (rows, d_model))
+        yr = ys["gate"].to_array(np.float32, (rows, 768))
+        worst = 0.0
+        for r in (0, rows - 1):
+            want = O.cq_gemv_lut2(t, O.cq_prepare(t, xr[r]))
+            worst = max(worst, float(np.abs(want - yr[r]).max() / (np.abs(want).max() + 1e-30)))
+        return worst
+
+    fp32_ms = timed(block_fp32)
+    worst_fp32 = sampled()
+    split_ms = timed(block_split)
+    worst_split = sampled()
+    # the q/k/v/gate launch alone, split path (x prepared above)
+    ts["q"].prepare_split(rows, x, xh, stream)
+    qkvg_ms = timed(lambda: N.cq_gemm_split_many(qkvg, rows, xh, yq, stream))
+    flops = sum(2.0 * rows * o * i for o, i in shapes.values())
+    qkvg_flops = 2.0 * rows * d_model * (576 + 96 + 128 + 768)
     ref_us = None
     if O.have_ref():
         R = O.ref()
         cb28 = np.concatenate([cb, np.zeros(24, np.float32)])
-        xhr = O.cq_prepare(t, xr[0])
+        xhr = O.cq_prepare(t, x.to_array(np.float32, (rows, d_model))[0])
         lut = np.zeros(t.in_pad // 2 * 16, np.float32)
         yv = np.zeros(o_, np.float32)
         t0 = time.perf_counter()
@@ -487,18 +503,21 @@ def cq_leg(N, stream, rows=B, d_model=768, reps=20):
         ref_us = (time.perf_counter() - t0) / n * 1e6
     for q in ts.values():
         q.close()
+    qkvg_tf = qkvg_flops / (qkvg_ms * 1e-3) / 1e12
     return {"workload": "CQ projections of one attention block for %d rows: 2-bit, group 128, d_model %d; "
                         "q 576, k 96, v 128, gate 768 from one prepared x in one launch, out_proj 768 "
                         "from 768" % (rows, d_model),
-            "block_ms": round(block_ms, 4), "block_tflops": round(flops / (block_ms * 1e-3) / 1e12, 1),
-            "gate_gemm_ms": round(gate_ms, 4),
-            "gate_gemm_tflops": round(gate_flops / (gate_ms * 1e-3) / 1e12, 1),
-            "peak_fp32_mfma_tflops": 157.3,
-            "frac_gate": round(gate_flops / (gate_ms * 1e-3) / 1e12 / 157.3, 4),
-            "rows_per_s": round(rows / (block_ms * 1e-3), 1),
-            "max_rel_delta_sampled": worst,
+            "block_ms": round(split_ms, 4), "block_tflops": round(flops / (split_ms * 1e-3) / 1e12, 1),
+            "qkvg_gemm_ms": round(qkvg_ms, 4), "qkvg_gemm_tflops": round(qkvg_tf, 1),
+            "mfma_issued_frac": round(3 * qkvg_tf / 2500.0, 4),
+            "rows_per_s": round(rows / (split_ms * 1e-3), 1),
+            "max_rel_delta_sampled": worst_split,
+            "fp32_path": {"block_ms": round(fp32_ms, 4), "block_tflops": round(flops / (fp32_ms * 1e-3) / 1e12, 1),
+                          "max_rel_delta_sampled": worst_fp32},
             "reference_cpu_us_per_row_gate": None if ref_us is None else round(ref_us, 1),
-            "note": "fp32 MFMA (v_mfma_f32_32x32x2_f32); weights decoded from the 2-bit codes in LDS"}
+            "note": "split path: fp16 MFMA (v_mfma_f32_32x32x16_f16) on fp16 pairs, three products per block, "
+                    "so the MFMA pipe issues 3x the algorithmic FLOPs (mfma_issued_frac is against 2.5 PF); "
+                    "fp32 path: v_mfma_f32_32x32x2_f32"}
 
 
 ENGINE_GEOM = (12, 2, 48, 64)      # q heads, kv heads, qk and v head dims of the archive
@@ -718,6 +737,8 @@ def main():
     ap.add_argument("--no-prefill", action="store_true")
     ap.add_argument("--calib", action="store_true",
                     help="first run a 4 GiB device copy (known traffic, for counter calibration)")
+    ap.add_argument("--leg", choices=["cq", "cq_prefill", "block", "block_prefill", "prefill", "front"],
+                    help="run only this leg and print its JSON object (for profiling one kernel family)")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py measures one GPU: this build has no multi-GPU path "
@@ -738,6 +759,14 @@ def main():
         log("calibration copy: 3 x %d bytes read + written" % nb)
         src.free()
         dst.free()
+    if args.leg:
+        stream = N.vp()
+        N._check(N.lib().nda_stream_create(N.C.byref(stream)))
+        legs = {"cq": lambda: cq_leg(N, stream), "cq_prefill": lambda: cq_leg(N, stream, rows=49787, reps=5),
+                "block": lambda: block_leg(N, stream), "block_prefill": lambda: block_prefill_leg(N, stream),
+                "prefill": lambda: prefill_leg(N, stream), "front": lambda: front_leg(N, stream)}
+        print(json.dumps(legs[args.leg]()), flush=True)
+        return
     rng = np.random.default_rng(SEED)
     lens = rng.integers(LMIN, LMAX + 1, B)          # positions attended at the first step
     total_steps = args.warmup + args.steps
@@ -831,8 +860,10 @@ def main():
         log("block prefill: %.0f prompt tok/s, pass %.3f ms, per pass %s" % (
             block_pf["prompt_tokens_per_s"], block_pf["ms_per_pass"], block_pf["kernel_ms_per_pass"]))
     cq = cq_leg(N, stream)
-    log("cq: block %.4f ms (%.1f TFLOP/s), gate gemm %.4f ms (%.1f TFLOP/s fp32 MFMA), sampled rel delta %.3g" % (
-        cq["block_ms"], cq["block_tflops"], cq["gate_gemm_ms"], cq["gate_gemm_tflops"], cq["max_rel_delta_sampled"]))
+    cq_pf = cq_leg(N, stream, rows=49787, reps=5)      # the row count of the block prefill leg
+    log("cq: block %.4f ms (%.1f TFLOP/s; fp32 path %.4f ms), q/k/v/gate gemm %.4f ms (%.1f TFLOP/s), "
+        "sampled rel delta %.3g" % (cq["block_ms"], cq["block_tflops"], cq["fp32_path"]["block_ms"],
+                                    cq["qkvg_gemm_ms"], cq["qkvg_gemm_tflops"], cq["max_rel_delta_sampled"]))
     engine = engine_session_leg(N)
     log("engine session: GPU %.1f us per layer call, reference CPU %s us" % (
         engine["gpu_us_per_layer_call"], engine["reference_cpu_us_per_layer_call"]))
@@ -890,6 +921,7 @@ def main():
         "engine_session": engine,
         "front": front,
         "cq_projections": cq,
+        "cq_projections_prefill_rows": cq_pf,
         "attention_block": block,
         "attention_block_prefill": block_pf,
         "shared_prefix": shared,
