@@ -288,6 +288,121 @@ __global__ __launch_bounds__(256) void cq_prepare_split_kernel(CqPrepSplitArgs a
         a.rexp[row] = sh;
 }
 
+// Register form for rows of up to 1536 columns and groups of at least 64:
+// one wave per row, lane l holding columns 512 h + 8 l .. +7 (h < 3). The
+// butterfly stages are the engine's (the same pairs, a + b and a - b, stage
+// by stage): len < 8 inside a lane, 8 <= len < 512 between lanes l and
+// l ^ (len / 8) (the upper lane's a - b as fmaf(-1, b, a), one rounding of
+// the same exact difference), len >= 512 between a lane's column blocks.
+// The values are the engine's bit for bit. A work-group is 8 consecutive
+// rows (8 waves); their 16-byte operand slots meet in LDS, and each 128-byte
+// line of the split rows (8 rows x one slot) is then written whole.
+constexpr int CQ_REG_COLS = 1536;
+
+__global__ __launch_bounds__(512) void cq_prepare_split_reg_kernel(CqPrepSplitArgs a)
+{
+    __shared__ __attribute__((aligned(16))) uint4 T[2][CQ_REG_COLS / 8][9];   // [plane][slot][row of 8 + pad]
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const uint32_t row0 = blockIdx.x * 8, row = row0 + wave;
+    const bool live = row < a.rows;
+    const float *x = a.x + (uint64_t)(live ? row : 0) * a.in;
+    float v[3][8];
+    const bool vec = (a.in & 3) == 0;                  // rows 16-byte aligned
+#pragma unroll
+    for (int h = 0; h < 3; h++) {
+        const uint32_t i0 = 512 * h + 8 * lane;
+        if (vec && live && i0 + 8 <= a.in) {           // two 16-byte loads
+            const float4 p = *reinterpret_cast<const float4 *>(x + i0);
+            const float4 q = *reinterpret_cast<const float4 *>(x + i0 + 4);
+            v[h][0] = p.x; v[h][1] = p.y; v[h][2] = p.z; v[h][3] = p.w;
+            v[h][4] = q.x; v[h][5] = q.y; v[h][6] = q.z; v[h][7] = q.w;
+        } else {
+#pragma unroll
+            for (int s = 0; s < 8; s++)
+                v[h][s] = live && i0 + s < a.in ? x[i0 + s] : 0.0f;
+        }
+    }
+    const int nh = (int)((a.in_pad + 511) / 512);       // column blocks in use (<= 3)
+    for (uint32_t len = 1; len < a.group; len <<= 1) {
+        if (len < 8) {
+#pragma unroll
+            for (int h = 0; h < 3; h++)
+                if (h < nh)
+#pragma unroll
+                for (int s = 0; s < 8; s++)
+                    if ((s & len) == 0) {
+                        const float u = v[h][s], w = v[h][s + len];
+                        v[h][s] = u + w;
+                        v[h][s + len] = u - w;
+                    }
+        } else if (len < 512) {
+            const int m = (int)(len >> 3);
+            const float sg = (lane & m) ? -1.0f : 1.0f;
+#pragma unroll
+            for (int h = 0; h < 3; h++)
+                if (h < nh)
+#pragma unroll
+                for (int s = 0; s < 8; s++) {
+                    const float w = __shfl_xor(v[h][s], m, 64);
+                    v[h][s] = fmaf(sg, v[h][s], w);     // lower lane: v + w; upper: w - v
+                }
+        } else {
+            const int m = (int)(len >> 9);
+#pragma unroll
+            for (int h = 0; h < 3; h++)
+                if ((h & m) == 0)
+#pragma unroll
+                    for (int s = 0; s < 8; s++) {
+                        const float u = v[h][s], w = v[h + m][s];
+                        v[h][s] = u + w;
+                        v[h + m][s] = u - w;
+                    }
+        }
+    }
+    float mx = 0.0f;
+#pragma unroll
+    for (int h = 0; h < 3; h++)
+#pragma unroll
+        for (int s = 0; s < 8; s++) {
+            v[h][s] *= a.scale;                         // the engine's prepared value
+            if (512 * h + 8 * lane < a.in_pad)
+                mx = fmaxf(mx, fabsf(v[h][s]));
+        }
+    mx = wave_max(mx);
+    int e = 0, sh = 0;
+    if (mx > 0.0f && mx <= FLT_MAX) {
+        (void)frexpf(mx, &e);
+        sh = 15 - e;                                   // mx * 2^sh in [2^14, 2^15)
+    }
+    // this row's operand slots into LDS, then whole lines out
+#pragma unroll
+    for (int h = 0; h < 3; h++) {
+        const uint32_t c = 64 * h + lane;              // slot: columns 8c .. 8c + 7
+        if (8 * c >= a.in_pad)
+            continue;
+        _Float16 h8[8], l8[8];
+#pragma unroll
+        for (int s = 0; s < 8; s++) {
+            float y = ldexpf(v[h][s], sh);
+            asm volatile("" : "+v"(y));                // both halves from this one value
+            h8[s] = (_Float16)y;
+            l8[s] = (_Float16)(y - (float)h8[s]);
+        }
+        T[0][c][wave] = __builtin_bit_cast(uint4, half8{h8[0], h8[1], h8[2], h8[3], h8[4], h8[5], h8[6], h8[7]});
+        T[1][c][wave] = __builtin_bit_cast(uint4, half8{l8[0], l8[1], l8[2], l8[3], l8[4], l8[5], l8[6], l8[7]});
+    }
+    if (live && lane == 0)
+        a.rexp[row] = sh;
+    __syncthreads();
+    // 8 rows' slot c of a plane is one 128-byte line (lanes row0 % 32 ..
+    // +7 of one operand): thread t writes row t % 8 of line t / 8
+    const uint32_t nslot = a.in_pad / 8, nkb = a.in_pad / 16;
+    for (uint32_t u = threadIdx.x; u < 2 * nslot * 8; u += 512) {
+        const uint32_t r = u & 7, c = (u >> 3) % nslot, p = (u >> 3) / nslot;
+        *reinterpret_cast<uint4 *>(a.xs + split_index(row0 + r, 8 * c, nkb, (int)p)) = T[p][c][r];
+    }
+}
+
 constexpr int CS_KT = 32;           // reduction columns per step: two MFMA k-blocks
 
 typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
@@ -496,6 +611,10 @@ hipError_t launch_cq_prepare_split(const CqPrepSplitArgs &a, hipStream_t s)
 {
     if (a.rows == 0)
         return hipSuccess;
+    if (a.in_pad <= (uint32_t)CQ_REG_COLS && a.group >= 64) {
+        hipLaunchKernelGGL(cq_prepare_split_reg_kernel, dim3((a.rows + 7) / 8), dim3(512), 0, s, a);
+        return hipGetLastError();
+    }
     CqPrepSplitArgs b = a;
     b.rpw = std::max(1u, std::min(4u, 16384u / a.in_pad));
     hipLaunchKernelGGL(cq_prepare_split_kernel, dim3((a.rows + b.rpw - 1) / b.rpw), dim3(256),

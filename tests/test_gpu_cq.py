@@ -181,7 +181,10 @@ def run_split(t, x):
     ((768, 768, 128, 2), 300, 1.0),    # gate / out_proj, several row tiles
     ((100, 200, 64, 2), 33, 1e-4),     # padding, partial tiles, small activations
     ((130, 1024, 256, 2), 129, 5e3),   # large activations
-    ((40, 96, 32, 2), 5, 1.0),         # the smallest group the path takes
+    ((40, 96, 32, 2), 5, 1.0),         # the smallest group the path takes (LDS prepare)
+    ((64, 1024, 1024, 2), 37, 1.0),    # register prepare, stages across column blocks
+    ((72, 1536, 512, 2), 45, 1.0),     # the widest row of the register prepare
+    ((48, 2300, 128, 2), 9, 1.0),      # past it: the LDS prepare
 ])
 def test_cq_split_prepare_and_gemm(shape, rows, scale):
     """The split form holds the engine's prepared row times 2^e exactly to
@@ -200,6 +203,13 @@ def test_cq_split_prepare_and_gemm(shape, rows, scale):
         v = want_xh * 2.0 ** int(e[r])
         pair = hi[r].astype(np.float64) + lo[r].astype(np.float64)
         assert np.all(np.abs(pair - v) <= 2.0 ** -22 * np.abs(v).max() + 1e-30), r
+        # exactly: hi the fp16 rounding of the scaled engine value, lo that of the rest
+        v32 = v.astype(np.float32)
+        assert np.array_equal(v32.astype(np.float64), v), r       # the scaling is exact
+        want_hi = v32.astype(np.float16)
+        want_lo = (v32 - want_hi.astype(np.float32)).astype(np.float16)
+        assert np.array_equal(hi[r].view(np.uint16), want_hi.view(np.uint16)), r
+        assert np.array_equal(lo[r].view(np.uint16), want_lo.view(np.uint16)), r
         m = np.abs(v).max()
         assert (m == 0 and e[r] == 0) or 2 ** 14 <= m < 2 ** 15, (r, m, e[r])
         want = O.cq_gemv_lut2(t, O.cq_prepare(t, x[r]))
