@@ -244,7 +244,7 @@ def decode_long(N, ctx, stream, lens, q, k, v, out, reps):
 
 
 def shared_prefix_leg(N, stream, nseq=1024, npre=213, nmin=32, nmax=64, dsteps=64, layers=LAYERS):
-    """Config 4: nseq sequences share one npre-token prefix (stored once per
+    """Shared prefix: nseq sequences share one npre-token prefix (stored once per
     layer); each prefills n ~ U[nmin, nmax] new tokens causally, then decodes
     dsteps tokens, through `layers` layers. Unique bytes count the prefix once
     per layer; logical bytes count it once per sequence."""

@@ -54,7 +54,7 @@ SESSIONS = {
                           ("restore", 0), ("tok", True), ("restore", 1), ("tok", True),
                           ("restore", 0), ("tok", True), ("restore", 1), ("tok", True)],
                   record="all"),
-    # config 2's shape on 2 layers: causal prefill of 256 tokens, window 256
+    # 8 heads x 64 on 2 layers: causal prefill of 256 tokens, window 256
     "prefill": dict(geom=(2, 8, 8, 64, 64, 256), seed=606,
                     script=[("tok", True)] * 256, record=list(range(0, 256, 17)) + [255]),
     # with the attention front (tap convolution + head norm + RoPE on raw

@@ -91,10 +91,10 @@ def check_cache(o, g, layers, positions):
                 assert np.array_equal(vs[0].view(np.uint32), ovs[li, sl].view(np.uint32)), (li, p)
 
 
-def test_cfg1_prefix_plus_prompt_int8():
+def test_prefix_213_plus_prompt_16_int8():
     """One layer, MHA 8x64, 213 pinned schema positions + 16 prompt tokens,
     int8 KV as the engine stores it."""
-    say("cfg1 int8 session 229 tokens")
+    say("int8 session 213 + 16 tokens")
     script = [("tok", True)] * 213 + [("snap",)] + [("tok", True)] * 16
     o, g, worst, _ = replay((1, 8, 8, 64, 64, 256), script, seed=1)
     assert worst <= TOL, worst
@@ -259,10 +259,10 @@ def test_no_gate_and_rep_variants():
 
 # ------------------------------------------------------ prefill and prefixes
 
-def test_cfg2_causal_prefill_int8_all_layers():
+def test_causal_prefill_256_tokens_8_layers_int8():
     """8 layers x 256-token causal prefill through nda_prefill against the
     engine's token-by-token prefill; codes bit-exact."""
-    say("cfg2 prefill 8x256 int8")
+    say("prefill 8 layers x 256 tokens int8")
     N = nda()
     Lyr, nh, nkv, d, S = 8, 8, 8, 64, 256
     rng = np.random.default_rng(11)
@@ -298,7 +298,7 @@ def _views_for(ctx, li, seq, pos, nh, dtype):
 
 @pytest.mark.parametrize("kv_dtype", [O.KV_F16, O.KV_INT8])
 def test_shared_prefix_prefill_then_decode(kv_dtype):
-    """Config 4's structure at small batch: one 213-token prefix built once,
+    """The shared-prefix flow at small batch: one 213-token prefix built once,
     shared by every sequence; ragged causal suffixes; decode steps."""
     say("shared prefix dtype", kv_dtype)
     N = nda()
@@ -431,11 +431,11 @@ def test_error_paths():
 
 # --------------------------------------------------- full-size sampled check
 
-def test_cfg3_full_shape_one_layer_sampled():
-    """Config 3's full shape on one layer (4096 ragged sequences, L in
+def test_decode_4096_ragged_sequences_one_layer_sampled():
+    """The batched decode at full size on one layer (4096 ragged sequences, L in
     [213, 1024], fp16): the whole batch decodes, and 24 sampled sequences match
     the oracle; a second step after advance matches too."""
-    say("cfg3 full shape 1 layer")
+    say("decode 4096 ragged sequences, 1 layer")
     N = nda()
     B, nh, d, W = 4096, 8, 64, 1024
     rng = np.random.default_rng(14)
