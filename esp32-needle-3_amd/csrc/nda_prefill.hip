@@ -98,6 +98,7 @@ void prefill_kernel(PrefillArgs a)
     const int tid = threadIdx.x;
     const int lane = tid & 63, wave = tid >> 6;
     const int jh = lane >> 5, ln = lane & 31;
+    const int xor32 = (lane ^ 32) << 2;         // ds_bpermute address of the partner lane
     // XCD-aware order: work-group w runs on XCD w % 8, so consecutive work
     // items (the row tiles of one sequence and kv-head, which read the same
     // K/V) are given to work-groups of one XCD and share its L2.
@@ -209,7 +210,9 @@ void prefill_kernel(PrefillArgs a)
             sg.sc[i] = 0.0f;
             if (pr.page[i] >= 0) {
                 const int off = pr.off[i];
-                const uint8_t *hb = a.pool + (uint64_t)pr.page[i] * a.pg.page_bytes + (uint64_t)g * a.pg.head_bytes;
+                // a page is under 4 GiB: one 32 x 32 -> 64-bit multiply-add
+                const uint8_t *hb = a.pool + (uint64_t)(uint32_t)pr.page[i] * (uint32_t)a.pg.page_bytes +
+                                    (uint64_t)g * a.pg.head_bytes;
                 const uint8_t *src = isv ? hb + (uint64_t)P * DK * ES + (uint64_t)off * DV * ES
                                          : hb + (uint64_t)off * DK * ES;
                 sg.w[i] = __builtin_nontemporal_load(reinterpret_cast<const u32x4 *>(src) + ch);
@@ -331,7 +334,7 @@ void prefill_kernel(PrefillArgs a)
         for (int i = 1; i < 15; i += 2)
             mt = max3(mt, st[i], st[i + 1]);
         mt = max3(mt, st[15], st[15]);
-        mt = max3(mt, __shfl_xor(mt, 32, 64), mt);
+        mt = max3(mt, __int_as_float(__builtin_amdgcn_ds_bpermute(xor32, __float_as_int(mt))), mt);
         // Lazy max: keep the running max unless the tile exceeds it by more
         // than 2^8 (weights stay <= 256, exact range for fp16 and fp32), and
         // skip the rescale sweep when no row of the wave moved.
