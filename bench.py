@@ -737,7 +737,7 @@ def main():
     ap.add_argument("--no-prefill", action="store_true")
     ap.add_argument("--calib", action="store_true",
                     help="first run a 4 GiB device copy (known traffic, for counter calibration)")
-    ap.add_argument("--leg", choices=["cq", "cq_prefill", "block", "block_prefill", "prefill", "front"],
+    ap.add_argument("--leg", choices=["cq", "cq_prefill", "block", "block_prefill", "prefill", "front", "shared"],
                     help="run only this leg and print its JSON object (for profiling one kernel family)")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
@@ -764,7 +764,8 @@ def main():
         N._check(N.lib().nda_stream_create(N.C.byref(stream)))
         legs = {"cq": lambda: cq_leg(N, stream), "cq_prefill": lambda: cq_leg(N, stream, rows=49787, reps=5),
                 "block": lambda: block_leg(N, stream), "block_prefill": lambda: block_prefill_leg(N, stream),
-                "prefill": lambda: prefill_leg(N, stream), "front": lambda: front_leg(N, stream)}
+                "prefill": lambda: prefill_leg(N, stream), "front": lambda: front_leg(N, stream),
+                "shared": lambda: shared_prefix_leg(N, stream)}
         print(json.dumps(legs[args.leg]()), flush=True)
         return
     rng = np.random.default_rng(SEED)

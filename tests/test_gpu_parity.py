@@ -366,6 +366,65 @@ def test_shared_prefix_prefill_then_decode(kv_dtype):
     ctx.prefix_free(pid)
 
 
+def test_prefill_gqa_chunks_on_shared_prefix():
+    """Prefill of several chunks on one shared prefix at the engine's GQA
+    shape (12 q / 2 kv heads, qk 48, int8): a 100-token prefix (not a whole
+    number of key tiles), a first and a second suffix chunk (own keys then
+    include earlier suffix tokens), gated; then a call that mixes in a
+    sequence without the prefix. Every output against the oracle's
+    attention."""
+    say("prefill gqa chunks on a shared prefix")
+    N = nda()
+    nh, nkv, qk, vd, W, B, npre = 12, 2, 48, 64, 384, 5, 100
+    rng = np.random.default_rng(21)
+    ctx = N.Context(1, nh, nkv, qk, vd, W, kv_dtype=O.KV_INT8, max_seqs=B + 2)
+
+    def chunk(seq_ids, n, shared):
+        T = int(sum(n))
+        q = rng.standard_normal((T, nh, qk)).astype(np.float32)
+        k = rng.standard_normal((T, nkv, qk)).astype(np.float32)
+        v = rng.standard_normal((T, nkv, vd)).astype(np.float32)
+        g = rng.standard_normal((T, nh, vd)).astype(np.float32)
+        dout = N.DevBuf(T * nh * vd * 4)
+        pos0 = [ctx.seq_state(b)[0] for b in seq_ids]
+        ctx.prefill(0, n, N.DevBuf.from_array(q), N.DevBuf.from_array(k), N.DevBuf.from_array(v), dout,
+                    gate=N.DevBuf.from_array(g), seq_ids=seq_ids)
+        ctx.sync()
+        got = dout.to_array(np.float32, (T, nh * vd))
+        worst, r = 0.0, 0
+        for b, nb, p0 in zip(seq_ids, n, pos0):
+            view, keep = _views_for(ctx, 0, b, p0 + int(nb) - 1, nh, O.KV_INT8)
+            for t in range(int(nb)):
+                pos = p0 + t
+                runs = [npre, pos + 1 - npre] if shared[b] else [pos + 1]
+                want = O.attend_runs(view, np.arange(pos + 1), runs, q[r], g[r])
+                worst = max(worst, maxdiff(got[r], want))
+                r += 1
+        for b, nb in zip(seq_ids, n):
+            ctx.advance(1, [b], int(nb))
+        return worst
+
+    q = rng.standard_normal((npre, nh, qk)).astype(np.float32)
+    k = rng.standard_normal((npre, nkv, qk)).astype(np.float32)
+    v = rng.standard_normal((npre, nkv, vd)).astype(np.float32)
+    ctx.prefill(0, [npre], N.DevBuf.from_array(q), N.DevBuf.from_array(k), N.DevBuf.from_array(v),
+                N.DevBuf(npre * nh * vd * 4), seq_ids=[B])
+    ctx.advance(1, [B], npre)
+    pid = ctx.prefix_build(B)
+    shared = {b: True for b in range(B)}
+    shared[B + 1] = False
+    for b in range(B):
+        ctx.seq_attach(b, pid)
+    worst = chunk(list(range(B)), [1, 17, 40, 33, 5], shared)          # first suffix chunks
+    worst = max(worst, chunk([3, 0, 4], [70, 9, 1], shared))            # second chunks, out of order
+    worst = max(worst, chunk([1, B + 1, 2], [6, 40, 12], shared))       # a sequence without the prefix
+    say("prefill gqa chunks worst", worst)
+    assert worst <= TOL, worst
+    for b in range(B):
+        ctx.seq_reset(b)
+    ctx.prefix_free(pid)
+
+
 def test_int8_store_edge_rows():
     """Exact .5 ties, zero rows, +-absmax, subnormal scales: codes and scales
     identical to the oracle's (which is pinned to the reference's store)."""
