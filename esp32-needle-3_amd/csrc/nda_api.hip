@@ -545,6 +545,7 @@ AttnArgs attn_args(nda_ctx *c, uint32_t layer, uint32_t rows, const float *q, co
     // grid.y and the partial-buffer stride: chunks of the longest row.
     a.max_chunks = std::max<uint32_t>(1, (max_total + a.chunk - 1) / a.chunk);
     a.qscale = (float)(1.4426950408889634 / std::sqrt((double)c->cfg.qk_head_dim));
+    a.avg_len = rows ? (uint32_t)std::min<uint64_t>(sum_total / rows, 0xFFFFFFFFu) : 0;
     return a;
 }
 

@@ -54,6 +54,7 @@ struct AttnArgs {
     float qscale;            /* log2(e) / sqrt(dk) */
     const float *k_new;      /* [rows][nkv][dk] fused append (decode), or null */
     const float *v_new;      /* [rows][nkv][dv] */
+    uint32_t avg_len;        /* mean visible positions per row (work-group size) */
 };
 
 /* One launch of the MFMA causal-prefill kernel. A work item is one tile of

@@ -658,21 +658,25 @@ __global__ __launch_bounds__(256) void fill_kv_kernel(FillKvArgs a)
 template <int ES, int DK, int REP>
 constexpr int lanes_per_pos() { return ES == 2 ? 8 : ((REP >= 8 && DK % 64 == 0) ? 8 : 4); }
 
-// Waves per decode work-group: 8 for MHA and narrow GQA, whose per-lane
-// state merges cheaply and whose rows are split across many waves; one wave
-// for wide GQA (rep >= 4), where each lane carries rep heads of state and the
-// cross-wave merge would cost more than it parallelises (rows of a few
-// hundred positions: 4.4x faster at 12 q / 2 kv heads, int8). NDA_ATT_NW
-// fixes one value for every geometry (a build-time tuning knob).
+// Waves per decode work-group. Wide GQA (rep >= 4): one, since each lane
+// carries rep heads of state and the cross-wave merge would cost more than
+// it parallelises (rows of a few hundred positions: 4.4x faster at 12 q /
+// 2 kv heads, int8). MHA and narrow GQA: eight for work items of 448
+// positions or more, whose rows split across many waves; two below, where
+// 8-wave groups leave the chip with too few of them (1024 sequences on a
+// 213-token prefix, ~300 positions: 1.59 M against 1.21 M tokens/s; 4096
+// rows of 213-1024: eight is 6% faster). NDA_ATT_NW fixes one value for
+// every geometry (a build-time tuning knob).
 template <int REP>
-constexpr int att_nw()
+constexpr int att_nw(bool long_items)
 {
 #ifdef NDA_ATT_NW
     return NDA_ATT_NW;
 #else
-    return REP >= 4 ? 1 : 8;
+    return REP >= 4 ? 1 : (long_items ? 8 : 2);
 #endif
 }
+constexpr uint32_t ATT_LONG_ITEM = 448;
 
 // Positions per lane group per step: as many loads in flight as registers
 // allow without spilling (the int8 and wide-GQA states are larger).
@@ -721,11 +725,10 @@ int attend_split(const Geo &g, const AttnArgs &a)
     return 1;
 }
 
-template <int ES, int DK, int DV, int REP, int HS>
+template <int ES, int DK, int DV, int REP, int HS, int NW>
 static void launch_attend_hs(const AttnArgs &a, hipStream_t s)
 {
     constexpr int R = REP / HS;
-    constexpr int NW = HS > 1 ? 1 : att_nw<REP>();
     const dim3 grid(a.rows * a.pg.nkv * HS, a.max_chunks);
     hipLaunchKernelGGL((attend_kernel<ES, DK, DV, R, lanes_per_pos<ES, DK, R>(), att_np<ES, R>(), NW, HS>), grid,
                        dim3(64 * NW), 0, s, a);
@@ -736,12 +739,15 @@ hipError_t launch_attend(const Geo &g, const AttnArgs &a, hipStream_t s)
     if (a.rows == 0)
         return hipSuccess;
     const int hs = attend_split(g, a);
+    const bool long_items = (a.avg_len < a.chunk ? a.avg_len : a.chunk) >= ATT_LONG_ITEM;
 #define X(ES, DK, DV, REP)                                                                      \
     if (es_of(g) == ES && g.dk == DK && g.dv == DV && g.rep == REP) {                          \
         if (hs > 1)                                                                             \
-            launch_attend_hs<ES, DK, DV, REP, att_hs<REP>()>(a, s);                             \
+            launch_attend_hs<ES, DK, DV, REP, att_hs<REP>(), 1>(a, s);                          \
+        else if (long_items)                                                                    \
+            launch_attend_hs<ES, DK, DV, REP, 1, att_nw<REP>(true)>(a, s);                      \
         else                                                                                    \
-            launch_attend_hs<ES, DK, DV, REP, 1>(a, s);                                         \
+            launch_attend_hs<ES, DK, DV, REP, 1, att_nw<REP>(false)>(a, s);                     \
         return hipGetLastError();                                                               \
     }
     NDA_FOR_GEOMETRIES(X)
