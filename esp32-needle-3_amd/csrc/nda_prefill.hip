@@ -98,7 +98,6 @@ void prefill_kernel(PrefillArgs a)
     const int tid = threadIdx.x;
     const int lane = tid & 63, wave = tid >> 6;
     const int jh = lane >> 5, ln = lane & 31;
-    const int xor32 = (lane ^ 32) << 2;         // ds_bpermute address of the partner lane
     // XCD-aware order: work-group w runs on XCD w % 8, so consecutive work
     // items (the row tiles of one sequence and kv-head, which read the same
     // K/V) are given to work-groups of one XCD and share its L2.
@@ -302,7 +301,9 @@ void prefill_kernel(PrefillArgs a)
         // from the softmax through the P.V MFMAs, so a wave with softmax
         // work wins issue over waves still in their S chains (4% on a
         // 512-token chunk over 8K-32K keys; a ping-pong of half the waves one
-        // phase behind, tried against it, lost 8-15%).
+        // phase behind, tried against it, lost 8-15%). The softmax is on
+        // each tile's critical path, so its cross-half max takes a lane swap
+        // (5% over an LDS permute).
         __builtin_amdgcn_s_setprio(0);
 #pragma unroll
         for (int kb = 0; kb < NKB; kb++) {
@@ -334,7 +335,12 @@ void prefill_kernel(PrefillArgs a)
         for (int i = 1; i < 15; i += 2)
             mt = max3(mt, st[i], st[i + 1]);
         mt = max3(mt, st[15], st[15]);
-        mt = max3(mt, __int_as_float(__builtin_amdgcn_ds_bpermute(xor32, __float_as_int(mt))), mt);
+        {
+            // the partner half's max without an LDS round trip: the swap
+            // returns (own, partner) in lanes 0-31 and (partner, own) in 32-63
+            const auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(mt), __float_as_uint(mt), false, false);
+            mt = max3(mt, __uint_as_float(sw[0]), __uint_as_float(sw[1]));
+        }
         // Lazy max: keep the running max unless the tile exceeds it by more
         // than 2^8 (weights stay <= 256, exact range for fp16 and fp32), and
         // skip the rescale sweep when no row of the wave moved.
