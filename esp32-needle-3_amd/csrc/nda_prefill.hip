@@ -80,6 +80,102 @@ __device__ __forceinline__ _Float16 code_at(uint32_t w, int i)
         return __builtin_bit_cast(_Float16, (uint16_t)(w >> (16 * i)));
 }
 
+
+// One thread's part in moving key tiles from the page pool to LDS: chunk
+// c = tid + i * NTHR of a tile, K chunks [key][KC] first, then V chunks
+// [key][VC]. Every load is issued, from clamped indexes: a key past kmax
+// reads key kmax-1 (a stored position, so finite data that the causal mask
+// and a zero weight remove) and a thread past the last chunk reads the last
+// chunk, and never stores it. With no conditional loads, no loaded value is
+// needed before its use a stage later, so the in-order load counter drains
+// only old loads.
+template <int ES, int DK, int DV, int NTHR>
+struct PfIO {
+    using T = PfTile<ES, DK, DV, NTHR>;
+    struct PageRef {
+        int32_t page[T::CPT];
+        int off[T::CPT];
+    };
+    const uint8_t *pool;
+    const int32_t *own_pages, *pre_pages;
+    uint32_t page_bytes, head_bytes, log2_page, g;
+    int tid, kmax, n_sh;
+
+    __device__ __forceinline__ void fetch_pages(int kt, PageRef &pr) const
+    {
+        const int P = 1 << log2_page;
+#pragma unroll
+        for (int i = 0; i < T::CPT; i++) {
+            const int c = min(tid + i * NTHR, T::NCHUNK - 1);
+            const bool isv = c >= PF_KT * T::KC;
+            const int cc = isv ? c - PF_KT * T::KC : c;
+            const int kl = isv ? cc / T::VC : cc / T::KC;
+            const int key = min(kt + kl, kmax - 1);
+            const bool sh = key < n_sh;
+            const int sl = sh ? key : key - n_sh;
+            pr.page[i] = (sh ? pre_pages : own_pages)[sl >> log2_page];
+            pr.off[i] = sl & (P - 1);
+        }
+    }
+    __device__ __forceinline__ void load(const PageRef &pr, Staged<T::CPT> &sg) const
+    {
+        const int P = 1 << log2_page;
+#pragma unroll
+        for (int i = 0; i < T::CPT; i++) {
+            const int c = min(tid + i * NTHR, T::NCHUNK - 1);
+            const bool isv = c >= PF_KT * T::KC;
+            const int cc = isv ? c - PF_KT * T::KC : c;
+            const int ch = isv ? cc % T::VC : cc % T::KC;
+            const int off = pr.off[i];
+            // a page is under 4 GiB: one 32 x 32 -> 64-bit multiply-add
+            const uint8_t *hb = pool + (uint64_t)(uint32_t)pr.page[i] * page_bytes + (uint64_t)g * head_bytes;
+            const uint8_t *src = isv ? hb + (uint64_t)P * DK * ES + (uint64_t)off * DV * ES
+                                     : hb + (uint64_t)off * DK * ES;
+            sg.w[i] = __builtin_nontemporal_load(reinterpret_cast<const u32x4 *>(src) + ch);
+            if constexpr (ES == 1)
+                sg.sc[i] = reinterpret_cast<const float *>(hb + (uint64_t)P * (DK + DV))[(isv ? P : 0) + off];
+            else
+                sg.sc[i] = 0.0f;
+        }
+    }
+    __device__ __forceinline__ void store(const Staged<T::CPT> &sg, _Float16 (*Ks)[T::KPAD],
+                                          _Float16 (*Vt)[T::VPAD], float *Ksc, float *Vsc) const
+    {
+#pragma unroll
+        for (int i = 0; i < T::CPT; i++) {
+            const int c = tid + i * NTHR;
+            if (c >= T::NCHUNK)
+                continue;
+            const bool isv = c >= PF_KT * T::KC;
+            const int cc = isv ? c - PF_KT * T::KC : c;
+            const int kl = isv ? cc / T::VC : cc / T::KC;
+            const int ch = isv ? cc % T::VC : cc % T::KC;
+            if (!isv) {
+                if constexpr (ES == 2) {
+                    *reinterpret_cast<u32x4 *>(&Ks[kl][ch * 8]) = sg.w[i];
+                } else {
+                    half8 lo, hi;
+#pragma unroll
+                    for (int e = 0; e < 8; e++) {
+                        lo[e] = code_at<1>(sg.w[i][e >> 2], e & 3);
+                        hi[e] = code_at<1>(sg.w[i][2 + (e >> 2)], e & 3);
+                    }
+                    *reinterpret_cast<half8 *>(&Ks[kl][ch * 16]) = lo;
+                    *reinterpret_cast<half8 *>(&Ks[kl][ch * 16 + 8]) = hi;
+                    if (ch == 0)
+                        Ksc[kl] = sg.sc[i];
+                }
+            } else {
+#pragma unroll
+                for (int e = 0; e < T::EPC; e++)
+                    Vt[ch * T::EPC + e][kl] = code_at<ES>(sg.w[i][e / (4 / ES)], e % (4 / ES));
+                if (ES == 1 && ch == 0)
+                    Vsc[kl] = sg.sc[i];
+            }
+        }
+    }
+};
+
 template <int ES, int DK, int DV, int REP, int W>
 __global__ __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(W >= 8 ? 4 : 1)))
 void prefill_kernel(PrefillArgs a)
@@ -164,146 +260,70 @@ void prefill_kernel(PrefillArgs a)
     float16v acc0 = {}, acc1 = {};
     float m = -FLT_MAX, lsum = 0.0f;
 
-    const int32_t *own_pages = a.page_table + (uint64_t)seq * a.pg.pages_per_seq;
-    const int32_t *pre_pages = sd.prefix >= 0 ? a.prefix_pages + (uint64_t)sd.prefix * a.pg.pages_per_seq
-                                              : nullptr;
-    const int P = 1 << a.pg.log2_page;
+    PfIO<ES, DK, DV, NTHR> io;
+    io.pool = a.pool;
+    io.own_pages = a.page_table + (uint64_t)seq * a.pg.pages_per_seq;
+    io.pre_pages = sd.prefix >= 0 ? a.prefix_pages + (uint64_t)sd.prefix * a.pg.pages_per_seq : nullptr;
+    io.page_bytes = a.pg.page_bytes;
+    io.head_bytes = a.pg.head_bytes;
+    io.log2_page = a.pg.log2_page;
+    io.g = g;
+    io.tid = tid;
+    io.kmax = kmax;
+    io.n_sh = n_sh;
+    const int ntile = (kmax + PF_KT - 1) / PF_KT;
+    const int jfull = min(kfull / PF_KT, ntile);    // tiles [0, jfull) visible to every row
 
-    // Chunk c of a tile: K chunks [key][KC] first, then V chunks [key][VC].
-    // Page ids of a tile are fetched one iteration before its data, so no
-    // data load waits on a page-table round trip.
-    struct PageRef {
-        int32_t page[T::CPT];
-        int off[T::CPT];
-    };
-    auto fetch_pages = [&](int kt, PageRef &pr) {
-#pragma unroll
-        for (int i = 0; i < T::CPT; i++) {
-            const int c = tid + i * NTHR;
-            const bool isv = c >= PF_KT * T::KC;
-            const int cc = isv ? c - PF_KT * T::KC : c;
-            const int kl = isv ? cc / T::VC : cc / T::KC;
-            const int key = kt + kl;
-            pr.page[i] = -1;
-            pr.off[i] = 0;
-            if (c < T::NCHUNK && key < kmax) {
-                if (key < n_sh) {
-                    pr.page[i] = pre_pages[key >> a.pg.log2_page];
-                    pr.off[i] = key & (P - 1);
-                } else {
-                    const int sl = key - n_sh;
-                    pr.page[i] = own_pages[sl >> a.pg.log2_page];
-                    pr.off[i] = sl & (P - 1);
-                }
-            }
-        }
-    };
-    auto load_tile = [&](const PageRef &pr, Staged<T::CPT> &sg) {
-#pragma unroll
-        for (int i = 0; i < T::CPT; i++) {
-            const int c = tid + i * NTHR;
-            const bool isv = c >= PF_KT * T::KC;
-            const int cc = isv ? c - PF_KT * T::KC : c;
-            const int ch = isv ? cc % T::VC : cc % T::KC;
-            sg.w[i] = u32x4{0u, 0u, 0u, 0u};
-            sg.sc[i] = 0.0f;
-            if (pr.page[i] >= 0) {
-                const int off = pr.off[i];
-                // a page is under 4 GiB: one 32 x 32 -> 64-bit multiply-add
-                const uint8_t *hb = a.pool + (uint64_t)(uint32_t)pr.page[i] * (uint32_t)a.pg.page_bytes +
-                                    (uint64_t)g * a.pg.head_bytes;
-                const uint8_t *src = isv ? hb + (uint64_t)P * DK * ES + (uint64_t)off * DV * ES
-                                         : hb + (uint64_t)off * DK * ES;
-                sg.w[i] = __builtin_nontemporal_load(reinterpret_cast<const u32x4 *>(src) + ch);
-                if (ES == 1 && ch == 0)
-                    sg.sc[i] = reinterpret_cast<const float *>(hb + (uint64_t)P * (DK + DV))[(isv ? P : 0) + off];
-            }
-        }
-    };
-    auto store_tile = [&](const Staged<T::CPT> &sg, int buf) {
-        _Float16 (*Ks)[T::KPAD] = Ks2[buf];
-        _Float16 (*Vt)[T::VPAD] = Vt2[buf];
-        float *Ksc = Ksc2[buf], *Vsc = Vsc2[buf];
-#pragma unroll
-        for (int i = 0; i < T::CPT; i++) {
-            const int c = tid + i * NTHR;
-            if (c >= T::NCHUNK)
-                continue;
-            const bool isv = c >= PF_KT * T::KC;
-            const int cc = isv ? c - PF_KT * T::KC : c;
-            const int kl = isv ? cc / T::VC : cc / T::KC;
-            const int ch = isv ? cc % T::VC : cc % T::KC;
-            if (!isv) {
-                if constexpr (ES == 2) {
-                    *reinterpret_cast<u32x4 *>(&Ks[kl][ch * 8]) = sg.w[i];
-                } else {
-                    half8 lo, hi;
-#pragma unroll
-                    for (int e = 0; e < 8; e++) {
-                        lo[e] = code_at<1>(sg.w[i][e >> 2], e & 3);
-                        hi[e] = code_at<1>(sg.w[i][2 + (e >> 2)], e & 3);
-                    }
-                    *reinterpret_cast<half8 *>(&Ks[kl][ch * 16]) = lo;
-                    *reinterpret_cast<half8 *>(&Ks[kl][ch * 16 + 8]) = hi;
-                    if (ch == 0)
-                        Ksc[kl] = sg.sc[i];
-                }
-            } else {
-#pragma unroll
-                for (int e = 0; e < T::EPC; e++)
-                    Vt[ch * T::EPC + e][kl] = code_at<ES>(sg.w[i][e / (4 / ES)], e % (4 / ES));
-                if (ES == 1 && ch == 0)
-                    Vsc[kl] = sg.sc[i];
-            }
-        }
-    };
-
-    // Register prefetch: with PD = 2, tile kt+32 waits in sg1 for its LDS
-    // store while tile kt+64 loads into sg2, so each load has two tiles of
-    // compute to land; the 8-wave variant keeps one tile in flight to stay
-    // within the 128 registers of 4 waves per SIMD. Page ids run one tile
-    // further ahead than the data.
+    // Register prefetch: with PD = 2, tile j+1 waits in registers for its
+    // LDS store while tile j+2 loads, so each load has two tiles of compute
+    // to land; the 8-wave variant keeps one tile in flight to stay within the
+    // 128 registers of 4 waves per SIMD. Tiles in flight and their page ids
+    // sit in rings indexed by tile parity (a register copy would wait on the
+    // newest load), and a tile's page ids are fetched before the data load
+    // issued beside them, so waiting for ids fetched a tile earlier never
+    // waits for the data load that followed them.
     constexpr int PD = W >= 8 ? 1 : 2;
-    Staged<T::CPT> sg1, sg2;
-    PageRef pr2, pr3;
-    fetch_pages(0, pr2);
-    load_tile(pr2, sg1);
-    store_tile(sg1, 0);
-    fetch_pages(PF_KT, pr2);
+    typename PfIO<ES, DK, DV, NTHR>::PageRef prn[2];
+    Staged<T::CPT> sg[PD];
+    io.fetch_pages(0, prn[0]);
+    io.fetch_pages(PF_KT, prn[1]);
+    io.load(prn[0], sg[0]);                     // tile 0
+    io.store(sg[0], Ks2[0], Vt2[0], Ksc2[0], Vsc2[0]);
+    io.fetch_pages(2 * PF_KT, prn[0]);
+    io.load(prn[1], sg[1 % PD]);                // tile 1
     if constexpr (PD == 2) {
-        load_tile(pr2, sg1);
-        fetch_pages(2 * PF_KT, pr2);
+        io.fetch_pages(3 * PF_KT, prn[1]);
+        io.load(prn[0], sg[0]);                 // tile 2
     }
     __syncthreads();
-    int cur = 0;
-    // One key tile; `masked` is a literal at both call sites, so the
-    // unmasked loop carries no diagonal-mask code at all.
-    auto tile = [&](const int kt, const bool masked) __attribute__((always_inline)) {
-        const bool more = kt + PF_KT < kmax;
-        // No `more` guard on the loads: page ids past kmax are -1, so such a
-        // tile loads nothing, and every path waits for the page ids at the
-        // same point (a guarded load left a path on which the wait moved
-        // behind the just-issued tile load).
-        if constexpr (PD == 2) {
-            load_tile(pr2, sg2);            // tile kt+64
-            fetch_pages(kt + 3 * PF_KT, pr3);
-        } else {
-            load_tile(pr2, sg1);            // tile kt+32
-            fetch_pages(kt + 2 * PF_KT, pr3);
-        }
-        const _Float16 (*Ks)[T::KPAD] = Ks2[cur];
-        const _Float16 (*Vt)[T::VPAD] = Vt2[cur];
-        const float *Ksc = Ksc2[cur], *Vsc = Vsc2[cur];
+
+    // One key tile j (parity PJ = j & 1); the LDS buffer of tile j is PJ.
+    // `masked` is a compile-time flag: the loop over tiles below the
+    // diagonal carries no mask code (whose registers would spill the 8-wave
+    // variant).
+    auto tile = [&](const int j, auto pj, auto masked) __attribute__((always_inline)) {
+        constexpr int PJ = decltype(pj)::value, Q1 = PJ ^ 1;
+        const int kt = j * PF_KT;
+        // ids of tile j+PD+1 into the slot of tile j+PD-1's (spent), then the
+        // data of tile j+PD; past kmax the loads read the last key (finite
+        // data, masked)
+        io.fetch_pages((j + PD + 1) * PF_KT, prn[(PJ + PD + 1) & 1]);
+        io.load(prn[(PJ + PD) & 1], sg[(PJ + PD) % PD]);
+        const _Float16 (*Ks)[T::KPAD] = Ks2[PJ];
+        const _Float16 (*Vt)[T::VPAD] = Vt2[PJ];
+        const float *Ksc = Ksc2[PJ], *Vsc = Vsc2[PJ];
 
         // ---- S^T = K . Q^T (keys x rows), accumulate hi then lo
         float16v st = {};
         // Wave priority: normal while this wave issues its S MFMAs, raised
         // from the softmax through the P.V MFMAs, so a wave with softmax
         // work wins issue over waves still in their S chains (4% on a
-        // 512-token chunk over 8K-32K keys; a ping-pong of half the waves one
-        // phase behind, tried against it, lost 8-15%). The softmax is on
-        // each tile's critical path, so its cross-half max takes a lane swap
-        // (5% over an LDS permute).
+        // 512-token chunk over 8K-32K keys). A ping-pong of two waves per
+        // SIMD, one in its MFMAs while the other runs its softmax, lost 3%
+        // against it: with one work-group per CU, latency the four resident
+        // waves hide here stays exposed. The softmax is on each tile's
+        // critical path, so its cross-half max takes a lane swap (5% over an
+        // LDS permute) and its max and sum are trees.
         __builtin_amdgcn_s_setprio(0);
 #pragma unroll
         for (int kb = 0; kb < NKB; kb++) {
@@ -320,24 +340,23 @@ void prefill_kernel(PrefillArgs a)
             for (int i = 0; i < 16; i++)
                 st[i] *= Ksc[8 * (i >> 2) + 4 * jh + (i & 3)];
         }
-        if (masked) {
+        if constexpr (decltype(masked)::value) {
 #pragma unroll
             for (int i = 0; i < 16; i++) {
                 const int kl = 8 * (i >> 2) + 4 * jh + (i & 3);
                 st[i] = kt + kl > qpos ? -INFINITY : st[i];
             }
         }
-        // tile max over the 16 scores and the partner lane's, on 3-input
-        // maxes (fmaxf would first make NaN-quieting copies of its inputs;
-        // scores are never NaN)
-        float mt = st[0];
-#pragma unroll
-        for (int i = 1; i < 15; i += 2)
-            mt = max3(mt, st[i], st[i + 1]);
-        mt = max3(mt, st[15], st[15]);
+        // tile max over the 16 scores (a tree of 3-input maxes: fmaxf would
+        // first make NaN-quieting copies of its inputs; scores are never NaN)
+        // and the partner lane's, without an LDS round trip: the swap
+        // returns (own, partner) in lanes 0-31 and (partner, own) in 32-63
+        const float x0 = max3(st[0], st[1], st[2]), x1 = max3(st[3], st[4], st[5]);
+        const float x2 = max3(st[6], st[7], st[8]), x3 = max3(st[9], st[10], st[11]);
+        const float x4 = max3(st[12], st[13], st[14]);
+        const float y0 = max3(x0, x1, x2), y1 = max3(x3, x4, st[15]);
+        float mt = max3(y0, y1, y1);
         {
-            // the partner half's max without an LDS round trip: the swap
-            // returns (own, partner) in lanes 0-31 and (partner, own) in 32-63
             const auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(mt), __float_as_uint(mt), false, false);
             mt = max3(mt, __uint_as_float(sw[0]), __uint_as_float(sw[1]));
         }
@@ -401,21 +420,29 @@ void prefill_kernel(PrefillArgs a)
             }
         }
         __builtin_amdgcn_s_setprio(0);
-        if (more)
-            store_tile(sg1, cur ^ 1);       // tile kt+32 into the other buffer (its readers are done)
-        if constexpr (PD == 2)
-            sg1 = sg2;
-        pr2 = pr3;
+        if (j + 1 < ntile)   // tile j+1 into the other buffer (its readers are done)
+            io.store(sg[(PJ + 1) % PD], Ks2[Q1], Vt2[Q1], Ksc2[Q1], Vsc2[Q1]);
         __syncthreads();
-        cur ^= 1;
     };
-    // tiles [0, kfull_end) are visible to every row of the work-group
-    const int kfull_end = min((kfull / PF_KT) * PF_KT, kmax);
-    int kt = 0;
-    for (; kt < kfull_end; kt += PF_KT)
-        tile(kt, false);
-    for (; kt < kmax; kt += PF_KT)
-        tile(kt, true);
+    using P0 = std::integral_constant<int, 0>;
+    using P1 = std::integral_constant<int, 1>;
+    using Full = std::false_type;
+    using Diag = std::true_type;
+    // Pairs of tiles keep each parity static. The unmasked loop stops at an
+    // even tile, so the masked loop starts on parity 0 as well (a visible
+    // tile taken into it masks nothing).
+    const int jeven = jfull & ~1;
+    int j = 0;
+    for (; j < jeven; j += 2) {
+        tile(j, P0{}, Full{});
+        tile(j + 1, P1{}, Full{});
+    }
+    for (; j + 1 < ntile; j += 2) {
+        tile(j, P0{}, Diag{});
+        tile(j + 1, P1{}, Diag{});
+    }
+    if (j < ntile)
+        tile(j, P0{}, Diag{});
 
     // ---- emit: lane holds row ln, dims 32*dt + 8*(i/4) + 4*jh + (i%4)
     lsum += __shfl_xor(lsum, 32, 64);
