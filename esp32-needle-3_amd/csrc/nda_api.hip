@@ -549,8 +549,49 @@ AttnArgs attn_args(nda_ctx *c, uint32_t layer, uint32_t rows, const float *q, co
     return a;
 }
 
+// GQA decode on MFMA: with 4 or more query heads per kv-head (int8 K/V),
+// one wave per (row, kv-head) runs the prefill kernel's tile arithmetic with
+// the group's heads as its rows (S^T = K.Q^T, O^T += V^T.P^T), where the
+// VALU kernel spends its time on per-lane dot products and their lane
+// reductions (2.5x on 4096 rows of the engine's 12/2-head shape). Launches
+// that fuse the store, carry per-row offsets or split rows stay on the VALU
+// kernel, and so do tiny ones (an engine session), whose VALU waves split
+// each row's positions between them.
+constexpr uint64_t MFMA_DECODE_MIN_ITEMS = 16;
+
+bool mfma_decode_geo(const nda_ctx *c)
+{
+    return decode_mfma_supported(c->geo) && !(c->cfg.flags & NDA_FLAG_DECODE_VALU);
+}
+
+bool mfma_decode(const nda_ctx *c, const AttnArgs &a)
+{
+    return mfma_decode_geo(c) && !a.k_new && !a.row_t && a.max_chunks == 1 &&
+           (uint64_t)a.rows * c->cfg.n_kv_heads >= MFMA_DECODE_MIN_ITEMS;
+}
+
 int run_attend(nda_ctx *c, AttnArgs &a, hipStream_t st)
 {
+    if (mfma_decode(c, a)) {
+        PrefillArgs pa{};
+        pa.q = a.q;
+        pa.gate = a.gate;
+        pa.out = a.out;
+        pa.pool = a.pool;
+        pa.page_table = a.page_table;
+        pa.prefix_pages = a.prefix_pages;
+        pa.seqs = a.seqs;
+        pa.row_seq = a.row_seq;
+        pa.pg = a.pg;
+        pa.n_items = a.rows * c->cfg.n_kv_heads;
+        pa.nh = a.nh;
+        pa.qscale = a.qscale;
+        ProfScope ps(c, NDA_K_DECODE, st);
+        hipError_t e = launch_decode_mfma(c->geo, pa, st);
+        if (e != hipSuccess)
+            return hip_fail(c, e, "decode (MFMA) kernel launch");
+        return NDA_OK;
+    }
     if (a.max_chunks > 1) {
         int rc = ensure_part(c, (size_t)a.rows * a.nh * a.max_chunks * (c->cfg.v_head_dim + 2));
         if (rc)
@@ -1084,13 +1125,16 @@ int nda_decode(nda_ctx *c, uint32_t layer, uint32_t nseq, const uint32_t *ids, c
 // engine session) fuse both into one launch: the decode work-group owning
 // the new slot quantises and stores it before attending. Large batches keep
 // two launches: a store plus barrier at the head of every one of tens of
-// thousands of work-groups costs more than the separate append kernel.
+// thousands of work-groups costs more than the separate append kernel; GQA
+// groups the MFMA decode serves switch to it (and so to two launches) from
+// 4 work items per CU.
 int nda_step(nda_ctx *c, uint32_t layer, uint32_t nseq, const uint32_t *ids, const float *q,
              const float *k, const float *v, const float *gate, float *out, void *stream)
 {
     if (c && nseq && (!k || !v))
         return fail(c, NDA_ERR_ARG, "null k/v");
-    if (c && (uint64_t)nseq * c->cfg.n_kv_heads >= 16ull * (uint64_t)c->cus) {
+    const uint64_t units = c ? (uint64_t)nseq * c->cfg.n_kv_heads : 0;
+    if (c && (units >= 16ull * (uint64_t)c->cus || (mfma_decode_geo(c) && units >= 4ull * (uint64_t)c->cus))) {
         if (int rc = nda_kv_append(c, layer, nseq, ids, k, v, stream))
             return rc;
         return decode_impl(c, layer, nseq, ids, q, nullptr, nullptr, gate, out, stream);

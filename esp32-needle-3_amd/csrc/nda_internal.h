@@ -71,6 +71,7 @@ struct PrefillArgs {
     const uint32_t *bseq;    /* [nseq] sequence id per batch index */
     const uint32_t *btok0;   /* [nseq] first packed token of the batch index */
     const uint32_t *bntok;   /* [nseq] tokens of the batch index */
+    const uint32_t *row_seq; /* decode launches (one wave per item): sequence of each row, or null */
     PageGeom pg;
     uint32_t n_items;
     uint32_t nh;
@@ -242,6 +243,10 @@ struct Geo {
 hipError_t launch_append(const Geo &g, const AppendArgs &a, hipStream_t s);
 hipError_t launch_attend(const Geo &g, const AttnArgs &a, hipStream_t s);
 hipError_t launch_prefill(const Geo &g, const PrefillArgs &a, int waves, hipStream_t s);
+/* GQA decode on MFMA: one wave per (row, kv-head) item, n_items = rows * nkv,
+ * items in (row, kv-head) order; a.row_seq as in AttnArgs. */
+bool decode_mfma_supported(const Geo &g);
+hipError_t launch_decode_mfma(const Geo &g, const PrefillArgs &a, hipStream_t s);
 hipError_t launch_combine(const Geo &g, const AttnArgs &a, hipStream_t s);
 hipError_t launch_copy(const Geo &g, const CopyArgs &a, hipStream_t s);
 hipError_t launch_gather(const Geo &g, const StageArgs &a, hipStream_t s);

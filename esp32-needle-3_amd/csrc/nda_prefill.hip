@@ -49,6 +49,7 @@ __device__ __forceinline__ float16v mfma32(half8 a, half8 b, float16v c)
 }
 
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 typedef __fp16 fp16x2 __attribute__((ext_vector_type(2)));
 
 template <int ES, int DK, int DV, int NTHR>
@@ -471,6 +472,313 @@ void prefill_kernel(PrefillArgs a)
             *reinterpret_cast<float4 *>(o + d0) = z;
         }
     }
+}
+
+// ------------------------------------------------------------ GQA decode
+//
+// Decode of a GQA group (rep >= 4) on MFMA: one wave per (row, kv-head), the
+// group's rep query heads as the wave's rows (32 row slots, rep of them
+// valid), every visible slot as its keys, in slot order (sinks, shared
+// prefix and ring alike; softmax does not depend on the order, and the
+// visible set is the engine's, engine/src/nd_model.c:2451-2483). The tile
+// arithmetic is the prefill kernel's (S^T = K.Q^T and O^T += V^T.P^T with
+// fp16 hi + lo operands, the lazy running max); only keys past the last
+// visible slot are masked. The per-lane dot products, lane reductions and
+// fp32 conversions that bound the VALU decode kernel at this shape move to
+// the matrix cores.
+//
+// Staging: lane (ln, jh) moves half jh of key ln of a 32-key tile (K codes
+// [DK/2 jh, +DK/2), V codes [32 jh, +32) and the key's K (jh 0) or V (jh 1)
+// scale), so each lane needs one page id a tile, fetched a tile ahead. The
+// loads are unconditional (a key past the last visible slot reads the last
+// one: finite data, masked). int8 codes become fp16 exactly with one byte
+// permute and one packed fp16 subtract per two codes: 0x64 over the byte
+// (code ^ 0x80) is the fp16 1024 + code + 128. One wave owns its LDS tile,
+// whose accesses complete in order, so one buffer serves.
+typedef _Float16 half2v __attribute__((ext_vector_type(2)));
+
+template <int SEL>
+__device__ __forceinline__ half2v codes2(uint32_t xs)   // xs = codes ^ 0x80808080
+{
+    const uint32_t u = __builtin_amdgcn_perm(0x64646464u, xs, (uint32_t)SEL);
+    return __builtin_bit_cast(half2v, u) - half2v{(_Float16)1152.0f, (_Float16)1152.0f};
+}
+
+template <int DK, int DV, int REP>
+__global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(3)))
+void decode_mfma_kernel(PrefillArgs a)
+{
+    static_assert(DK % 16 == 0 && DV == 64 && REP <= 32, "decode tiles: dk multiple of 16, dv 64");
+    constexpr int NKB = DK / 16;
+    constexpr int KPAD = DK + 8, VPAD = PF_KT + 4;
+    constexpr int KH = DK / 2, VH = DV / 2;     // codes a lane moves per key
+    static_assert(KH % 8 == 0 && VH % 16 == 0, "lane halves are whole 8- and 16-byte loads");
+    __shared__ __attribute__((aligned(16))) _Float16 Ks[PF_KT][KPAD];
+    __shared__ __attribute__((aligned(16))) _Float16 Vt[DV][VPAD];
+    __shared__ float Sc[2][PF_KT];              // K, V scales of the tile's keys
+
+    const int lane = threadIdx.x;
+    const int jh = lane >> 5, ln = lane & 31;
+    const uint32_t nkv = a.pg.nkv;
+    const uint32_t b = blockIdx.x / nkv, g = blockIdx.x % nkv;
+    const uint32_t seq = a.row_seq ? a.row_seq[b] : b;
+    const SeqDev sd = a.seqs[seq];
+    const Visible vis = visible(sd, sd.pos, (int)a.pg.window);
+    const int n_sh = vis.n_sh, total = vis.n_sh + vis.n_own;
+
+    const bool rvalid = ln < REP;
+    const uint64_t qrow = (uint64_t)b * a.nh + g * REP + (rvalid ? ln : 0);
+    half8 qh[NKB], ql[NKB];
+    {
+        const float *qr = a.q + qrow * DK + 8 * jh;
+        float4 qv[NKB][2];
+#pragma unroll
+        for (int kb = 0; kb < NKB; kb++) {
+            qv[kb][0] = *reinterpret_cast<const float4 *>(qr + 16 * kb);
+            qv[kb][1] = *reinterpret_cast<const float4 *>(qr + 16 * kb + 4);
+        }
+        const float qs = rvalid ? a.qscale : 0.0f;
+#pragma unroll
+        for (int kb = 0; kb < NKB; kb++) {
+            const float xs[8] = {qv[kb][0].x, qv[kb][0].y, qv[kb][0].z, qv[kb][0].w,
+                                 qv[kb][1].x, qv[kb][1].y, qv[kb][1].z, qv[kb][1].w};
+#pragma unroll
+            for (int s = 0; s < 8; s++) {
+                float x = xs[s] * qs;
+                asm volatile("" : "+v"(x));
+                const _Float16 hi = (_Float16)x;
+                qh[kb][s] = hi;
+                ql[kb][s] = (_Float16)(x - (float)hi);
+            }
+        }
+    }
+
+    const int P = 1 << a.pg.log2_page;
+    const int32_t *own = a.page_table + (uint64_t)seq * a.pg.pages_per_seq;
+    const int32_t *pre = sd.prefix >= 0 ? a.prefix_pages + (uint64_t)sd.prefix * a.pg.pages_per_seq : own;
+    // page id (loaded) and in-page offset of this lane's key of tile j
+    auto fetch = [&](int j, int32_t &pid, int &off) __attribute__((always_inline)) {
+        const int key = min(j * PF_KT + ln, total - 1);
+        const bool sh = key < n_sh;
+        const int sl = sh ? key : key - n_sh;
+        pid = (sh ? pre : own)[sl >> a.pg.log2_page];
+        off = sl & (P - 1);
+    };
+    struct Stage {
+        uint32_t k[KH / 4], v[VH / 4];
+        float sc;
+    };
+    auto load = [&](int32_t pid, int off, Stage &sg) __attribute__((always_inline)) {
+        // a page is under 4 GiB: one 32 x 32 -> 64-bit multiply-add
+        const uint8_t *hb = a.pool + (uint64_t)(uint32_t)pid * (uint32_t)a.pg.page_bytes + (uint64_t)g * a.pg.head_bytes;
+        const uint8_t *kp = hb + off * DK + KH * jh;
+        const uint8_t *vp = hb + P * DK + off * DV + VH * jh;
+#pragma unroll
+        for (int i = 0; i < KH / 8; i++) {
+            const u32x2 x = __builtin_nontemporal_load(reinterpret_cast<const u32x2 *>(kp) + i);
+            sg.k[2 * i] = x.x;
+            sg.k[2 * i + 1] = x.y;
+        }
+#pragma unroll
+        for (int i = 0; i < VH / 16; i++) {
+            const u32x4 x = __builtin_nontemporal_load(reinterpret_cast<const u32x4 *>(vp) + i);
+            sg.v[4 * i] = x.x;
+            sg.v[4 * i + 1] = x.y;
+            sg.v[4 * i + 2] = x.z;
+            sg.v[4 * i + 3] = x.w;
+        }
+        sg.sc = reinterpret_cast<const float *>(hb + P * (DK + DV))[jh * P + off];
+    };
+    auto store = [&](const Stage &sg) __attribute__((always_inline)) {
+#pragma unroll
+        for (int i = 0; i < KH / 8; i++) {
+            const uint32_t x0 = sg.k[2 * i] ^ 0x80808080u, x1 = sg.k[2 * i + 1] ^ 0x80808080u;
+            const half2v c0 = codes2<0x04010400>(x0), c1 = codes2<0x04030402>(x0);
+            const half2v c2 = codes2<0x04010400>(x1), c3 = codes2<0x04030402>(x1);
+            *reinterpret_cast<half8 *>(&Ks[ln][KH * jh + 8 * i]) =
+                half8{c0[0], c0[1], c1[0], c1[1], c2[0], c2[1], c3[0], c3[1]};
+        }
+#pragma unroll
+        for (int i = 0; i < VH / 4; i++) {
+            const uint32_t x = sg.v[i] ^ 0x80808080u;
+            const half2v c0 = codes2<0x04010400>(x), c1 = codes2<0x04030402>(x);
+            Vt[VH * jh + 4 * i + 0][ln] = c0[0];
+            Vt[VH * jh + 4 * i + 1][ln] = c0[1];
+            Vt[VH * jh + 4 * i + 2][ln] = c1[0];
+            Vt[VH * jh + 4 * i + 3][ln] = c1[1];
+        }
+        Sc[jh][ln] = sg.sc;
+    };
+
+    float16v acc0 = {}, acc1 = {};
+    float m = -FLT_MAX, lsum = 0.0f;
+    const int qlast = total - 1;                // keys past it are masked
+    const int ntile = (total + PF_KT - 1) / PF_KT;
+    const int jfull = total / PF_KT;            // tiles [0, jfull) are all visible
+
+    int32_t pid[2];
+    int poff[2];
+    Stage sg;
+    fetch(0, pid[0], poff[0]);
+    fetch(1, pid[1], poff[1]);
+    load(pid[0], poff[0], sg);
+    store(sg);
+
+    // tile j (parity PJ): ids of tile j+2 into tile j's slot, data of tile
+    // j+1, the tile's arithmetic, then tile j+1 into LDS
+    auto tile = [&](const int j, auto pj, auto masked) __attribute__((always_inline)) {
+        constexpr int PJ = decltype(pj)::value, Q1 = PJ ^ 1;
+        const int kt = j * PF_KT;
+        fetch(j + 2, pid[PJ], poff[PJ]);
+        load(pid[Q1], poff[Q1], sg);
+
+        float16v st = {};
+        __builtin_amdgcn_s_setprio(0);
+#pragma unroll
+        for (int kb = 0; kb < NKB; kb++) {
+            const half8 ka = *reinterpret_cast<const half8 *>(&Ks[ln][16 * kb + 8 * jh]);
+            st = mfma32(ka, qh[kb], st);
+            st = mfma32(ka, ql[kb], st);
+        }
+        __builtin_amdgcn_s_setprio(1);
+#pragma unroll
+        for (int i = 0; i < 16; i++)
+            st[i] *= Sc[0][8 * (i >> 2) + 4 * jh + (i & 3)];
+        if constexpr (decltype(masked)::value) {
+#pragma unroll
+            for (int i = 0; i < 16; i++) {
+                const int kl = 8 * (i >> 2) + 4 * jh + (i & 3);
+                st[i] = kt + kl > qlast ? -INFINITY : st[i];
+            }
+        }
+        const float x0 = max3(st[0], st[1], st[2]), x1 = max3(st[3], st[4], st[5]);
+        const float x2 = max3(st[6], st[7], st[8]), x3 = max3(st[9], st[10], st[11]);
+        const float x4 = max3(st[12], st[13], st[14]);
+        const float y0 = max3(x0, x1, x2), y1 = max3(x3, x4, st[15]);
+        float mt = max3(y0, y1, y1);
+        {
+            const auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(mt), __float_as_uint(mt), false, false);
+            mt = max3(mt, __uint_as_float(sw[0]), __uint_as_float(sw[1]));
+        }
+        const bool grow = mt > m + 8.0f;
+        if (__builtin_expect(__ballot(grow) != 0, 0)) {
+            const float mnew = grow ? mt : m;
+            const float rs = fast_exp2(m - mnew);
+            m = mnew;
+            lsum *= rs;
+#pragma unroll
+            for (int i = 0; i < 16; i++) {
+                acc0[i] *= rs;
+                acc1[i] *= rs;
+            }
+        }
+        u32x4 phw[2], plw[2];
+#pragma unroll
+        for (int i = 0; i < 16; i += 2) {
+            float p0 = fast_exp2(st[i] - m), p1 = fast_exp2(st[i + 1] - m);
+            lsum += p0 + p1;
+            p0 *= Sc[1][8 * (i >> 2) + 4 * jh + (i & 3)];
+            p1 *= Sc[1][8 * (i >> 2) + 4 * jh + ((i + 1) & 3)];
+            const fp16x2 hh = __builtin_amdgcn_cvt_pkrtz(p0, p1);
+            const uint32_t hw = __builtin_bit_cast(uint32_t, hh);
+            uint32_t lw;
+            asm("v_fma_mixlo_f16 %0, %1, -1.0, %2 op_sel_hi:[1,0,0]" : "=v"(lw) : "v"(hw), "v"(p0));
+            asm("v_fma_mixhi_f16 %0, %1, -1.0, %2 op_sel:[1,0,0] op_sel_hi:[1,0,0]" : "+v"(lw) : "v"(hw), "v"(p1));
+            phw[i >> 3][(i & 7) >> 1] = hw;
+            plw[i >> 3][(i & 7) >> 1] = lw;
+        }
+        half8 ph[2], pl[2];
+        ph[0] = __builtin_bit_cast(half8, phw[0]);
+        ph[1] = __builtin_bit_cast(half8, phw[1]);
+        pl[0] = __builtin_bit_cast(half8, plw[0]);
+        pl[1] = __builtin_bit_cast(half8, plw[1]);
+#pragma unroll
+        for (int kb2 = 0; kb2 < 2; kb2++) {
+#pragma unroll
+            for (int dt = 0; dt < 2; dt++) {
+                const _Float16 *vr = &Vt[32 * dt + ln][16 * kb2 + 4 * jh];
+                const half4 v0 = *reinterpret_cast<const half4 *>(vr);
+                const half4 v1 = *reinterpret_cast<const half4 *>(vr + 8);
+                const half8 va = {v0[0], v0[1], v0[2], v0[3], v1[0], v1[1], v1[2], v1[3]};
+                if (dt == 0) {
+                    acc0 = mfma32(va, ph[kb2], acc0);
+                    acc0 = mfma32(va, pl[kb2], acc0);
+                } else {
+                    acc1 = mfma32(va, ph[kb2], acc1);
+                    acc1 = mfma32(va, pl[kb2], acc1);
+                }
+            }
+        }
+        __builtin_amdgcn_s_setprio(0);
+        if (j + 1 < ntile)      // after this tile's last LDS reads, in the wave's order
+            store(sg);
+    };
+    using P0 = std::integral_constant<int, 0>;
+    using P1 = std::integral_constant<int, 1>;
+    const int jeven = jfull & ~1;
+    int j = 0;
+    for (; j < jeven; j += 2) {
+        tile(j, P0{}, std::false_type{});
+        tile(j + 1, P1{}, std::false_type{});
+    }
+    for (; j + 1 < ntile; j += 2) {
+        tile(j, P0{}, std::true_type{});
+        tile(j + 1, P1{}, std::true_type{});
+    }
+    if (j < ntile)
+        tile(j, P0{}, std::true_type{});
+
+    lsum += __shfl_xor(lsum, 32, 64);
+    if (!rvalid)
+        return;
+    const float inv = 1.0f / lsum;
+    float *o = a.out + qrow * DV;
+    const float *gt = a.gate ? a.gate + qrow * DV : nullptr;
+#pragma unroll
+    for (int dt = 0; dt < 2; dt++) {
+#pragma unroll
+        for (int i4 = 0; i4 < 4; i4++) {
+            const int d0 = 32 * dt + 8 * i4 + 4 * jh;
+            float4 z;
+            const float16v &acc = dt == 0 ? acc0 : acc1;
+            z.x = acc[4 * i4 + 0] * inv;
+            z.y = acc[4 * i4 + 1] * inv;
+            z.z = acc[4 * i4 + 2] * inv;
+            z.w = acc[4 * i4 + 3] * inv;
+            if (gt) {
+                z.x *= sigmoid_dev(gt[d0 + 0]);
+                z.y *= sigmoid_dev(gt[d0 + 1]);
+                z.z *= sigmoid_dev(gt[d0 + 2]);
+                z.w *= sigmoid_dev(gt[d0 + 3]);
+            }
+            *reinterpret_cast<float4 *>(o + d0) = z;
+        }
+    }
+}
+
+// GQA decode geometries of the MFMA kernel (int8 K/V, 4+ heads per kv-head)
+#define NDA_DEC_GEOMETRIES(X) X(48, 64, 6) X(64, 64, 4) X(64, 64, 6) X(64, 64, 8)
+
+bool decode_mfma_supported(const Geo &g)
+{
+#define X(DK, DV, REP) if (!g.kv_f16 && g.dk == DK && g.dv == DV && g.rep == REP) return true;
+    NDA_DEC_GEOMETRIES(X)
+#undef X
+    return false;
+}
+
+hipError_t launch_decode_mfma(const Geo &g, const PrefillArgs &a, hipStream_t s)
+{
+    if (a.n_items == 0)
+        return hipSuccess;
+#define X(DK, DV, REP)                                                                            \
+    if (!g.kv_f16 && g.dk == DK && g.dv == DV && g.rep == REP) {                                  \
+        hipLaunchKernelGGL((decode_mfma_kernel<DK, DV, REP>), dim3(a.n_items), dim3(64), 0, s, a); \
+        return hipGetLastError();                                                                 \
+    }
+    NDA_DEC_GEOMETRIES(X)
+#undef X
+    return hipErrorNotSupported;
 }
 
 #define NDA_PF_GEOMETRIES(X) \

@@ -19,6 +19,7 @@ NDA_OK = 0
 ERRORS = {-1: "NDA_ERR_ARG", -2: "NDA_ERR_NOMEM", -3: "NDA_ERR_HIP", -4: "NDA_ERR_RANGE",
           -5: "NDA_ERR_STATE", -6: "NDA_ERR_UNSUPPORTED", -7: "NDA_ERR_NODEV"}
 KV_INT8, KV_F16 = 0, 1
+FLAG_PREFILL_VALU, FLAG_DECODE_VALU = 1, 2   # nda_config.flags (include/nda.h)
 K_APPEND, K_DECODE, K_COMBINE, K_PREFILL, K_FRONT, K_PROJ = 0, 1, 2, 3, 4, 5
 K_COUNT = 6
 FLAG_PREFILL_VALU = 1

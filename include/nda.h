@@ -68,6 +68,10 @@ typedef struct {
 /* Prefill through the per-row VALU decode kernel instead of the MFMA
  * kernel (same results within rounding; for comparison and tiny chunks). */
 #define NDA_FLAG_PREFILL_VALU 1u
+/* Decode GQA groups (4 or more query heads per kv-head) through the VALU
+ * decode kernel instead of the MFMA one (same results within rounding; for
+ * comparison). */
+#define NDA_FLAG_DECODE_VALU 2u
 
 /* ---- lifecycle ---- */
 
