@@ -504,51 +504,86 @@ __device__ __forceinline__ half2v codes2(uint32_t xs)   // xs = codes ^ 0x808080
     return __builtin_bit_cast(half2v, u) - half2v{(_Float16)1152.0f, (_Float16)1152.0f};
 }
 
+typedef float float4v __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ float4v mfma16k32(half8 a, half8 b, float4v c)
+{
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
+}
+
+__device__ __forceinline__ float4v mfma16k16(half4 a, half4 b, float4v c)
+{
+    return __builtin_amdgcn_mfma_f32_16x16x16f16(a, b, c, 0, 0, 0);
+}
+
+// 16 x 16 tiles: lane l = 16 g + r holds MFMA row / column r and the k (or
+// output row) slots of lane group g. A wave's 16 row slots hold the group's
+// rep heads; a 32-key tile is two 16-key blocks of S^T = K.Q^T (lane: row r,
+// keys 16 b + 4 g + i), whose eight scores per lane are, in that order, the
+// P^T operand of O^T += V^T.P^T over the 32 keys (lane group g's k slots),
+// so V^T is read in the same key order. A row's softmax state spans the four
+// lane groups (a max and a sum across them).
 template <int DK, int DV, int REP>
-__global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(3)))
+__global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(4)))
 void decode_mfma_kernel(PrefillArgs a)
 {
-    static_assert(DK % 16 == 0 && DV == 64 && REP <= 32, "decode tiles: dk multiple of 16, dv 64");
-    constexpr int NKB = DK / 16;
+    static_assert(DK % 16 == 0 && DV == 64 && REP <= 16, "decode tiles: dk multiple of 16, dv 64, rep <= 16");
+    constexpr int NS = DK / 32;                 // 32-dim steps of S (16x16x32)
+    constexpr bool TAIL = DK % 32 == 16;        // a last 16-dim step (16x16x16)
     constexpr int KPAD = DK + 8, VPAD = PF_KT + 4;
     constexpr int KH = DK / 2, VH = DV / 2;     // codes a lane moves per key
     static_assert(KH % 8 == 0 && VH % 16 == 0, "lane halves are whole 8- and 16-byte loads");
     __shared__ __attribute__((aligned(16))) _Float16 Ks[PF_KT][KPAD];
     __shared__ __attribute__((aligned(16))) _Float16 Vt[DV][VPAD];
-    __shared__ float Sc[2][PF_KT];              // K, V scales of the tile's keys
+    __shared__ __attribute__((aligned(16))) float Sc[2][PF_KT];   // K, V scales of the tile's keys
 
     const int lane = threadIdx.x;
-    const int jh = lane >> 5, ln = lane & 31;
+    const int jh = lane >> 5, ln = lane & 31;   // staging: key ln, half jh
+    const int g = lane >> 4, r = lane & 15;     // MFMA: lane group, row / column
     const uint32_t nkv = a.pg.nkv;
-    const uint32_t b = blockIdx.x / nkv, g = blockIdx.x % nkv;
+    const uint32_t b = blockIdx.x / nkv, kvh = blockIdx.x % nkv;
     const uint32_t seq = a.row_seq ? a.row_seq[b] : b;
     const SeqDev sd = a.seqs[seq];
     const Visible vis = visible(sd, sd.pos, (int)a.pg.window);
     const int n_sh = vis.n_sh, total = vis.n_sh + vis.n_own;
 
-    const bool rvalid = ln < REP;
-    const uint64_t qrow = (uint64_t)b * a.nh + g * REP + (rvalid ? ln : 0);
-    half8 qh[NKB], ql[NKB];
+    // Q^T operand, hi and lo: row r, dims 32 s + 8 g + [0, 8) and the tail
+    // 32 NS + 4 g + [0, 4); hi and lo from one rounded fp32 value
+    const bool rvalid = r < REP;
+    const uint64_t qrow = (uint64_t)b * a.nh + kvh * REP + (rvalid ? r : 0);
+    half8 qh[NS > 0 ? NS : 1], ql[NS > 0 ? NS : 1];
+    half4 qh4, ql4;
     {
-        const float *qr = a.q + qrow * DK + 8 * jh;
-        float4 qv[NKB][2];
-#pragma unroll
-        for (int kb = 0; kb < NKB; kb++) {
-            qv[kb][0] = *reinterpret_cast<const float4 *>(qr + 16 * kb);
-            qv[kb][1] = *reinterpret_cast<const float4 *>(qr + 16 * kb + 4);
-        }
+        const float *qr = a.q + qrow * DK;
         const float qs = rvalid ? a.qscale : 0.0f;
+        auto split = [&](float v, _Float16 &hi, _Float16 &lo) __attribute__((always_inline)) {
+            float x = v * qs;
+            asm volatile("" : "+v"(x));
+            hi = (_Float16)x;
+            lo = (_Float16)(x - (float)hi);
+        };
 #pragma unroll
-        for (int kb = 0; kb < NKB; kb++) {
-            const float xs[8] = {qv[kb][0].x, qv[kb][0].y, qv[kb][0].z, qv[kb][0].w,
-                                 qv[kb][1].x, qv[kb][1].y, qv[kb][1].z, qv[kb][1].w};
+        for (int st = 0; st < NS; st++) {
+            const float4 v0 = *reinterpret_cast<const float4 *>(qr + 32 * st + 8 * g);
+            const float4 v1 = *reinterpret_cast<const float4 *>(qr + 32 * st + 8 * g + 4);
+            const float xs[8] = {v0.x, v0.y, v0.z, v0.w, v1.x, v1.y, v1.z, v1.w};
 #pragma unroll
-            for (int s = 0; s < 8; s++) {
-                float x = xs[s] * qs;
-                asm volatile("" : "+v"(x));
-                const _Float16 hi = (_Float16)x;
-                qh[kb][s] = hi;
-                ql[kb][s] = (_Float16)(x - (float)hi);
+            for (int i = 0; i < 8; i++) {
+                _Float16 hi, lo;
+                split(xs[i], hi, lo);
+                qh[st][i] = hi;
+                ql[st][i] = lo;
+            }
+        }
+        if constexpr (TAIL) {
+            const float4 v = *reinterpret_cast<const float4 *>(qr + 32 * NS + 4 * g);
+            const float xs[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                _Float16 hi, lo;
+                split(xs[i], hi, lo);
+                qh4[i] = hi;
+                ql4[i] = lo;
             }
         }
     }
@@ -570,7 +605,7 @@ void decode_mfma_kernel(PrefillArgs a)
     };
     auto load = [&](int32_t pid, int off, Stage &sg) __attribute__((always_inline)) {
         // a page is under 4 GiB: one 32 x 32 -> 64-bit multiply-add
-        const uint8_t *hb = a.pool + (uint64_t)(uint32_t)pid * (uint32_t)a.pg.page_bytes + (uint64_t)g * a.pg.head_bytes;
+        const uint8_t *hb = a.pool + (uint64_t)(uint32_t)pid * (uint32_t)a.pg.page_bytes + (uint64_t)kvh * a.pg.head_bytes;
         const uint8_t *kp = hb + off * DK + KH * jh;
         const uint8_t *vp = hb + P * DK + off * DV + VH * jh;
 #pragma unroll
@@ -610,7 +645,7 @@ void decode_mfma_kernel(PrefillArgs a)
         Sc[jh][ln] = sg.sc;
     };
 
-    float16v acc0 = {}, acc1 = {};
+    float4v acc[4] = {};                        // O^T: dims 16 d + 4 g + i, row r
     float m = -FLT_MAX, lsum = 0.0f;
     const int qlast = total - 1;                // keys past it are masked
     const int ntile = (total + PF_KT - 1) / PF_KT;
@@ -625,37 +660,53 @@ void decode_mfma_kernel(PrefillArgs a)
     store(sg);
 
     // tile j (parity PJ): ids of tile j+2 into tile j's slot, data of tile
-    // j+1, the tile's arithmetic, then tile j+1 into LDS
+    // j+1, the tile's arithmetic, then tile j+1 into LDS (two tiles in
+    // flight measured the same: the wave's chain through a tile, not the
+    // load latency, is what the resident waves hide)
     auto tile = [&](const int j, auto pj, auto masked) __attribute__((always_inline)) {
         constexpr int PJ = decltype(pj)::value, Q1 = PJ ^ 1;
         const int kt = j * PF_KT;
         fetch(j + 2, pid[PJ], poff[PJ]);
         load(pid[Q1], poff[Q1], sg);
 
-        float16v st = {};
+        float4v st[2];
         __builtin_amdgcn_s_setprio(0);
 #pragma unroll
-        for (int kb = 0; kb < NKB; kb++) {
-            const half8 ka = *reinterpret_cast<const half8 *>(&Ks[ln][16 * kb + 8 * jh]);
-            st = mfma32(ka, qh[kb], st);
-            st = mfma32(ka, ql[kb], st);
-        }
-        __builtin_amdgcn_s_setprio(1);
+        for (int kb = 0; kb < 2; kb++) {
+            const _Float16 *kr = &Ks[16 * kb + r][0];
+            st[kb] = float4v{};
 #pragma unroll
-        for (int i = 0; i < 16; i++)
-            st[i] *= Sc[0][8 * (i >> 2) + 4 * jh + (i & 3)];
-        if constexpr (decltype(masked)::value) {
-#pragma unroll
-            for (int i = 0; i < 16; i++) {
-                const int kl = 8 * (i >> 2) + 4 * jh + (i & 3);
-                st[i] = kt + kl > qlast ? -INFINITY : st[i];
+            for (int s2 = 0; s2 < NS; s2++) {
+                const half8 ka = *reinterpret_cast<const half8 *>(kr + 32 * s2 + 8 * g);
+                st[kb] = mfma16k32(ka, qh[s2], st[kb]);
+                st[kb] = mfma16k32(ka, ql[s2], st[kb]);
+            }
+            if constexpr (TAIL) {
+                const half4 ka = *reinterpret_cast<const half4 *>(kr + 32 * NS + 4 * g);
+                st[kb] = mfma16k16(ka, qh4, st[kb]);
+                st[kb] = mfma16k16(ka, ql4, st[kb]);
             }
         }
-        const float x0 = max3(st[0], st[1], st[2]), x1 = max3(st[3], st[4], st[5]);
-        const float x2 = max3(st[6], st[7], st[8]), x3 = max3(st[9], st[10], st[11]);
-        const float x4 = max3(st[12], st[13], st[14]);
-        const float y0 = max3(x0, x1, x2), y1 = max3(x3, x4, st[15]);
-        float mt = max3(y0, y1, y1);
+        __builtin_amdgcn_s_setprio(1);
+        // scores of keys 16 kb + 4 g + i: k scales, then the mask
+        {
+            const float4 k0 = *reinterpret_cast<const float4 *>(&Sc[0][4 * g]);
+            const float4 k1 = *reinterpret_cast<const float4 *>(&Sc[0][16 + 4 * g]);
+            st[0] *= float4v{k0.x, k0.y, k0.z, k0.w};
+            st[1] *= float4v{k1.x, k1.y, k1.z, k1.w};
+        }
+        if constexpr (decltype(masked)::value) {
+#pragma unroll
+            for (int kb = 0; kb < 2; kb++)
+#pragma unroll
+                for (int i = 0; i < 4; i++)
+                    st[kb][i] = kt + 16 * kb + 4 * g + i > qlast ? -INFINITY : st[kb][i];
+        }
+        // the row's tile max over its 32 keys: 8 in this lane, then across
+        // the four lane groups (lanes r + 16 g)
+        const float y0 = max3(st[0][0], st[0][1], st[0][2]), y1 = max3(st[0][3], st[1][0], st[1][1]);
+        float mt = max3(y0, y1, max3(st[1][2], st[1][3], st[1][3]));
+        mt = max3(mt, __shfl_xor(mt, 16, 64), mt);
         {
             const auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(mt), __float_as_uint(mt), false, false);
             mt = max3(mt, __uint_as_float(sw[0]), __uint_as_float(sw[1]));
@@ -667,47 +718,44 @@ void decode_mfma_kernel(PrefillArgs a)
             m = mnew;
             lsum *= rs;
 #pragma unroll
-            for (int i = 0; i < 16; i++) {
-                acc0[i] *= rs;
-                acc1[i] *= rs;
-            }
+            for (int d = 0; d < 4; d++)
+                acc[d] *= rs;
         }
-        u32x4 phw[2], plw[2];
+        float p[8];
 #pragma unroll
-        for (int i = 0; i < 16; i += 2) {
-            float p0 = fast_exp2(st[i] - m), p1 = fast_exp2(st[i + 1] - m);
-            lsum += p0 + p1;
-            p0 *= Sc[1][8 * (i >> 2) + 4 * jh + (i & 3)];
-            p1 *= Sc[1][8 * (i >> 2) + 4 * jh + ((i + 1) & 3)];
-            const fp16x2 hh = __builtin_amdgcn_cvt_pkrtz(p0, p1);
+        for (int kb = 0; kb < 2; kb++)
+#pragma unroll
+            for (int i = 0; i < 4; i++)
+                p[4 * kb + i] = fast_exp2(st[kb][i] - m);
+        lsum += ((p[0] + p[1]) + (p[2] + p[3])) + ((p[4] + p[5]) + (p[6] + p[7]));
+        {
+            const float4 v0 = *reinterpret_cast<const float4 *>(&Sc[1][4 * g]);
+            const float4 v1 = *reinterpret_cast<const float4 *>(&Sc[1][16 + 4 * g]);
+            p[0] *= v0.x; p[1] *= v0.y; p[2] *= v0.z; p[3] *= v0.w;
+            p[4] *= v1.x; p[5] *= v1.y; p[6] *= v1.z; p[7] *= v1.w;
+        }
+        // P^T operand (hi, lo): slots = the eight keys in lane order; hi = p
+        // rounded toward zero to fp16, lo = the remainder
+        u32x4 phw, plw;
+#pragma unroll
+        for (int i = 0; i < 8; i += 2) {
+            const fp16x2 hh = __builtin_amdgcn_cvt_pkrtz(p[i], p[i + 1]);
             const uint32_t hw = __builtin_bit_cast(uint32_t, hh);
             uint32_t lw;
-            asm("v_fma_mixlo_f16 %0, %1, -1.0, %2 op_sel_hi:[1,0,0]" : "=v"(lw) : "v"(hw), "v"(p0));
-            asm("v_fma_mixhi_f16 %0, %1, -1.0, %2 op_sel:[1,0,0] op_sel_hi:[1,0,0]" : "+v"(lw) : "v"(hw), "v"(p1));
-            phw[i >> 3][(i & 7) >> 1] = hw;
-            plw[i >> 3][(i & 7) >> 1] = lw;
+            asm("v_fma_mixlo_f16 %0, %1, -1.0, %2 op_sel_hi:[1,0,0]" : "=v"(lw) : "v"(hw), "v"(p[i]));
+            asm("v_fma_mixhi_f16 %0, %1, -1.0, %2 op_sel:[1,0,0] op_sel_hi:[1,0,0]" : "+v"(lw) : "v"(hw), "v"(p[i + 1]));
+            phw[i >> 1] = hw;
+            plw[i >> 1] = lw;
         }
-        half8 ph[2], pl[2];
-        ph[0] = __builtin_bit_cast(half8, phw[0]);
-        ph[1] = __builtin_bit_cast(half8, phw[1]);
-        pl[0] = __builtin_bit_cast(half8, plw[0]);
-        pl[1] = __builtin_bit_cast(half8, plw[1]);
+        const half8 ph = __builtin_bit_cast(half8, phw), pl = __builtin_bit_cast(half8, plw);
 #pragma unroll
-        for (int kb2 = 0; kb2 < 2; kb2++) {
-#pragma unroll
-            for (int dt = 0; dt < 2; dt++) {
-                const _Float16 *vr = &Vt[32 * dt + ln][16 * kb2 + 4 * jh];
-                const half4 v0 = *reinterpret_cast<const half4 *>(vr);
-                const half4 v1 = *reinterpret_cast<const half4 *>(vr + 8);
-                const half8 va = {v0[0], v0[1], v0[2], v0[3], v1[0], v1[1], v1[2], v1[3]};
-                if (dt == 0) {
-                    acc0 = mfma32(va, ph[kb2], acc0);
-                    acc0 = mfma32(va, pl[kb2], acc0);
-                } else {
-                    acc1 = mfma32(va, ph[kb2], acc1);
-                    acc1 = mfma32(va, pl[kb2], acc1);
-                }
-            }
+        for (int d = 0; d < 4; d++) {
+            const _Float16 *vr = &Vt[16 * d + r][4 * g];
+            const half4 v0 = *reinterpret_cast<const half4 *>(vr);
+            const half4 v1 = *reinterpret_cast<const half4 *>(vr + 16);
+            const half8 va = {v0[0], v0[1], v0[2], v0[3], v1[0], v1[1], v1[2], v1[3]};
+            acc[d] = mfma16k32(va, ph, acc[d]);
+            acc[d] = mfma16k32(va, pl, acc[d]);
         }
         __builtin_amdgcn_s_setprio(0);
         if (j + 1 < ntile)      // after this tile's last LDS reads, in the wave's order
@@ -728,6 +776,7 @@ void decode_mfma_kernel(PrefillArgs a)
     if (j < ntile)
         tile(j, P0{}, std::true_type{});
 
+    lsum += __shfl_xor(lsum, 16, 64);
     lsum += __shfl_xor(lsum, 32, 64);
     if (!rvalid)
         return;
@@ -735,24 +784,20 @@ void decode_mfma_kernel(PrefillArgs a)
     float *o = a.out + qrow * DV;
     const float *gt = a.gate ? a.gate + qrow * DV : nullptr;
 #pragma unroll
-    for (int dt = 0; dt < 2; dt++) {
-#pragma unroll
-        for (int i4 = 0; i4 < 4; i4++) {
-            const int d0 = 32 * dt + 8 * i4 + 4 * jh;
-            float4 z;
-            const float16v &acc = dt == 0 ? acc0 : acc1;
-            z.x = acc[4 * i4 + 0] * inv;
-            z.y = acc[4 * i4 + 1] * inv;
-            z.z = acc[4 * i4 + 2] * inv;
-            z.w = acc[4 * i4 + 3] * inv;
-            if (gt) {
-                z.x *= sigmoid_dev(gt[d0 + 0]);
-                z.y *= sigmoid_dev(gt[d0 + 1]);
-                z.z *= sigmoid_dev(gt[d0 + 2]);
-                z.w *= sigmoid_dev(gt[d0 + 3]);
-            }
-            *reinterpret_cast<float4 *>(o + d0) = z;
+    for (int d = 0; d < 4; d++) {
+        const int d0 = 16 * d + 4 * g;
+        float4 z;
+        z.x = acc[d][0] * inv;
+        z.y = acc[d][1] * inv;
+        z.z = acc[d][2] * inv;
+        z.w = acc[d][3] * inv;
+        if (gt) {
+            z.x *= sigmoid_dev(gt[d0 + 0]);
+            z.y *= sigmoid_dev(gt[d0 + 1]);
+            z.z *= sigmoid_dev(gt[d0 + 2]);
+            z.w *= sigmoid_dev(gt[d0 + 3]);
         }
+        *reinterpret_cast<float4 *>(o + d0) = z;
     }
 }
 
