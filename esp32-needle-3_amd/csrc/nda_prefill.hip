@@ -301,9 +301,12 @@ void prefill_kernel(PrefillArgs a)
     // One key tile j (parity PJ = j & 1); the LDS buffer of tile j is PJ.
     // `masked` is a compile-time flag: the loop over tiles below the
     // diagonal carries no mask code (whose registers would spill the 8-wave
-    // variant).
-    auto tile = [&](const int j, auto pj, auto masked) __attribute__((always_inline)) {
+    // variant). With fp16 K/V the S MFMAs of every tile after the first
+    // start from -m, so they return s - m and the exps need no subtraction
+    // (the first tile, with no running max yet, starts from zero).
+    auto tile = [&](const int j, auto pj, auto masked, auto first) __attribute__((always_inline)) {
         constexpr int PJ = decltype(pj)::value, Q1 = PJ ^ 1;
+        constexpr bool REL = ES == 2 && !decltype(first)::value;   // scores relative to m
         const int kt = j * PF_KT;
         // ids of tile j+PD+1 into the slot of tile j+PD-1's (spent), then the
         // data of tile j+PD; past kmax the loads read the last key (finite
@@ -315,7 +318,10 @@ void prefill_kernel(PrefillArgs a)
         const float *Ksc = Ksc2[PJ], *Vsc = Vsc2[PJ];
 
         // ---- S^T = K . Q^T (keys x rows), accumulate hi then lo
-        float16v st = {};
+        float16v st;
+#pragma unroll
+        for (int i = 0; i < 16; i++)
+            st[i] = REL ? -m : 0.0f;
         // Wave priority: normal while this wave issues its S MFMAs, raised
         // from the softmax through the P.V MFMAs, so a wave with softmax
         // work wins issue over waves still in their S chains (4% on a
@@ -364,16 +370,29 @@ void prefill_kernel(PrefillArgs a)
         // Lazy max: keep the running max unless the tile exceeds it by more
         // than 2^8 (weights stay <= 256, exact range for fp16 and fp32), and
         // skip the rescale sweep when no row of the wave moved.
-        const bool grow = mt > m + 8.0f;
+        const bool grow = REL ? mt > 8.0f : mt > m + 8.0f;
         if (__builtin_expect(__ballot(grow) != 0, 0)) {
-            const float mnew = grow ? mt : m;
-            const float rs = fast_exp2(m - mnew);
-            m = mnew;
-            lsum *= rs;
+            if constexpr (REL) {
+                const float d = grow ? mt : 0.0f;     // the running max moves by d
+                const float rs = fast_exp2(-d);
+                m += d;
+                lsum *= rs;
 #pragma unroll
-            for (int i = 0; i < 16; i++) {
-                acc0[i] *= rs;
-                acc1[i] *= rs;
+                for (int i = 0; i < 16; i++) {
+                    acc0[i] *= rs;
+                    acc1[i] *= rs;
+                    st[i] -= d;
+                }
+            } else {
+                const float mnew = grow ? mt : m;
+                const float rs = fast_exp2(m - mnew);
+                m = mnew;
+                lsum *= rs;
+#pragma unroll
+                for (int i = 0; i < 16; i++) {
+                    acc0[i] *= rs;
+                    acc1[i] *= rs;
+                }
             }
         }
         // P^T operand (hi, lo) for the two 16-key blocks: slots = registers
@@ -381,7 +400,7 @@ void prefill_kernel(PrefillArgs a)
         u32x4 phw[2], plw[2];
 #pragma unroll
         for (int i = 0; i < 16; i += 2) {
-            float p0 = fast_exp2(st[i] - m), p1 = fast_exp2(st[i + 1] - m);
+            float p0 = fast_exp2(REL ? st[i] : st[i] - m), p1 = fast_exp2(REL ? st[i + 1] : st[i + 1] - m);
             lsum += p0 + p1;
             if constexpr (ES == 1) {
                 p0 *= Vsc[8 * (i >> 2) + 4 * jh + (i & 3)];
@@ -429,21 +448,39 @@ void prefill_kernel(PrefillArgs a)
     using P1 = std::integral_constant<int, 1>;
     using Full = std::false_type;
     using Diag = std::true_type;
-    // Pairs of tiles keep each parity static. The unmasked loop stops at an
-    // even tile, so the masked loop starts on parity 0 as well (a visible
-    // tile taken into it masks nothing).
+    using First = std::true_type;
+    using Next = std::false_type;
+    // Pairs of tiles keep each parity static, the first pair holding the
+    // first tile (whose running max starts from its own scores). The
+    // unmasked loop stops at an even tile, so the masked loop starts on
+    // parity 0 as well (a visible tile taken into it masks nothing). (A
+    // variant that peeled tile 0 and paired (odd, even) tiles after it gave
+    // wrong int8 results with two tiles in flight; this order is the tested
+    // one.)
     const int jeven = jfull & ~1;
-    int j = 0;
+    int j;
+    if (jeven >= 2) {
+        tile(0, P0{}, Full{}, First{});
+        tile(1, P1{}, Full{}, Next{});
+        j = 2;
+    } else if (ntile >= 2) {
+        tile(0, P0{}, Diag{}, First{});
+        tile(1, P1{}, Diag{}, Next{});
+        j = 2;
+    } else {
+        tile(0, P0{}, Diag{}, First{});
+        j = 1;
+    }
     for (; j < jeven; j += 2) {
-        tile(j, P0{}, Full{});
-        tile(j + 1, P1{}, Full{});
+        tile(j, P0{}, Full{}, Next{});
+        tile(j + 1, P1{}, Full{}, Next{});
     }
     for (; j + 1 < ntile; j += 2) {
-        tile(j, P0{}, Diag{});
-        tile(j + 1, P1{}, Diag{});
+        tile(j, P0{}, Diag{}, Next{});
+        tile(j + 1, P1{}, Diag{}, Next{});
     }
     if (j < ntile)
-        tile(j, P0{}, Diag{});
+        tile(j, P0{}, Diag{}, Next{});
 
     // ---- emit: lane holds row ln, dims 32*dt + 8*(i/4) + 4*jh + (i%4)
     lsum += __shfl_xor(lsum, 32, 64);
