@@ -1779,6 +1779,10 @@ struct nda_cq {
     uint8_t *packed = nullptr;     // [out][rowbytes]
     uint16_t *norms = nullptr;     // [out][ngroup], 2-byte aligned copy
     float *cb = nullptr;           // [1 << bits]
+    // split GEMM decode data (2-bit tensors, group >= 32)
+    uint32_t *cw = nullptr;
+    uint4 *tab = nullptr;
+    int32_t *cexp = nullptr;
 };
 
 int nda_cq_create(uint32_t out, uint32_t in, uint32_t group, uint32_t bits, const void *blob,
@@ -1814,6 +1818,29 @@ int nda_cq_create(uint32_t out, uint32_t in, uint32_t group, uint32_t bits, cons
         nda_cq_destroy(t);
         return NDA_ERR_HIP;
     }
+    if (bits == 2 && group >= 32) {
+        CqTabArgs ta{};
+        ta.packed = t->packed;
+        ta.norms = t->norms;
+        ta.cb = t->cb;
+        ta.out = out;
+        ta.in_pad = t->in_pad;
+        ta.ngroup = t->ngroup;
+        ta.rowbytes = t->rowbytes;
+        if (hipMalloc(&t->cw, (size_t)t->in_pad / 32 * out * 8) != hipSuccess ||
+            hipMalloc(&t->tab, (size_t)t->ngroup * out * 16) != hipSuccess ||
+            hipMalloc(&t->cexp, (size_t)out * 4) != hipSuccess) {
+            nda_cq_destroy(t);
+            return NDA_ERR_NOMEM;
+        }
+        ta.cw = t->cw;
+        ta.tab = t->tab;
+        ta.cexp = t->cexp;
+        if (launch_cq_split_tables(ta, nullptr) != hipSuccess || hipStreamSynchronize(nullptr) != hipSuccess) {
+            nda_cq_destroy(t);
+            return NDA_ERR_HIP;
+        }
+    }
     *tp = t;
     return NDA_OK;
 }
@@ -1822,7 +1849,8 @@ int nda_cq_destroy(nda_cq *t)
 {
     if (!t)
         return NDA_OK;
-    for (void *b : {(void *)t->packed, (void *)t->norms, (void *)t->cb})
+    for (void *b : {(void *)t->packed, (void *)t->norms, (void *)t->cb, (void *)t->cw, (void *)t->tab,
+                    (void *)t->cexp})
         if (b)
             (void)hipFree(b);
     delete t;
@@ -1940,9 +1968,6 @@ int nda_cq_gemm_split_many(const nda_cq *const *ts, uint32_t n, uint32_t rows, c
     a.rexp = (const int32_t *)(a.xs + split_rows(rows) * t0->in_pad * 2);
     a.rows = rows;
     a.in_pad = t0->in_pad;
-    a.group = t0->group;
-    a.ngroup = t0->ngroup;
-    a.rowbytes = t0->rowbytes;
     a.log2_group = (uint32_t)__builtin_ctz(t0->group);
     a.nt = n;
     uint32_t tiles = 0;
@@ -1955,9 +1980,9 @@ int nda_cq_gemm_split_many(const nda_cq *const *ts, uint32_t n, uint32_t rows, c
         if (!cq_split_ok(t))
             return NDA_ERR_UNSUPPORTED;
         a.y[i] = ys[i];
-        a.packed[i] = t->packed;
-        a.norms[i] = t->norms;
-        a.cb[i] = t->cb;
+        a.cw[i] = t->cw;
+        a.tab[i] = t->tab;
+        a.cexp[i] = t->cexp;
         a.out[i] = t->out;
         a.tile0[i] = tiles;
         tiles += (t->out + CQ_SPLIT_NT - 1) / CQ_SPLIT_NT;

@@ -202,15 +202,17 @@ __global__ __launch_bounds__(256) void cq_gemm_kernel(CqGemmArgs a)
 // For 2-bit tensors with group >= 32 the GEMM runs on fp16 MFMA
 // (v_mfma_f32_32x32x16_f16, 16x the fp32 rate) with each fp32 operand
 // carried as a pair of fp16 values:
-//   xh * 2^rexp[r]  = xa + xb     per row, from the split prepare
-//   cb[c] * 2^ecb   = ca + cb'    per tensor, its four codebook entries
-//   sum_k w x  ~  sum_k (ca xa + ca xb + cb' xa)   (cb' xb, 2^-22 relative, dropped)
-// Products and sums are fp32 inside the MFMA. A group's sum is scaled by
-// its norm into the running total, and the total by 2^-(rexp + ecb) at the
-// end. The powers of two put each row's and the codebook's largest |value|
-// in [2^14, 2^15), so every fp16 part is a normal number with its full 11
-// bits: the pairs hold 22 significant bits, and the result stays within
-// fp32 reassociation of the engine's matvec (a few 2^-22 of sum |w x|).
+//   xh * 2^rexp[r]             = xa + xb   per row, from the split prepare
+//   cb[c] * norm * 2^cexp[o]   = wa + wb   per (column, group), at tensor creation
+//   sum_k w x  ~  sum_k (wa xa + wa xb + wb xa)   (wb xb, 2^-22 relative, dropped)
+// Products and sums are fp32 inside the MFMA, and the total is scaled by
+// 2^-(rexp + cexp) at the end. The powers of two put each row's and each
+// column's largest |value| in [2^14, 2^15), so the large parts are normal
+// fp16 numbers with their full 11 bits: the pairs hold 22 significant bits
+// of the engine's fp32 values, and the result stays within fp32
+// reassociation of the engine's matvec (a few 2^-22 of sum |w x|; the
+// engine applies the norm to the group's dot product, here it sits in the
+// weights).
 //
 // The split rows are stored in the order the MFMA reads them: per block of
 // 32 rows and 16 columns, per plane (a, b), the 64 lanes' 16-byte operands
@@ -407,136 +409,214 @@ constexpr int CS_KT = 32;           // reduction columns per step: two MFMA k-bl
 
 typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 
-// Work-group = 128 rows x 128 outputs of one tensor, 4 waves of 64 x 64
-// (2 x 2 blocks of 32 x 32) that share only the code tables: each wave loads
-// its X operands straight from the split rows (one step ahead, in two
-// register sets used in turn) and decodes its W operands from the codes
-// through two 256-entry tables (one byte = four 2-bit codes -> their four
-// fp16 a parts, and their four b parts). No barrier inside the loop. Loads
-// for rows or outputs past the end read row 0 instead (in bounds); what
-// they feed lands only in rows or columns that are never stored.
+// Decode data of a 2-bit tensor, written once when the tensor is created
+// (one thread per output column o):
+//   cexp[o]          power of two that puts the column's largest |cb[c] *
+//                    norm| in [2^14, 2^15) (0 for an all-zero column)
+//   tab[g][o]        the four weights cb[c] * norm[o][g] of group g (the
+//                    engine's fp32 product, scaled by 2^cexp[o]), each as an
+//                    fp16 pair a + b, laid out as two v_perm byte tables:
+//                    {a high bytes, a low bytes, b high bytes, b low bytes},
+//                    entry c at byte c of each
+//   cw[s][o][h]      for step s (columns 32 s ..) and lane half h: the
+//                    lane's 16 codes as one word, code b of group q (the
+//                    columns 32 s + 16 (q / 2) + 8 h + 4 (q % 2) + b) at bit
+//                    8 b + 2 q, so (w >> 2 q) & 0x03030303 puts four codes
+//                    in four bytes; with them and the same bytes + 4, two
+//                    v_perms give the selectors {c, c + 4, c', c' + 4} of
+//                    two operand dwords (the low then the high byte of
+//                    entry c, then those of entry c')
+// so one v_perm per operand dword decodes two weights in either plane.
+__global__ __launch_bounds__(256) void cq_split_tables_kernel(CqTabArgs a)
+{
+    const uint32_t o = blockIdx.x * 256 + threadIdx.x;
+    if (o >= a.out)
+        return;
+    const float cb[4] = {a.cb[0], a.cb[1], a.cb[2], a.cb[3]};
+    const uint16_t *nr = a.norms + (uint64_t)o * a.ngroup;
+    float m = 0.0f;
+    for (uint32_t g = 0; g < a.ngroup; g++) {
+        const float nf = half_bits_to_float(nr[g]);
+#pragma unroll
+        for (int c = 0; c < 4; c++)
+            m = fmaxf(m, fabsf(cb[c] * nf));
+    }
+    int e = 0, sh = 0;
+    if (m > 0.0f && m <= FLT_MAX) {
+        (void)frexpf(m, &e);
+        sh = 15 - e;
+    }
+    a.cexp[o] = sh;
+    for (uint32_t g = 0; g < a.ngroup; g++) {
+        const float nf = half_bits_to_float(nr[g]);
+        uint32_t t[4] = {0u, 0u, 0u, 0u};               // a hi, a lo, b hi, b lo bytes
+#pragma unroll
+        for (int c = 0; c < 4; c++) {
+            float v = ldexpf(cb[c] * nf, sh);
+            asm volatile("" : "+v"(v));                 // both halves from this one value
+            const _Float16 h = (_Float16)v, l = (_Float16)(v - (float)h);
+            const uint32_t hb = __builtin_bit_cast(uint16_t, h), lb = __builtin_bit_cast(uint16_t, l);
+            t[0] |= (hb >> 8) << (8 * c);
+            t[1] |= (hb & 0xFFu) << (8 * c);
+            t[2] |= (lb >> 8) << (8 * c);
+            t[3] |= (lb & 0xFFu) << (8 * c);
+        }
+        a.tab[(uint64_t)g * a.out + o] = uint4{t[0], t[1], t[2], t[3]};
+    }
+    const uint8_t *row = a.packed + (uint64_t)o * a.rowbytes;
+    const uint32_t nsteps = a.in_pad / CS_KT;
+    for (uint32_t s = 0; s < nsteps; s++)
+        for (uint32_t h = 0; h < 2; h++) {
+            uint32_t w = 0;
+            for (uint32_t q = 0; q < 4; q++)
+                for (uint32_t b = 0; b < 4; b++) {
+                    const uint32_t k = CS_KT * s + 16 * (q >> 1) + 8 * h + 4 * (q & 1) + b;
+                    w |= ((row[k >> 2] >> (2 * (k & 3))) & 3u) << (8 * b + 2 * q);
+                }
+            a.cw[((uint64_t)s * a.out + o) * 2 + h] = w;
+        }
+}
+
+// Work item = 128 rows x 128 outputs of one tensor, 4 waves of 64 x 64
+// (2 x 2 blocks of 32 x 32), each wave independent of the others: it loads
+// its X operands straight from the split rows and its weights' codes and
+// group tables (one step ahead, in two register sets used in turn) and
+// decodes each W operand dword with one v_perm (its selector from the
+// codes by a shift, a mask and a v_perm per two dwords). The norms are inside the
+// tables, so one sum per block runs over all groups. No LDS, no barrier.
+//
+// The grid is persistent: work-group w runs on XCD w % 8 and walks the
+// items of that XCD's contiguous range, w / 8, w / 8 + G8, ... (G8
+// work-groups per XCD). Consecutive items are the output tiles of one row
+// tile, so the work-groups of an XCD running side by side read the same X
+// rows from its L2. The prefetch runs across items: during an item's last
+// step the next item's first step is loaded, and every step's loads carry
+// the row and column exponents its item's stores need, so an item's end
+// waits on nothing. Loads for rows or outputs past the end read row or
+// column 0 instead (in bounds); what they feed lands only in rows or
+// columns that are never stored.
 template <int OB>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(OB >= 2 ? 2 : 3)))
 void cq_gemm_split_kernel(CqSplitArgs a)
 {
-    __shared__ u32x2 luta[256], lutb[256];
-
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int ln = lane & 31, jh = lane >> 5;
-    // XCD-aware order: work-group w runs on XCD w % 8; consecutive work
-    // items are the output tiles of one row tile, which read the same X
-    // rows, so they go to one XCD and share its L2. The grid is padded to a
-    // multiple of 8.
-    const uint32_t nwg = gridDim.x, item = (blockIdx.x % 8u) * (nwg / 8u) + blockIdx.x / 8u;
-    const uint32_t ntiles = a.tile0[a.nt];
-    const uint32_t rtile = item / ntiles, otile = item % ntiles;
-    if (rtile * CQ_SPLIT_MT >= a.rows)
-        return;                         // padding
-    uint32_t ti = 0;
-    while (ti + 1 < a.nt && otile >= a.tile0[ti + 1])
-        ti++;
-    const uint32_t out = a.out[ti];
-    float *y = a.y[ti];
-    const uint32_t r0 = rtile * CQ_SPLIT_MT, o0 = (otile - a.tile0[ti]) * (64 * OB);
     const int wr = (wave & 1) * 64, wo = (wave >> 1) * 32 * OB;
+    const uint32_t ntiles = a.tile0[a.nt];
+    const uint32_t total = (a.rows + CQ_SPLIT_MT - 1) / CQ_SPLIT_MT * ntiles;
+    const uint32_t G8 = gridDim.x / 8u, T8 = (total + 7u) / 8u, xcd = blockIdx.x % 8u;
+    const uint32_t first = xcd * T8 + blockIdx.x / 8u, last = min(total, (xcd + 1u) * T8);
+    if (first >= last)
+        return;
+    const uint32_t nkb = a.in_pad / 16, nsteps = a.in_pad / CS_KT;
 
-    // the codebook as fp16 pairs, scaled so its largest |entry| is in [2^14, 2^15)
-    const float *cbp = a.cb[ti];
-    const float cbv[4] = {cbp[0], cbp[1], cbp[2], cbp[3]};
-    const float cm = fmaxf(fmaxf(fabsf(cbv[0]), fabsf(cbv[1])), fmaxf(fabsf(cbv[2]), fabsf(cbv[3])));
-    int ecb = 0;
-    if (cm > 0.0f && cm <= FLT_MAX) {
-        int e;
-        (void)frexpf(cm, &e);
-        ecb = 15 - e;
-    }
-    {
-        uint32_t hw[2] = {0u, 0u}, lw[2] = {0u, 0u};
+    // item it: row tile it / ntiles, output tile it % ntiles (tensor ti)
+    struct Item {
+        uint32_t r0, o0, ti, out;
+    };
+    auto item = [&](uint32_t it) {
+        Item m;
+        const uint32_t rt = it / ntiles, ot = it % ntiles;
+        uint32_t ti = 0;
+        while (ti + 1 < a.nt && ot >= a.tile0[ti + 1])
+            ti++;
+        m.r0 = rt * CQ_SPLIT_MT;
+        m.ti = ti;
+        m.out = a.out[ti];
+        m.o0 = (ot - a.tile0[ti]) * (64 * OB);
+        return m;
+    };
+    // where an item's operands are: this wave's X row blocks, and this
+    // lane's output columns m.o0 + wo + 32 ob + ln (byte offsets of their
+    // selectors, lane half jh, and group tables)
+    struct Src {
+        const half8 *xr[2];
+        const char *cb, *tb;
+        const int32_t *ce;
+        uint64_t ss, ts;
+        uint32_t soff[OB], toff[OB], oc[OB], row;
+    };
+    auto source = [&](const Item &m) {
+        Src q;
+        const uint32_t RB0 = (m.r0 + wr) >> 5;
 #pragma unroll
-        for (int j = 0; j < 4; j++) {
-            const int c = (tid >> (2 * j)) & 3;
-            float v = ldexpf(c == 0 ? cbv[0] : c == 1 ? cbv[1] : c == 2 ? cbv[2] : cbv[3], ecb);
-            asm volatile("" : "+v"(v));
-            const _Float16 h = (_Float16)v, l = (_Float16)(v - (float)h);
-            hw[j >> 1] |= (uint32_t)__builtin_bit_cast(uint16_t, h) << (16 * (j & 1));
-            lw[j >> 1] |= (uint32_t)__builtin_bit_cast(uint16_t, l) << (16 * (j & 1));
+        for (int rb = 0; rb < 2; rb++) {
+            const bool ok = m.r0 + wr + 32 * rb < a.rows;
+            q.xr[rb] = reinterpret_cast<const half8 *>(a.xs) + (uint64_t)(ok ? RB0 + rb : 0) * nkb * 128;
         }
-        luta[tid] = u32x2{hw[0], hw[1]};
-        lutb[tid] = u32x2{lw[0], lw[1]};
-    }
-
-    // X operands of this wave: row blocks RB0 + rb, per k-block both planes
-    const uint32_t nkb = a.in_pad / 16;
-    const uint32_t RB0 = (r0 + wr) >> 5;
-    const half8 *xrow[2];
+        q.cb = reinterpret_cast<const char *>(a.cw[m.ti]);
+        q.tb = reinterpret_cast<const char *>(a.tab[m.ti]);
+        q.ce = a.cexp[m.ti];
+        q.ss = (uint64_t)m.out * 8;
+        q.ts = (uint64_t)m.out * 16;
 #pragma unroll
-    for (int rb = 0; rb < 2; rb++) {
-        const bool ok = r0 + wr + 32 * rb < a.rows;
-        xrow[rb] = reinterpret_cast<const half8 *>(a.xs) + (uint64_t)(ok ? RB0 + rb : 0) * nkb * 128 + lane;
-    }
-    // this lane's two output columns, o0 + wo + 32 ob + ln: 32 codes per step
-    // each (two words); lane half jh uses the 16-bit half jh of word ks
-    const uint8_t *crow[OB];
-    const uint16_t *nrow[OB];
-#pragma unroll
-    for (int ob = 0; ob < OB; ob++) {
-        const uint32_t o = o0 + wo + 32 * ob + ln, oc = o < out ? o : 0;
-        crow[ob] = a.packed[ti] + (uint64_t)oc * a.rowbytes;
-        nrow[ob] = a.norms[ti] + (uint64_t)oc * a.ngroup;
-    }
+        for (int ob = 0; ob < OB; ob++) {
+            const uint32_t o = m.o0 + wo + 32 * ob + ln, oc = o < m.out ? o : 0;
+            q.oc[ob] = oc;
+            q.soff[ob] = (oc * 2 + jh) * 4;
+            q.toff[ob] = oc * 16;
+        }
+        q.row = min(m.r0 + wr + lane, a.rows - 1);      // lane t: row r0 + wr + t
+        return q;
+    };
     struct Step {
         half8 x[2][2][2];               // [ks][rb][plane]
-        uint2 c[OB];                    // [ob] codes
-        uint16_t nb[OB];                // [ob] the norm of the step's group
+        uint32_t cw[OB];                // [ob] the step's 16 codes
+        uint4 tab[OB];
+        int32_t rx, ce[OB];             // the item's row and column exponents
     };
-    auto load = [&](uint32_t k0, Step &st) {
+    auto load = [&](const Src &q, uint32_t s, Step &st) {
 #pragma unroll
         for (int ks = 0; ks < 2; ks++)
 #pragma unroll
             for (int rb = 0; rb < 2; rb++)
 #pragma unroll
                 for (int p = 0; p < 2; p++)
-                    st.x[ks][rb][p] = xrow[rb][((k0 >> 4) + ks) * 128 + 64 * p];
+                    st.x[ks][rb][p] = q.xr[rb][((2 * s + ks) * 2 + p) * 64 + lane];
+        const char *cb = q.cb + s * q.ss;
+        const char *tb = q.tb + ((s * CS_KT) >> a.log2_group) * q.ts;
 #pragma unroll
         for (int ob = 0; ob < OB; ob++) {
-            st.c[ob] = *reinterpret_cast<const uint2 *>(crow[ob] + k0 / 4);
-            st.nb[ob] = nrow[ob][k0 >> a.log2_group];
+            st.cw[ob] = *reinterpret_cast<const uint32_t *>(cb + q.soff[ob]);
+            st.tab[ob] = *reinterpret_cast<const uint4 *>(tb + q.toff[ob]);
+            st.ce[ob] = q.ce[q.oc[ob]];
         }
+        st.rx = a.rexp[q.row];
     };
 
-    float16v acc[2][OB], ysum[2][OB];
+    float16v acc[2][OB];
 #pragma unroll
     for (int rb = 0; rb < 2; rb++)
 #pragma unroll
         for (int ob = 0; ob < OB; ob++)
-            ysum[rb][ob] = float16v{};
-    // One step: 24 MFMAs; `first` starts the group's sums from zero (a literal
-    // at each call site, so each variant carries no branch).
-    auto compute = [&](const Step &st, const bool first) __attribute__((always_inline)) {
+            acc[rb][ob] = float16v{};
+    // One step: 24 MFMAs (OB = 2), the three products of each block in
+    // turn over the four blocks, so consecutive MFMAs never wait on each
+    // other's results.
+    auto compute = [&](const Step &st) __attribute__((always_inline)) {
 #pragma unroll
         for (int ks = 0; ks < 2; ks++) {
             half8 wa[OB], wb[OB];
 #pragma unroll
             for (int ob = 0; ob < OB; ob++) {
-                const uint32_t c16 = ((ks ? st.c[ob].y : st.c[ob].x) >> (16 * jh)) & 0xFFFFu;
-                // separate index registers for the two tables: merged into
-                // one read per byte, the a and b parts would land in the
-                // wrong registers and need moves into operand order
-                uint32_t i0 = c16 & 0xFFu, i1 = c16 >> 8, j0 = i0, j1 = i1;
-                asm volatile("" : "+v"(j0), "+v"(j1));
-                const u32x2 a0 = luta[i0], a1 = luta[i1];
-                const u32x2 b0 = lutb[j0], b1 = lutb[j1];
-                wa[ob] = __builtin_bit_cast(half8, u32x4{a0.x, a0.y, a1.x, a1.y});
-                wb[ob] = __builtin_bit_cast(half8, u32x4{b0.x, b0.y, b1.x, b1.y});
+                const uint4 tb = st.tab[ob];
+                const uint32_t b0 = (st.cw[ob] >> (4 * ks)) & 0x03030303u, h0 = b0 | 0x04040404u;
+                const uint32_t b1 = (st.cw[ob] >> (4 * ks + 2)) & 0x03030303u, h1 = b1 | 0x04040404u;
+                const uint4 sl = {__builtin_amdgcn_perm(h0, b0, 0x05010400u), __builtin_amdgcn_perm(h0, b0, 0x07030602u),
+                                  __builtin_amdgcn_perm(h1, b1, 0x05010400u), __builtin_amdgcn_perm(h1, b1, 0x07030602u)};
+                const u32x4 ua = {__builtin_amdgcn_perm(tb.x, tb.y, sl.x), __builtin_amdgcn_perm(tb.x, tb.y, sl.y),
+                                  __builtin_amdgcn_perm(tb.x, tb.y, sl.z), __builtin_amdgcn_perm(tb.x, tb.y, sl.w)};
+                const u32x4 ub = {__builtin_amdgcn_perm(tb.z, tb.w, sl.x), __builtin_amdgcn_perm(tb.z, tb.w, sl.y),
+                                  __builtin_amdgcn_perm(tb.z, tb.w, sl.z), __builtin_amdgcn_perm(tb.z, tb.w, sl.w)};
+                wa[ob] = __builtin_bit_cast(half8, ua);
+                wb[ob] = __builtin_bit_cast(half8, ub);
             }
-            // the three products of each block in turn over the four blocks,
-            // so consecutive MFMAs never wait on each other's results
 #pragma unroll
             for (int rb = 0; rb < 2; rb++)
 #pragma unroll
                 for (int ob = 0; ob < OB; ob++)
-                    acc[rb][ob] = __builtin_amdgcn_mfma_f32_32x32x16_f16(
-                        st.x[ks][rb][0], wa[ob], (first && ks == 0) ? float16v{} : acc[rb][ob], 0, 0, 0);
+                    acc[rb][ob] = __builtin_amdgcn_mfma_f32_32x32x16_f16(st.x[ks][rb][0], wa[ob], acc[rb][ob], 0, 0, 0);
 #pragma unroll
             for (int rb = 0; rb < 2; rb++)
 #pragma unroll
@@ -549,62 +629,90 @@ void cq_gemm_split_kernel(CqSplitArgs a)
                     acc[rb][ob] = __builtin_amdgcn_mfma_f32_32x32x16_f16(st.x[ks][rb][0], wb[ob], acc[rb][ob], 0, 0, 0);
         }
     };
-    // A group's end folds its sums into the totals with its norms, which
-    // every step of the group loads beside its operands (so their wait is
-    // that of the step's own data).
-    auto fold = [&](const Step &st) {
-#pragma unroll
-        for (int rb = 0; rb < 2; rb++)
-#pragma unroll
-            for (int ob = 0; ob < OB; ob++) {
-                const float nrm = half_bits_to_float(st.nb[ob]);
-#pragma unroll
-                for (int i = 0; i < 16; i++)
-                    ysum[rb][ob][i] = fmaf(nrm, acc[rb][ob][i], ysum[rb][ob][i]);
-            }
-    };
-    const uint32_t nsteps = a.in_pad / CS_KT, gmask = (a.group / CS_KT) - 1;   // steps per group: a power of two
-    auto step = [&](const Step &st, uint32_t s) __attribute__((always_inline)) {
-        if ((s & gmask) == 0)
-            compute(st, true);
-        else
-            compute(st, false);
-        if (((s + 1) & gmask) == 0)
-            fold(st);
-    };
-
-    // Steps in pairs, so the two register sets alternate without copies.
-    // Every load is unconditional (a pair's last one re-reads a valid step
-    // when nothing is left), so each wait covers exactly the step it feeds
-    // and the next step's loads stay in flight. in_pad is a multiple of the
-    // group, itself a multiple of one step.
-    Step s0, s1;
-    load(0, s0);
-    __syncthreads();                    // the tables are written
-    uint32_t s = 0;
-    for (; s + 2 <= nsteps; s += 2) {
-        load((s + 1) * CS_KT, s1);
-        step(s0, s);
-        load(min(s + 2, nsteps - 1) * CS_KT, s0);
-        step(s1, s + 1);
-    }
-    if (s < nsteps)
-        step(s0, s);
-    // D layout: lane holds output column ln of each block, rows 8 (i/4) + 4 jh + (i%4)
-#pragma unroll
-    for (int ob = 0; ob < OB; ob++) {
-        const uint32_t o = o0 + wo + 32 * ob + ln;
-        if (o >= out)
-            continue;
+    // An item's end: the sums out, scaled by 2^-(rexp + cexp), then zeroed.
+    // D layout: lane holds output column ln of each block, rows 8 (i/4) +
+    // 4 jh + (i%4) of the block; lane t of the wave holds row t's exponent.
+    auto finish = [&](const Item &m, const Step &st) {
+        float *y = a.y[m.ti];
 #pragma unroll
         for (int rb = 0; rb < 2; rb++)
 #pragma unroll
             for (int i = 0; i < 16; i++) {
-                const uint32_t row = r0 + wr + 32 * rb + 8 * (i >> 2) + 4 * jh + (i & 3);
-                if (row < a.rows)
-                    y[(uint64_t)row * out + o] = ldexpf(ysum[rb][ob][i], -(a.rexp[row] + ecb));
+                const int t = 32 * rb + 8 * (i >> 2) + 4 * jh + (i & 3);
+                const int rx = __shfl(st.rx, t, 64);
+                const uint32_t row = m.r0 + wr + t;
+#pragma unroll
+                for (int ob = 0; ob < OB; ob++) {
+                    const uint32_t o = m.o0 + wo + 32 * ob + ln;
+                    if (row < a.rows && o < m.out)
+                        y[(uint64_t)row * m.out + o] = ldexpf(acc[rb][ob][i], -(rx + st.ce[ob]));
+                }
             }
+#pragma unroll
+        for (int rb = 0; rb < 2; rb++)
+#pragma unroll
+            for (int ob = 0; ob < OB; ob++)
+                acc[rb][ob] = float16v{};
+    };
+
+    // Loads run one step ahead of the MFMAs at (lit, ls); when nothing is
+    // left they re-read the last step, so every load is unconditional and
+    // each wait covers exactly the step it feeds. The scheduling barriers
+    // keep each step's loads ahead of the previous step's MFMAs (left to
+    // itself the scheduler sinks them next to their use).
+    uint32_t lit = first, ls = 0, cit = first, cs = 0;
+    Item mc = item(first);
+    Src q = source(mc);
+    auto next_load = [&]() {
+        if (++ls == nsteps) {
+            if (lit + G8 < last) {
+                lit += G8;
+                ls = 0;
+                q = source(item(lit));
+            } else {
+                ls = nsteps - 1;
+            }
+        }
+    };
+    Step s0, s1;
+    load(q, ls, s0);
+    next_load();
+    for (;;) {
+        load(q, ls, s1);
+        next_load();
+        __builtin_amdgcn_sched_barrier(0);
+        compute(s0);
+        __builtin_amdgcn_sched_barrier(0);
+        if (++cs == nsteps) {
+            finish(mc, s0);
+            if (cit + G8 >= last)
+                break;
+            cit += G8;
+            cs = 0;
+            mc = item(cit);
+        }
+        load(q, ls, s0);
+        next_load();
+        __builtin_amdgcn_sched_barrier(0);
+        compute(s1);
+        __builtin_amdgcn_sched_barrier(0);
+        if (++cs == nsteps) {
+            finish(mc, s1);
+            if (cit + G8 >= last)
+                break;
+            cit += G8;
+            cs = 0;
+            mc = item(cit);
+        }
     }
+}
+
+hipError_t launch_cq_split_tables(const CqTabArgs &a, hipStream_t s)
+{
+    if (a.out == 0)
+        return hipSuccess;
+    hipLaunchKernelGGL(cq_split_tables_kernel, dim3((a.out + 255) / 256), dim3(256), 0, s, a);
+    return hipGetLastError();
 }
 
 hipError_t launch_cq_prepare_split(const CqPrepSplitArgs &a, hipStream_t s)
@@ -627,9 +735,18 @@ hipError_t launch_cq_gemm_split(const CqSplitArgs &a, hipStream_t s)
     if (a.rows == 0 || a.nt == 0 || a.tile0[a.nt] == 0)
         return hipSuccess;
     const uint64_t items = (uint64_t)((a.rows + CQ_SPLIT_MT - 1) / CQ_SPLIT_MT) * a.tile0[a.nt];
-    const uint64_t grid = (items + 7) / 8 * 8;
-    if (grid > 0x7FFFFFFFull)
+    if (items > 0x7FFFFFFFull)
         return hipErrorInvalidValue;
+    // persistent: at most two work-groups per CU (the kernel's occupancy),
+    // a multiple of 8 so that every XCD holds the same number
+    static int cus[64];
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64)
+        return hipErrorInvalidDevice;
+    if (cus[dev] <= 0 && hipDeviceGetAttribute(&cus[dev], hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess)
+        return hipErrorInvalidDevice;
+    const uint64_t slots = std::max<uint64_t>(8, (uint64_t)cus[dev] * 2 / 8 * 8);
+    const uint64_t grid = std::min<uint64_t>((items + 7) / 8 * 8, slots);
     hipLaunchKernelGGL(cq_gemm_split_kernel<CQ_SPLIT_OB>, dim3((uint32_t)grid), dim3(256), 0, s, a);
     return hipGetLastError();
 }

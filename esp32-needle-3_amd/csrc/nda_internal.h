@@ -205,13 +205,24 @@ struct CqSplitArgs {
     const _Float16 *xs;
     const int32_t *rexp;
     float *y[CQ_MAX_T];
-    const uint8_t *packed[CQ_MAX_T];
-    const uint16_t *norms[CQ_MAX_T];
-    const float *cb[CQ_MAX_T];
+    const uint32_t *cw[CQ_MAX_T];       /* decode data from cq_split_tables_kernel */
+    const uint4 *tab[CQ_MAX_T];
+    const int32_t *cexp[CQ_MAX_T];
     uint32_t out[CQ_MAX_T];
-    uint32_t tile0[CQ_MAX_T + 1];       /* first grid.y tile (of CQ_SPLIT_NT outputs) per tensor */
+    uint32_t tile0[CQ_MAX_T + 1];       /* first tile (of CQ_SPLIT_NT outputs) per tensor */
     uint32_t nt;
-    uint32_t rows, in_pad, group, ngroup, rowbytes, log2_group;
+    uint32_t rows, in_pad, log2_group;
+};
+/* One 2-bit tensor's decode data for the split GEMM, built at creation:
+ * cw [in_pad / 32][out][2] words, tab [ngroup][out] uint4, cexp [out]. */
+struct CqTabArgs {
+    const uint8_t *packed;
+    const uint16_t *norms;
+    const float *cb;
+    uint32_t *cw;
+    uint4 *tab;
+    int32_t *cexp;
+    uint32_t out, in_pad, ngroup, rowbytes;
 };
 #ifndef NDA_CQ_OB
 #define NDA_CQ_OB 2
@@ -224,6 +235,7 @@ hipError_t launch_cq_prepare(const CqPrepArgs &a, hipStream_t s);
 hipError_t launch_cq_gemm(const CqGemmArgs &a, hipStream_t s);
 hipError_t launch_cq_prepare_split(const CqPrepSplitArgs &a, hipStream_t s);
 hipError_t launch_cq_gemm_split(const CqSplitArgs &a, hipStream_t s);
+hipError_t launch_cq_split_tables(const CqTabArgs &a, hipStream_t s);
 
 /* Compiled geometries: (KV element bytes, qk_head_dim, v_head_dim, GQA rep). */
 #define NDA_FOR_GEOMETRIES(X) \
