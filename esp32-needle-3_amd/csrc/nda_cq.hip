@@ -303,7 +303,8 @@ constexpr int CQ_REG_COLS = 1536;
 
 __global__ __launch_bounds__(512) void cq_prepare_split_reg_kernel(CqPrepSplitArgs a)
 {
-    __shared__ __attribute__((aligned(16))) uint4 T[2][CQ_REG_COLS / 8][9];   // [plane][slot][row of 8 + pad]
+    // [plane][slot][row of 8 + pad], sized to the row: in_pad / 8 slots
+    extern __shared__ __attribute__((aligned(16))) uint4 T[];
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const uint32_t row0 = blockIdx.x * 8, row = row0 + wave;
     const bool live = row < a.rows;
@@ -377,6 +378,7 @@ __global__ __launch_bounds__(512) void cq_prepare_split_reg_kernel(CqPrepSplitAr
         sh = 15 - e;                                   // mx * 2^sh in [2^14, 2^15)
     }
     // this row's operand slots into LDS, then whole lines out
+    const uint32_t nslot = a.in_pad / 8;
 #pragma unroll
     for (int h = 0; h < 3; h++) {
         const uint32_t c = 64 * h + lane;              // slot: columns 8c .. 8c + 7
@@ -390,18 +392,18 @@ __global__ __launch_bounds__(512) void cq_prepare_split_reg_kernel(CqPrepSplitAr
             h8[s] = (_Float16)y;
             l8[s] = (_Float16)(y - (float)h8[s]);
         }
-        T[0][c][wave] = __builtin_bit_cast(uint4, half8{h8[0], h8[1], h8[2], h8[3], h8[4], h8[5], h8[6], h8[7]});
-        T[1][c][wave] = __builtin_bit_cast(uint4, half8{l8[0], l8[1], l8[2], l8[3], l8[4], l8[5], l8[6], l8[7]});
+        T[c * 9 + wave] = __builtin_bit_cast(uint4, half8{h8[0], h8[1], h8[2], h8[3], h8[4], h8[5], h8[6], h8[7]});
+        T[(nslot + c) * 9 + wave] = __builtin_bit_cast(uint4, half8{l8[0], l8[1], l8[2], l8[3], l8[4], l8[5], l8[6], l8[7]});
     }
     if (live && lane == 0)
         a.rexp[row] = sh;
     __syncthreads();
     // 8 rows' slot c of a plane is one 128-byte line (lanes row0 % 32 ..
     // +7 of one operand): thread t writes row t % 8 of line t / 8
-    const uint32_t nslot = a.in_pad / 8, nkb = a.in_pad / 16;
+    const uint32_t nkb = a.in_pad / 16;
     for (uint32_t u = threadIdx.x; u < 2 * nslot * 8; u += 512) {
         const uint32_t r = u & 7, c = (u >> 3) % nslot, p = (u >> 3) / nslot;
-        *reinterpret_cast<uint4 *>(a.xs + split_index(row0 + r, 8 * c, nkb, (int)p)) = T[p][c][r];
+        *reinterpret_cast<uint4 *>(a.xs + split_index(row0 + r, 8 * c, nkb, (int)p)) = T[(p * nslot + c) * 9 + r];
     }
 }
 
@@ -720,7 +722,8 @@ hipError_t launch_cq_prepare_split(const CqPrepSplitArgs &a, hipStream_t s)
     if (a.rows == 0)
         return hipSuccess;
     if (a.in_pad <= (uint32_t)CQ_REG_COLS && a.group >= 64) {
-        hipLaunchKernelGGL(cq_prepare_split_reg_kernel, dim3((a.rows + 7) / 8), dim3(512), 0, s, a);
+        hipLaunchKernelGGL(cq_prepare_split_reg_kernel, dim3((a.rows + 7) / 8), dim3(512),
+                           (size_t)a.in_pad / 8 * 2 * 9 * sizeof(uint4), s, a);
         return hipGetLastError();
     }
     CqPrepSplitArgs b = a;
