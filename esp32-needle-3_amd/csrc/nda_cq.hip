@@ -291,7 +291,7 @@ __global__ __launch_bounds__(256) void cq_prepare_split_kernel(CqPrepSplitArgs a
 }
 
 // Register form for rows of up to 1536 columns and groups of at least 64:
-// one wave per row, lane l holding columns 512 h + 8 l .. +7 (h < 3). The
+// one wave per row, lane l holding columns 512 h + 8 l .. +7 (h < NH). The
 // butterfly stages are the engine's (the same pairs, a + b and a - b, stage
 // by stage): len < 8 inside a lane, 8 <= len < 512 between lanes l and
 // l ^ (len / 8) (the upper lane's a - b as fmaf(-1, b, a), one rounding of
@@ -301,6 +301,7 @@ __global__ __launch_bounds__(256) void cq_prepare_split_kernel(CqPrepSplitArgs a
 // line of the split rows (8 rows x one slot) is then written whole.
 constexpr int CQ_REG_COLS = 1536;
 
+template <int NH>       // column blocks of 512 in use: in_pad <= 512 NH
 __global__ __launch_bounds__(512) void cq_prepare_split_reg_kernel(CqPrepSplitArgs a)
 {
     // [plane][slot][row of 8 + pad], sized to the row: in_pad / 8 slots
@@ -309,28 +310,41 @@ __global__ __launch_bounds__(512) void cq_prepare_split_reg_kernel(CqPrepSplitAr
     const uint32_t row0 = blockIdx.x * 8, row = row0 + wave;
     const bool live = row < a.rows;
     const float *x = a.x + (uint64_t)(live ? row : 0) * a.in;
-    float v[3][8];
-    const bool vec = (a.in & 3) == 0;                  // rows 16-byte aligned
+    float v[NH][8];
+    if ((a.in & 3) == 0) {
+        // rows 16-byte aligned: 16-byte loads from clamped (in-bounds)
+        // addresses, columns past the row's end selected to zero
 #pragma unroll
-    for (int h = 0; h < 3; h++) {
-        const uint32_t i0 = 512 * h + 8 * lane;
-        if (vec && live && i0 + 8 <= a.in) {           // two 16-byte loads
-            const float4 p = *reinterpret_cast<const float4 *>(x + i0);
-            const float4 q = *reinterpret_cast<const float4 *>(x + i0 + 4);
-            v[h][0] = p.x; v[h][1] = p.y; v[h][2] = p.z; v[h][3] = p.w;
-            v[h][4] = q.x; v[h][5] = q.y; v[h][6] = q.z; v[h][7] = q.w;
-        } else {
+        for (int h = 0; h < NH; h++)
 #pragma unroll
-            for (int s = 0; s < 8; s++)
-                v[h][s] = live && i0 + s < a.in ? x[i0 + s] : 0.0f;
-        }
+            for (int f = 0; f < 2; f++) {
+                const uint32_t i0 = 512 * h + 8 * lane + 4 * f;
+                const float4 p = *reinterpret_cast<const float4 *>(x + min(i0, a.in - 4));
+                const bool ok = live && i0 + 4 <= a.in;
+                v[h][4 * f + 0] = ok ? p.x : 0.0f;
+                v[h][4 * f + 1] = ok ? p.y : 0.0f;
+                v[h][4 * f + 2] = ok ? p.z : 0.0f;
+                v[h][4 * f + 3] = ok ? p.w : 0.0f;
+            }
+    } else {
+#pragma unroll
+        for (int h = 0; h < NH; h++)
+#pragma unroll
+            for (int s = 0; s < 8; s++) {
+                const uint32_t i = 512 * h + 8 * lane + s;
+                v[h][s] = live && i < a.in ? x[i] : 0.0f;
+            }
     }
-    const int nh = (int)((a.in_pad + 511) / 512);       // column blocks in use (<= 3)
-    for (uint32_t len = 1; len < a.group; len <<= 1) {
-        if (len < 8) {
+    // stage len = 2^lg, lg a compile-time index (so every register index is
+    // fixed); group <= in_pad <= 1536 makes len <= 512
 #pragma unroll
-            for (int h = 0; h < 3; h++)
-                if (h < nh)
+    for (int lg = 0; lg < 10; lg++) {
+        const int len = 1 << lg;
+        if ((uint32_t)len >= a.group)
+            break;
+        if (lg < 3) {
+#pragma unroll
+            for (int h = 0; h < NH; h++)
 #pragma unroll
                 for (int s = 0; s < 8; s++)
                     if ((s & len) == 0) {
@@ -338,33 +352,30 @@ __global__ __launch_bounds__(512) void cq_prepare_split_reg_kernel(CqPrepSplitAr
                         v[h][s] = u + w;
                         v[h][s + len] = u - w;
                     }
-        } else if (len < 512) {
-            const int m = (int)(len >> 3);
+        } else if (lg < 9) {
+            const int m = len >> 3;
             const float sg = (lane & m) ? -1.0f : 1.0f;
 #pragma unroll
-            for (int h = 0; h < 3; h++)
-                if (h < nh)
+            for (int h = 0; h < NH; h++)
 #pragma unroll
                 for (int s = 0; s < 8; s++) {
                     const float w = __shfl_xor(v[h][s], m, 64);
                     v[h][s] = fmaf(sg, v[h][s], w);     // lower lane: v + w; upper: w - v
                 }
         } else {
-            const int m = (int)(len >> 9);
+            if constexpr (NH >= 2) {
 #pragma unroll
-            for (int h = 0; h < 3; h++)
-                if ((h & m) == 0)
-#pragma unroll
-                    for (int s = 0; s < 8; s++) {
-                        const float u = v[h][s], w = v[h + m][s];
-                        v[h][s] = u + w;
-                        v[h + m][s] = u - w;
-                    }
+                for (int s = 0; s < 8; s++) {           // len 512: blocks 0 and 1
+                    const float u = v[0][s], w = v[1][s];
+                    v[0][s] = u + w;
+                    v[1][s] = u - w;
+                }
+            }
         }
     }
     float mx = 0.0f;
 #pragma unroll
-    for (int h = 0; h < 3; h++)
+    for (int h = 0; h < NH; h++)
 #pragma unroll
         for (int s = 0; s < 8; s++) {
             v[h][s] *= a.scale;                         // the engine's prepared value
@@ -380,7 +391,7 @@ __global__ __launch_bounds__(512) void cq_prepare_split_reg_kernel(CqPrepSplitAr
     // this row's operand slots into LDS, then whole lines out
     const uint32_t nslot = a.in_pad / 8;
 #pragma unroll
-    for (int h = 0; h < 3; h++) {
+    for (int h = 0; h < NH; h++) {
         const uint32_t c = 64 * h + lane;              // slot: columns 8c .. 8c + 7
         if (8 * c >= a.in_pad)
             continue;
@@ -722,8 +733,14 @@ hipError_t launch_cq_prepare_split(const CqPrepSplitArgs &a, hipStream_t s)
     if (a.rows == 0)
         return hipSuccess;
     if (a.in_pad <= (uint32_t)CQ_REG_COLS && a.group >= 64) {
-        hipLaunchKernelGGL(cq_prepare_split_reg_kernel, dim3((a.rows + 7) / 8), dim3(512),
-                           (size_t)a.in_pad / 8 * 2 * 9 * sizeof(uint4), s, a);
+        const size_t lds = (size_t)a.in_pad / 8 * 2 * 9 * sizeof(uint4);
+        const dim3 grid((a.rows + 7) / 8);
+        if (a.in_pad <= 512)
+            hipLaunchKernelGGL(cq_prepare_split_reg_kernel<1>, grid, dim3(512), lds, s, a);
+        else if (a.in_pad <= 1024)
+            hipLaunchKernelGGL(cq_prepare_split_reg_kernel<2>, grid, dim3(512), lds, s, a);
+        else
+            hipLaunchKernelGGL(cq_prepare_split_reg_kernel<3>, grid, dim3(512), lds, s, a);
         return hipGetLastError();
     }
     CqPrepSplitArgs b = a;
