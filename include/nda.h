@@ -225,7 +225,12 @@ typedef struct nda_cq nda_cq;
 
 /* Copies one tensor to the device. blob: host, the tensor payload (packed
  * rows then norms); codebook: host, the 2^bits entries for this width
- * (nd_cact_codebook). group a power of two in 16..4096, bits 2..4. */
+ * (nd_cact_codebook). group a power of two in 16..4096, bits 2..4. A 2-bit
+ * tensor with group >= 32 also gets the split path's decode data, built on
+ * the device before the call returns (a kernel on the null stream, then a
+ * wait on it): its codes re-ordered into per-lane words (the size of the
+ * packed codes), and per (row, group) the four weights codebook[c] * norm
+ * as fp16 pairs (16 bytes), with one exponent per row. */
 int nda_cq_create(uint32_t out, uint32_t in, uint32_t group, uint32_t bits, const void *blob,
                   const float *codebook, nda_cq **t);
 int nda_cq_destroy(nda_cq *t);
@@ -247,10 +252,11 @@ int nda_cq_gemm_many(const nda_cq *const *ts, uint32_t n, uint32_t rows, const f
  * NDA_ERR_UNSUPPORTED). The prepared form xs (device, 16-byte aligned,
  * nda_cq_split_bytes) holds per row the engine's prepared values times a
  * power of two 2^e as an fp16 pair hi + lo: plane hi [rows][in_pad], plane
- * lo [rows][in_pad], then e [rows] (int32). Codebook entries are split the
- * same way; the fourth product (lo x lo, 2^-22 relative) is dropped, so the
- * result is within a few 2^-22 of sum |w x| of the engine's. The attention
- * block calls take this path when all five tensors allow it. */
+ * lo [rows][in_pad], then e [rows] (int32). The weights codebook[c] * norm
+ * are split the same way, per (row, group), when the tensor is created; the
+ * fourth product (lo x lo, 2^-22 relative) is dropped, so the result is
+ * within a few 2^-22 of sum |w x| of the engine's. The attention block calls
+ * take this path when all five tensors allow it. */
 size_t nda_cq_split_bytes(const nda_cq *t, uint32_t rows);
 int nda_cq_prepare_split(const nda_cq *t, uint32_t rows, const float *x, void *xs, void *stream);
 int nda_cq_gemm_split(const nda_cq *t, uint32_t rows, const void *xs, float *y, void *stream);
