@@ -254,3 +254,55 @@ def test_cq_split_many_matches_single_and_rejects():
     assert e.value.code == -6
     for q in qs + [q4, q16]:
         q.close()
+
+
+def test_cq_split_persistent_walks_and_column_scales():
+    """q/k/v/gate over 6181 rows: 49 row tiles x 13 output tiles = 637 items
+    for the 512 persistent work-groups, so a work-group walks two items
+    (across tensors and row tiles, the next item's loads issued during the
+    last step of the one before). The launch equals the four single-tensor
+    launches (under 512 items each: one item per work-group) bit for bit,
+    and sampled rows are within the reassociation bound of the oracle.
+    Columns 5-7 of q probe the per-column scaling: all norms zero (exponent
+    0, output exactly 0), the fp16 maximum beside subnormal norms, and all
+    norms subnormal."""
+    N = nda()
+    say("cq split persistent walks")
+    shapes = [576, 96, 128, 768]
+    rows, inp, group = 6181, 768, 128
+    ts = [make_cq_tensor(900 + i, o, inp, group, 2, special_norms=True) for i, o in enumerate(shapes)]
+    t = ts[0]
+    ng = inp // group
+    pb = t.out * inp // 4
+    blob = np.array(t.blob, copy=True)
+    nrm = blob[pb:].view(np.float16).reshape(t.out, ng)
+    nrm[5, :] = 0.0
+    nrm[6, :] = np.float16(6e-8)                     # the smallest fp16 subnormal
+    nrm[6, 2] = np.float16(65504.0)
+    nrm[7, :] = np.float16(-6e-8)
+    ts[0] = O.CQTensor(t.out, inp, group, 2, blob, t.cb())
+    qs = [N.CQ(o, inp, group, 2, tt.blob, tt.cb()) for o, tt in zip(shapes, ts)]
+    x = np.stack([det_normal(7000 + r, inp) for r in range(rows)])
+    dx = N.DevBuf.from_array(x)
+    dxs = N.DevBuf(qs[0].split_bytes(rows))
+    qs[0].prepare_split(rows, dx, dxs)
+    one = [N.DevBuf(rows * o * 4) for o in shapes]
+    many = [N.DevBuf(rows * o * 4) for o in shapes]
+    for q, y in zip(qs, one):
+        q.gemm_split(rows, dxs, y)
+    N.cq_gemm_split_many(qs, rows, dxs, many)
+    N.device_sync()
+    sample = sorted(set(list(range(0, rows, 193)) + [rows - 37, rows - 2, rows - 1]))
+    for i, (o, a, b) in enumerate(zip(shapes, one, many)):
+        ya = a.to_array(np.uint32, (rows, o))
+        assert np.array_equal(ya, b.to_array(np.uint32, (rows, o))), shapes[i]
+        y = ya.view(np.float32)
+        if i == 0:
+            assert np.all(y[:, 5] == 0.0)
+        sc = abs_scale(ts[i], x[sample])
+        for j, r in enumerate(sample):
+            want = O.cq_gemv_lut2(ts[i], O.cq_prepare(ts[i], x[r]))
+            err = np.abs(y[r].astype(np.float64) - want)
+            assert np.all(err <= 1e-5 * sc[:, j] + 1e-6), (shapes[i], r, float(err.max()))
+    for q in qs:
+        q.close()
