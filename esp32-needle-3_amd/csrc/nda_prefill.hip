@@ -36,11 +36,43 @@ typedef float float16v __attribute__((ext_vector_type(16)));
 
 constexpr int PF_KT = 32;   // keys per tile
 
+// Everything here is plain code the backend can see: it owes wait states
+// between a VALU write and an MFMA or v_permlane32_swap read of the same
+// VGPR (two on gfx950), and it cannot count them across an inline-asm
+// instruction. An asm v_fma_mixhi_f16 feeding an MFMA operand got one wait
+// state, so the MFMA read whatever the register held before: a stale lo half
+// of P, which gave results that depended on register allocation.
+//
+// The tree of maxes becomes v_max3_f32 (scores are never NaN).
 __device__ __forceinline__ float max3(float a, float b, float c)
 {
-    float r;
-    asm("v_max3_f32 %0, %1, %2, %3" : "=v"(r) : "v"(a), "v"(b), "v"(c));
-    return r;
+    return __builtin_fmaxf(__builtin_fmaxf(a, b), c);
+}
+
+// -1.0f that the optimiser cannot see through (one SGPR per kernel, so it
+// costs no VGPR): with it, fma(hi, neg1, p) stays an fma over a widened fp16
+// operand and is selected as one v_fma_mixlo/mixhi_f16 per value; with a
+// literal -1 it is folded into a subtraction and costs a conversion, a
+// subtraction and a packing.
+__device__ __forceinline__ float opaque_neg1()
+{
+    float n = -1.0f;
+    asm volatile("" : "+s"(n));
+    return n;
+}
+
+// lo halves of a pair of softmax weights whose hi halves (rounded toward zero
+// to fp16) are packed in hw: fp16(p - hi), rounded to nearest. p - hi is
+// exact in fp32, so the one rounding is the conversion to fp16.
+typedef _Float16 half2v __attribute__((ext_vector_type(2)));
+
+__device__ __forceinline__ uint32_t split_lo2(uint32_t hw, float p0, float p1, float neg1)
+{
+    const half2v h = __builtin_bit_cast(half2v, hw);
+    half2v l;
+    l[0] = (_Float16)__builtin_fmaf((float)h[0], neg1, p0);
+    l[1] = (_Float16)__builtin_fmaf((float)h[1], neg1, p1);
+    return __builtin_bit_cast(uint32_t, l);
 }
 
 __device__ __forceinline__ float16v mfma32(half8 a, half8 b, float16v c)
@@ -260,6 +292,7 @@ void prefill_kernel(PrefillArgs a)
 
     float16v acc0 = {}, acc1 = {};
     float m = -FLT_MAX, lsum = 0.0f;
+    const float neg1 = opaque_neg1();
 
     PfIO<ES, DK, DV, NTHR> io;
     io.pool = a.pool;
@@ -395,35 +428,27 @@ void prefill_kernel(PrefillArgs a)
                 }
             }
         }
-        // P^T operand (hi, lo) for the two 16-key blocks: slots = registers
-        // 8*kb2 + s. hi = p rounded toward zero to fp16, lo = the remainder.
-        u32x4 phw[2], plw[2];
-#pragma unroll
-        for (int i = 0; i < 16; i += 2) {
-            float p0 = fast_exp2(REL ? st[i] : st[i] - m), p1 = fast_exp2(REL ? st[i + 1] : st[i + 1] - m);
-            lsum += p0 + p1;
-            if constexpr (ES == 1) {
-                p0 *= Vsc[8 * (i >> 2) + 4 * jh + (i & 3)];
-                p1 *= Vsc[8 * (i >> 2) + 4 * jh + ((i + 1) & 3)];
-            }
-            const fp16x2 h = __builtin_amdgcn_cvt_pkrtz(p0, p1);
-            const uint32_t hw = __builtin_bit_cast(uint32_t, h);
-            // lo = fp16(p - hi): one mixed-precision FMA per element, the fp16
-            // hi half widened inside the FMA, written into its half of lw.
-            uint32_t lw;
-            asm("v_fma_mixlo_f16 %0, %1, -1.0, %2 op_sel_hi:[1,0,0]" : "=v"(lw) : "v"(hw), "v"(p0));
-            asm("v_fma_mixhi_f16 %0, %1, -1.0, %2 op_sel:[1,0,0] op_sel_hi:[1,0,0]" : "+v"(lw) : "v"(hw), "v"(p1));
-            phw[i >> 3][(i & 7) >> 1] = hw;
-            plw[i >> 3][(i & 7) >> 1] = lw;
-        }
-        half8 ph[2], pl[2];
-        ph[0] = __builtin_bit_cast(half8, phw[0]);
-        ph[1] = __builtin_bit_cast(half8, phw[1]);
-        pl[0] = __builtin_bit_cast(half8, plw[0]);
-        pl[1] = __builtin_bit_cast(half8, plw[1]);
-        // ---- O^T += V^T . P^T; V^T slots = keys 16*kb2 + 8*(s/4) + 4*jh + (s%4)
+        // P^T operand (hi, lo) and O^T += V^T . P^T, one 16-key block at a
+        // time (keys 16*kb2 + 8*(s/4) + 4*jh + (s%4) in slot s): a block's
+        // weights are made just before its MFMAs, which keeps their live
+        // ranges short. hi = p rounded toward zero to fp16, lo = the remainder.
 #pragma unroll
         for (int kb2 = 0; kb2 < 2; kb2++) {
+            u32x4 phw, plw;
+#pragma unroll
+            for (int i = 8 * kb2; i < 8 * kb2 + 8; i += 2) {
+                float p0 = fast_exp2(REL ? st[i] : st[i] - m), p1 = fast_exp2(REL ? st[i + 1] : st[i + 1] - m);
+                lsum += p0 + p1;
+                if constexpr (ES == 1) {
+                    p0 *= Vsc[8 * (i >> 2) + 4 * jh + (i & 3)];
+                    p1 *= Vsc[8 * (i >> 2) + 4 * jh + ((i + 1) & 3)];
+                }
+                const fp16x2 h = __builtin_amdgcn_cvt_pkrtz(p0, p1);
+                const uint32_t hw = __builtin_bit_cast(uint32_t, h);
+                phw[(i & 7) >> 1] = hw;
+                plw[(i & 7) >> 1] = split_lo2(hw, p0, p1, neg1);
+            }
+            const half8 ph = __builtin_bit_cast(half8, phw), pl = __builtin_bit_cast(half8, plw);
 #pragma unroll
             for (int dt = 0; dt < 2; dt++) {
                 const _Float16 *vr = &Vt[32 * dt + ln][16 * kb2 + 4 * jh];
@@ -431,13 +456,15 @@ void prefill_kernel(PrefillArgs a)
                 const half4 v1 = *reinterpret_cast<const half4 *>(vr + 8);
                 const half8 va = {v0[0], v0[1], v0[2], v0[3], v1[0], v1[1], v1[2], v1[3]};
                 if (dt == 0) {
-                    acc0 = mfma32(va, ph[kb2], acc0);
-                    acc0 = mfma32(va, pl[kb2], acc0);
+                    acc0 = mfma32(va, ph, acc0);
+                    acc0 = mfma32(va, pl, acc0);
                 } else {
-                    acc1 = mfma32(va, ph[kb2], acc1);
-                    acc1 = mfma32(va, pl[kb2], acc1);
+                    acc1 = mfma32(va, ph, acc1);
+                    acc1 = mfma32(va, pl, acc1);
                 }
             }
+            if (kb2 == 0)
+                __builtin_amdgcn_sched_barrier(0);
         }
         __builtin_amdgcn_s_setprio(0);
         if (j + 1 < ntile)   // tile j+1 into the other buffer (its readers are done)
@@ -532,8 +559,6 @@ void prefill_kernel(PrefillArgs a)
 // permute and one packed fp16 subtract per two codes: 0x64 over the byte
 // (code ^ 0x80) is the fp16 1024 + code + 128. One wave owns its LDS tile,
 // whose accesses complete in order, so one buffer serves.
-typedef _Float16 half2v __attribute__((ext_vector_type(2)));
-
 template <int SEL>
 __device__ __forceinline__ half2v codes2(uint32_t xs)   // xs = codes ^ 0x80808080
 {
@@ -546,11 +571,6 @@ typedef float float4v __attribute__((ext_vector_type(4)));
 __device__ __forceinline__ float4v mfma16k32(half8 a, half8 b, float4v c)
 {
     return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
-}
-
-__device__ __forceinline__ float4v mfma16k16(half4 a, half4 b, float4v c)
-{
-    return __builtin_amdgcn_mfma_f32_16x16x16f16(a, b, c, 0, 0, 0);
 }
 
 // 16 x 16 tiles: lane l = 16 g + r holds MFMA row / column r and the k (or
@@ -566,7 +586,13 @@ void decode_mfma_kernel(PrefillArgs a)
 {
     static_assert(DK % 16 == 0 && DV == 64 && REP <= 16, "decode tiles: dk multiple of 16, dv 64, rep <= 16");
     constexpr int NS = DK / 32;                 // 32-dim steps of S (16x16x32)
-    constexpr bool TAIL = DK % 32 == 16;        // a last 16-dim step (16x16x16)
+    // A last 16-dim step (qk 48) runs on the same 16x16x32 instruction, its
+    // upper four k slots zero in both operands. Every accumulation chain
+    // thus keeps one opcode: an MFMA reading as its accumulator the result
+    // of the MFMA issued just before it, of another opcode (16x16x16 after
+    // 16x16x32), gave wrong results on gfx950 although the compiler puts no
+    // wait state between them, as it does for the same opcode.
+    constexpr bool TAIL = DK % 32 == 16;
     constexpr int KPAD = DK + 8, VPAD = PF_KT + 4;
     constexpr int KH = DK / 2, VH = DV / 2;     // codes a lane moves per key
     static_assert(KH % 8 == 0 && VH % 16 == 0, "lane halves are whole 8- and 16-byte loads");
@@ -585,11 +611,12 @@ void decode_mfma_kernel(PrefillArgs a)
     const int n_sh = vis.n_sh, total = vis.n_sh + vis.n_own;
 
     // Q^T operand, hi and lo: row r, dims 32 s + 8 g + [0, 8) and the tail
-    // 32 NS + 4 g + [0, 4); hi and lo from one rounded fp32 value
+    // 32 NS + 4 g + [0, 4) (then four zero slots); hi and lo from one rounded
+    // fp32 value
     const bool rvalid = r < REP;
     const uint64_t qrow = (uint64_t)b * a.nh + kvh * REP + (rvalid ? r : 0);
     half8 qh[NS > 0 ? NS : 1], ql[NS > 0 ? NS : 1];
-    half4 qh4, ql4;
+    half8 qht = {}, qlt = {};
     {
         const float *qr = a.q + qrow * DK;
         const float qs = rvalid ? a.qscale : 0.0f;
@@ -619,8 +646,8 @@ void decode_mfma_kernel(PrefillArgs a)
             for (int i = 0; i < 4; i++) {
                 _Float16 hi, lo;
                 split(xs[i], hi, lo);
-                qh4[i] = hi;
-                ql4[i] = lo;
+                qht[i] = hi;
+                qlt[i] = lo;
             }
         }
     }
@@ -684,6 +711,7 @@ void decode_mfma_kernel(PrefillArgs a)
 
     float4v acc[4] = {};                        // O^T: dims 16 d + 4 g + i, row r
     float m = -FLT_MAX, lsum = 0.0f;
+    const float neg1 = opaque_neg1();
     const int qlast = total - 1;                // keys past it are masked
     const int ntile = (total + PF_KT - 1) / PF_KT;
     const int jfull = total / PF_KT;            // tiles [0, jfull) are all visible
@@ -719,9 +747,10 @@ void decode_mfma_kernel(PrefillArgs a)
                 st[kb] = mfma16k32(ka, ql[s2], st[kb]);
             }
             if constexpr (TAIL) {
-                const half4 ka = *reinterpret_cast<const half4 *>(kr + 32 * NS + 4 * g);
-                st[kb] = mfma16k16(ka, qh4, st[kb]);
-                st[kb] = mfma16k16(ka, ql4, st[kb]);
+                const half4 k4 = *reinterpret_cast<const half4 *>(kr + 32 * NS + 4 * g);
+                const half8 ka = {k4[0], k4[1], k4[2], k4[3], 0, 0, 0, 0};
+                st[kb] = mfma16k32(ka, qht, st[kb]);
+                st[kb] = mfma16k32(ka, qlt, st[kb]);
             }
         }
         __builtin_amdgcn_s_setprio(1);
@@ -778,11 +807,8 @@ void decode_mfma_kernel(PrefillArgs a)
         for (int i = 0; i < 8; i += 2) {
             const fp16x2 hh = __builtin_amdgcn_cvt_pkrtz(p[i], p[i + 1]);
             const uint32_t hw = __builtin_bit_cast(uint32_t, hh);
-            uint32_t lw;
-            asm("v_fma_mixlo_f16 %0, %1, -1.0, %2 op_sel_hi:[1,0,0]" : "=v"(lw) : "v"(hw), "v"(p[i]));
-            asm("v_fma_mixhi_f16 %0, %1, -1.0, %2 op_sel:[1,0,0] op_sel_hi:[1,0,0]" : "+v"(lw) : "v"(hw), "v"(p[i + 1]));
             phw[i >> 1] = hw;
-            plw[i >> 1] = lw;
+            plw[i >> 1] = split_lo2(hw, p[i], p[i + 1], neg1);
         }
         const half8 ph = __builtin_bit_cast(half8, phw), pl = __builtin_bit_cast(half8, plw);
 #pragma unroll
@@ -795,8 +821,16 @@ void decode_mfma_kernel(PrefillArgs a)
             acc[d] = mfma16k32(va, pl, acc[d]);
         }
         __builtin_amdgcn_s_setprio(0);
-        if (j + 1 < ntile)      // after this tile's last LDS reads, in the wave's order
+        // Tile j+1 into LDS after this tile's last LDS reads. Other lanes of
+        // the wave read what this lane stores, and the wave's LDS accesses
+        // complete in issue order; the wave barriers (scheduling barriers,
+        // no instruction) keep the compiler from moving LDS accesses of one
+        // tile across the store of the next.
+        if (j + 1 < ntile) {
+            __builtin_amdgcn_wave_barrier();
             store(sg);
+            __builtin_amdgcn_wave_barrier();
+        }
     };
     using P0 = std::integral_constant<int, 0>;
     using P1 = std::integral_constant<int, 1>;

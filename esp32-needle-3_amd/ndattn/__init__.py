@@ -11,8 +11,8 @@ import os
 import numpy as np
 
 PKG_DIR = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
-# NDATTN_LIB selects another build of the same library (tuning variants).
-LIB_PATH = os.environ.get("NDATTN_LIB", os.path.join(PKG_DIR, "libndattn.so"))
+# The in-tree build is the only library this module loads.
+LIB_PATH = os.path.join(PKG_DIR, "libndattn.so")
 HOST_LIB_PATH = os.path.join(PKG_DIR, "libndhost.so")
 
 NDA_OK = 0
