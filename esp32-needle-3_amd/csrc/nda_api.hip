@@ -14,6 +14,7 @@
 #include <cstdarg>
 #include <cstdio>
 #include <cstring>
+#include <mutex>
 #include <new>
 #include <string>
 #include <unordered_set>
@@ -21,7 +22,35 @@
 
 using namespace nda;
 
+// Scratch of nda_decode_noalloc: the launch's sequence ids, then its split-KV
+// partials. One array per GPU, held until the process ends. Host code never
+// uses this name as an address (on the host it is only a stand-in): each
+// device's address comes from hipGetSymbolAddress, taken once per device in
+// nda_create with that device current, and is kept in g_scratch.
+static __device__ __align__(256) uint8_t scratch[NDA_NOALLOC_SCRATCH_BYTES];
+
 namespace {
+
+constexpr int MAX_DEVICES = 64;
+std::mutex g_scratch_mu;
+uint8_t *g_scratch[MAX_DEVICES] = {};
+
+// This device's address of `scratch` (resolved on first use per device).
+hipError_t scratch_address(int dev, uint8_t **out)
+{
+    if (dev < 0 || dev >= MAX_DEVICES)
+        return hipErrorInvalidDevice;
+    std::lock_guard<std::mutex> lk(g_scratch_mu);
+    if (!g_scratch[dev]) {
+        void *p = nullptr;
+        const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        if (e != hipSuccess)
+            return e;
+        g_scratch[dev] = static_cast<uint8_t *>(p);
+    }
+    *out = g_scratch[dev];
+    return hipSuccess;
+}
 
 constexpr uint32_t MIN_RECENT = 64;   // ND_MIN_RECENT, engine/src/nd_model.c:1311-1312
 
@@ -69,6 +98,7 @@ struct nda_ctx {
     uint32_t *d_pf = nullptr;           // prefill work list staging
     size_t pf_cap = 0;                  // uint32 entries
     uint64_t dev_bytes = 0;
+    uint8_t *scratch = nullptr;         // this device's nda_decode_noalloc scratch
 
     std::vector<int32_t> pages, prefix_pages;
     std::vector<SeqHost> seqs;
@@ -370,9 +400,9 @@ struct ProfScope {
     int kind;
     hipStream_t st;
     hipEvent_t a = nullptr, b = nullptr;
-    ProfScope(nda_ctx *c_, int k, hipStream_t s) : c(c_), kind(k), st(s)
+    ProfScope(nda_ctx *c_, int k, hipStream_t s, bool on = true) : c(c_), kind(k), st(s)
     {
-        if (c->prof) {
+        if (c->prof && on) {
             a = take_event(c);
             b = take_event(c);
             if (a && b)
@@ -570,7 +600,11 @@ bool mfma_decode(const nda_ctx *c, const AttnArgs &a)
            (uint64_t)a.rows * c->cfg.n_kv_heads >= MFMA_DECODE_MIN_ITEMS;
 }
 
-int run_attend(nda_ctx *c, AttnArgs &a, hipStream_t st)
+// part: split-KV partials of at least rows * nh * max_chunks * (v_hd + 2)
+// floats, or null for the context's own buffer (grown on demand). prof: record
+// profiling events (nda_decode_noalloc records none: creating an event may
+// allocate).
+int run_attend(nda_ctx *c, AttnArgs &a, hipStream_t st, float *part = nullptr, bool prof = true)
 {
     if (mfma_decode(c, a)) {
         PrefillArgs pa{};
@@ -586,26 +620,30 @@ int run_attend(nda_ctx *c, AttnArgs &a, hipStream_t st)
         pa.n_items = a.rows * c->cfg.n_kv_heads;
         pa.nh = a.nh;
         pa.qscale = a.qscale;
-        ProfScope ps(c, NDA_K_DECODE, st);
+        ProfScope ps(c, NDA_K_DECODE, st, prof);
         hipError_t e = launch_decode_mfma(c->geo, pa, st);
         if (e != hipSuccess)
             return hip_fail(c, e, "decode (MFMA) kernel launch");
         return NDA_OK;
     }
     if (a.max_chunks > 1) {
-        int rc = ensure_part(c, (size_t)a.rows * a.nh * a.max_chunks * (c->cfg.v_head_dim + 2));
-        if (rc)
-            return rc;
-        a.part = c->d_part;
+        if (part) {
+            a.part = part;
+        } else {
+            int rc = ensure_part(c, (size_t)a.rows * a.nh * a.max_chunks * (c->cfg.v_head_dim + 2));
+            if (rc)
+                return rc;
+            a.part = c->d_part;
+        }
     }
     {
-        ProfScope ps(c, NDA_K_DECODE, st);
+        ProfScope ps(c, NDA_K_DECODE, st, prof);
         hipError_t e = launch_attend(c->geo, a, st);
         if (e != hipSuccess)
             return hip_fail(c, e, "attend kernel launch");
     }
     if (a.max_chunks > 1) {
-        ProfScope ps(c, NDA_K_COMBINE, st);
+        ProfScope ps(c, NDA_K_COMBINE, st, prof);
         hipError_t e = launch_combine(c->geo, a, st);
         if (e != hipSuccess)
             return hip_fail(c, e, "combine kernel launch");
@@ -685,6 +723,11 @@ int nda_create(const nda_config *cfg_in, nda_ctx **out)
         if (hipGetDevice(&dev) == hipSuccess && hipGetDeviceProperties(&prop, dev) == hipSuccess &&
             prop.multiProcessorCount > 0)
             c->cus = prop.multiProcessorCount;
+        // the device's nda_decode_noalloc scratch, with this device current
+        if (hipGetDevice(&dev) != hipSuccess || scratch_address(dev, &c->scratch) != hipSuccess) {
+            delete c;
+            return NDA_ERR_HIP;
+        }
     }
 
     const uint64_t pool_bytes = c->pg.layer_bytes * cfg.n_layers;
@@ -1063,19 +1106,42 @@ int nda_kv_append(nda_ctx *c, uint32_t layer, uint32_t nseq, const uint32_t *ids
 }
 
 // Decode, optionally with the append of this position fused in (k/v set).
-static int decode_impl(nda_ctx *c, uint32_t layer, uint32_t nseq, const uint32_t *ids, const float *q,
-                       const float *k, const float *v, const float *gate, float *out, void *stream)
+// What nda_decode and nda_decode_noalloc check before any launch: arguments,
+// and every visible slot backed (written by an append, a write or an attach;
+// an unbacked one means the caller skipped the append). Returns the longest
+// visible run and the sum over the listed sequences.
+static int decode_check(nda_ctx *c, uint32_t layer, uint32_t nseq, const uint32_t *ids, const float *q,
+                        float *out, uint32_t *max_total, uint64_t *sum_total)
 {
     if (!c || (nseq && (!q || !out)))
         return c ? fail(c, NDA_ERR_ARG, "null q/out") : NDA_ERR_ARG;
-    if (nseq && k && !v)
-        return fail(c, NDA_ERR_ARG, "null v");
     if (layer >= c->cfg.n_layers)
         return fail(c, NDA_ERR_ARG, "layer %u out of range", layer);
     if (int rc = check_ids(c, nseq, ids))
         return rc;
-    hipStream_t st = (hipStream_t)stream;
-    if (k) {
+    *max_total = 0;
+    *sum_total = 0;
+    for (uint32_t b = 0; b < nseq; b++) {
+        const uint32_t qq = sid(ids, b);
+        const SeqHost &s = c->seqs[qq];
+        const Vis vv = visible(s, s.pos, c->cfg.window);
+        *max_total = std::max(*max_total, vv.n_sh + vv.n_own);
+        *sum_total += vv.n_sh + vv.n_own;
+        if (vv.n_own) {
+            const int32_t *row = &c->pages[(size_t)qq * c->pg.pages_per_seq];
+            if (row[(vv.n_own - 1) >> c->pg.log2_page] < 0 || row[0] < 0)
+                return fail(c, NDA_ERR_STATE, "sequence %u: slot of position %u never stored", qq, s.pos);
+        }
+    }
+    return NDA_OK;
+}
+
+static int decode_impl(nda_ctx *c, uint32_t layer, uint32_t nseq, const uint32_t *ids, const float *q,
+                       const float *k, const float *v, const float *gate, float *out, void *stream)
+{
+    if (c && nseq && k && !v)
+        return fail(c, NDA_ERR_ARG, "null v");
+    if (c && k && q && out && layer < c->cfg.n_layers && !check_ids(c, nseq, ids)) {
         for (uint32_t b = 0; b < nseq; b++) {
             const uint32_t qq = sid(ids, b);
             if (int rc = back_positions(c, qq, c->seqs[qq].pos, 1))
@@ -1086,22 +1152,11 @@ static int decode_impl(nda_ctx *c, uint32_t layer, uint32_t nseq, const uint32_t
             s.stored_end = std::max(s.stored_end, s.pos + 1);
         }
     }
-    // Every visible slot must be backed (written by an append, a write or an
-    // attach); an unbacked one means the caller skipped the append.
-    uint32_t max_total = 0;
-    uint64_t sum_total = 0;
-    for (uint32_t b = 0; b < nseq; b++) {
-        const uint32_t qq = sid(ids, b);
-        const SeqHost &s = c->seqs[qq];
-        const Vis vv = visible(s, s.pos, c->cfg.window);
-        max_total = std::max(max_total, vv.n_sh + vv.n_own);
-        sum_total += vv.n_sh + vv.n_own;
-        if (vv.n_own) {
-            const int32_t *row = &c->pages[(size_t)qq * c->pg.pages_per_seq];
-            if (row[(vv.n_own - 1) >> c->pg.log2_page] < 0 || row[0] < 0)
-                return fail(c, NDA_ERR_STATE, "sequence %u: slot of position %u never stored", qq, s.pos);
-        }
-    }
+    uint32_t max_total;
+    uint64_t sum_total;
+    if (int rc = decode_check(c, layer, nseq, ids, q, out, &max_total, &sum_total))
+        return rc;
+    hipStream_t st = (hipStream_t)stream;
     if (int rc = sync_tables(c, st))
         return rc;
     const uint32_t *d_seq, *d_t;
@@ -1119,6 +1174,42 @@ int nda_decode(nda_ctx *c, uint32_t layer, uint32_t nseq, const uint32_t *ids, c
                const float *gate, float *out, void *stream)
 {
     return decode_impl(c, layer, nseq, ids, q, nullptr, nullptr, gate, out, stream);
+}
+
+// nda_decode with its scratch in this device's static array instead of
+// context buffers grown by hipMalloc: the ids are copied to the array's head
+// and the split-KV partials follow at the next 256-byte boundary. Nothing in
+// the array must start at zero: the merge reads only the partials the same
+// call's attend launch writes. No profiling events are recorded.
+int nda_decode_noalloc(nda_ctx *c, uint32_t layer, uint32_t nseq, const uint32_t *ids, const float *q,
+                       const float *gate, float *out, void *stream)
+{
+    uint32_t max_total;
+    uint64_t sum_total;
+    if (int rc = decode_check(c, layer, nseq, ids, q, out, &max_total, &sum_total))
+        return rc;
+    if (!c->scratch)
+        return fail(c, NDA_ERR_STATE, "nda_decode_noalloc: no scratch address for this device");
+    hipStream_t st = (hipStream_t)stream;
+    AttnArgs a = attn_args(c, layer, nseq, q, gate, out, max_total, sum_total);
+    const uint64_t ids_bytes = ids ? (uint64_t)nseq * sizeof(uint32_t) : 0;
+    const uint64_t part_off = (ids_bytes + 255) & ~(uint64_t)255;
+    const bool split = a.max_chunks > 1 && !mfma_decode(c, a);
+    const uint64_t part_bytes =
+        split ? (uint64_t)a.rows * a.nh * a.max_chunks * (c->cfg.v_head_dim + 2) * sizeof(float) : 0;
+    if (part_off + part_bytes > NDA_NOALLOC_SCRATCH_BYTES)
+        return fail(c, NDA_ERR_RANGE,
+                    "nda_decode_noalloc: %u sequence ids and %u-chunk split-KV partials need %llu bytes of "
+                    "scratch, more than its %u",
+                    ids ? nseq : 0u, a.max_chunks, (unsigned long long)(part_off + part_bytes),
+                    (unsigned)NDA_NOALLOC_SCRATCH_BYTES);
+    if (int rc = sync_tables(c, st))
+        return rc;
+    if (ids) {
+        HIPC(c, hipMemcpyAsync(c->scratch, ids, ids_bytes, hipMemcpyHostToDevice, st));
+        a.row_seq = reinterpret_cast<const uint32_t *>(c->scratch);
+    }
+    return run_attend(c, a, st, split ? reinterpret_cast<float *>(c->scratch + part_off) : nullptr, false);
 }
 
 // Store, then attend. Small batches (launch latency dominates, e.g. one

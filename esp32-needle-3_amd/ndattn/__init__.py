@@ -30,7 +30,7 @@ ABI_SYMBOLS = [
     "nda_seq_reset", "nda_seq_set_sink", "nda_seq_state", "nda_seq_set_pos",
     "nda_seq_reserve", "nda_advance",
     "nda_prefix_build", "nda_seq_attach", "nda_seq_rewind", "nda_prefix_free",
-    "nda_kv_append", "nda_decode", "nda_step", "nda_prefill", "nda_sync",
+    "nda_kv_append", "nda_decode", "nda_decode_noalloc", "nda_step", "nda_prefill", "nda_sync",
     "nda_kv_read", "nda_kv_write", "nda_kv_fill_normal",
     "nda_dev_alloc", "nda_dev_free", "nda_h2d", "nda_d2h", "nda_d2d", "nda_memset", "nda_fill_normal",
     "nda_host_alloc", "nda_host_free", "nda_h2d_async", "nda_d2h_async",
@@ -98,6 +98,7 @@ def lib():
             "nda_prefix_free": (C.c_int, [vp, i32]),
             "nda_kv_append": (C.c_int, [vp, u32, u32, vp, vp, vp, vp]),
             "nda_decode": (C.c_int, [vp, u32, u32, vp, vp, vp, vp, vp]),
+            "nda_decode_noalloc": (C.c_int, [vp, u32, u32, vp, vp, vp, vp, vp]),
             "nda_step": (C.c_int, [vp, u32, u32, vp, vp, vp, vp, vp, vp, vp]),
             "nda_prefill": (C.c_int, [vp, u32, u32, vp, vp, vp, vp, vp, vp, vp, vp]),
             "nda_sync": (C.c_int, [vp, vp]),
@@ -358,6 +359,11 @@ class Context:
     def decode(self, layer, nseq, q, out, gate=None, seq_ids=None, stream=None):
         keep, p = _ids(seq_ids)
         self._c(lib().nda_decode(self.h, layer, nseq, p, _dp(q), _dp(gate), _dp(out), stream))
+
+    def decode_noalloc(self, layer, nseq, q, out, gate=None, seq_ids=None, stream=None):
+        """nda_decode_noalloc: nda_decode with its scratch in the GPU's static array."""
+        keep, p = _ids(seq_ids)
+        self._c(lib().nda_decode_noalloc(self.h, layer, nseq, p, _dp(q), _dp(gate), _dp(out), stream))
 
     def step(self, layer, nseq, q, k, v, out, gate=None, seq_ids=None, stream=None):
         keep, p = _ids(seq_ids)

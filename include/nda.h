@@ -141,6 +141,24 @@ int nda_kv_append(nda_ctx *ctx, uint32_t layer, uint32_t nseq, const uint32_t *s
 int nda_decode(nda_ctx *ctx, uint32_t layer, uint32_t nseq, const uint32_t *seq_ids,
                const float *q, const float *gate, float *out, void *stream);
 
+/* Bytes of the per-GPU scratch array nda_decode_noalloc works in. */
+#define NDA_NOALLOC_SCRATCH_BYTES (16u << 20)
+
+/* nda_decode that allocates nothing: no counterpart in the reference. For
+ * callers that must not allocate device memory (tight serving loops,
+ * harnesses that forbid hipMalloc). Same arguments, kernels and results as
+ * nda_decode; the sequence ids and the split-KV partials (long rows cut into
+ * chunks merged by log-sum-exp) live in one static device array of
+ * NDA_NOALLOC_SCRATCH_BYTES per GPU, held until the process ends, instead of
+ * context buffers grown by hipMalloc. A call whose ids (4 bytes each, after
+ * 256-byte alignment) plus partials (rows * n_heads * chunks * (v_head_dim +
+ * 2) floats) exceed it returns NDA_ERR_RANGE and changes nothing. Every call
+ * on one GPU shares that GPU's array: calls that overlap on one GPU (other
+ * streams, other contexts, other host threads) race. Records no profiling
+ * events. */
+int nda_decode_noalloc(nda_ctx *ctx, uint32_t layer, uint32_t nseq, const uint32_t *seq_ids,
+                       const float *q, const float *gate, float *out, void *stream);
+
 /* nda_kv_append + nda_decode, in the order attention() runs them (store
  * first; the current token is attended). Small batches run it as one fused
  * launch, large ones as the two kernels; the results are the same. */
