@@ -108,7 +108,7 @@ def test_block_batched(kv_dtype):
         orc.append(o)
     rng = np.random.default_rng(3)
     bx, bo = N.DevBuf(B * dm * 4), N.DevBuf(B * dm * 4)
-    worst, flips, codes = 0.0, 0, 0
+    worst, flips, codes, sc_rel = 0.0, 0, 0, 0.0
     for step in range(40):
         ids = [b for b in range(B) if step >= 3 * b]       # sequences join at different steps
         n = len(ids)
@@ -134,18 +134,24 @@ def test_block_batched(kv_dtype):
             for j, p in enumerate(range(max(0, pos - W + 1), pos)):
                 sl = O.lib().ndo_kv_slot(W, 0, p)
                 if kv_dtype == O.KV_INT8:
-                    d = np.abs(k[j].astype(np.int32) - ok[li, sl].astype(np.int32))
-                    assert d.max() <= 1
-                    flips += int((d != 0).sum())
-                    codes += d.size
+                    for got_c, want_c in ((k[j], ok[li, sl]), (v[j], ov[li, sl])):
+                        d = np.abs(got_c.astype(np.int32) - want_c.astype(np.int32))
+                        assert d.max() <= 1, (b, li, p)
+                        flips += int((d != 0).sum())
+                        codes += d.size
+                    # scales: absmax / 127 of rows equal up to the projections' reassociation
+                    for got_s, want_s in ((ks[j], oks[li, sl]), (vs[j], ovs[li, sl])):
+                        rel = np.abs(got_s.astype(np.float64) - want_s) / np.abs(want_s.astype(np.float64))
+                        sc_rel = max(sc_rel, float(rel.max()))
                 else:   # fp16 rows: values within the projections' reassociation
                     for got_r, want_r in ((k[j], ok[li, sl]), (v[j], ov[li, sl])):
                         gv = got_r.view(np.float16).astype(np.float64)
                         wv = want_r.view(np.float16).astype(np.float64)
                         assert np.all(np.abs(gv - wv) <= 2e-3 * np.maximum(1.0, np.abs(wv))), (b, li, p)
-    say("block batched worst (relative)", worst, "code flips", flips, "of", codes)
+    say("block batched worst (relative)", worst, "code flips", flips, "of", codes, "scale rel", sc_rel)
     assert worst <= TOL, worst
     assert flips <= max(1, codes // 1000), (flips, codes)
+    assert sc_rel <= 1e-5, sc_rel
     for layer in cqs:
         for c in layer:
             c.close()
