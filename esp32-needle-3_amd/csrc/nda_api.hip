@@ -699,6 +699,8 @@ int nda_create(const nda_config *cfg_in, nda_ctx **out)
     c->pg.page_bytes = c->pg.head_bytes * cfg.n_kv_heads;
     c->pg.window = cfg.window;
     c->pg.nkv = cfg.n_kv_heads;
+    c->pg.dk = cfg.qk_head_dim;
+    c->pg.dv = cfg.v_head_dim;
     c->max_pages = cfg.max_pages ? cfg.max_pages
                                  : (uint64_t)(cfg.max_seqs + cfg.max_prefixes) * c->pg.pages_per_seq;
     if (c->max_pages > (uint64_t)INT32_MAX) {
@@ -1318,7 +1320,9 @@ int nda_prefill(nda_ctx *c, uint32_t layer, uint32_t nseq, const uint32_t *ids, 
         if (e != hipSuccess)
             return hip_fail(c, e, "append kernel launch");
     }
-    if (c->cfg.flags & NDA_FLAG_PREFILL_VALU) {
+    // The VALU kernel serves shapes the MFMA tiles are not built for (and
+    // every shape when the config asks for it).
+    if ((c->cfg.flags & NDA_FLAG_PREFILL_VALU) || !prefill_mfma_supported(c->geo)) {
         AttnArgs a = attn_args(c, layer, (uint32_t)rows, q, gate, out, max_total, sum_total);
         a.row_seq = d_seq;
         a.row_t = d_t;
@@ -1395,6 +1399,11 @@ int nda_front_init(nda_ctx *c, const nda_front_config *fc)
         return fail(c, NDA_ERR_STATE, "attention front already initialised");
     if (fc->taps < 1 || fc->taps > 8)
         return fail(c, NDA_ERR_ARG, "taps %u outside 1..8", fc->taps);
+    if (!geometry_fast(c->geo))
+        return fail(c, NDA_ERR_UNSUPPORTED,
+                    "attention front: no kernel for qk %d / v %d / rep %d (the front is built for 64/64 with rep "
+                    "1, 2, 4, 6, 8 and 48/64 with rep 1, 2, 6)",
+                    c->geo.dk, c->geo.dv, c->geo.rep);
     if (!(fc->rope_theta > 0.0f))
         return fail(c, NDA_ERR_ARG, "rope_theta must be positive");
     const nda_config &g = c->cfg;

@@ -73,27 +73,28 @@ __device__ __forceinline__ int8_t quant_code(float x, float scale, float r)
 }
 
 // Store one row of K and V (lane = element) for slot `off` of a page's
-// kv-head block at hb. Shared by the append kernel and the fused append of
-// the decode kernel.
-template <int ES, int DK, int DV>
-__device__ __forceinline__ void store_row(uint8_t *hb, int off, int P, float kx, float vx, int lane)
+// kv-head block at hb, whose rows are dk and dv elements long. Shared by the
+// append kernel, the fused append of the decode kernel and the front.
+template <int ES>
+__device__ __forceinline__ void store_row(uint8_t *hb, int off, int P, float kx, float vx, int lane, int dk,
+                                          int dv)
 {
     if constexpr (ES == 2) {
-        if (lane < DK)
-            reinterpret_cast<_Float16 *>(hb + (uint64_t)off * DK * 2)[lane] = (_Float16)kx;
-        if (lane < DV)
-            reinterpret_cast<_Float16 *>(hb + (uint64_t)P * DK * 2 + (uint64_t)off * DV * 2)[lane] = (_Float16)vx;
+        if (lane < dk)
+            reinterpret_cast<_Float16 *>(hb + (uint64_t)off * dk * 2)[lane] = (_Float16)kx;
+        if (lane < dv)
+            reinterpret_cast<_Float16 *>(hb + (uint64_t)P * dk * 2 + (uint64_t)off * dv * 2)[lane] = (_Float16)vx;
     } else {
         const float ak = wave_max(fabsf(kx)), av = wave_max(fabsf(vx));
         const float sk = ak > 0.0f ? __fdiv_rn(ak, 127.0f) : 1.0f;
         const float sv = av > 0.0f ? __fdiv_rn(av, 127.0f) : 1.0f;
         const float rk = __fdiv_rn(1.0f, sk), rv = __fdiv_rn(1.0f, sv);
-        if (lane < DK)
-            reinterpret_cast<int8_t *>(hb + (uint64_t)off * DK)[lane] = quant_code(kx, sk, rk);
-        if (lane < DV)
-            reinterpret_cast<int8_t *>(hb + (uint64_t)P * DK + (uint64_t)off * DV)[lane] = quant_code(vx, sv, rv);
+        if (lane < dk)
+            reinterpret_cast<int8_t *>(hb + (uint64_t)off * dk)[lane] = quant_code(kx, sk, rk);
+        if (lane < dv)
+            reinterpret_cast<int8_t *>(hb + (uint64_t)P * dk + (uint64_t)off * dv)[lane] = quant_code(vx, sv, rv);
         if (lane == 0) {
-            float *sc = reinterpret_cast<float *>(hb + (uint64_t)P * (DK + DV));
+            float *sc = reinterpret_cast<float *>(hb + (uint64_t)P * (dk + dv));
             sc[off] = sk;
             sc[P + off] = sv;
         }

@@ -184,7 +184,7 @@ __global__ __launch_bounds__((64 * FrontShape<DK, DV, REP>::W)) void front_kerne
     uint8_t *hb = a.pool + (uint64_t)page * a.pg.page_bytes + (uint64_t)g * a.pg.head_bytes;
     const float kx = tid < DK ? ylds[REP * S::STRIDE + tid] : 0.0f;
     const float vx = tid < DV ? vlds[tid] : 0.0f;
-    store_row<ES, DK, DV>(hb, slot & (P - 1), P, kx, vx, tid);
+    store_row<ES>(hb, slot & (P - 1), P, kx, vx, tid, DK, DV);
 }
 
 // Raw rows of each sequence's last `taps` tokens into their history slots,

@@ -31,6 +31,7 @@ struct PageGeom {
     uint64_t layer_bytes;   /* page_bytes * max_pages */
     uint32_t window;
     uint32_t nkv;
+    uint32_t dk, dv;        /* qk_head_dim, v_head_dim */
 };
 
 /* One launch of the decode / causal kernel. A "row" is one query token of
@@ -237,7 +238,11 @@ hipError_t launch_cq_prepare_split(const CqPrepSplitArgs &a, hipStream_t s);
 hipError_t launch_cq_gemm_split(const CqSplitArgs &a, hipStream_t s);
 hipError_t launch_cq_split_tables(const CqTabArgs &a, hipStream_t s);
 
-/* Compiled geometries: (KV element bytes, qk_head_dim, v_head_dim, GQA rep). */
+/* Geometries with kernels specialised for their head dims (KV element bytes,
+ * qk_head_dim, v_head_dim, GQA rep): the engine's archive shape and the MHA
+ * 8 x 64 shape. Every other shape the engine accepts (head dims multiples of 4
+ * up to 64, rep 1-8) runs on the same kernels instantiated for dims padded to
+ * 64, with the true dims read at run time. */
 #define NDA_FOR_GEOMETRIES(X) \
     X(2, 64, 64, 1) X(2, 64, 64, 2) X(2, 64, 64, 4) X(2, 64, 64, 6) X(2, 64, 64, 8) \
     X(2, 48, 64, 1) X(2, 48, 64, 2) X(2, 48, 64, 6) \
@@ -267,7 +272,9 @@ hipError_t launch_fill_kv(const Geo &g, const FillKvArgs &a, hipStream_t s);
 hipError_t launch_advance(SeqDev *seqs, const uint32_t *seq_list, uint32_t nseq, uint32_t n, hipStream_t s);
 hipError_t launch_fill_normal(void *dst, uint64_t n, int dtype, uint64_t seed, float scale,
                               hipStream_t s);
-bool geometry_supported(const Geo &g);
+bool geometry_supported(const Geo &g);   /* any shape the engine accepts */
+bool geometry_fast(const Geo &g);        /* one of NDA_FOR_GEOMETRIES */
+bool prefill_mfma_supported(const Geo &g);
 
 /* nda_front.hip */
 hipError_t launch_front(const Geo &g, const FrontArgs &a, hipStream_t s);

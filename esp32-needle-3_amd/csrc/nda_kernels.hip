@@ -89,6 +89,16 @@ __device__ __forceinline__ void load_words(Words<NB> &d, const uint8_t *p)
     }
 }
 
+// The first nb bytes of a slice (whole dwords; nb may be <= 0), the rest zero:
+// a lane's part of a row whose true length is shorter than the padded one.
+template <int NB>
+__device__ __forceinline__ void load_words_upto(Words<NB> &d, const uint8_t *p, int nb)
+{
+#pragma unroll
+    for (int i = 0; i < NB / 4; i++)
+        d.w[i] = 4 * i < nb ? __builtin_nontemporal_load(reinterpret_cast<const uint32_t *>(p) + i) : 0u;
+}
+
 // Element e of a loaded slice as float: int8 code or fp16 value.
 template <int ES>
 __device__ __forceinline__ float elem(const uint32_t *w, int e)
@@ -123,13 +133,17 @@ struct AttnState {
 };
 
 // One wave step over positions blk0 + j*PW + grp, j < NP, of a page list.
-template <bool MASK, int ES, int DK, int DV, int REP, int G, int NP, int NW>
+// RT: the rows are a.pg.dk / a.pg.dv elements long (multiples of 4, at most
+// DK / DV, the padded register layout); lanes load only their part of the
+// true row, and the padding reads as zero.
+template <bool MASK, bool RT, int ES, int DK, int DV, int REP, int G, int NP, int NW>
 __device__ __forceinline__ void attn_step(AttnState<ES, DK, DV, REP, G, NP, NW> &st,
                                           const AttnArgs &a, const int32_t *pages, uint32_t g,
                                           int blk0, int s0, int s1, int grp, int li)
 {
     using C = AttnCfg<ES, DK, DV, REP, G, NP, NW>;
     const int P = 1 << a.pg.log2_page;
+    const int dk = RT ? (int)a.pg.dk : DK, dv = RT ? (int)a.pg.dv : DV;
     Words<C::KB> kw[NP];
     Words<C::VB> vw[NP];
     float ks[NP], vs[NP];
@@ -147,10 +161,17 @@ __device__ __forceinline__ void attn_step(AttnState<ES, DK, DV, REP, G, NP, NW> 
         if (page >= 0) {
             const uint8_t *hb = a.pool + (uint64_t)page * a.pg.page_bytes + (uint64_t)g * a.pg.head_bytes;
             const int off = s & (P - 1);
-            load_words<C::KB>(kw[j], hb + (uint64_t)off * DK * ES + li * C::KB);
-            load_words<C::VB>(vw[j], hb + (uint64_t)P * DK * ES + (uint64_t)off * DV * ES + li * C::VB);
+            const uint8_t *kp = hb + (uint64_t)off * dk * ES + li * C::KB;
+            const uint8_t *vp = hb + (uint64_t)P * dk * ES + (uint64_t)off * dv * ES + li * C::VB;
+            if constexpr (RT) {
+                load_words_upto<C::KB>(kw[j], kp, dk * ES - li * C::KB);
+                load_words_upto<C::VB>(vw[j], vp, dv * ES - li * C::VB);
+            } else {
+                load_words<C::KB>(kw[j], kp);
+                load_words<C::VB>(vw[j], vp);
+            }
             if constexpr (ES == 1) {
-                const float *sc = reinterpret_cast<const float *>(hb + (uint64_t)P * (DK + DV));
+                const float *sc = reinterpret_cast<const float *>(hb + (uint64_t)P * (dk + dv));
                 ks[j] = sc[off];
                 vs[j] = sc[P + off];
             } else {
@@ -230,7 +251,7 @@ __device__ __forceinline__ void attn_step(AttnState<ES, DK, DV, REP, G, NP, NW> 
     }
 }
 
-template <int ES, int DK, int DV, int REP, int G, int NP, int NW>
+template <bool RT, int ES, int DK, int DV, int REP, int G, int NP, int NW>
 __device__ __forceinline__ void attn_run(AttnState<ES, DK, DV, REP, G, NP, NW> &st, const AttnArgs &a,
                                          const int32_t *pages, uint32_t g, int s0, int s1, int wave,
                                          int grp, int li)
@@ -240,9 +261,9 @@ __device__ __forceinline__ void attn_run(AttnState<ES, DK, DV, REP, G, NP, NW> &
     const int start = (s0 / C::PW) * C::PW;
     for (int it = start + wave * BLK; it < s1; it += NW * BLK) {
         if (it >= s0 && it + BLK <= s1)
-            attn_step<false>(st, a, pages, g, it, s0, s1, grp, li);
+            attn_step<false, RT>(st, a, pages, g, it, s0, s1, grp, li);
         else
-            attn_step<true>(st, a, pages, g, it, s0, s1, grp, li);
+            attn_step<true, RT>(st, a, pages, g, it, s0, s1, grp, li);
     }
 }
 
@@ -262,10 +283,12 @@ __device__ __forceinline__ void merge_state(float &m, float &l, float *acc, int 
 // that split the kv-head's query heads between them (REP each, REP * HS in
 // the group): each reads the kv-head's K/V, so the per-lane state of a wide
 // GQA group (heads x head dim) divides by HS and more units fit a CU.
-template <int ES, int DK, int DV, int REP, int G, int NP, int NW, int HS>
+// RT: head dims read at run time (a.pg.dk, a.pg.dv), DK / DV the padding.
+template <int ES, int DK, int DV, int REP, int G, int NP, int NW, int HS, bool RT>
 __global__ __launch_bounds__(64 * NW) void attend_kernel(AttnArgs a)
 {
     using C = AttnCfg<ES, DK, DV, REP, G, NP, NW>;
+    const int dk = RT ? (int)a.pg.dk : DK, dv = RT ? (int)a.pg.dv : DV;
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int grp = lane / G, li = lane % G;
     const uint32_t nkv = a.pg.nkv;
@@ -297,9 +320,9 @@ __global__ __launch_bounds__(64 * NW) void attend_kernel(AttnArgs a)
                     const int P = 1 << a.pg.log2_page;
                     uint8_t *hb = const_cast<uint8_t *>(a.pool) + (uint64_t)page * a.pg.page_bytes +
                                   (uint64_t)g * a.pg.head_bytes;
-                    const float kx = lane < DK ? a.k_new[((uint64_t)row * nkv + g) * DK + lane] : 0.0f;
-                    const float vx = lane < DV ? a.v_new[((uint64_t)row * nkv + g) * DV + lane] : 0.0f;
-                    store_row<ES, DK, DV>(hb, nslot & (P - 1), P, kx, vx, lane);
+                    const float kx = lane < dk ? a.k_new[((uint64_t)row * nkv + g) * dk + lane] : 0.0f;
+                    const float vx = lane < dv ? a.v_new[((uint64_t)row * nkv + g) * dv + lane] : 0.0f;
+                    store_row<ES>(hb, nslot & (P - 1), P, kx, vx, lane, dk, dv);
                 }
             }
             // Workgroup-scope release/acquire + barrier: all waves of the group
@@ -312,10 +335,10 @@ __global__ __launch_bounds__(64 * NW) void attend_kernel(AttnArgs a)
     AttnState<ES, DK, DV, REP, G, NP, NW> st;
 #pragma unroll
     for (int t = 0; t < REP; t++) {
-        const float *qh = a.q + ((uint64_t)row * a.nh + gv * REP + t) * DK + li * C::EK;
+        const float *qh = a.q + ((uint64_t)row * a.nh + gv * REP + t) * dk + li * C::EK;
 #pragma unroll
         for (int e = 0; e < C::EK; e++)
-            st.qr[t][e] = qh[e] * a.qscale;
+            st.qr[t][e] = (!RT || li * C::EK + e < dk) ? qh[e] * a.qscale : 0.0f;
         st.m[t] = -FLT_MAX;
         st.l[t] = 0.0f;
 #pragma unroll
@@ -324,11 +347,11 @@ __global__ __launch_bounds__(64 * NW) void attend_kernel(AttnArgs a)
     }
 
     if (c0 < vis.n_sh)
-        attn_run(st, a, a.prefix_pages + (uint64_t)sd.prefix * a.pg.pages_per_seq, g, c0,
-                 min(c1, vis.n_sh), wave, grp, li);
+        attn_run<RT>(st, a, a.prefix_pages + (uint64_t)sd.prefix * a.pg.pages_per_seq, g, c0,
+                     min(c1, vis.n_sh), wave, grp, li);
     if (c1 > vis.n_sh)
-        attn_run(st, a, a.page_table + (uint64_t)seq * a.pg.pages_per_seq, g,
-                 max(c0, vis.n_sh) - vis.n_sh, c1 - vis.n_sh, wave, grp, li);
+        attn_run<RT>(st, a, a.page_table + (uint64_t)seq * a.pg.pages_per_seq, g,
+                     max(c0, vis.n_sh) - vis.n_sh, c1 - vis.n_sh, wave, grp, li);
 
     // Merge the lane groups of this wave: lanes li, li+G, li+2G, ...
 #pragma unroll
@@ -381,32 +404,35 @@ __global__ __launch_bounds__(64 * NW) void attend_kernel(AttnArgs a)
         const uint32_t h = gv * REP + t;
         if (nchunks == 1) {
             const float inv = 1.0f / st.l[t];
-            float *o = a.out + ((uint64_t)row * a.nh + h) * DV + li * C::EV;
-            const float *gt = a.gate ? a.gate + ((uint64_t)row * a.nh + h) * DV + li * C::EV : nullptr;
+            float *o = a.out + ((uint64_t)row * a.nh + h) * dv + li * C::EV;
+            const float *gt = a.gate ? a.gate + ((uint64_t)row * a.nh + h) * dv + li * C::EV : nullptr;
 #pragma unroll
             for (int e = 0; e < C::EV; e++) {
-                float z = st.acc[t][e] * inv;
-                if (gt)
-                    z *= sigmoid_dev(gt[e]);
-                o[e] = z;
+                if (!RT || li * C::EV + e < dv) {
+                    float z = st.acc[t][e] * inv;
+                    if (gt)
+                        z *= sigmoid_dev(gt[e]);
+                    o[e] = z;
+                }
             }
         } else {
-            float *r = a.part + (((uint64_t)row * a.nh + h) * a.max_chunks + chunk) * (DV + 2);
+            float *r = a.part + (((uint64_t)row * a.nh + h) * a.max_chunks + chunk) * (dv + 2);
 #pragma unroll
             for (int e = 0; e < C::EV; e++)
-                r[li * C::EV + e] = st.acc[t][e];
+                if (!RT || li * C::EV + e < dv)
+                    r[li * C::EV + e] = st.acc[t][e];
             if (li == 0) {
-                r[DV] = st.m[t];
-                r[DV + 1] = st.l[t];
+                r[dv] = st.m[t];
+                r[dv + 1] = st.l[t];
             }
         }
     }
 }
 
-// Split-KV merge: one wave per (row, head), lane = output element.
-template <int DV>
+// Split-KV merge: one wave per (row, head), lane = output element (dv <= 64).
 __global__ __launch_bounds__(256) void combine_kernel(AttnArgs a)
 {
+    const int DV = (int)a.pg.dv;
     const int lane = threadIdx.x & 63;
     const uint64_t wid = (uint64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
     if (wid >= (uint64_t)a.rows * a.nh)
@@ -441,10 +467,11 @@ __global__ __launch_bounds__(256) void combine_kernel(AttnArgs a)
 
 // ------------------------------------------------------------- KV append
 
-template <int ES, int DK, int DV>
+// One wave per (row, kv-head), lane = element (head dims <= 64).
+template <int ES>
 __global__ __launch_bounds__(256) void append_kernel(AppendArgs a)
 {
-    static_assert(DK <= 64 && DV <= 64, "one lane per element");
+    const int DK = (int)a.pg.dk, DV = (int)a.pg.dv;
     const int lane = threadIdx.x & 63;
     const uint64_t unit = (uint64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
     const uint32_t nkv = a.pg.nkv;
@@ -464,15 +491,15 @@ __global__ __launch_bounds__(256) void append_kernel(AppendArgs a)
 
     const float kx = lane < DK ? a.k[((uint64_t)row * nkv + g) * DK + lane] : 0.0f;
     const float vx = lane < DV ? a.v[((uint64_t)row * nkv + g) * DV + lane] : 0.0f;
-    store_row<ES, DK, DV>(hb, off, P, kx, vx, lane);
+    store_row<ES>(hb, off, P, kx, vx, lane, DK, DV);
 }
 
 // ------------------------------------------------------ copies and staging
 
 // Bytes of one slot of one kv-head: K row, V row (+ the two scales).
-template <int ES, int DK, int DV>
+template <int ES>
 __device__ __forceinline__ void copy_slot(uint8_t *dhb, int doff, const uint8_t *shb, int soff, int P,
-                                          int tid, int nthr)
+                                          int tid, int nthr, int DK, int DV)
 {
     const uint32_t *sk = reinterpret_cast<const uint32_t *>(shb + (uint64_t)soff * DK * ES);
     uint32_t *dk = reinterpret_cast<uint32_t *>(dhb + (uint64_t)doff * DK * ES);
@@ -491,7 +518,7 @@ __device__ __forceinline__ void copy_slot(uint8_t *dhb, int doff, const uint8_t 
 }
 
 // grid (count, n_layers), one block per (slot, layer), heads in a loop.
-template <int ES, int DK, int DV>
+template <int ES>
 __global__ __launch_bounds__(64) void copy_kernel(CopyArgs a)
 {
     const uint32_t i = blockIdx.x, l = blockIdx.y;
@@ -505,14 +532,15 @@ __global__ __launch_bounds__(64) void copy_kernel(CopyArgs a)
     const uint8_t *sp = a.pool + l * a.pg.layer_bytes + (uint64_t)spg * a.pg.page_bytes;
     uint8_t *dp = a.pool + l * a.pg.layer_bytes + (uint64_t)dpg * a.pg.page_bytes;
     for (uint32_t g = 0; g < a.pg.nkv; g++)
-        copy_slot<ES, DK, DV>(dp + g * a.pg.head_bytes, ds & (P - 1), sp + g * a.pg.head_bytes,
-                              ss & (P - 1), P, threadIdx.x, blockDim.x);
+        copy_slot<ES>(dp + g * a.pg.head_bytes, ds & (P - 1), sp + g * a.pg.head_bytes, ss & (P - 1), P,
+                      threadIdx.x, blockDim.x, (int)a.pg.dk, (int)a.pg.dv);
 }
 
 // One block per staged position: pool <-> [count][nkv][d] staging.
-template <int ES, int DK, int DV, bool SCATTER>
+template <int ES, bool SCATTER>
 __global__ __launch_bounds__(64) void stage_kernel(StageArgs a)
 {
+    const int DK = (int)a.pg.dk, DV = (int)a.pg.dv;
     const uint32_t i = blockIdx.x;
     if (i >= a.count)
         return;
@@ -601,9 +629,10 @@ __global__ __launch_bounds__(256) void fill_normal_kernel(void *dst, uint64_t n,
 // (layer, seq, slot, head, element) depends on those indices only. ES 1:
 // int8 codes round(32 x) clamped to +-127 with scales 1/32, so the
 // dequantised values are N(0,1) to within the code step.
-template <int ES, int DK, int DV>
+template <int ES>
 __global__ __launch_bounds__(256) void fill_kv_kernel(FillKvArgs a)
 {
+    const uint32_t DK = a.pg.dk, DV = a.pg.dv;
     const uint32_t bi = blockIdx.x, l = blockIdx.y;
     if (bi >= a.nseq || l >= a.n_layers)
         return;
@@ -692,7 +721,7 @@ constexpr int att_np()
 
 static inline int es_of(const Geo &g) { return g.kv_f16 ? 2 : 1; }
 
-bool geometry_supported(const Geo &g)
+bool geometry_fast(const Geo &g)
 {
 #define X(ES, DK, DV, REP) if (es_of(g) == ES && g.dk == DK && g.dv == DV && g.rep == REP) return true;
     NDA_FOR_GEOMETRIES(X)
@@ -700,10 +729,21 @@ bool geometry_supported(const Geo &g)
     return false;
 }
 
+// The shapes the engine's attn_heads defines (engine/include/nd_model.h:244-245,
+// engine/src/nd_model.c:2118-2139): head dims up to ND_KV_HD_CAP (64) and up
+// to ND_KV_REP_CAP (8) query heads per kv-head. Its staging converts whole
+// 4-byte words of codes (kv_stage_pair, :79-94) and its P.V loops step four
+// elements, so only head dims that are multiples of 4 are well defined there.
+bool geometry_supported(const Geo &g)
+{
+    return g.dk >= 4 && g.dk <= 64 && g.dk % 4 == 0 && g.dv >= 4 && g.dv <= 64 && g.dv % 4 == 0 &&
+           g.rep >= 1 && g.rep <= 8;
+}
+
 static inline unsigned blocks_for(uint64_t waves) { return (unsigned)((waves + 3) / 4); }
 
-// Query heads per work-group for a GQA group of REP: the widest groups
-// (rep >= 6) split in two, except when the launch also stores the new row
+// Query heads per work-group for a GQA group of REP: the widest even groups
+// (rep 6, 8) split in two, except when the launch also stores the new row
 // (one work-group per kv-head must own that store).
 template <int REP>
 constexpr int att_hs()
@@ -711,46 +751,63 @@ constexpr int att_hs()
 #ifdef NDA_ATT_HS
     return REP % NDA_ATT_HS == 0 ? NDA_ATT_HS : 1;
 #else
-    return REP >= 6 ? 2 : 1;
+    return REP >= 6 && REP % 2 == 0 ? 2 : 1;
 #endif
 }
 
-int attend_split(const Geo &g, const AttnArgs &a)
-{
-    if (a.k_new)
-        return 1;
-#define X(ES, DK, DV, REP) if (es_of(g) == ES && g.dk == DK && g.dv == DV && g.rep == REP) return att_hs<REP>();
-    NDA_FOR_GEOMETRIES(X)
-#undef X
-    return 1;
-}
+// Lanes per position of the padded (run-time dims) instances: 8, so a lane
+// holds 8 elements of K and of V (16-byte fp16 or 8-byte int8 slices).
+template <int ES, int REP>
+constexpr int lanes_rt() { return 8; }
 
-template <int ES, int DK, int DV, int REP, int HS, int NW>
+template <int ES, int DK, int DV, int REP, int HS, int NW, bool RT>
 static void launch_attend_hs(const AttnArgs &a, hipStream_t s)
 {
     constexpr int R = REP / HS;
+    constexpr int G = RT ? lanes_rt<ES, R>() : lanes_per_pos<ES, DK, R>();
     const dim3 grid(a.rows * a.pg.nkv * HS, a.max_chunks);
-    hipLaunchKernelGGL((attend_kernel<ES, DK, DV, R, lanes_per_pos<ES, DK, R>(), att_np<ES, R>(), NW, HS>), grid,
-                       dim3(64 * NW), 0, s, a);
+    hipLaunchKernelGGL((attend_kernel<ES, DK, DV, R, G, att_np<ES, R>(), NW, HS, RT>), grid, dim3(64 * NW), 0, s,
+                       a);
 }
+
+template <int ES, int DK, int DV, int REP, bool RT>
+static void launch_attend_geo(const AttnArgs &a, bool long_items, hipStream_t s)
+{
+    if (att_hs<REP>() > 1 && !a.k_new)
+        launch_attend_hs<ES, DK, DV, REP, att_hs<REP>(), 1, RT>(a, s);
+    else if (long_items)
+        launch_attend_hs<ES, DK, DV, REP, 1, att_nw<REP>(true), RT>(a, s);
+    else
+        launch_attend_hs<ES, DK, DV, REP, 1, att_nw<REP>(false), RT>(a, s);
+}
+
+// Shapes outside NDA_FOR_GEOMETRIES: dims padded to 64, one instance per
+// (element size, rep).
+#define NDA_RT_REPS(X) X(1) X(2) X(3) X(4) X(5) X(6) X(7) X(8)
 
 hipError_t launch_attend(const Geo &g, const AttnArgs &a, hipStream_t s)
 {
     if (a.rows == 0)
         return hipSuccess;
-    const int hs = attend_split(g, a);
+    if (!geometry_supported(g) || (int)a.pg.dk != g.dk || (int)a.pg.dv != g.dv)
+        return hipErrorNotSupported;
     const bool long_items = (a.avg_len < a.chunk ? a.avg_len : a.chunk) >= ATT_LONG_ITEM;
 #define X(ES, DK, DV, REP)                                                                      \
     if (es_of(g) == ES && g.dk == DK && g.dv == DV && g.rep == REP) {                          \
-        if (hs > 1)                                                                             \
-            launch_attend_hs<ES, DK, DV, REP, att_hs<REP>(), 1>(a, s);                          \
-        else if (long_items)                                                                    \
-            launch_attend_hs<ES, DK, DV, REP, 1, att_nw<REP>(true)>(a, s);                      \
-        else                                                                                    \
-            launch_attend_hs<ES, DK, DV, REP, 1, att_nw<REP>(false)>(a, s);                     \
+        launch_attend_geo<ES, DK, DV, REP, false>(a, long_items, s);                            \
         return hipGetLastError();                                                               \
     }
     NDA_FOR_GEOMETRIES(X)
+#undef X
+#define X(REP)                                                                                  \
+    if (g.rep == REP) {                                                                         \
+        if (g.kv_f16)                                                                           \
+            launch_attend_geo<2, 64, 64, REP, true>(a, long_items, s);                          \
+        else                                                                                    \
+            launch_attend_geo<1, 64, 64, REP, true>(a, long_items, s);                          \
+        return hipGetLastError();                                                               \
+    }
+    NDA_RT_REPS(X)
 #undef X
     return hipErrorNotSupported;
 }
@@ -759,58 +816,53 @@ hipError_t launch_combine(const Geo &g, const AttnArgs &a, hipStream_t s)
 {
     if (a.rows == 0 || a.max_chunks <= 1)
         return hipSuccess;
-    if (g.dv != 64)
+    if (g.dv > 64)
         return hipErrorNotSupported;
-    hipLaunchKernelGGL(combine_kernel<64>, dim3(blocks_for((uint64_t)a.rows * a.nh)), dim3(256), 0, s, a);
+    hipLaunchKernelGGL(combine_kernel, dim3(blocks_for((uint64_t)a.rows * a.nh)), dim3(256), 0, s, a);
     return hipGetLastError();
 }
-
-#define NDA_FOR_SHAPES(X) X(2, 64, 64) X(2, 48, 64) X(1, 64, 64) X(1, 48, 64)
 
 hipError_t launch_append(const Geo &g, const AppendArgs &a, hipStream_t s)
 {
     if (a.rows == 0)
         return hipSuccess;
+    if (!geometry_supported(g))
+        return hipErrorNotSupported;
     const unsigned nb = blocks_for((uint64_t)a.rows * a.pg.nkv);
-#define X(ES, DK, DV)                                                                          \
-    if (es_of(g) == ES && g.dk == DK && g.dv == DV) {                                         \
-        hipLaunchKernelGGL((append_kernel<ES, DK, DV>), dim3(nb), dim3(256), 0, s, a);         \
-        return hipGetLastError();                                                              \
-    }
-    NDA_FOR_SHAPES(X)
-#undef X
-    return hipErrorNotSupported;
+    if (g.kv_f16)
+        hipLaunchKernelGGL((append_kernel<2>), dim3(nb), dim3(256), 0, s, a);
+    else
+        hipLaunchKernelGGL((append_kernel<1>), dim3(nb), dim3(256), 0, s, a);
+    return hipGetLastError();
 }
 
 hipError_t launch_copy(const Geo &g, const CopyArgs &a, hipStream_t s)
 {
     if (a.count == 0 || a.n_layers == 0)
         return hipSuccess;
-#define X(ES, DK, DV)                                                                          \
-    if (es_of(g) == ES && g.dk == DK && g.dv == DV) {                                         \
-        hipLaunchKernelGGL((copy_kernel<ES, DK, DV>), dim3(a.count, a.n_layers), dim3(64), 0, s, a); \
-        return hipGetLastError();                                                              \
-    }
-    NDA_FOR_SHAPES(X)
-#undef X
-    return hipErrorNotSupported;
+    if (g.kv_f16)
+        hipLaunchKernelGGL((copy_kernel<2>), dim3(a.count, a.n_layers), dim3(64), 0, s, a);
+    else
+        hipLaunchKernelGGL((copy_kernel<1>), dim3(a.count, a.n_layers), dim3(64), 0, s, a);
+    return hipGetLastError();
 }
 
 static hipError_t launch_stage(const Geo &g, const StageArgs &a, hipStream_t s, bool scatter)
 {
     if (a.count == 0)
         return hipSuccess;
-#define X(ES, DK, DV)                                                                          \
-    if (es_of(g) == ES && g.dk == DK && g.dv == DV) {                                         \
-        if (scatter)                                                                           \
-            hipLaunchKernelGGL((stage_kernel<ES, DK, DV, true>), dim3(a.count), dim3(64), 0, s, a); \
-        else                                                                                   \
-            hipLaunchKernelGGL((stage_kernel<ES, DK, DV, false>), dim3(a.count), dim3(64), 0, s, a); \
-        return hipGetLastError();                                                              \
+    if (g.kv_f16) {
+        if (scatter)
+            hipLaunchKernelGGL((stage_kernel<2, true>), dim3(a.count), dim3(64), 0, s, a);
+        else
+            hipLaunchKernelGGL((stage_kernel<2, false>), dim3(a.count), dim3(64), 0, s, a);
+    } else {
+        if (scatter)
+            hipLaunchKernelGGL((stage_kernel<1, true>), dim3(a.count), dim3(64), 0, s, a);
+        else
+            hipLaunchKernelGGL((stage_kernel<1, false>), dim3(a.count), dim3(64), 0, s, a);
     }
-    NDA_FOR_SHAPES(X)
-#undef X
-    return hipErrorNotSupported;
+    return hipGetLastError();
 }
 
 hipError_t launch_gather(const Geo &g, const StageArgs &a, hipStream_t s) { return launch_stage(g, a, s, false); }
@@ -821,14 +873,11 @@ hipError_t launch_fill_kv(const Geo &g, const FillKvArgs &a, hipStream_t s)
     if (a.nseq == 0 || a.n_layers == 0)
         return hipSuccess;
     dim3 grid(a.nseq, a.n_layers);
-#define X(ES, DK, DV)                                                                          \
-    if ((g.kv_f16 ? 2 : 1) == ES && g.dk == DK && g.dv == DV) {                               \
-        hipLaunchKernelGGL((fill_kv_kernel<ES, DK, DV>), grid, dim3(256), 0, s, a);           \
-        return hipGetLastError();                                                              \
-    }
-    NDA_FOR_SHAPES(X)
-#undef X
-    return hipErrorNotSupported;
+    if (g.kv_f16)
+        hipLaunchKernelGGL((fill_kv_kernel<2>), grid, dim3(256), 0, s, a);
+    else
+        hipLaunchKernelGGL((fill_kv_kernel<1>), grid, dim3(256), 0, s, a);
+    return hipGetLastError();
 }
 
 hipError_t launch_advance(SeqDev *seqs, const uint32_t *seq_list, uint32_t nseq, uint32_t n, hipStream_t s)

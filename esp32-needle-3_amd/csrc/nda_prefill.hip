@@ -903,6 +903,14 @@ hipError_t launch_decode_mfma(const Geo &g, const PrefillArgs &a, hipStream_t s)
     X(1, 64, 64, 1) X(1, 64, 64, 2) X(1, 64, 64, 4) X(1, 64, 64, 6) X(1, 64, 64, 8) \
     X(1, 48, 64, 1) X(1, 48, 64, 2) X(1, 48, 64, 6)
 
+bool prefill_mfma_supported(const Geo &g)
+{
+#define X(ES, DK, DV, REP) if ((g.kv_f16 ? 2 : 1) == ES && g.dk == DK && g.dv == DV && g.rep == REP) return true;
+    NDA_PF_GEOMETRIES(X)
+#undef X
+    return false;
+}
+
 // Geometries whose 8-wave variant fits the 128-register budget of 4 waves per
 // SIMD; the others run 4-wave work-groups.
 static bool pf_w8_fits(const Geo &g) { return g.kv_f16 && g.rep == 1; }

@@ -34,7 +34,8 @@ extern "C" {
 #define NDA_ERR_HIP         -3   /* a HIP runtime call failed */
 #define NDA_ERR_RANGE       -4   /* position / length outside what the window holds */
 #define NDA_ERR_STATE       -5   /* call not valid in the sequence's current state */
-#define NDA_ERR_UNSUPPORTED -6   /* geometry has no compiled kernel */
+#define NDA_ERR_UNSUPPORTED -6   /* a shape the engine does not define, or the front / block
+                                    calls for a shape they are not built for */
 #define NDA_ERR_NODEV       -7   /* no usable gfx950 device */
 
 /* KV element types. INT8: symmetric int8 codes + fp32 scale per (slot,
@@ -51,9 +52,11 @@ typedef struct nda_ctx nda_ctx;
 typedef struct {
     uint32_t n_layers;
     uint32_t n_heads;        /* query heads */
-    uint32_t n_kv_heads;     /* n_heads % n_kv_heads == 0 (GQA) */
-    uint32_t qk_head_dim;    /* 48 or 64 */
-    uint32_t v_head_dim;     /* 64 */
+    uint32_t n_kv_heads;     /* n_heads % n_kv_heads == 0, at most 8 query heads per
+                                kv-head (ND_KV_REP_CAP, nd_model.h:245) */
+    uint32_t qk_head_dim;    /* 4..64, a multiple of 4 (ND_KV_HD_CAP, nd_model.h:244; the
+                                engine's staging converts whole 4-byte words, nd_model.c:79-94) */
+    uint32_t v_head_dim;     /* 4..64, a multiple of 4 */
     uint32_t window;         /* KV slots per sequence per layer (sinks + ring) */
     uint32_t page_size;      /* positions per page: 16, 32 or 64 (0 = 16) */
     uint32_t kv_dtype;       /* NDA_KV_INT8 | NDA_KV_F16 */
@@ -201,7 +204,10 @@ typedef struct {
 
 /* Allocates the tap histories and the rotary table (cos/sin of
  * pos * theta^(-2i/qk_head_dim), as nd_model_open :1233-1236 and
- * nd_model_step_hidden :2949-2954 compute them). Once per context. */
+ * nd_model_step_hidden :2949-2954 compute them). Once per context. The front
+ * (and with it the attention block calls) is built for qk/v 64/64 with 1, 2,
+ * 4, 6 or 8 query heads per kv-head and 48/64 with 1, 2 or 6; other shapes
+ * return NDA_ERR_UNSUPPORTED. */
 int nda_front_init(nda_ctx *ctx, const nda_front_config *fc);
 /* One layer's weights from HOST arrays, the engine's staged fp32 slots
  * (fp16_slot[li][4..8]): tap_q [taps][n_heads*qk_head_dim],

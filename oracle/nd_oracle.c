@@ -205,15 +205,33 @@ typedef struct {
     float *oh;
 } head_state;
 
-/* Score of one position, ascending pair sums: s += q[i]k[i] + q[i+1]k[i+1].
- * This is both the head-pair dot (qk_dot8, nd_model.c:2038-2083, for qk_hd a
- * multiple of 8) and the single-head dot (nd_model.c:2259-2266). */
+/* Score of one position, ascending pair sums: s += q[i]k[i] + q[i+1]k[i+1]:
+ * the dot of a head outside a pair (the last head of an odd group,
+ * nd_model.c:2259-2266). */
 static float dot_pairs(const float *q, const float *k, uint32_t n)
 {
     float s = 0.0f;
     uint32_t i;
     for (i = 0; i + 1u < n; i += 2u)
         s += q[i] * k[i] + q[i + 1u] * k[i + 1u];
+    for (; i < n; i++)
+        s += q[i] * k[i];
+    return s;
+}
+
+/* Score of one position for a head of a PAIR (qk_dot8, nd_model.c:2038-2083):
+ * ascending pair sums over whole 8-column groups, then the remaining columns
+ * one term at a time. Equals dot_pairs when qk_hd is a multiple of 8. */
+static float dot_pairs8(const float *q, const float *k, uint32_t n)
+{
+    float s = 0.0f;
+    uint32_t i;
+    for (i = 0; i + 7u < n; i += 8u) {
+        s += q[i] * k[i] + q[i + 1u] * k[i + 1u];
+        s += q[i + 2u] * k[i + 2u] + q[i + 3u] * k[i + 3u];
+        s += q[i + 4u] * k[i + 4u] + q[i + 5u] * k[i + 5u];
+        s += q[i + 6u] * k[i + 6u] + q[i + 7u] * k[i + 7u];
+    }
     for (; i < n; i++)
         s += q[i] * k[i];
     return s;
@@ -297,9 +315,13 @@ static void visit_run(const ndo_kv_view *kv, uint32_t g, uint32_t rep, const flo
         stage_row(kv, kv->v, sl0, g, kv->v_hd, vf0);
         stage_row(kv, kv->v, sl1, g, kv->v_hd, vf1);
         for (t = 0; t < rep; t++) {
+            /* heads go in pairs (t, t+1) through qk_dot8; an odd group's last
+             * head takes the single-head dot (nd_model.c:2201-2266) */
+            float (*dot)(const float *, const float *, uint32_t) =
+                (t | 1u) < rep ? dot_pairs8 : dot_pairs;
             const float *qh = q + (size_t)(g * rep + t) * kv->qk_hd;
-            float s0 = dot_pairs(qh, kf0, kv->qk_hd) * sc0;
-            float s1 = dot_pairs(qh, kf1, kv->qk_hd) * sc1;
+            float s0 = dot(qh, kf0, kv->qk_hd) * sc0;
+            float s1 = dot(qh, kf1, kv->qk_hd) * sc1;
             pair_step(&hs[t], s0, s1, vs0, vs1, vf0, vf1, kv->v_hd);
         }
     }

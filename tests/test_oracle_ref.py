@@ -144,8 +144,12 @@ def _run_pair(geom, kv_steps, events, seed):
         assert np.array_equal(np.asarray(a).view(np.uint8), np.asarray(b).view(np.uint8))
 
 
+# MHA 8x64, the archive's 12/2 qk48, GQA 2/3/5/7/8, and head dims the engine
+# allows besides (multiples of 4 up to ND_KV_HD_CAP 64: qk 32, qk 36 and 20,
+# whose last 4 columns qk_dot8 sums one term at a time, v 20 and 32)
 @pytest.mark.parametrize("geom", [(1, 8, 8, 64, 64, 300), (2, 12, 2, 48, 64, 384), (1, 6, 3, 48, 64, 90),
-                                  (1, 16, 2, 64, 64, 200), (1, 3, 1, 64, 64, 64)])
+                                  (1, 16, 2, 64, 64, 200), (1, 3, 1, 64, 64, 64), (1, 10, 2, 32, 32, 150),
+                                  (1, 14, 2, 36, 20, 120), (1, 4, 2, 20, 64, 100), (1, 5, 1, 64, 16, 80)])
 def test_sessions_bit_exact(geom):
     def ev(n):
         out = [("tok", True, 1.0)] * 40 + [("snap",)] + [("tok", i % 2 == 0, 1.0 + (i % 5)) for i in range(n)]
