@@ -62,14 +62,16 @@ def log(*a):
     print(*a, file=sys.stderr, flush=True)
 
 
-def cpu_baseline(lens_all, seconds, nthreads):
-    """The oracle's fp16 decode (the engine's attn_heads restated, fp16 KV)
-    on a bounded sample of the same workload, threaded over sequences as the
-    engine's nd_parallel_rows seam splits rows. Returns decode tokens/s."""
+def cpu_port_f16(lens_all, seconds, nthreads, nseq=128, seed_off=1):
+    """The oracle's fp16 decode (the engine's attn_heads restated with fp16
+    KV; the reference has no fp16 cache) on a bounded sample of sequences
+    drawn from lens_all, split over nthreads threads by sequence as the
+    engine's nd_parallel_rows seam splits rows (nd_quant.h:213-230).
+    Returns (tokens/s through LAYERS layers, attention FLOP/s, sample)."""
     import ndoracle as O
 
-    rng = np.random.default_rng(SEED + 1)
-    S = 128
+    rng = np.random.default_rng(SEED + seed_off)
+    S = nseq
     lens = np.ascontiguousarray(rng.choice(lens_all, S), np.uint32)
     koff = np.zeros(S, np.uint64)
     koff[1:] = np.cumsum(lens[:-1].astype(np.uint64) * H * D)
@@ -89,23 +91,26 @@ def cpu_baseline(lens_all, seconds, nthreads):
         el = time.perf_counter() - t0
         if el >= seconds and calls >= 2:
             break
-    # tokens per second through all LAYERS layers
     tok_s = calls * S / el / LAYERS
-    return tok_s, "%d sequences (L mean %.0f) x %d layer-calls, %.1f s" % (S, lens.mean(), calls, el)
+    flops = calls * float(lens.sum() + S) * H * 2 * (D + D) / el
+    return tok_s, flops, "%d sequences (L mean %.0f) x %d layer-calls, %.1f s" % (S, lens.mean(), calls, el)
 
 
-def cpu_reference_int8(lens_all, seconds):
+def cpu_reference_int8(lens_all, seconds, threads):
     """The reference engine's own store + attn_heads (oracle/_ref, compiled
     from its sources) on the same shapes in its own dtype (int8 KV + scales,
-    MHA 8 x 64), one session per sequence, serial as the host build runs it
-    (rows_serial). Caches hold random int8 codes; the timed call is one
-    decode token (store + attend) per (sequence, layer). Returns tokens/s."""
+    MHA 8 x 64), one session per sequence. For each thread count in
+    `threads`: 1 is the host build's serial rows_serial; more runs the
+    sessions side by side on that many threads (the reference's attention
+    path has no shared writable state). Caches hold random int8 codes; one
+    round is one decode token (store + attend) per sequence on one layer.
+    Timed in C with CLOCK_MONOTONIC. Returns {threads: baseline object}."""
     import ctypes as C
     import ndoracle as O
     if not O.have_ref():
         return None
     rng = np.random.default_rng(SEED + 2)
-    S = 32
+    S = 64
     lens = rng.choice(lens_all, S)
     sess = []
     for L in lens:
@@ -117,24 +122,24 @@ def cpu_reference_int8(lens_all, seconds):
         vs[:] = rng.uniform(0.01, 0.03, vs.shape).astype(np.float32)
         O.ref().ref_set_pos(r.m, int(L) - 1)
         sess.append(r)
+    models = (C.c_void_p * S)(*[r.m for r in sess])
     q = rng.standard_normal(H * D).astype(np.float32)
     kn = rng.standard_normal(H * D).astype(np.float32)
     vn = rng.standard_normal(H * D).astype(np.float32)
-    out = np.zeros(H * D, np.float32)
-    f = O.ref().ref_attention
-    calls, t0 = 0, time.perf_counter()
-    while True:
-        for r in sess:
-            f(r.m, 0, q.ctypes.data, kn.ctypes.data, vn.ctypes.data, None, out.ctypes.data)
-        calls += S
-        el = time.perf_counter() - t0
-        if el >= seconds:
-            break
+    res = {}
+    for nt in threads:
+        out = np.zeros(nt * H * D, np.float32)
+        args = (models, S, 0, q.ctypes.data, kn.ctypes.data, vn.ctypes.data, out.ctypes.data, H * D)
+        one = O.ref().ref_attention_rounds(*args, 1, nt)
+        rounds = max(2, int(seconds / max(one, 1e-6)))
+        el = O.ref().ref_attention_rounds(*args, rounds, nt)
+        res[nt] = {"value": round(rounds * S / el / LAYERS, 1), "unit": "tokens/s", "cores": nt,
+                   "kind": "reference",
+                   "sample": "%d sequences (L mean %.0f), int8 KV (the engine's dtype), %d layer-calls, %.1f s"
+                             % (S, lens.mean(), rounds * S, el)}
     for r in sess:
         r.close()
-    return {"value": round(calls / el / LAYERS, 1), "unit": "tokens/s", "cores": 1, "kind": "reference",
-            "sample": "%d sequences (L mean %.0f), int8 KV (the engine's dtype), %d layer-calls, %.1f s"
-                      % (S, lens.mean(), calls, el)}
+    return res
 
 
 def prefill_leg(N, stream, nseq=256, lmin=8192, lmax=32768, chunk=512, reps=3):
@@ -758,7 +763,7 @@ def main():
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-cpu", action="store_true")
-    ap.add_argument("--cpu-seconds", type=float, default=12.0)
+    ap.add_argument("--cpu-seconds", type=float, default=20.0)
     ap.add_argument("--split-chunk", type=int, default=0)
     ap.add_argument("--page-size", type=int, default=16)
     ap.add_argument("--no-prefill", action="store_true")
@@ -908,17 +913,31 @@ def main():
         log("prefill: %.1f TFLOP/s (%.3f of 2.5 PF), kernel %.3f ms, sampled max |delta| %.3g" %
             (prefill["tflops"], prefill["frac"], prefill["kernel_ms"], prefill["max_abs_delta_sampled"]))
 
-    cpu = None
-    cpu_ref = None
+    cpu = cpu_1 = cpu_ref = cpu_long = None
     if not args.no_cpu:
         ncores = min(16, os.cpu_count() or 1)
-        c_tok, sample = cpu_baseline(lens, args.cpu_seconds, ncores)
+        sec = args.cpu_seconds
+        c_tok, _, sample = cpu_port_f16(lens, sec * 0.3, ncores)
         cpu = {"value": round(c_tok, 1), "unit": "tokens/s", "cores": ncores, "kind": "port",
                "sample": sample + ", fp16 KV, no gate, oracle attn_heads restatement"}
-        log("cpu baseline: %.1f tok/s on %d threads" % (c_tok, ncores))
-        cpu_ref = cpu_reference_int8(lens, args.cpu_seconds / 2)
+        c1, _, sample1 = cpu_port_f16(lens, sec * 0.2, 1, nseq=32)
+        cpu_1 = {"value": round(c1, 1), "unit": "tokens/s", "cores": 1, "kind": "port",
+                 "sample": sample1 + ", fp16 KV, no gate, oracle attn_heads restatement"}
+        log("cpu baseline (port, fp16): %.1f tok/s on %d threads, %.1f tok/s on 1" % (c_tok, ncores, c1))
+        cpu_ref = cpu_reference_int8(lens, sec * 0.15, (1, ncores))
         if cpu_ref:
-            log("cpu reference (int8, 1 thread): %.1f tok/s" % cpu_ref["value"])
+            cpu_ref = {"1": cpu_ref[1], str(ncores): cpu_ref[ncores]}
+            log("cpu reference (int8): %.1f tok/s on 1 thread, %.1f on %d" % (
+                cpu_ref["1"]["value"], cpu_ref[str(ncores)]["value"], ncores))
+        # the long-context decode (8K-32K positions), a 16-sequence subsample
+        rng_l = np.random.default_rng(SEED + 5)
+        lt, lf, lsample = cpu_port_f16(rng_l.integers(8192, 32769, 256), sec * 0.2, ncores, nseq=16,
+                                       seed_off=5)
+        cpu_long = {"value": round(lt * LAYERS, 1), "unit": "tokens/s per layer", "cores": ncores,
+                    "kind": "port", "attention_GFLOPs": round(lf / 1e9, 2),
+                    "sample": lsample + ", fp16 KV, L ~ U[8192, 32768], one layer"}
+        log("cpu long-context decode (port): %.1f tok/s per layer, %.1f GFLOP/s on %d threads" % (
+            lt * LAYERS, lf / 1e9, ncores))
 
     res = {
         "metric": "decode attn tokens/s + HBM GB/s (% peak) at B=4096; prefill TFLOP/s",
@@ -944,7 +963,9 @@ def main():
                      "kernel": "attend_kernel<f16,64,64,rep1>", "kernel_ms": round(dec_ms, 4),
                      "bytes_per_launch": int(dec_bytes_per_launch)},
         "cpu_baseline": cpu,
+        "cpu_baseline_1core": cpu_1,
         "cpu_reference_int8": cpu_ref,
+        "cpu_long_context_decode": cpu_long,
         "prefill": prefill,
         "engine_session": engine,
         "front": front,

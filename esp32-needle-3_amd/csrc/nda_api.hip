@@ -52,6 +52,35 @@ hipError_t scratch_address(int dev, uint8_t **out)
     return hipSuccess;
 }
 
+// Device memory of every context, CQ tensor and nda_dev_alloc block comes
+// from this pair (the engine's ND_ALLOC / ND_FREE seam, nd_model.h:35-68);
+// nda_set_allocator replaces it.
+void *default_alloc(size_t bytes, void *)
+{
+    void *p = nullptr;
+    return hipMalloc(&p, bytes) == hipSuccess ? p : nullptr;
+}
+void default_free(void *p, void *) { (void)hipFree(p); }
+
+std::mutex g_alloc_mu;
+nda_alloc_fn g_alloc = default_alloc;
+nda_free_fn g_free = default_free;
+void *g_alloc_user = nullptr;
+
+void *dev_alloc(size_t bytes)
+{
+    std::lock_guard<std::mutex> lk(g_alloc_mu);
+    return g_alloc(bytes ? bytes : 1, g_alloc_user);
+}
+
+void dev_free(void *p)
+{
+    if (!p)
+        return;
+    std::lock_guard<std::mutex> lk(g_alloc_mu);
+    g_free(p, g_alloc_user);
+}
+
 constexpr uint32_t MIN_RECENT = 64;   // ND_MIN_RECENT, engine/src/nd_model.c:1311-1312
 
 struct Prefix {
@@ -104,6 +133,8 @@ struct nda_ctx {
     std::vector<SeqHost> seqs;
     std::vector<Prefix> prefixes;
     std::vector<int32_t> free_pages;
+    std::vector<size_t> journal;        // page-table entries backed by the open transaction
+    int txn_depth = 0;
     bool seqs_dirty = true;
     uint32_t dirty_lo = UINT32_MAX, dirty_hi = 0;   // page-table rows to upload
     bool prefix_dirty = true;
@@ -237,10 +268,45 @@ int back_slots(nda_ctx *c, uint32_t seq, uint32_t s0, uint32_t s1)
             row[i] = c->free_pages.back();
             c->free_pages.pop_back();
             mark_rows(c, seq);
+            if (c->txn_depth)
+                c->journal.push_back((size_t)seq * c->pg.pages_per_seq + i);
         }
     }
     return NDA_OK;
 }
+
+// The pages a call backs stay journaled until it commits; a call that fails
+// part-way (the pool runs out for a later sequence, a buffer cannot grow)
+// gives them back in reverse order, so the page tables and the free list are
+// as before the call.
+struct PageTxn {
+    nda_ctx *c;
+    size_t mark;
+    bool open = true;
+    explicit PageTxn(nda_ctx *c_) : c(c_), mark(c_->journal.size()) { c->txn_depth++; }
+    void commit()
+    {
+        if (open) {
+            open = false;
+            c->txn_depth--;
+            if (!c->txn_depth)
+                c->journal.clear();
+        }
+    }
+    ~PageTxn()
+    {
+        if (!open)
+            return;
+        while (c->journal.size() > mark) {
+            const size_t idx = c->journal.back();
+            c->journal.pop_back();
+            c->free_pages.push_back(c->pages[idx]);
+            c->pages[idx] = -1;
+            mark_rows(c, (uint32_t)(idx / c->pg.pages_per_seq));
+        }
+        c->txn_depth--;
+    }
+};
 
 // Back the own slot(s) of positions [p0, p0 + n) (no wrap inside, n >= 1).
 int back_positions(nda_ctx *c, uint32_t seq, uint32_t p0, uint32_t n)
@@ -295,91 +361,46 @@ int sync_tables(nda_ctx *c, hipStream_t st)
     return NDA_OK;
 }
 
-int ensure_rows(nda_ctx *c, size_t rows)
-{
-    if (rows * 2 <= c->rows_cap)
-        return NDA_OK;
-    if (c->d_rows) {
-        (void)hipDeviceSynchronize();   // launches still reading the old staging
-        (void)hipFree(c->d_rows);
-        c->dev_bytes -= c->rows_cap * sizeof(uint32_t);
-        c->d_rows = nullptr;
-    }
-    size_t cap = std::max<size_t>(rows * 2, 8192);
-    HIPC(c, hipMalloc(&c->d_rows, cap * sizeof(uint32_t)));
-    c->rows_cap = cap;
-    c->dev_bytes += cap * sizeof(uint32_t);
-    return NDA_OK;
-}
-
-int ensure_part(nda_ctx *c, size_t floats)
-{
-    if (floats <= c->part_cap)
-        return NDA_OK;
-    if (c->d_part) {
-        (void)hipDeviceSynchronize();
-        (void)hipFree(c->d_part);
-        c->dev_bytes -= c->part_cap * sizeof(float);
-        c->d_part = nullptr;
-    }
-    HIPC(c, hipMalloc(&c->d_part, floats * sizeof(float)));
-    c->part_cap = floats;
-    c->dev_bytes += floats * sizeof(float);
-    return NDA_OK;
-}
-
-int ensure_pf(nda_ctx *c, size_t n)
-{
-    if (n <= c->pf_cap)
-        return NDA_OK;
-    if (c->d_pf) {
-        (void)hipDeviceSynchronize();
-        (void)hipFree(c->d_pf);
-        c->dev_bytes -= c->pf_cap * sizeof(uint32_t);
-        c->d_pf = nullptr;
-    }
-    size_t cap = std::max<size_t>(n * 2, 16384);
-    HIPC(c, hipMalloc(&c->d_pf, cap * sizeof(uint32_t)));
-    c->pf_cap = cap;
-    c->dev_bytes += cap * sizeof(uint32_t);
-    return NDA_OK;
-}
-
-int ensure_stage(nda_ctx *c, size_t bytes)
-{
-    if (bytes <= c->stage_cap)
-        return NDA_OK;
-    if (c->d_stage) {
-        (void)hipDeviceSynchronize();
-        (void)hipFree(c->d_stage);
-        c->dev_bytes -= c->stage_cap;
-        c->d_stage = nullptr;
-    }
-    HIPC(c, hipMalloc(&c->d_stage, bytes));
-    c->stage_cap = bytes;
-    c->dev_bytes += bytes;
-    return NDA_OK;
-}
-
-// Grows a device staging buffer (elements of T); the old one may still be
-// read by queued launches, so the device is drained before it is freed.
+// Grows a device staging buffer to n_alloc elements of T when it holds fewer
+// than `need`. The new buffer is allocated first: a failed allocation returns
+// NDA_ERR_NOMEM with the old buffer and the context unchanged. Queued
+// launches may still read the old buffer, so the device is drained before it
+// is freed.
 template <typename T>
-int ensure_buf(nda_ctx *c, T *&buf, size_t &cap, size_t need)
+int grow_buf(nda_ctx *c, T *&buf, size_t &cap, size_t need, size_t n_alloc)
 {
     if (need <= cap)
         return NDA_OK;
+    T *nb = static_cast<T *>(dev_alloc(n_alloc * sizeof(T)));
+    if (!nb)
+        return fail(c, NDA_ERR_NOMEM, "device allocation of %zu bytes failed", n_alloc * sizeof(T));
     if (buf) {
         (void)hipDeviceSynchronize();
-        (void)hipFree(buf);
+        dev_free(buf);
         c->dev_bytes -= cap * sizeof(T);
-        buf = nullptr;
-        cap = 0;
     }
-    const size_t n = std::max<size_t>(need, 4096);
-    HIPC(c, hipMalloc((void **)&buf, n * sizeof(T)));
-    cap = n;
-    c->dev_bytes += n * sizeof(T);
+    buf = nb;
+    cap = n_alloc;
+    c->dev_bytes += n_alloc * sizeof(T);
     return NDA_OK;
+}
+
+// row_seq | row_t staging for `rows` rows
+int ensure_rows(nda_ctx *c, size_t rows)
+{
+    return grow_buf(c, c->d_rows, c->rows_cap, rows * 2, std::max<size_t>(rows * 2, 8192));
+}
+
+int ensure_part(nda_ctx *c, size_t floats) { return grow_buf(c, c->d_part, c->part_cap, floats, floats); }
+
+int ensure_pf(nda_ctx *c, size_t n) { return grow_buf(c, c->d_pf, c->pf_cap, n, std::max<size_t>(n * 2, 16384)); }
+
+int ensure_stage(nda_ctx *c, size_t bytes) { return grow_buf(c, c->d_stage, c->stage_cap, bytes, bytes); }
+
+template <typename T>
+int ensure_buf(nda_ctx *c, T *&buf, size_t &cap, size_t need)
+{
+    return grow_buf(c, buf, cap, need, std::max<size_t>(need, 4096));
 }
 
 hipEvent_t take_event(nda_ctx *c)
@@ -510,6 +531,15 @@ int hist_flush(nda_ctx *c, hipStream_t st)
     return NDA_OK;
 }
 
+// Room on the device for `extra` more queued history copies, taken before a
+// call changes any state (so a failed allocation changes nothing).
+int hist_reserve(nda_ctx *c, size_t extra)
+{
+    if (!c->taps)
+        return NDA_OK;
+    return ensure_buf(c, c->d_hist_ops, c->hist_ops_cap, c->hist_pending.size() + extra);
+}
+
 // Upload seq ids (and optional per-row offsets) for a launch; returns device
 // pointers, null when the identity mapping applies.
 int upload_rows(nda_ctx *c, uint32_t rows, const uint32_t *row_seq, const uint32_t *row_t,
@@ -604,6 +634,21 @@ bool mfma_decode(const nda_ctx *c, const AttnArgs &a)
 // floats, or null for the context's own buffer (grown on demand). prof: record
 // profiling events (nda_decode_noalloc records none: creating an event may
 // allocate).
+// Device buffers an attention launch over `rows` rows needs: the row staging
+// (staged: ids or per-row offsets are uploaded) and, for rows split into
+// chunks (which the VALU kernel serves), the partials. Taken before a call
+// changes any state, so that a failed allocation changes nothing.
+int reserve_attend(nda_ctx *c, uint32_t rows, bool staged, uint32_t max_total, uint64_t sum_total)
+{
+    if (staged)
+        if (int rc = ensure_rows(c, rows))
+            return rc;
+    const AttnArgs a = attn_args(c, 0, rows, nullptr, nullptr, nullptr, max_total, sum_total);
+    if (a.max_chunks > 1)
+        return ensure_part(c, (size_t)a.rows * a.nh * a.max_chunks * (c->cfg.v_head_dim + 2));
+    return NDA_OK;
+}
+
 int run_attend(nda_ctx *c, AttnArgs &a, hipStream_t st, float *part = nullptr, bool prof = true)
 {
     if (mfma_decode(c, a)) {
@@ -733,17 +778,18 @@ int nda_create(const nda_config *cfg_in, nda_ctx **out)
     }
 
     const uint64_t pool_bytes = c->pg.layer_bytes * cfg.n_layers;
-    hipError_t e = hipMalloc(&c->pool, pool_bytes);
-    if (e != hipSuccess) {
+    c->pool = static_cast<uint8_t *>(dev_alloc(pool_bytes));
+    if (!c->pool) {
         delete c;
-        return e == hipErrorOutOfMemory ? NDA_ERR_NOMEM : NDA_ERR_HIP;
+        return NDA_ERR_NOMEM;
     }
     c->dev_bytes = pool_bytes;
     const size_t pt = (size_t)cfg.max_seqs * c->pg.pages_per_seq;
     const size_t ppt = (size_t)cfg.max_prefixes * c->pg.pages_per_seq;
-    if (hipMalloc(&c->d_pages, pt * 4) != hipSuccess ||
-        hipMalloc(&c->d_prefix_pages, ppt * 4) != hipSuccess ||
-        hipMalloc(&c->d_seqs, (size_t)cfg.max_seqs * sizeof(SeqDev)) != hipSuccess) {
+    c->d_pages = static_cast<int32_t *>(dev_alloc(pt * 4));
+    c->d_prefix_pages = static_cast<int32_t *>(dev_alloc(ppt * 4));
+    c->d_seqs = static_cast<SeqDev *>(dev_alloc((size_t)cfg.max_seqs * sizeof(SeqDev)));
+    if (!c->d_pages || !c->d_prefix_pages || !c->d_seqs) {
         nda_destroy(c);
         return NDA_ERR_NOMEM;
     }
@@ -783,8 +829,7 @@ void nda_destroy(nda_ctx *c)
                     c->d_front_w, c->d_front_norm, c->d_rope, c->d_qfront, c->d_front_rows,
                     c->d_hist_ops, c->d_bscr};
     for (void *b : bufs)
-        if (b)
-            (void)hipFree(b);
+        dev_free(b);
     delete c;
 }
 
@@ -862,7 +907,11 @@ int nda_seq_reserve(nda_ctx *c, uint32_t seq, uint32_t n)
     const SeqHost &s = c->seqs[seq];
     // Once the ring is full every slot is backed; cap at one full cycle.
     uint32_t cap = c->cfg.window - (s.prefix >= 0 ? s.n_sink : 0);
-    return back_positions(c, seq, s.pos, std::min(n, cap));
+    PageTxn txn(c);
+    if (int rc = back_positions(c, seq, s.pos, std::min(n, cap)))
+        return rc;
+    txn.commit();
+    return NDA_OK;
 }
 
 int nda_advance(nda_ctx *c, uint32_t nseq, const uint32_t *ids, uint32_t n, void *stream)
@@ -873,6 +922,9 @@ int nda_advance(nda_ctx *c, uint32_t nseq, const uint32_t *ids, uint32_t n, void
         return rc;
     if (nseq == 0 || n == 0)
         return NDA_OK;
+    if (!c->seqs_dirty && ids)
+        if (int rc = ensure_rows(c, nseq))
+            return rc;
     for (uint32_t b = 0; b < nseq; b++)
         c->seqs[sid(ids, b)].pos += n;
     if (c->seqs_dirty)      // a full upload is pending anyway
@@ -913,6 +965,8 @@ int nda_prefix_build(nda_ctx *c, uint32_t seq, int32_t *prefix_id, void *stream)
     const uint32_t npages = (len + c->cfg.page_size - 1) / c->cfg.page_size;
     if (npages > c->free_pages.size())
         return fail(c, NDA_ERR_NOMEM, "page pool exhausted building a prefix");
+    if (int rc = hist_reserve(c, 2))
+        return rc;
     int32_t *prow = &c->prefix_pages[(size_t)id * c->pg.pages_per_seq];
     for (uint32_t i = 0; i < npages; i++) {
         prow[i] = c->free_pages.back();
@@ -981,10 +1035,23 @@ int nda_seq_attach(nda_ctx *c, uint32_t seq, int32_t id, void *stream)
         return fail(c, NDA_ERR_ARG, "prefix %d does not exist", id);
     hipStream_t st = (hipStream_t)stream;
     SeqHost &s = c->seqs[seq];
+    const Prefix &pf = c->prefixes[id];
+    {
+        // the ring tail's pages, from the free pool plus this sequence's own
+        const uint32_t tail = pf.len > pf.n_sink ? pf.len - pf.n_sink : 0u;
+        const size_t need = (tail + c->cfg.page_size - 1) / c->cfg.page_size;
+        size_t have = c->free_pages.size();
+        const int32_t *row = &c->pages[(size_t)seq * c->pg.pages_per_seq];
+        for (uint32_t i = 0; i < c->pg.pages_per_seq; i++)
+            have += row[i] >= 0;
+        if (need > have)
+            return fail(c, NDA_ERR_NOMEM, "page pool exhausted: need %zu pages, %zu free", need, have);
+        if (int rc = hist_reserve(c, 2))
+            return rc;
+    }
     if (s.prefix >= 0)
         c->prefixes[s.prefix].refs--;
     release_pages(c, seq);
-    const Prefix &pf = c->prefixes[id];
     s = SeqHost();
     s.prefix = id;
     s.n_sink = pf.n_sink;
@@ -1076,11 +1143,16 @@ int nda_kv_append(nda_ctx *c, uint32_t layer, uint32_t nseq, const uint32_t *ids
     if (int rc = check_ids(c, nseq, ids))
         return rc;
     hipStream_t st = (hipStream_t)stream;
+    if (ids)
+        if (int rc = ensure_rows(c, nseq))
+            return rc;
+    PageTxn txn(c);
     for (uint32_t b = 0; b < nseq; b++) {
         const uint32_t q = sid(ids, b);
         if (int rc = back_positions(c, q, c->seqs[q].pos, 1))
             return rc;
     }
+    txn.commit();
     for (uint32_t b = 0; b < nseq; b++) {
         SeqHost &s = c->seqs[sid(ids, b)];
         s.stored_end = std::max(s.stored_end, s.pos + 1);
@@ -1143,21 +1215,33 @@ static int decode_impl(nda_ctx *c, uint32_t layer, uint32_t nseq, const uint32_t
 {
     if (c && nseq && k && !v)
         return fail(c, NDA_ERR_ARG, "null v");
-    if (c && k && q && out && layer < c->cfg.n_layers && !check_ids(c, nseq, ids)) {
+    if (!c || (nseq && (!q || !out)))
+        return c ? fail(c, NDA_ERR_ARG, "null q/out") : NDA_ERR_ARG;
+    if (layer >= c->cfg.n_layers)
+        return fail(c, NDA_ERR_ARG, "layer %u out of range", layer);
+    if (int rc = check_ids(c, nseq, ids))
+        return rc;
+    // The fused store backs this position's slot first; the pages go back if
+    // anything below fails.
+    PageTxn txn(c);
+    if (k)
         for (uint32_t b = 0; b < nseq; b++) {
             const uint32_t qq = sid(ids, b);
             if (int rc = back_positions(c, qq, c->seqs[qq].pos, 1))
                 return rc;
         }
-        for (uint32_t b = 0; b < nseq; b++) {
-            SeqHost &s = c->seqs[sid(ids, b)];
-            s.stored_end = std::max(s.stored_end, s.pos + 1);
-        }
-    }
     uint32_t max_total;
     uint64_t sum_total;
     if (int rc = decode_check(c, layer, nseq, ids, q, out, &max_total, &sum_total))
         return rc;
+    if (int rc = reserve_attend(c, nseq, ids != nullptr, max_total, sum_total))
+        return rc;
+    txn.commit();
+    if (k)
+        for (uint32_t b = 0; b < nseq; b++) {
+            SeqHost &s = c->seqs[sid(ids, b)];
+            s.stored_end = std::max(s.stored_end, s.pos + 1);
+        }
     hipStream_t st = (hipStream_t)stream;
     if (int rc = sync_tables(c, st))
         return rc;
@@ -1252,6 +1336,67 @@ static int prefill_check(nda_ctx *c, uint32_t nseq, const uint32_t *ids, const u
     return NDA_OK;
 }
 
+// What one nda_prefill call launches: rows, the visible runs they attend,
+// the kernel (VALU or MFMA) and the MFMA work-group size and work list.
+struct PrefillPlan {
+    uint64_t rows = 0, sum_total = 0;
+    uint32_t max_total = 0, rep = 1, trows = 0, nseq = 0;
+    int waves = 4;
+    bool valu = false;
+    size_t n_items = 0;
+};
+
+static int prefill_plan(nda_ctx *c, uint32_t nseq, const uint32_t *ids, const uint32_t *n_tokens, PrefillPlan &pl)
+{
+    pl = PrefillPlan();
+    pl.nseq = nseq;
+    for (uint32_t b = 0; b < nseq; b++) {
+        const SeqHost &s = c->seqs[sid(ids, b)];
+        if (n_tokens[b]) {
+            const Vis v = visible(s, s.pos + n_tokens[b] - 1, c->cfg.window);
+            pl.max_total = std::max(pl.max_total, v.n_sh + v.n_own);
+            pl.sum_total += (uint64_t)n_tokens[b] * (v.n_sh + v.n_own);
+        }
+        pl.rows += n_tokens[b];
+    }
+    if (pl.rows > (1u << 26))
+        return fail(c, NDA_ERR_ARG, "too many prefill tokens (%llu)", (unsigned long long)pl.rows);
+    // The VALU kernel serves shapes the MFMA tiles are not built for (and
+    // every shape when the config asks for it).
+    pl.valu = (c->cfg.flags & NDA_FLAG_PREFILL_VALU) || !prefill_mfma_supported(c->geo);
+    // MFMA work items = (batch index, kv-head, tile of 32*W query rows).
+    // Work-group size by the longest chunk: 64-row groups for short
+    // suffixes, 256-row groups (K/V staged once for 8 waves) for long ones.
+    pl.rep = c->cfg.n_heads / c->cfg.n_kv_heads;
+    uint32_t max_rows = 0;
+    for (uint32_t b = 0; b < nseq; b++)
+        max_rows = std::max(max_rows, n_tokens[b] * pl.rep);
+    pl.waves = max_rows <= 64 ? 2 : (max_rows >= 256 ? 8 : 4);
+    if (pl.waves == 8 && !(c->geo.kv_f16 && c->geo.rep == 1))
+        pl.waves = 4;
+#ifdef NDA_PF_FORCE_W     // build-time tuning knob: one work-group size for every chunk
+    pl.waves = NDA_PF_FORCE_W;
+#endif
+    pl.trows = 32u * pl.waves;
+    for (uint32_t b = 0; b < nseq; b++)
+        pl.n_items += (size_t)c->cfg.n_kv_heads * ((n_tokens[b] * pl.rep + pl.trows - 1) / pl.trows);
+    pl.n_items = (pl.n_items + 7) / 8 * 8;     // the kernel's XCD remap needs a multiple of 8
+    return NDA_OK;
+}
+
+// The device buffers a planned prefill needs: row staging and either the
+// partials of split VALU rows or the MFMA work list.
+static int prefill_reserve(nda_ctx *c, const PrefillPlan &pl)
+{
+    if (pl.rows == 0)
+        return NDA_OK;
+    if (pl.valu)
+        return reserve_attend(c, (uint32_t)pl.rows, true, pl.max_total, pl.sum_total);
+    if (int rc = ensure_rows(c, pl.rows))
+        return rc;
+    return ensure_pf(c, 3 * (size_t)pl.nseq + 3 * pl.n_items);
+}
+
 int nda_prefill(nda_ctx *c, uint32_t layer, uint32_t nseq, const uint32_t *ids, const uint32_t *n_tokens,
                 const float *q, const float *k, const float *v, const float *gate, float *out, void *stream)
 {
@@ -1266,28 +1411,28 @@ int nda_prefill(nda_ctx *c, uint32_t layer, uint32_t nseq, const uint32_t *ids, 
     if (int rc = prefill_check(c, nseq, ids, n_tokens))
         return rc;
     hipStream_t st = (hipStream_t)stream;
-    uint64_t rows = 0;
-    uint32_t max_total = 0;
-    uint64_t sum_total = 0;
-    for (uint32_t b = 0; b < nseq; b++) {
-        const SeqHost &s = c->seqs[sid(ids, b)];
-        if (n_tokens[b]) {
-            const Vis v = visible(s, s.pos + n_tokens[b] - 1, c->cfg.window);
-            max_total = std::max(max_total, v.n_sh + v.n_own);
-            sum_total += (uint64_t)n_tokens[b] * (v.n_sh + v.n_own);
-        }
-        rows += n_tokens[b];
-    }
-    if (rows == 0)
+    PrefillPlan pl;
+    if (int rc = prefill_plan(c, nseq, ids, n_tokens, pl))
+        return rc;
+    if (pl.rows == 0)
         return NDA_OK;
-    if (rows > (1u << 26))
-        return fail(c, NDA_ERR_ARG, "too many prefill tokens (%llu)", (unsigned long long)rows);
+    const uint64_t rows = pl.rows;
+    const uint32_t max_total = pl.max_total, rep = pl.rep, trows = pl.trows;
+    const uint64_t sum_total = pl.sum_total;
+    const bool valu = pl.valu;
+    const int waves = pl.waves;
+    // Buffers first, then pages (given back if the pool runs out part-way):
+    // a call that fails for want of memory changes nothing.
+    if (int rc = prefill_reserve(c, pl))
+        return rc;
+    PageTxn txn(c);
     for (uint32_t b = 0; b < nseq; b++) {
         const uint32_t qq = sid(ids, b);
         if (n_tokens[b])
             if (int rc = back_positions(c, qq, c->seqs[qq].pos, n_tokens[b]))
                 return rc;
     }
+    txn.commit();
     for (uint32_t b = 0; b < nseq; b++) {
         SeqHost &s = c->seqs[sid(ids, b)];
         if (n_tokens[b])
@@ -1320,28 +1465,12 @@ int nda_prefill(nda_ctx *c, uint32_t layer, uint32_t nseq, const uint32_t *ids, 
         if (e != hipSuccess)
             return hip_fail(c, e, "append kernel launch");
     }
-    // The VALU kernel serves shapes the MFMA tiles are not built for (and
-    // every shape when the config asks for it).
-    if ((c->cfg.flags & NDA_FLAG_PREFILL_VALU) || !prefill_mfma_supported(c->geo)) {
+    if (valu) {
         AttnArgs a = attn_args(c, layer, (uint32_t)rows, q, gate, out, max_total, sum_total);
         a.row_seq = d_seq;
         a.row_t = d_t;
         return run_attend(c, a, st);
     }
-    // MFMA path: work items = (batch index, tile of 32*W query rows).
-    const uint32_t rep = c->cfg.n_heads / c->cfg.n_kv_heads;
-    uint32_t max_rows = 0;
-    for (uint32_t b = 0; b < nseq; b++)
-        max_rows = std::max(max_rows, n_tokens[b] * rep);
-    // Work-group size by the longest chunk: 64-row groups for short
-    // suffixes, 256-row groups (K/V staged once for 8 waves) for long ones.
-    int waves = max_rows <= 64 ? 2 : (max_rows >= 256 ? 8 : 4);
-    if (waves == 8 && !(c->geo.kv_f16 && c->geo.rep == 1))
-        waves = 4;
-#ifdef NDA_PF_FORCE_W     // build-time tuning knob: one work-group size for every chunk
-    waves = NDA_PF_FORCE_W;
-#endif
-    const uint32_t trows = 32u * waves;
     std::vector<uint32_t> host(3 * (size_t)nseq);
     std::vector<uint32_t> items;
     for (uint32_t b = 0, tok = 0; b < nseq; b++) {
@@ -1424,24 +1553,29 @@ int nda_front_init(nda_ctx *c, const nda_front_config *fc)
             const float angle = (float)p * inv[i];
             rope[(size_t)p * half + i] = make_float2(cosf(angle), sinf(angle));
         }
-    auto alloc = [&](void **ptr, size_t bytes) -> int {
-        HIPC(c, hipMalloc(ptr, bytes));
-        c->dev_bytes += bytes;
-        return NDA_OK;
-    };
+    // All six buffers or none: a failed allocation frees the ones made here.
     const size_t hist_bytes = block * sizeof(float);
-    if (int rc = alloc((void **)&c->d_hist, hist_bytes * g.max_seqs))
-        return rc;
-    if (int rc = alloc((void **)&c->d_snap_hist, hist_bytes * g.max_seqs))
-        return rc;
-    if (int rc = alloc((void **)&c->d_prefix_hist, hist_bytes * std::max(1u, g.max_prefixes)))
-        return rc;
-    if (int rc = alloc((void **)&c->d_front_w, (size_t)g.n_layers * fc->taps * dcol * sizeof(float)))
-        return rc;
-    if (int rc = alloc((void **)&c->d_front_norm, (size_t)g.n_layers * 2 * g.qk_head_dim * sizeof(float)))
-        return rc;
-    if (int rc = alloc((void **)&c->d_rope, rope.size() * sizeof(float2)))
-        return rc;
+    struct {
+        void **ptr;
+        size_t bytes;
+    } bufs[] = {{(void **)&c->d_hist, hist_bytes * g.max_seqs},
+                {(void **)&c->d_snap_hist, hist_bytes * g.max_seqs},
+                {(void **)&c->d_prefix_hist, hist_bytes * std::max(1u, g.max_prefixes)},
+                {(void **)&c->d_front_w, (size_t)g.n_layers * fc->taps * dcol * sizeof(float)},
+                {(void **)&c->d_front_norm, (size_t)g.n_layers * 2 * g.qk_head_dim * sizeof(float)},
+                {(void **)&c->d_rope, rope.size() * sizeof(float2)}};
+    for (auto &b : bufs) {
+        *b.ptr = dev_alloc(b.bytes);
+        if (!*b.ptr) {
+            for (auto &u : bufs) {
+                dev_free(*u.ptr);
+                *u.ptr = nullptr;
+            }
+            return fail(c, NDA_ERR_NOMEM, "device allocation of %zu bytes failed", b.bytes);
+        }
+    }
+    for (auto &b : bufs)
+        c->dev_bytes += b.bytes;
     HIPC(c, hipMemset(c->d_hist, 0, hist_bytes * g.max_seqs));
     HIPC(c, hipMemset(c->d_snap_hist, 0, hist_bytes * g.max_seqs));
     HIPC(c, hipMemcpy(c->d_rope, rope.data(), rope.size() * sizeof(float2), hipMemcpyHostToDevice));
@@ -1630,11 +1764,27 @@ int nda_attention(nda_ctx *c, uint32_t layer, uint32_t nseq, const uint32_t *ids
     if (!aligned16(q) || !aligned16(k) || !aligned16(v))
         return fail(c, NDA_ERR_ARG, "q/k/v must be 16-byte aligned");
     hipStream_t st = (hipStream_t)stream;
+    // Buffers first (the front's q, the row staging, the decode's partials),
+    // then pages: a call that fails for want of memory changes nothing.
+    const size_t dq = (size_t)c->cfg.n_heads * c->cfg.qk_head_dim;
+    if (int rc = ensure_buf(c, c->d_qfront, c->qfront_cap, (size_t)nseq * dq))
+        return rc;
+    if (int rc = hist_reserve(c, 0))
+        return rc;
+    PageTxn txn(c);
+    uint32_t max_total = 0;
+    uint64_t sum_total = 0;
     for (uint32_t b = 0; b < nseq; b++) {
         const uint32_t qq = sid(ids, b);
         if (int rc = back_positions(c, qq, c->seqs[qq].pos, 1))
             return rc;
+        const Vis vv = visible(c->seqs[qq], c->seqs[qq].pos, c->cfg.window);
+        max_total = std::max(max_total, vv.n_sh + vv.n_own);
+        sum_total += vv.n_sh + vv.n_own;
     }
+    if (int rc = reserve_attend(c, nseq, ids != nullptr, max_total, sum_total))
+        return rc;
+    txn.commit();
     for (uint32_t b = 0; b < nseq; b++) {
         SeqHost &s = c->seqs[sid(ids, b)];
         s.stored_end = std::max(s.stored_end, s.pos + 1);
@@ -1642,9 +1792,6 @@ int nda_attention(nda_ctx *c, uint32_t layer, uint32_t nseq, const uint32_t *ids
     if (int rc = sync_tables(c, st))
         return rc;
     if (int rc = hist_flush(c, st))
-        return rc;
-    const size_t dq = (size_t)c->cfg.n_heads * c->cfg.qk_head_dim;
-    if (int rc = ensure_buf(c, c->d_qfront, c->qfront_cap, (size_t)nseq * dq))
         return rc;
     const uint32_t *d_seq, *d_t;
     if (int rc = upload_rows(c, nseq, ids, nullptr, st, &d_seq, &d_t))
@@ -1741,10 +1888,8 @@ static int kv_stage(nda_ctx *c, uint32_t layer, uint32_t seq, uint32_t p0, uint3
         return fail(c, NDA_ERR_ARG, "bad layer or null buffer");
     if (count == 0)
         return NDA_OK;
-    std::vector<int32_t> pg;
-    std::vector<uint32_t> off;
-    if (int rc = locate(c, seq, p0, count, write, pg, off))
-        return rc;
+    if (write && c->cfg.kv_dtype == NDA_KV_INT8 && (!ks || !vs))
+        return fail(c, NDA_ERR_ARG, "int8 write needs scales");
     const size_t es = c->cfg.kv_dtype == NDA_KV_F16 ? 2 : 1;
     const size_t nkv = c->cfg.n_kv_heads;
     const size_t kb = count * nkv * c->cfg.qk_head_dim * es, vb = count * nkv * c->cfg.v_head_dim * es;
@@ -1753,6 +1898,12 @@ static int kv_stage(nda_ctx *c, uint32_t layer, uint32_t seq, uint32_t p0, uint3
     const size_t total = kb + vb + 2 * sb + ib + 64;
     if (int rc = ensure_stage(c, total))
         return rc;
+    std::vector<int32_t> pg;
+    std::vector<uint32_t> off;
+    PageTxn txn(c);
+    if (int rc = locate(c, seq, p0, count, write, pg, off))
+        return rc;
+    txn.commit();
     uint8_t *d = c->d_stage;
     StageArgs a{};
     a.pool = c->pool + (uint64_t)layer * c->pg.layer_bytes;
@@ -1772,8 +1923,6 @@ static int kv_stage(nda_ctx *c, uint32_t layer, uint32_t seq, uint32_t p0, uint3
         HIPC(c, hipMemcpy(a.stage_k, k, kb, hipMemcpyHostToDevice));
         HIPC(c, hipMemcpy(a.stage_v, v, vb, hipMemcpyHostToDevice));
         if (c->cfg.kv_dtype == NDA_KV_INT8) {
-            if (!ks || !vs)
-                return fail(c, NDA_ERR_ARG, "int8 write needs scales");
             HIPC(c, hipMemcpy(a.stage_ks, ks, sb, hipMemcpyHostToDevice));
             HIPC(c, hipMemcpy(a.stage_vs, vs, sb, hipMemcpyHostToDevice));
         }
@@ -1818,6 +1967,10 @@ int nda_kv_fill_normal(nda_ctx *c, uint32_t nseq, const uint32_t *ids, uint64_t 
     if (int rc = check_ids(c, nseq, ids))
         return rc;
     hipStream_t st = (hipStream_t)stream;
+    if (ids)
+        if (int rc = ensure_rows(c, nseq))
+            return rc;
+    PageTxn txn(c);
     for (uint32_t b = 0; b < nseq; b++) {
         const uint32_t qq = sid(ids, b);
         const SeqHost &s = c->seqs[qq];
@@ -1827,6 +1980,7 @@ int nda_kv_fill_normal(nda_ctx *c, uint32_t nseq, const uint32_t *ids, uint64_t 
         if (int rc = back_slots(c, qq, 0, v.n_own))
             return rc;
     }
+    txn.commit();
     for (uint32_t b = 0; b < nseq; b++) {
         SeqHost &s = c->seqs[sid(ids, b)];
         s.stored_end = std::max(s.stored_end, s.pos);
@@ -1856,11 +2010,26 @@ int nda_dev_alloc(void **ptr, size_t bytes)
 {
     if (!ptr)
         return NDA_ERR_ARG;
-    hipError_t e = hipMalloc(ptr, bytes ? bytes : 1);
-    return e == hipSuccess ? NDA_OK : (e == hipErrorOutOfMemory ? NDA_ERR_NOMEM : NDA_ERR_HIP);
+    *ptr = dev_alloc(bytes);
+    return *ptr ? NDA_OK : NDA_ERR_NOMEM;
 }
 
-int nda_dev_free(void *ptr) { return hipFree(ptr) == hipSuccess ? NDA_OK : NDA_ERR_HIP; }
+int nda_dev_free(void *ptr)
+{
+    dev_free(ptr);
+    return NDA_OK;
+}
+
+int nda_set_allocator(nda_alloc_fn alloc, nda_free_fn free_fn, void *user)
+{
+    if (!alloc != !free_fn)
+        return NDA_ERR_ARG;
+    std::lock_guard<std::mutex> lk(g_alloc_mu);
+    g_alloc = alloc ? alloc : default_alloc;
+    g_free = alloc ? free_fn : default_free;
+    g_alloc_user = alloc ? user : nullptr;
+    return NDA_OK;
+}
 
 int nda_h2d(void *dst, const void *src, size_t bytes)
 {
@@ -1909,9 +2078,14 @@ int nda_cq_create(uint32_t out, uint32_t in, uint32_t group, uint32_t bits, cons
     }
     const size_t pb = (size_t)out * t->rowbytes, nb = (size_t)out * t->ngroup * 2;
     // +4 bytes: the bitstream reader may touch the byte after a straddling field
-    if (hipMalloc(&t->packed, pb + 4) != hipSuccess || hipMalloc(&t->norms, nb) != hipSuccess ||
-        hipMalloc(&t->cb, sizeof(float) << bits) != hipSuccess ||
-        hipMemcpy(t->packed, blob, pb, hipMemcpyHostToDevice) != hipSuccess ||
+    t->packed = static_cast<uint8_t *>(dev_alloc(pb + 4));
+    t->norms = static_cast<uint16_t *>(dev_alloc(nb));
+    t->cb = static_cast<float *>(dev_alloc(sizeof(float) << bits));
+    if (!t->packed || !t->norms || !t->cb) {
+        nda_cq_destroy(t);
+        return NDA_ERR_NOMEM;
+    }
+    if (hipMemcpy(t->packed, blob, pb, hipMemcpyHostToDevice) != hipSuccess ||
         hipMemset(t->packed + pb, 0, 4) != hipSuccess ||
         hipMemcpy(t->norms, (const uint8_t *)blob + pb, nb, hipMemcpyHostToDevice) != hipSuccess ||
         hipMemcpy(t->cb, codebook, sizeof(float) << bits, hipMemcpyHostToDevice) != hipSuccess) {
@@ -1927,9 +2101,10 @@ int nda_cq_create(uint32_t out, uint32_t in, uint32_t group, uint32_t bits, cons
         ta.in_pad = t->in_pad;
         ta.ngroup = t->ngroup;
         ta.rowbytes = t->rowbytes;
-        if (hipMalloc(&t->cw, (size_t)t->in_pad / 32 * out * 8) != hipSuccess ||
-            hipMalloc(&t->tab, (size_t)t->ngroup * out * 16) != hipSuccess ||
-            hipMalloc(&t->cexp, (size_t)out * 4) != hipSuccess) {
+        t->cw = static_cast<uint32_t *>(dev_alloc((size_t)t->in_pad / 32 * out * 8));
+        t->tab = static_cast<uint4 *>(dev_alloc((size_t)t->ngroup * out * 16));
+        t->cexp = static_cast<int32_t *>(dev_alloc((size_t)out * 4));
+        if (!t->cw || !t->tab || !t->cexp) {
             nda_cq_destroy(t);
             return NDA_ERR_NOMEM;
         }
@@ -1951,8 +2126,7 @@ int nda_cq_destroy(nda_cq *t)
         return NDA_OK;
     for (void *b : {(void *)t->packed, (void *)t->norms, (void *)t->cb, (void *)t->cw, (void *)t->tab,
                     (void *)t->cexp})
-        if (b)
-            (void)hipFree(b);
+        dev_free(b);
     delete t;
     return NDA_OK;
 }
@@ -2208,20 +2382,12 @@ int nda_prefill_block(nda_ctx *c, uint32_t layer, uint32_t nseq, const uint32_t 
     if (c->taps)
         if (int rc = front_check(c, layer, nseq, ids, n_tokens))
             return rc;
-    // Pages first: a full pool is reported before anything (tap histories
-    // included) has changed.
-    uint64_t rows = 0;
-    for (uint32_t b = 0; b < nseq; b++) {
-        const uint32_t qq = sid(ids, b);
-        if (n_tokens[b])
-            if (int rc = back_positions(c, qq, c->seqs[qq].pos, n_tokens[b]))
-                return rc;
-        rows += n_tokens[b];
-    }
+    PrefillPlan pl;
+    if (int rc = prefill_plan(c, nseq, ids, n_tokens, pl))
+        return rc;
+    const uint64_t rows = pl.rows;
     if (rows == 0)
         return NDA_OK;
-    if (rows > (1u << 26))
-        return fail(c, NDA_ERR_ARG, "too many prefill tokens (%llu)", (unsigned long long)rows);
     hipStream_t st = (hipStream_t)stream;
     const auto &w = c->blk[layer];
     const nda_config &g = c->cfg;
@@ -2232,8 +2398,30 @@ int nda_prefill_block(nda_ctx *c, uint32_t layer, uint32_t nseq, const uint32_t 
     const size_t nq = r4(w[0]->out), nk = r4(w[1]->out), nv = r4(w[2]->out), ng = r4(w[3]->out),
                  na = r4((size_t)g.n_heads * g.v_head_dim);
     const size_t nf = c->taps ? nq + nk + nv : 0;    // the front's outputs
+    // Every buffer the pass needs (its scratch, the front's row lists and
+    // history copies, the prefill's staging), then the pages: a call that
+    // fails for want of memory or pages changes nothing, tap histories
+    // included.
     if (int rc = ensure_buf(c, c->d_bscr, c->bscr_cap, pxh + (nq + nk + nv + ng + nf + na) * rows + pah))
         return rc;
+    if (c->taps) {
+        if (int rc = ensure_buf(c, c->d_front_rows, c->front_rows_cap, 3 * rows))
+            return rc;
+        if (int rc = hist_reserve(c, 0))
+            return rc;
+    }
+    if (int rc = prefill_reserve(c, pl))
+        return rc;
+    {
+        PageTxn txn(c);
+        for (uint32_t b = 0; b < nseq; b++) {
+            const uint32_t qq = sid(ids, b);
+            if (n_tokens[b])
+                if (int rc = back_positions(c, qq, c->seqs[qq].pos, n_tokens[b]))
+                    return rc;
+        }
+        txn.commit();
+    }
     // [part][row], each part at its tensor's own row width
     float *xh = c->d_bscr, *yq = xh + pxh, *yk = yq + nq * rows, *yv = yk + nk * rows,
           *yg = yv + nv * rows, *fq = yg + ng * rows, *fk = fq + nq * rows, *fv = fk + nk * rows,

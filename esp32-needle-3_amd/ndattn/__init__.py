@@ -32,7 +32,7 @@ ABI_SYMBOLS = [
     "nda_prefix_build", "nda_seq_attach", "nda_seq_rewind", "nda_prefix_free",
     "nda_kv_append", "nda_decode", "nda_decode_noalloc", "nda_step", "nda_prefill", "nda_sync",
     "nda_kv_read", "nda_kv_write", "nda_kv_fill_normal",
-    "nda_dev_alloc", "nda_dev_free", "nda_h2d", "nda_d2h", "nda_d2d", "nda_memset", "nda_fill_normal",
+    "nda_set_allocator", "nda_dev_alloc", "nda_dev_free", "nda_h2d", "nda_d2h", "nda_d2d", "nda_memset", "nda_fill_normal",
     "nda_host_alloc", "nda_host_free", "nda_h2d_async", "nda_d2h_async",
     "nda_stream_create", "nda_stream_destroy", "nda_device_sync", "nda_device_info",
     "nda_prof_enable", "nda_prof_read",
@@ -105,6 +105,7 @@ def lib():
             "nda_kv_read": (C.c_int, [vp, u32, u32, u32, u32, vp, vp, vp, vp]),
             "nda_kv_write": (C.c_int, [vp, u32, u32, u32, u32, vp, vp, vp, vp]),
             "nda_kv_fill_normal": (C.c_int, [vp, u32, vp, u64, vp]),
+            "nda_set_allocator": (C.c_int, [vp, vp, vp]),
             "nda_dev_alloc": (C.c_int, [C.POINTER(vp), C.c_size_t]),
             "nda_dev_free": (C.c_int, [vp]),
             "nda_h2d": (C.c_int, [vp, vp, C.c_size_t]),

@@ -344,7 +344,24 @@ int nda_kv_write(nda_ctx *ctx, uint32_t layer, uint32_t seq, uint32_t p0, uint32
 int nda_kv_fill_normal(nda_ctx *ctx, uint32_t nseq, const uint32_t *seq_ids, uint64_t seed,
                        void *stream);
 
-/* ---- device plumbing for hosts without their own allocator ---- */
+/* ---- device memory ---- */
+
+/* The device allocator every context, CQ tensor and nda_dev_alloc block is
+ * taken from: alloc returns `bytes` of device memory (16-byte aligned) or
+ * NULL, free releases a block alloc returned. Replaces the engine's platform
+ * allocation seams ND_ALLOC / ND_FREE (nd_model.h:35-68), which pick where
+ * its KV cache and scratch live; here they are set at run time for the
+ * process. NULL, NULL restores hipMalloc / hipFree. Blocks are freed through
+ * the free function current at that time, so switch only between
+ * allocators that can free each other's blocks (for example wrappers of one
+ * underlying allocator). A call that cannot get the memory it needs returns
+ * NDA_ERR_NOMEM and changes no session state. */
+typedef void *(*nda_alloc_fn)(size_t bytes, void *user);
+typedef void (*nda_free_fn)(void *ptr, void *user);
+int nda_set_allocator(nda_alloc_fn alloc, nda_free_fn free_fn, void *user);
+
+/* Device plumbing for hosts without their own allocator (through the
+ * allocator above). */
 int nda_dev_alloc(void **ptr, size_t bytes);
 int nda_dev_free(void *ptr);
 int nda_h2d(void *dst, const void *src, size_t bytes);

@@ -126,6 +126,24 @@ uint16_t ndo_f32_to_f16(float f)
     }
 }
 
+/* ndo_f16_to_f32 of every 16-bit pattern, built once: the same values,
+ * without the per-element branches. */
+static float g_f16_tab[65536];
+static pthread_once_t g_f16_once = PTHREAD_ONCE_INIT;
+
+static void f16_table_init(void)
+{
+    uint32_t h;
+    for (h = 0; h < 65536u; h++)
+        g_f16_tab[h] = ndo_f16_to_f32((uint16_t)h);
+}
+
+static const float *f16_table(void)
+{
+    pthread_once(&g_f16_once, f16_table_init);
+    return g_f16_tab;
+}
+
 /* Quotient by the residual (Markstein) form with one reciprocal: r = 1/scale,
  * y = x*r, e = fma(-scale, y, x), q = fma(e, r, y); plain x/scale for
  * |x| >= 1e30. Clamped to +-127 and rounded half-to-even by lrintf; a NaN
@@ -189,8 +207,9 @@ static void stage_row(const ndo_kv_view *kv, const void *base, uint32_t slot, ui
             dst[i] = (float)r[i];
     } else {
         const uint16_t *r = (const uint16_t *)base + off;
+        const float *tab = f16_table();
         for (i = 0; i < hd; i++)
-            dst[i] = ndo_f16_to_f32(r[i]);
+            dst[i] = tab[r[i]];
     }
 }
 
@@ -219,22 +238,29 @@ static float dot_pairs(const float *q, const float *k, uint32_t n)
     return s;
 }
 
-/* Score of one position for a head of a PAIR (qk_dot8, nd_model.c:2038-2083):
- * ascending pair sums over whole 8-column groups, then the remaining columns
- * one term at a time. Equals dot_pairs when qk_hd is a multiple of 8. */
-static float dot_pairs8(const float *q, const float *k, uint32_t n)
+/* The four scores of a head PAIR (A, B) over two positions (0, 1), as
+ * qk_dot8 computes them (nd_model.c:2038-2083): per score, ascending pair
+ * sums over whole 8-column groups, then the remaining columns one term at a
+ * time (equal to dot_pairs when qk_hd is a multiple of 8). */
+static void dot4_pairs8(const float *qA, const float *qB, const float *k0, const float *k1, uint32_t n,
+                        float *s)
 {
-    float s = 0.0f;
-    uint32_t i;
-    for (i = 0; i + 7u < n; i += 8u) {
-        s += q[i] * k[i] + q[i + 1u] * k[i + 1u];
-        s += q[i + 2u] * k[i + 2u] + q[i + 3u] * k[i + 3u];
-        s += q[i + 4u] * k[i + 4u] + q[i + 5u] * k[i + 5u];
-        s += q[i + 6u] * k[i + 6u] + q[i + 7u] * k[i + 7u];
+    float a0 = 0.0f, a1 = 0.0f, b0 = 0.0f, b1 = 0.0f;
+    uint32_t i, j;
+    for (i = 0; i + 7u < n; i += 8u)
+        for (j = i; j < i + 8u; j += 2u) {
+            a0 += qA[j] * k0[j] + qA[j + 1u] * k0[j + 1u];
+            a1 += qA[j] * k1[j] + qA[j + 1u] * k1[j + 1u];
+            b0 += qB[j] * k0[j] + qB[j + 1u] * k0[j + 1u];
+            b1 += qB[j] * k1[j] + qB[j + 1u] * k1[j + 1u];
+        }
+    for (; i < n; i++) {
+        a0 += qA[i] * k0[i];
+        a1 += qA[i] * k1[i];
+        b0 += qB[i] * k0[i];
+        b1 += qB[i] * k1[i];
     }
-    for (; i < n; i++)
-        s += q[i] * k[i];
-    return s;
+    s[0] = a0; s[1] = a1; s[2] = b0; s[3] = b1;
 }
 
 /* Sequential dot of the odd-tail position (nd_model.c:2319-2320). */
@@ -271,6 +297,54 @@ static void pair_step(head_state *h, float s0, float s1, float vs0, float vs1,
     for (i = 0; i < v_hd; i++) {
         h->oh[i] += wv0 * vf0[i];
         h->oh[i] += wv1 * vf1[i];
+    }
+}
+
+/* The max/rescale/exp/denominator part of a pair step for one head
+ * (nd_model.c:2217-2249); returns whether oh must be rescaled by *r. */
+static int pair_softmax(head_state *h, float s0, float s1, float *r, float *w0, float *w1)
+{
+    float mnew = s0 > s1 ? s0 : s1;
+    int rs = 0;
+    if (mnew > h->mx) {
+        if (h->denom > 0.0f) {
+            *r = ndo_expf(h->mx - mnew);
+            h->denom *= *r;
+            rs = 1;
+        }
+        h->mx = mnew;
+    }
+    ndo_expf_pair(s0 - h->mx, s1 - h->mx, w0, w1);
+    h->denom += *w0 + *w1;
+    return rs;
+}
+
+/* A pair step for two heads sharing the staged rows (pv_pair2,
+ * nd_model.c:1958-2024): each head's softmax step, then one pass over the
+ * cells applying each head's rescale and its w0 and w1 terms in pair_step's
+ * per-cell order. */
+static void pair_step2(head_state *a, head_state *b, const float *sc, float sc0, float sc1, float vs0,
+                       float vs1, const float *vf0, const float *vf1, uint32_t v_hd)
+{
+    float ra = 1.0f, rb = 1.0f, wa0, wa1, wb0, wb1, va0, va1, vb0, vb1;
+    int rsa = pair_softmax(a, sc[0] * sc0, sc[1] * sc1, &ra, &wa0, &wa1);
+    int rsb = pair_softmax(b, sc[2] * sc0, sc[3] * sc1, &rb, &wb0, &wb1);
+    uint32_t i;
+    if (rsa)
+        for (i = 0; i < v_hd; i++)
+            a->oh[i] *= ra;
+    if (rsb)
+        for (i = 0; i < v_hd; i++)
+            b->oh[i] *= rb;
+    va0 = wa0 * vs0;
+    va1 = wa1 * vs1;
+    vb0 = wb0 * vs0;
+    vb1 = wb1 * vs1;
+    for (i = 0; i < v_hd; i++) {
+        a->oh[i] += va0 * vf0[i];
+        a->oh[i] += va1 * vf1[i];
+        b->oh[i] += vb0 * vf0[i];
+        b->oh[i] += vb1 * vf1[i];
     }
 }
 
@@ -314,14 +388,18 @@ static void visit_run(const ndo_kv_view *kv, uint32_t g, uint32_t rep, const flo
         stage_row(kv, kv->k, sl1, g, kv->qk_hd, kf1);
         stage_row(kv, kv->v, sl0, g, kv->v_hd, vf0);
         stage_row(kv, kv->v, sl1, g, kv->v_hd, vf1);
-        for (t = 0; t < rep; t++) {
-            /* heads go in pairs (t, t+1) through qk_dot8; an odd group's last
-             * head takes the single-head dot (nd_model.c:2201-2266) */
-            float (*dot)(const float *, const float *, uint32_t) =
-                (t | 1u) < rep ? dot_pairs8 : dot_pairs;
+        /* heads go in pairs (t, t+1) through qk_dot8; an odd group's last
+         * head takes the single-head dot (nd_model.c:2201-2266) */
+        for (t = 0; t + 1u < rep; t += 2u) {
+            const float *qA = q + (size_t)(g * rep + t) * kv->qk_hd;
+            float sc[4];
+            dot4_pairs8(qA, qA + kv->qk_hd, kf0, kf1, kv->qk_hd, sc);
+            pair_step2(&hs[t], &hs[t + 1u], sc, sc0, sc1, vs0, vs1, vf0, vf1, kv->v_hd);
+        }
+        if (t < rep) {
             const float *qh = q + (size_t)(g * rep + t) * kv->qk_hd;
-            float s0 = dot(qh, kf0, kv->qk_hd) * sc0;
-            float s1 = dot(qh, kf1, kv->qk_hd) * sc1;
+            float s0 = dot_pairs(qh, kf0, kv->qk_hd) * sc0;
+            float s1 = dot_pairs(qh, kf1, kv->qk_hd) * sc1;
             pair_step(&hs[t], s0, s1, vs0, vs1, vf0, vf1, kv->v_hd);
         }
     }

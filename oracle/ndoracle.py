@@ -190,6 +190,9 @@ def ref():
         R.ref_block_setup.argtypes = [C.c_void_p, C.c_uint32, C.c_uint32, C.c_void_p, C.c_void_p]
         R.ref_block_setup.restype = C.c_int
         R.ref_attention_block.argtypes = [C.c_void_p, C.c_uint32] + [C.c_void_p] * 7
+        R.ref_attention_rounds.restype = C.c_double
+        R.ref_attention_rounds.argtypes = [C.c_void_p, C.c_uint32, C.c_uint32] + [C.c_void_p] * 4 + \
+            [C.c_uint32] * 3
         _ref = R
     return _ref
 

@@ -10,6 +10,6 @@ SRCS = $(ENG)/src/nd_quant.c $(ENG)/src/nd_cact.c $(ENG)/src/nd_tokenizer.c
 
 _ref/libndref.so: ref_harness.c $(SRCS) $(ENG)/src/nd_model.c
 	mkdir -p _ref
-	$(CC) $(CFLAGS) -shared -o $@ ref_harness.c $(SRCS) -lm
+	$(CC) $(CFLAGS) -shared -o $@ ref_harness.c $(SRCS) -lm -lpthread
 
 .PHONY: _ref/libndref.so

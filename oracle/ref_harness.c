@@ -20,7 +20,9 @@
  */
 #include "nd_model.c"
 
+#include <pthread.h>
 #include <stdio.h>
+#include <time.h>
 
 uint32_t ref_kv_slot(uint32_t window, uint32_t n_sink, uint32_t p)
 {
@@ -374,4 +376,65 @@ void ref_attention_block(void *vm, uint32_t li, const float *tap_q, const float 
     m->fp16_slot[li][7] = (float *)norm_q;
     m->fp16_slot[li][8] = (float *)norm_k;
     attention(m, li, xin, out);
+}
+
+/* ------------------------------------------------- CPU baseline timing */
+
+/* The batched-decode CPU baseline: n independent sessions (one per
+ * sequence), each taking one store + attention() step per round, split over
+ * nthreads threads by contiguous session ranges - the engine has one session
+ * per model and no shared writable state on this path, so sessions run side
+ * by side as separate models would. Each thread writes its own output row.
+ * Returns the wall time of `rounds` rounds in seconds, CLOCK_MONOTONIC (as
+ * host/nd_prof.c:45-49 times the engine). */
+typedef struct {
+    void **models;
+    uint32_t lo, hi, li, rounds;
+    const float *q, *k, *v;
+    float *out;
+} ref_rounds_job;
+
+static void *ref_rounds_worker(void *arg)
+{
+    ref_rounds_job *j = (ref_rounds_job *)arg;
+    uint32_t r, s;
+    for (r = 0; r < j->rounds; r++)
+        for (s = j->lo; s < j->hi; s++)
+            ref_attention(j->models[s], j->li, j->q, j->k, j->v, NULL, j->out);
+    return NULL;
+}
+
+double ref_attention_rounds(void **models, uint32_t n, uint32_t li, const float *q, const float *k,
+                            const float *v, float *out, uint32_t out_stride, uint32_t rounds,
+                            uint32_t nthreads)
+{
+    pthread_t th[256];
+    ref_rounds_job jobs[256];
+    struct timespec t0, t1;
+    uint32_t t;
+    if (nthreads < 1)
+        nthreads = 1;
+    if (nthreads > 256)
+        nthreads = 256;
+    if (nthreads > n)
+        nthreads = n;
+    for (t = 0; t < nthreads; t++) {
+        jobs[t].models = models;
+        jobs[t].lo = (uint32_t)((uint64_t)n * t / nthreads);
+        jobs[t].hi = (uint32_t)((uint64_t)n * (t + 1) / nthreads);
+        jobs[t].li = li;
+        jobs[t].rounds = rounds;
+        jobs[t].q = q;
+        jobs[t].k = k;
+        jobs[t].v = v;
+        jobs[t].out = out + (size_t)t * out_stride;
+    }
+    clock_gettime(CLOCK_MONOTONIC, &t0);
+    for (t = 1; t < nthreads; t++)
+        pthread_create(&th[t], NULL, ref_rounds_worker, &jobs[t]);
+    ref_rounds_worker(&jobs[0]);
+    for (t = 1; t < nthreads; t++)
+        pthread_join(th[t], NULL);
+    clock_gettime(CLOCK_MONOTONIC, &t1);
+    return (double)(t1.tv_sec - t0.tv_sec) + 1e-9 * (double)(t1.tv_nsec - t0.tv_nsec);
 }
