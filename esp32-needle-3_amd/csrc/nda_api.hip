@@ -7,6 +7,7 @@
 // refreshed on the caller's stream right before the launch that reads them.
 #include "nda.h"
 #include "nda_internal.h"
+#include "nda_state.h"
 
 #include <algorithm>
 #include <array>
@@ -21,6 +22,7 @@
 #include <vector>
 
 using namespace nda;
+using namespace nda_host;
 
 // Scratch of nda_decode_noalloc: the launch's sequence ids, then its split-KV
 // partials. One array per GPU, held until the process ends. Host code never
@@ -81,24 +83,6 @@ void dev_free(void *p)
     g_free(p, g_alloc_user);
 }
 
-constexpr uint32_t MIN_RECENT = 64;   // ND_MIN_RECENT, engine/src/nd_model.c:1311-1312
-
-struct Prefix {
-    bool used = false;
-    uint32_t len = 0;       // positions stored: [0, len)
-    uint32_t n_sink = 0;    // pinned count (clamped len)
-    uint32_t refs = 0;      // sequences attached
-};
-
-struct SeqHost {
-    uint32_t pos = 0, n_sink = 0;
-    int32_t prefix = -1;
-    bool has_snap = false;
-    uint32_t snap_pos = 0;
-    uint32_t stored_end = 0;   // one past the highest position stored
-    uint32_t ring_lo = 0;      // ring positions in [n_sink, ring_lo) were overwritten before a rewind
-};
-
 struct ProfRec {
     int kind;
     hipEvent_t a, b;
@@ -129,15 +113,10 @@ struct nda_ctx {
     uint64_t dev_bytes = 0;
     uint8_t *scratch = nullptr;         // this device's nda_decode_noalloc scratch
 
-    std::vector<int32_t> pages, prefix_pages;
+    PageTables pt;                      // page tables, free list, journal (host mirror)
     std::vector<SeqHost> seqs;
     std::vector<Prefix> prefixes;
-    std::vector<int32_t> free_pages;
-    std::vector<size_t> journal;        // page-table entries backed by the open transaction
-    int txn_depth = 0;
     bool seqs_dirty = true;
-    uint32_t dirty_lo = UINT32_MAX, dirty_hi = 0;   // page-table rows to upload
-    bool prefix_dirty = true;
 
     // attention front (nda_front_init): tap histories, weights, rotary table
     uint32_t taps = 0, max_pos = 0, dcol = 0;
@@ -201,134 +180,25 @@ int hip_fail(nda_ctx *c, hipError_t e, const char *what)
             return hip_fail((c), e_, #call);               \
     } while (0)
 
-inline uint32_t clamp_sink(uint32_t window, uint32_t n)
-{
-    uint32_t cap = window > MIN_RECENT ? window - MIN_RECENT : 0;
-    return n < cap ? n : cap;
-}
-
-// Same mapping as the kernels' own_slot (kv_slot, nd_model.c:1302-1309).
-inline uint32_t own_slot(const SeqHost &s, uint32_t p, uint32_t window)
-{
-    if (s.prefix >= 0)
-        return (p - s.n_sink) % (window - s.n_sink);
-    if (p < s.n_sink)
-        return p;
-    return s.n_sink + (p - s.n_sink) % (window - s.n_sink);
-}
-
-struct Vis {
-    uint32_t n_sh, n_own;
-};
-
-inline Vis visible(const SeqHost &s, uint32_t p, uint32_t window)
-{
-    uint32_t sinks = std::min(s.n_sink, p + 1);
-    uint32_t rcap = window - s.n_sink;
-    uint32_t rcount = (p + 1 <= s.n_sink) ? 0 : std::min(p + 1 - s.n_sink, rcap);
-    Vis v;
-    v.n_sh = s.prefix >= 0 ? sinks : 0;
-    v.n_own = s.prefix >= 0 ? rcount : sinks + rcount;
-    return v;
-}
-
-inline void mark_rows(nda_ctx *c, uint32_t seq)
-{
-    c->dirty_lo = std::min(c->dirty_lo, seq);
-    c->dirty_hi = std::max(c->dirty_hi, seq + 1);
-}
-
-void release_pages(nda_ctx *c, uint32_t seq)
-{
-    int32_t *row = &c->pages[(size_t)seq * c->pg.pages_per_seq];
-    for (uint32_t i = 0; i < c->pg.pages_per_seq; i++) {
-        if (row[i] >= 0) {
-            c->free_pages.push_back(row[i]);
-            row[i] = -1;
-        }
-    }
-    mark_rows(c, seq);
-}
+void release_pages(nda_ctx *c, uint32_t seq) { c->pt.release(seq); }
 
 // Back own slots [s0, s1) of a sequence with pages. All-or-nothing.
 int back_slots(nda_ctx *c, uint32_t seq, uint32_t s0, uint32_t s1)
 {
-    if (s1 <= s0)
-        return NDA_OK;
-    int32_t *row = &c->pages[(size_t)seq * c->pg.pages_per_seq];
-    uint32_t p0 = s0 >> c->pg.log2_page, p1 = (s1 - 1) >> c->pg.log2_page;
-    size_t need = 0;
-    for (uint32_t i = p0; i <= p1; i++)
-        need += row[i] < 0;
-    if (need > c->free_pages.size())
-        return fail(c, NDA_ERR_NOMEM, "page pool exhausted: need %zu pages, %zu free", need,
-                    c->free_pages.size());
-    for (uint32_t i = p0; i <= p1; i++) {
-        if (row[i] < 0) {
-            row[i] = c->free_pages.back();
-            c->free_pages.pop_back();
-            mark_rows(c, seq);
-            if (c->txn_depth)
-                c->journal.push_back((size_t)seq * c->pg.pages_per_seq + i);
-        }
-    }
+    if (!c->pt.back_slots(seq, s0, s1))
+        return fail(c, NDA_ERR_NOMEM, "page pool exhausted: need %zu pages, %zu free", c->pt.need(seq, s0, s1),
+                    c->pt.free_pages.size());
     return NDA_OK;
 }
 
-// The pages a call backs stay journaled until it commits; a call that fails
-// part-way (the pool runs out for a later sequence, a buffer cannot grow)
-// gives them back in reverse order, so the page tables and the free list are
-// as before the call.
-struct PageTxn {
-    nda_ctx *c;
-    size_t mark;
-    bool open = true;
-    explicit PageTxn(nda_ctx *c_) : c(c_), mark(c_->journal.size()) { c->txn_depth++; }
-    void commit()
-    {
-        if (open) {
-            open = false;
-            c->txn_depth--;
-            if (!c->txn_depth)
-                c->journal.clear();
-        }
-    }
-    ~PageTxn()
-    {
-        if (!open)
-            return;
-        while (c->journal.size() > mark) {
-            const size_t idx = c->journal.back();
-            c->journal.pop_back();
-            c->free_pages.push_back(c->pages[idx]);
-            c->pages[idx] = -1;
-            mark_rows(c, (uint32_t)(idx / c->pg.pages_per_seq));
-        }
-        c->txn_depth--;
-    }
-};
-
-// Back the own slot(s) of positions [p0, p0 + n) (no wrap inside, n >= 1).
+// Back the own slot(s) of positions [p0, p0 + n) (no wrap inside, n >= 1);
+// pages an earlier run took before the pool ran out stay until the caller's
+// transaction gives them back.
 int back_positions(nda_ctx *c, uint32_t seq, uint32_t p0, uint32_t n)
 {
-    const SeqHost &s = c->seqs[seq];
-    const uint32_t W = c->pg.window;
-    // Positions map to consecutive slots until the ring wraps; walk in runs.
-    uint32_t p = p0, end = p0 + n;
-    while (p < end) {
-        uint32_t sl = own_slot(s, p, W);
-        uint32_t run;
-        if (s.prefix < 0 && p < s.n_sink)
-            run = std::min(end, s.n_sink) - p;
-        else {
-            uint32_t ring_end = (s.prefix >= 0 ? 0u : s.n_sink) + (W - s.n_sink);
-            run = std::min(end - p, ring_end - sl);
-        }
-        int rc = back_slots(c, seq, sl, sl + run);
-        if (rc)
-            return rc;
-        p += run;
-    }
+    if (!c->pt.back_positions(seq, c->seqs[seq], p0, n, c->pg.window))
+        return fail(c, NDA_ERR_NOMEM, "page pool exhausted (sequence %u, %zu pages free)", seq,
+                    c->pt.free_pages.size());
     return NDA_OK;
 }
 
@@ -345,18 +215,18 @@ int sync_tables(nda_ctx *c, hipStream_t st)
         HIPC(c, hipMemcpyAsync(c->d_seqs, tmp.data(), tmp.size() * sizeof(SeqDev), hipMemcpyHostToDevice, st));
         c->seqs_dirty = false;
     }
-    if (c->dirty_lo < c->dirty_hi) {
-        size_t off = (size_t)c->dirty_lo * c->pg.pages_per_seq;
-        size_t n = (size_t)(c->dirty_hi - c->dirty_lo) * c->pg.pages_per_seq;
-        HIPC(c, hipMemcpyAsync(c->d_pages + off, c->pages.data() + off, n * sizeof(int32_t),
+    if (c->pt.dirty_lo < c->pt.dirty_hi) {
+        size_t off = (size_t)c->pt.dirty_lo * c->pg.pages_per_seq;
+        size_t n = (size_t)(c->pt.dirty_hi - c->pt.dirty_lo) * c->pg.pages_per_seq;
+        HIPC(c, hipMemcpyAsync(c->d_pages + off, c->pt.pages.data() + off, n * sizeof(int32_t),
                                hipMemcpyHostToDevice, st));
-        c->dirty_lo = UINT32_MAX;
-        c->dirty_hi = 0;
+        c->pt.dirty_lo = UINT32_MAX;
+        c->pt.dirty_hi = 0;
     }
-    if (c->prefix_dirty) {
-        HIPC(c, hipMemcpyAsync(c->d_prefix_pages, c->prefix_pages.data(),
-                               c->prefix_pages.size() * sizeof(int32_t), hipMemcpyHostToDevice, st));
-        c->prefix_dirty = false;
+    if (c->pt.prefix_dirty) {
+        HIPC(c, hipMemcpyAsync(c->d_prefix_pages, c->pt.prefix_pages.data(),
+                               c->pt.prefix_pages.size() * sizeof(int32_t), hipMemcpyHostToDevice, st));
+        c->pt.prefix_dirty = false;
     }
     return NDA_OK;
 }
@@ -795,20 +665,13 @@ int nda_create(const nda_config *cfg_in, nda_ctx **out)
     }
     c->dev_bytes += pt * 4 + ppt * 4 + (size_t)cfg.max_seqs * sizeof(SeqDev);
     try {
-        c->pages.assign(pt, -1);
-        c->prefix_pages.assign(ppt, -1);
+        c->pt.init(cfg.max_seqs, cfg.max_prefixes, c->pg.pages_per_seq, c->pg.log2_page, c->max_pages);
         c->seqs.assign(cfg.max_seqs, SeqHost());
         c->prefixes.assign(cfg.max_prefixes, Prefix());
-        c->free_pages.resize(c->max_pages);
     } catch (...) {
         nda_destroy(c);
         return NDA_ERR_NOMEM;
     }
-    // Hand out low page ids first.
-    for (uint64_t i = 0; i < c->max_pages; i++)
-        c->free_pages[i] = (int32_t)(c->max_pages - 1 - i);
-    c->dirty_lo = 0;
-    c->dirty_hi = cfg.max_seqs;
     *out = c;
     return NDA_OK;
 }
@@ -907,7 +770,7 @@ int nda_seq_reserve(nda_ctx *c, uint32_t seq, uint32_t n)
     const SeqHost &s = c->seqs[seq];
     // Once the ring is full every slot is backed; cap at one full cycle.
     uint32_t cap = c->cfg.window - (s.prefix >= 0 ? s.n_sink : 0);
-    PageTxn txn(c);
+    PageTxn txn(c->pt);
     if (int rc = back_positions(c, seq, s.pos, std::min(n, cap)))
         return rc;
     txn.commit();
@@ -963,16 +826,11 @@ int nda_prefix_build(nda_ctx *c, uint32_t seq, int32_t *prefix_id, void *stream)
     if (id < 0)
         return fail(c, NDA_ERR_NOMEM, "all %u prefix segments in use", c->cfg.max_prefixes);
     const uint32_t npages = (len + c->cfg.page_size - 1) / c->cfg.page_size;
-    if (npages > c->free_pages.size())
+    if (npages > c->pt.free_pages.size())
         return fail(c, NDA_ERR_NOMEM, "page pool exhausted building a prefix");
     if (int rc = hist_reserve(c, 2))
         return rc;
-    int32_t *prow = &c->prefix_pages[(size_t)id * c->pg.pages_per_seq];
-    for (uint32_t i = 0; i < npages; i++) {
-        prow[i] = c->free_pages.back();
-        c->free_pages.pop_back();
-    }
-    c->prefix_dirty = true;
+    c->pt.take_prefix(id, npages);
     if (int rc = sync_tables(c, st))
         return rc;
 
@@ -1040,10 +898,7 @@ int nda_seq_attach(nda_ctx *c, uint32_t seq, int32_t id, void *stream)
         // the ring tail's pages, from the free pool plus this sequence's own
         const uint32_t tail = pf.len > pf.n_sink ? pf.len - pf.n_sink : 0u;
         const size_t need = (tail + c->cfg.page_size - 1) / c->cfg.page_size;
-        size_t have = c->free_pages.size();
-        const int32_t *row = &c->pages[(size_t)seq * c->pg.pages_per_seq];
-        for (uint32_t i = 0; i < c->pg.pages_per_seq; i++)
-            have += row[i] >= 0;
+        const size_t have = c->pt.free_pages.size() + c->pt.backed(seq);
         if (need > have)
             return fail(c, NDA_ERR_NOMEM, "page pool exhausted: need %zu pages, %zu free", need, have);
         if (int rc = hist_reserve(c, 2))
@@ -1122,14 +977,8 @@ int nda_prefix_free(nda_ctx *c, int32_t id)
         return fail(c, NDA_ERR_ARG, "prefix %d does not exist", id);
     if (c->prefixes[id].refs)
         return fail(c, NDA_ERR_STATE, "prefix %d is attached to %u sequences", id, c->prefixes[id].refs);
-    int32_t *prow = &c->prefix_pages[(size_t)id * c->pg.pages_per_seq];
-    for (uint32_t i = 0; i < c->pg.pages_per_seq; i++)
-        if (prow[i] >= 0) {
-            c->free_pages.push_back(prow[i]);
-            prow[i] = -1;
-        }
+    c->pt.release_prefix(id);
     c->prefixes[id] = Prefix();
-    c->prefix_dirty = true;
     return NDA_OK;
 }
 
@@ -1146,7 +995,7 @@ int nda_kv_append(nda_ctx *c, uint32_t layer, uint32_t nseq, const uint32_t *ids
     if (ids)
         if (int rc = ensure_rows(c, nseq))
             return rc;
-    PageTxn txn(c);
+    PageTxn txn(c->pt);
     for (uint32_t b = 0; b < nseq; b++) {
         const uint32_t q = sid(ids, b);
         if (int rc = back_positions(c, q, c->seqs[q].pos, 1))
@@ -1202,7 +1051,7 @@ static int decode_check(nda_ctx *c, uint32_t layer, uint32_t nseq, const uint32_
         *max_total = std::max(*max_total, vv.n_sh + vv.n_own);
         *sum_total += vv.n_sh + vv.n_own;
         if (vv.n_own) {
-            const int32_t *row = &c->pages[(size_t)qq * c->pg.pages_per_seq];
+            const int32_t *row = &c->pt.pages[(size_t)qq * c->pg.pages_per_seq];
             if (row[(vv.n_own - 1) >> c->pg.log2_page] < 0 || row[0] < 0)
                 return fail(c, NDA_ERR_STATE, "sequence %u: slot of position %u never stored", qq, s.pos);
         }
@@ -1223,7 +1072,7 @@ static int decode_impl(nda_ctx *c, uint32_t layer, uint32_t nseq, const uint32_t
         return rc;
     // The fused store backs this position's slot first; the pages go back if
     // anything below fails.
-    PageTxn txn(c);
+    PageTxn txn(c->pt);
     if (k)
         for (uint32_t b = 0; b < nseq; b++) {
             const uint32_t qq = sid(ids, b);
@@ -1425,7 +1274,7 @@ int nda_prefill(nda_ctx *c, uint32_t layer, uint32_t nseq, const uint32_t *ids, 
     // a call that fails for want of memory changes nothing.
     if (int rc = prefill_reserve(c, pl))
         return rc;
-    PageTxn txn(c);
+    PageTxn txn(c->pt);
     for (uint32_t b = 0; b < nseq; b++) {
         const uint32_t qq = sid(ids, b);
         if (n_tokens[b])
@@ -1771,7 +1620,7 @@ int nda_attention(nda_ctx *c, uint32_t layer, uint32_t nseq, const uint32_t *ids
         return rc;
     if (int rc = hist_reserve(c, 0))
         return rc;
-    PageTxn txn(c);
+    PageTxn txn(c->pt);
     uint32_t max_total = 0;
     uint64_t sum_total = 0;
     for (uint32_t b = 0; b < nseq; b++) {
@@ -1853,7 +1702,7 @@ static int locate(nda_ctx *c, uint32_t seq, uint32_t p0, uint32_t count, bool fo
         if (s.prefix >= 0 && p < s.n_sink) {
             if (for_write)
                 return fail(c, NDA_ERR_STATE, "position %u belongs to the shared prefix", p);
-            pg[i] = c->prefix_pages[(size_t)s.prefix * c->pg.pages_per_seq + p / P];
+            pg[i] = c->pt.prefix_pages[(size_t)s.prefix * c->pg.pages_per_seq + p / P];
             off[i] = p % P;
             continue;
         }
@@ -1869,7 +1718,7 @@ static int locate(nda_ctx *c, uint32_t seq, uint32_t p0, uint32_t count, bool fo
         if (for_write)
             if (int rc = back_slots(c, seq, sl, sl + 1))
                 return rc;
-        pg[i] = c->pages[(size_t)seq * c->pg.pages_per_seq + sl / P];
+        pg[i] = c->pt.pages[(size_t)seq * c->pg.pages_per_seq + sl / P];
         off[i] = sl % P;
         if (pg[i] < 0)
             return fail(c, NDA_ERR_STATE, "position %u was never stored", p);
@@ -1900,7 +1749,7 @@ static int kv_stage(nda_ctx *c, uint32_t layer, uint32_t seq, uint32_t p0, uint3
         return rc;
     std::vector<int32_t> pg;
     std::vector<uint32_t> off;
-    PageTxn txn(c);
+    PageTxn txn(c->pt);
     if (int rc = locate(c, seq, p0, count, write, pg, off))
         return rc;
     txn.commit();
@@ -1970,7 +1819,7 @@ int nda_kv_fill_normal(nda_ctx *c, uint32_t nseq, const uint32_t *ids, uint64_t 
     if (ids)
         if (int rc = ensure_rows(c, nseq))
             return rc;
-    PageTxn txn(c);
+    PageTxn txn(c->pt);
     for (uint32_t b = 0; b < nseq; b++) {
         const uint32_t qq = sid(ids, b);
         const SeqHost &s = c->seqs[qq];
@@ -2413,7 +2262,7 @@ int nda_prefill_block(nda_ctx *c, uint32_t layer, uint32_t nseq, const uint32_t 
     if (int rc = prefill_reserve(c, pl))
         return rc;
     {
-        PageTxn txn(c);
+        PageTxn txn(c->pt);
         for (uint32_t b = 0; b < nseq; b++) {
             const uint32_t qq = sid(ids, b);
             if (n_tokens[b])
