@@ -541,24 +541,24 @@ void prefill_kernel(PrefillArgs a)
 // ------------------------------------------------------------ GQA decode
 //
 // Decode of a GQA group (rep >= 4) on MFMA: one wave per (row, kv-head), the
-// group's rep query heads as the wave's rows (32 row slots, rep of them
+// group's rep query heads as the wave's columns (16 slots, rep of them
 // valid), every visible slot as its keys, in slot order (sinks, shared
 // prefix and ring alike; softmax does not depend on the order, and the
-// visible set is the engine's, engine/src/nd_model.c:2451-2483). The tile
-// arithmetic is the prefill kernel's (S^T = K.Q^T and O^T += V^T.P^T with
-// fp16 hi + lo operands, the lazy running max); only keys past the last
-// visible slot are masked. The per-lane dot products, lane reductions and
-// fp32 conversions that bound the VALU decode kernel at this shape move to
-// the matrix cores.
+// visible set is the engine's, engine/src/nd_model.c:2451-2483). Per 32-key
+// tile:
+//   S^T[32 keys x 16 cols]  = K . Q^T          v_mfma_f32_16x16x32_f16
+//   O^T[64 dims x 16 cols] += V^T . P^T
+// Q and P are fp16 hi + lo pairs (two MFMAs each): fp32-level accuracy, as in
+// the prefill kernel; the lazy running max likewise.
 //
-// Staging: lane (ln, jh) moves half jh of key ln of a 32-key tile (K codes
-// [DK/2 jh, +DK/2), V codes [32 jh, +32) and the key's K (jh 0) or V (jh 1)
-// scale), so each lane needs one page id a tile, fetched a tile ahead. The
-// loads are unconditional (a key past the last visible slot reads the last
-// one: finite data, masked). int8 codes become fp16 exactly with one byte
-// permute and one packed fp16 subtract per two codes: 0x64 over the byte
-// (code ^ 0x80) is the fp16 1024 + code + 128. One wave owns its LDS tile,
-// whose accesses complete in order, so one buffer serves.
+// K/V stay int8 codes in LDS, written raw with 16-byte stores from the
+// registers a tile was loaded into, and become fp16 as they are read into an
+// operand: one xor, two byte permutes and two packed fp16 subtracts per four
+// codes (0x64 over the byte code ^ 0x80 is the fp16 1024 + code + 128). V^T
+// comes out of row-major V with ds_read_b64_tr_b8 (in each 16-lane group,
+// output lane i byte j is byte i % 8 at the address of lane 2 j + i / 8). The
+// k scale multiplies S and the v scale folds into P: the engine's
+// dequantisation (engine/src/nd_model.c:2179-2180, :2250-2252).
 template <int SEL>
 __device__ __forceinline__ half2v codes2(uint32_t xs)   // xs = codes ^ 0x80808080
 {
@@ -566,25 +566,58 @@ __device__ __forceinline__ half2v codes2(uint32_t xs)   // xs = codes ^ 0x808080
     return __builtin_bit_cast(half2v, u) - half2v{(_Float16)1152.0f, (_Float16)1152.0f};
 }
 
+// eight int8 codes (bytes 0..7 of w) as fp16, in byte order
+__device__ __forceinline__ half8 codes8(u32x2 w)
+{
+    const uint32_t x0 = w.x ^ 0x80808080u, x1 = w.y ^ 0x80808080u;
+    const half2v c0 = codes2<0x04010400>(x0), c1 = codes2<0x04030402>(x0);
+    const half2v c2 = codes2<0x04010400>(x1), c3 = codes2<0x04030402>(x1);
+    return half8{c0[0], c0[1], c1[0], c1[1], c2[0], c2[1], c3[0], c3[1]};
+}
+
+// four int8 codes as the low k slots of an operand whose upper four are zero
+__device__ __forceinline__ half8 codes4(uint32_t w)
+{
+    const uint32_t x = w ^ 0x80808080u;
+    const half2v c0 = codes2<0x04010400>(x), c1 = codes2<0x04030402>(x);
+    return half8{c0[0], c0[1], c1[0], c1[1], 0, 0, 0, 0};
+}
+
 typedef float float4v __attribute__((ext_vector_type(4)));
+typedef int v2i __attribute__((ext_vector_type(2)));
+typedef __attribute__((address_space(3))) v2i lds_v2i;
+typedef const __attribute__((address_space(4))) int32_t *cptr;
 
 __device__ __forceinline__ float4v mfma16k32(half8 a, half8 b, float4v c)
 {
     return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
 }
 
-// 16 x 16 tiles: lane l = 16 g + r holds MFMA row / column r and the k (or
-// output row) slots of lane group g. A wave's 16 row slots hold the group's
-// rep heads; a 32-key tile is two 16-key blocks of S^T = K.Q^T (lane: row r,
-// keys 16 b + 4 g + i), whose eight scores per lane are, in that order, the
-// P^T operand of O^T += V^T.P^T over the 32 keys (lane group g's k slots),
-// so V^T is read in the same key order. A row's softmax state spans the four
-// lane groups (a max and a sum across them).
+// Lane layouts (16 x 16 tiles): lane l = 16 g + r holds MFMA row / column r
+// and the k (or output row) slots of lane group g. Row r of S block kb reads
+// key 8 (r / 4) + 4 kb + r % 4, so the S^T rows lane (r, g) receives are keys
+// 8 g + 4 kb + i: its eight scores are keys 8 g .. 8 g + 7 in order, which is
+// the k-slot order of the P^T operand, and V^T is read for the same keys.
+// A column's softmax state spans the four lane groups (a max and a sum
+// across them).
+//
+// Tiles are 32 slots of one segment (the shared prefix's pages, then the
+// sequence's own), aligned to 32 within it, so a tile's keys 16 h .. 16 h + 15
+// are consecutive slots of one page: per half tile, one load each reads its
+// K rows, V rows and scales, contiguous runs of the page (every cache line
+// requested once). A segment's last tile can be partial: its surplus keys
+// read slots of the same pages (or half 0 again) and are masked.
+//
+// A wave keeps one tile in flight in registers (loaded while the previous
+// one is computed) and one in its LDS buffer. Splitting a row's tiles over
+// more waves (and merging their states) measured no faster: the launch is
+// bound by its memory stream, not by the wave count.
 template <int DK, int DV, int REP>
 __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(4)))
 void decode_mfma_kernel(PrefillArgs a)
 {
-    static_assert(DK % 16 == 0 && DV == 64 && REP <= 16, "decode tiles: dk multiple of 16, dv 64, rep <= 16");
+    static_assert(DK % 16 == 0 && DK <= 64 && DV == 64 && REP <= 16,
+                  "decode tiles: dk multiple of 16 up to 64, dv 64, rep <= 16");
     constexpr int NS = DK / 32;                 // 32-dim steps of S (16x16x32)
     // A last 16-dim step (qk 48) runs on the same 16x16x32 instruction, its
     // upper four k slots zero in both operands. Every accumulation chain
@@ -593,30 +626,106 @@ void decode_mfma_kernel(PrefillArgs a)
     // 16x16x32), gave wrong results on gfx950 although the compiler puts no
     // wait state between them, as it does for the same opcode.
     constexpr bool TAIL = DK % 32 == 16;
-    constexpr int KPAD = DK + 8, VPAD = PF_KT + 4;
-    constexpr int KH = DK / 2, VH = DV / 2;     // codes a lane moves per key
-    static_assert(KH % 8 == 0 && VH % 16 == 0, "lane halves are whole 8- and 16-byte loads");
-    __shared__ __attribute__((aligned(16))) _Float16 Ks[PF_KT][KPAD];
-    __shared__ __attribute__((aligned(16))) _Float16 Vt[DV][VPAD];
-    __shared__ __attribute__((aligned(16))) float Sc[2][PF_KT];   // K, V scales of the tile's keys
+    constexpr int VSTR = DV + 16;               // V row stride: spreads the transposed reads over the banks
+    constexpr int KB = PF_KT * DK, VB = PF_KT * VSTR;
+    __shared__ __attribute__((aligned(16))) uint8_t lds[KB + VB + PF_KT * 8];   // K, V, k scales, v scales
 
     const int lane = threadIdx.x;
-    const int jh = lane >> 5, ln = lane & 31;   // staging: key ln, half jh
     const int g = lane >> 4, r = lane & 15;     // MFMA: lane group, row / column
     const uint32_t nkv = a.pg.nkv;
     const uint32_t b = blockIdx.x / nkv, kvh = blockIdx.x % nkv;
-    const uint32_t seq = a.row_seq ? a.row_seq[b] : b;
-    const SeqDev sd = a.seqs[seq];
+    // row ids, sequence state and page tables are read-only during the
+    // launch and uniform per wave: read through the constant address space
+    // (scalar loads)
+    const uint32_t seq = a.row_seq ? *(const __attribute__((address_space(4))) uint32_t *)(a.row_seq + b) : b;
+    SeqDev sd;
+    {
+        const cptr sp = (cptr)(a.seqs + seq);
+        sd.pos = sp[0];
+        sd.n_sink = sp[1];
+        sd.prefix = sp[2];
+    }
     const Visible vis = visible(sd, sd.pos, (int)a.pg.window);
-    const int n_sh = vis.n_sh, total = vis.n_sh + vis.n_own;
+    const int n_sh = vis.n_sh, n_own = vis.n_own;
 
-    // Q^T operand, hi and lo: row r, dims 32 s + 8 g + [0, 8) and the tail
+    // Load plan of a half tile (16 keys), per lane: K chunk c = lane % DK (16
+    // bytes; with qk 48 lanes 48..63 repeat chunks 0..15: same data, same LDS
+    // bytes), V chunk `lane`, and scale word `lane % 32` (16 k scales, then
+    // 16 v scales). Offsets are from the kv-head block of the half's page;
+    // the half's first slot adds sip * DK, sip * DV and sip * 4.
+    const int P = 1 << a.pg.log2_page;
+    const uint32_t kc = 16 * (lane % DK);
+    const uint32_t gv = P * DK + 16 * lane;
+    const int lv = KB + (lane >> 2) * VSTR + 16 * (lane & 3);
+    const int sw = lane & 31, which = sw >> 4;
+    const uint32_t gs = P * (DK + DV) + which * 4 * P + 4 * (sw & 15);
+    const int ls = KB + VB + 128 * which + 4 * (sw & 15);
+
+    const cptr own = (cptr)(a.page_table + (uint64_t)seq * a.pg.pages_per_seq);
+    const cptr pre = sd.prefix >= 0 ? (cptr)(a.prefix_pages + (uint64_t)sd.prefix * a.pg.pages_per_seq) : own;
+    const int tiles_sh = (n_sh + PF_KT - 1) / PF_KT;
+    const int ntile = tiles_sh + (n_own + PF_KT - 1) / PF_KT;
+    // tile j: its segment's visible slots from its first on
+    auto remaining = [&](int j) __attribute__((always_inline)) {
+        return j < tiles_sh ? n_sh - PF_KT * j : n_own - PF_KT * (j - tiles_sh);
+    };
+    // tile j: page ids and first in-page slots of its halves (half 1 past
+    // the segment's end rereads half 0)
+    struct TileRef {
+        int32_t pid[2];
+        int sip[2];
+    };
+    auto fetch = [&](int j, TileRef &tr_) __attribute__((always_inline)) {
+        j = min(j, ntile - 1);
+        const bool sh = j < tiles_sh;
+        const int s0 = PF_KT * (sh ? j : j - tiles_sh);
+        const int len = sh ? n_sh : n_own;
+        const cptr rows = sh ? pre : own;
+        const int s1 = s0 + 16 < len ? s0 + 16 : s0;
+        tr_.pid[0] = rows[s0 >> a.pg.log2_page];
+        tr_.pid[1] = rows[s1 >> a.pg.log2_page];
+        tr_.sip[0] = s0 & (P - 1);
+        tr_.sip[1] = s1 & (P - 1);
+    };
+    struct Stage {
+        u32x4 k[2], v[2];
+        float sc[2];
+    };
+    auto load = [&](const TileRef &t_, Stage &sg) __attribute__((always_inline)) {
+#pragma unroll
+        for (int h = 0; h < 2; h++) {
+            // a page is under 4 GiB: one 32 x 32 -> 64-bit multiply-add
+            const uint8_t *hb = a.pool + (uint64_t)(uint32_t)t_.pid[h] * (uint32_t)a.pg.page_bytes +
+                                (uint64_t)kvh * a.pg.head_bytes;
+            const uint32_t sip = (uint32_t)t_.sip[h];
+            sg.k[h] = __builtin_nontemporal_load(reinterpret_cast<const u32x4 *>(hb + (kc + sip * DK)));
+            sg.v[h] = __builtin_nontemporal_load(reinterpret_cast<const u32x4 *>(hb + (gv + sip * DV)));
+            sg.sc[h] = __builtin_nontemporal_load(reinterpret_cast<const float *>(hb + (gs + sip * 4)));
+        }
+    };
+    auto store = [&](const Stage &sg) __attribute__((always_inline)) {
+#pragma unroll
+        for (int h = 0; h < 2; h++) {
+            *reinterpret_cast<u32x4 *>(lds + kc + 16 * DK * h) = sg.k[h];
+            *reinterpret_cast<u32x4 *>(lds + lv + 16 * VSTR * h) = sg.v[h];
+            *reinterpret_cast<float *>(lds + ls + 64 * h) = sg.sc[h];
+        }
+    };
+
+    // the first tile goes out before the q loads, so that their latencies
+    // overlap; tref then holds the references of the next tile
+    TileRef tref;
+    Stage sg;
+    fetch(0, tref);
+    load(tref, sg);
+    fetch(1, tref);
+
+    // Q^T operand, hi and lo: column r, dims 32 s + 8 g + [0, 8) and the tail
     // 32 NS + 4 g + [0, 4) (then four zero slots); hi and lo from one rounded
     // fp32 value
     const bool rvalid = r < REP;
     const uint64_t qrow = (uint64_t)b * a.nh + kvh * REP + (rvalid ? r : 0);
-    half8 qh[NS > 0 ? NS : 1], ql[NS > 0 ? NS : 1];
-    half8 qht = {}, qlt = {};
+    half8 qh[NS + TAIL], ql[NS + TAIL];
     {
         const float *qr = a.q + qrow * DK;
         const float qs = rvalid ? a.qscale : 0.0f;
@@ -642,140 +751,100 @@ void decode_mfma_kernel(PrefillArgs a)
         if constexpr (TAIL) {
             const float4 v = *reinterpret_cast<const float4 *>(qr + 32 * NS + 4 * g);
             const float xs[4] = {v.x, v.y, v.z, v.w};
+            qh[NS] = half8{};
+            ql[NS] = half8{};
 #pragma unroll
             for (int i = 0; i < 4; i++) {
                 _Float16 hi, lo;
                 split(xs[i], hi, lo);
-                qht[i] = hi;
-                qlt[i] = lo;
+                qh[NS][i] = hi;
+                ql[NS][i] = lo;
             }
         }
     }
 
-    const int P = 1 << a.pg.log2_page;
-    const int32_t *own = a.page_table + (uint64_t)seq * a.pg.pages_per_seq;
-    const int32_t *pre = sd.prefix >= 0 ? a.prefix_pages + (uint64_t)sd.prefix * a.pg.pages_per_seq : own;
-    // page id (loaded) and in-page offset of this lane's key of tile j
-    auto fetch = [&](int j, int32_t &pid, int &off) __attribute__((always_inline)) {
-        const int key = min(j * PF_KT + ln, total - 1);
-        const bool sh = key < n_sh;
-        const int sl = sh ? key : key - n_sh;
-        pid = (sh ? pre : own)[sl >> a.pg.log2_page];
-        off = sl & (P - 1);
-    };
-    struct Stage {
-        uint32_t k[KH / 4], v[VH / 4];
-        float sc;
-    };
-    auto load = [&](int32_t pid, int off, Stage &sg) __attribute__((always_inline)) {
-        // a page is under 4 GiB: one 32 x 32 -> 64-bit multiply-add
-        const uint8_t *hb = a.pool + (uint64_t)(uint32_t)pid * (uint32_t)a.pg.page_bytes + (uint64_t)kvh * a.pg.head_bytes;
-        const uint8_t *kp = hb + off * DK + KH * jh;
-        const uint8_t *vp = hb + P * DK + off * DV + VH * jh;
-#pragma unroll
-        for (int i = 0; i < KH / 8; i++) {
-            const u32x2 x = __builtin_nontemporal_load(reinterpret_cast<const u32x2 *>(kp) + i);
-            sg.k[2 * i] = x.x;
-            sg.k[2 * i + 1] = x.y;
-        }
-#pragma unroll
-        for (int i = 0; i < VH / 16; i++) {
-            const u32x4 x = __builtin_nontemporal_load(reinterpret_cast<const u32x4 *>(vp) + i);
-            sg.v[4 * i] = x.x;
-            sg.v[4 * i + 1] = x.y;
-            sg.v[4 * i + 2] = x.z;
-            sg.v[4 * i + 3] = x.w;
-        }
-        sg.sc = reinterpret_cast<const float *>(hb + P * (DK + DV))[jh * P + off];
-    };
-    auto store = [&](const Stage &sg) __attribute__((always_inline)) {
-#pragma unroll
-        for (int i = 0; i < KH / 8; i++) {
-            const uint32_t x0 = sg.k[2 * i] ^ 0x80808080u, x1 = sg.k[2 * i + 1] ^ 0x80808080u;
-            const half2v c0 = codes2<0x04010400>(x0), c1 = codes2<0x04030402>(x0);
-            const half2v c2 = codes2<0x04010400>(x1), c3 = codes2<0x04030402>(x1);
-            *reinterpret_cast<half8 *>(&Ks[ln][KH * jh + 8 * i]) =
-                half8{c0[0], c0[1], c1[0], c1[1], c2[0], c2[1], c3[0], c3[1]};
-        }
-#pragma unroll
-        for (int i = 0; i < VH / 4; i++) {
-            const uint32_t x = sg.v[i] ^ 0x80808080u;
-            const half2v c0 = codes2<0x04010400>(x), c1 = codes2<0x04030402>(x);
-            Vt[VH * jh + 4 * i + 0][ln] = c0[0];
-            Vt[VH * jh + 4 * i + 1][ln] = c0[1];
-            Vt[VH * jh + 4 * i + 2][ln] = c1[0];
-            Vt[VH * jh + 4 * i + 3][ln] = c1[1];
-        }
-        Sc[jh][ln] = sg.sc;
-    };
+    // lane-constant LDS offsets: the S operand rows (block 0; block 1 is 4
+    // rows on), the V^T rows (dims 0..15), the k scales of the keys whose
+    // scores this lane holds (v scales 128 bytes on)
+    const int koff = (8 * (r >> 2) + (r & 3)) * DK;
+    const int voff = KB + (8 * g + (r >> 1)) * VSTR + 8 * (r & 1);
+    const int soff = KB + VB + 32 * g;
 
-    float4v acc[4] = {};                        // O^T: dims 16 d + 4 g + i, row r
+    float4v acc[4] = {};                        // O^T: dims 16 d + 4 g + i, column r
     float m = -FLT_MAX, lsum = 0.0f;
     const float neg1 = opaque_neg1();
-    const int qlast = total - 1;                // keys past it are masked
-    const int ntile = (total + PF_KT - 1) / PF_KT;
-    const int jfull = total / PF_KT;            // tiles [0, jfull) are all visible
 
-    int32_t pid[2];
-    int poff[2];
-    Stage sg;
-    fetch(0, pid[0], poff[0]);
-    fetch(1, pid[1], poff[1]);
-    load(pid[0], poff[0], sg);
-    store(sg);
+    // the gate of this lane's output dims 16 d + 4 g + [0, 4), loaded with
+    // the last tile's arithmetic, so that its latency does not end the wave
+    const float *gt = a.gate ? a.gate + qrow * DV : nullptr;
+    float4 gv4[4];
 
-    // tile j (parity PJ): ids of tile j+2 into tile j's slot, data of tile
-    // j+1, the tile's arithmetic, then tile j+1 into LDS (two tiles in
-    // flight measured the same: the wave's chain through a tile, not the
-    // load latency, is what the resident waves hide)
-    auto tile = [&](const int j, auto pj, auto masked) __attribute__((always_inline)) {
-        constexpr int PJ = decltype(pj)::value, Q1 = PJ ^ 1;
-        const int kt = j * PF_KT;
-        fetch(j + 2, pid[PJ], poff[PJ]);
-        load(pid[Q1], poff[Q1], sg);
+    // tile j: the load of the next tile (references fetched a tile ago), the
+    // references of the one after, the tile's arithmetic, then the next tile
+    // into LDS; the last tile loads the gate instead
+    auto tile = [&](const int j, auto masked, auto last) __attribute__((always_inline)) {
+        constexpr bool more = !decltype(last)::value;
+        const int rem = remaining(j) - 8 * g;   // this lane's visible keys of the tile
+        if constexpr (more) {
+            load(tref, sg);
+            fetch(j + 2, tref);
+        } else {
+#pragma unroll
+            for (int d = 0; d < 4; d++)
+                gv4[d] = gt && rvalid ? *reinterpret_cast<const float4 *>(gt + 16 * d + 4 * g) : float4{0, 0, 0, 0};
+        }
 
         float4v st[2];
         __builtin_amdgcn_s_setprio(0);
 #pragma unroll
         for (int kb = 0; kb < 2; kb++) {
-            const _Float16 *kr = &Ks[16 * kb + r][0];
+            const uint8_t *kr = lds + koff + kb * 4 * DK;
             st[kb] = float4v{};
 #pragma unroll
-            for (int s2 = 0; s2 < NS; s2++) {
-                const half8 ka = *reinterpret_cast<const half8 *>(kr + 32 * s2 + 8 * g);
-                st[kb] = mfma16k32(ka, qh[s2], st[kb]);
-                st[kb] = mfma16k32(ka, ql[s2], st[kb]);
+            for (int s = 0; s < NS; s++) {
+                const half8 ka = codes8(*reinterpret_cast<const u32x2 *>(kr + 32 * s + 8 * g));
+                st[kb] = mfma16k32(ka, qh[s], st[kb]);
+                st[kb] = mfma16k32(ka, ql[s], st[kb]);
             }
             if constexpr (TAIL) {
-                const half4 k4 = *reinterpret_cast<const half4 *>(kr + 32 * NS + 4 * g);
-                const half8 ka = {k4[0], k4[1], k4[2], k4[3], 0, 0, 0, 0};
-                st[kb] = mfma16k32(ka, qht, st[kb]);
-                st[kb] = mfma16k32(ka, qlt, st[kb]);
+                const half8 ka = codes4(*reinterpret_cast<const uint32_t *>(kr + 32 * NS + 4 * g));
+                st[kb] = mfma16k32(ka, qh[NS], st[kb]);
+                st[kb] = mfma16k32(ka, ql[NS], st[kb]);
             }
         }
+        __builtin_amdgcn_sched_barrier(0);
         __builtin_amdgcn_s_setprio(1);
-        // scores of keys 16 kb + 4 g + i: k scales, then the mask
-        {
-            const float4 k0 = *reinterpret_cast<const float4 *>(&Sc[0][4 * g]);
-            const float4 k1 = *reinterpret_cast<const float4 *>(&Sc[0][16 + 4 * g]);
-            st[0] *= float4v{k0.x, k0.y, k0.z, k0.w};
-            st[1] *= float4v{k1.x, k1.y, k1.z, k1.w};
+        // scores of keys 8 g + 4 kb + i: k scales, then the mask (a masked
+        // key's v scale, possibly never written, becomes 0)
+        float vsc[8];
+#pragma unroll
+        for (int kb = 0; kb < 2; kb++) {
+            const float4 ks = *reinterpret_cast<const float4 *>(lds + soff + 16 * kb);
+            const float4 vs = *reinterpret_cast<const float4 *>(lds + soff + 128 + 16 * kb);
+            st[kb] *= float4v{ks.x, ks.y, ks.z, ks.w};
+            vsc[4 * kb + 0] = vs.x;
+            vsc[4 * kb + 1] = vs.y;
+            vsc[4 * kb + 2] = vs.z;
+            vsc[4 * kb + 3] = vs.w;
         }
         if constexpr (decltype(masked)::value) {
 #pragma unroll
             for (int kb = 0; kb < 2; kb++)
 #pragma unroll
-                for (int i = 0; i < 4; i++)
-                    st[kb][i] = kt + 16 * kb + 4 * g + i > qlast ? -INFINITY : st[kb][i];
+                for (int i = 0; i < 4; i++) {
+                    const bool out = 4 * kb + i >= rem;
+                    st[kb][i] = out ? -INFINITY : st[kb][i];
+                    vsc[4 * kb + i] = out ? 0.0f : vsc[4 * kb + i];
+                }
         }
-        // the row's tile max over its 32 keys: 8 in this lane, then across
+        // the column's tile max over its 32 keys: 8 in this lane, then across
         // the four lane groups (lanes r + 16 g)
         const float y0 = max3(st[0][0], st[0][1], st[0][2]), y1 = max3(st[0][3], st[1][0], st[1][1]);
         float mt = max3(y0, y1, max3(st[1][2], st[1][3], st[1][3]));
         mt = max3(mt, __shfl_xor(mt, 16, 64), mt);
         {
-            const auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(mt), __float_as_uint(mt), false, false);
-            mt = max3(mt, __uint_as_float(sw[0]), __uint_as_float(sw[1]));
+            const auto sw2 = __builtin_amdgcn_permlane32_swap(__float_as_uint(mt), __float_as_uint(mt), false, false);
+            mt = max3(mt, __uint_as_float(sw2[0]), __uint_as_float(sw2[1]));
         }
         const bool grow = mt > m + 8.0f;
         if (__builtin_expect(__ballot(grow) != 0, 0)) {
@@ -794,14 +863,11 @@ void decode_mfma_kernel(PrefillArgs a)
             for (int i = 0; i < 4; i++)
                 p[4 * kb + i] = fast_exp2(st[kb][i] - m);
         lsum += ((p[0] + p[1]) + (p[2] + p[3])) + ((p[4] + p[5]) + (p[6] + p[7]));
-        {
-            const float4 v0 = *reinterpret_cast<const float4 *>(&Sc[1][4 * g]);
-            const float4 v1 = *reinterpret_cast<const float4 *>(&Sc[1][16 + 4 * g]);
-            p[0] *= v0.x; p[1] *= v0.y; p[2] *= v0.z; p[3] *= v0.w;
-            p[4] *= v1.x; p[5] *= v1.y; p[6] *= v1.z; p[7] *= v1.w;
-        }
-        // P^T operand (hi, lo): slots = the eight keys in lane order; hi = p
-        // rounded toward zero to fp16, lo = the remainder
+#pragma unroll
+        for (int i = 0; i < 8; i++)
+            p[i] *= vsc[i];
+        // P^T operand (hi, lo): slots = keys 8 g .. 8 g + 7; hi = p rounded
+        // toward zero to fp16, lo = the remainder
         u32x4 phw, plw;
 #pragma unroll
         for (int i = 0; i < 8; i += 2) {
@@ -811,41 +877,38 @@ void decode_mfma_kernel(PrefillArgs a)
             plw[i >> 1] = split_lo2(hw, p[i], p[i + 1], neg1);
         }
         const half8 ph = __builtin_bit_cast(half8, phw), pl = __builtin_bit_cast(half8, plw);
+        __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
         for (int d = 0; d < 4; d++) {
-            const _Float16 *vr = &Vt[16 * d + r][4 * g];
-            const half4 v0 = *reinterpret_cast<const half4 *>(vr);
-            const half4 v1 = *reinterpret_cast<const half4 *>(vr + 16);
-            const half8 va = {v0[0], v0[1], v0[2], v0[3], v1[0], v1[1], v1[2], v1[3]};
+            const v2i w = __builtin_amdgcn_ds_read_tr8_b64_v2i32(
+                (lds_v2i *)(__attribute__((address_space(3))) void *)(lds + voff + 16 * d));
+            const half8 va = codes8(u32x2{(uint32_t)w.x, (uint32_t)w.y});
             acc[d] = mfma16k32(va, ph, acc[d]);
             acc[d] = mfma16k32(va, pl, acc[d]);
         }
         __builtin_amdgcn_s_setprio(0);
-        // Tile j+1 into LDS after this tile's last LDS reads. Other lanes of
-        // the wave read what this lane stores, and the wave's LDS accesses
+        // The next tile into LDS after this tile's last LDS reads. Other lanes
+        // of the wave read what this lane stores, and the wave's LDS accesses
         // complete in issue order; the wave barriers (scheduling barriers,
         // no instruction) keep the compiler from moving LDS accesses of one
         // tile across the store of the next.
-        if (j + 1 < ntile) {
+        if constexpr (more) {
             __builtin_amdgcn_wave_barrier();
             store(sg);
             __builtin_amdgcn_wave_barrier();
         }
     };
-    using P0 = std::integral_constant<int, 0>;
-    using P1 = std::integral_constant<int, 1>;
-    const int jeven = jfull & ~1;
-    int j = 0;
-    for (; j < jeven; j += 2) {
-        tile(j, P0{}, std::false_type{});
-        tile(j + 1, P1{}, std::false_type{});
+    store(sg);
+    for (int j = 0; j + 1 < ntile; j++) {
+        if (remaining(j) >= PF_KT)
+            tile(j, std::false_type{}, std::false_type{});
+        else
+            tile(j, std::true_type{}, std::false_type{});
     }
-    for (; j + 1 < ntile; j += 2) {
-        tile(j, P0{}, std::true_type{});
-        tile(j + 1, P1{}, std::true_type{});
-    }
-    if (j < ntile)
-        tile(j, P0{}, std::true_type{});
+    if (remaining(ntile - 1) >= PF_KT)
+        tile(ntile - 1, std::false_type{}, std::true_type{});
+    else
+        tile(ntile - 1, std::true_type{}, std::true_type{});
 
     lsum += __shfl_xor(lsum, 16, 64);
     lsum += __shfl_xor(lsum, 32, 64);
@@ -853,7 +916,6 @@ void decode_mfma_kernel(PrefillArgs a)
         return;
     const float inv = 1.0f / lsum;
     float *o = a.out + qrow * DV;
-    const float *gt = a.gate ? a.gate + qrow * DV : nullptr;
 #pragma unroll
     for (int d = 0; d < 4; d++) {
         const int d0 = 16 * d + 4 * g;
@@ -863,10 +925,10 @@ void decode_mfma_kernel(PrefillArgs a)
         z.z = acc[d][2] * inv;
         z.w = acc[d][3] * inv;
         if (gt) {
-            z.x *= sigmoid_dev(gt[d0 + 0]);
-            z.y *= sigmoid_dev(gt[d0 + 1]);
-            z.z *= sigmoid_dev(gt[d0 + 2]);
-            z.w *= sigmoid_dev(gt[d0 + 3]);
+            z.x *= sigmoid_dev(gv4[d].x);
+            z.y *= sigmoid_dev(gv4[d].y);
+            z.z *= sigmoid_dev(gv4[d].z);
+            z.w *= sigmoid_dev(gv4[d].w);
         }
         *reinterpret_cast<float4 *>(o + d0) = z;
     }
@@ -887,10 +949,10 @@ hipError_t launch_decode_mfma(const Geo &g, const PrefillArgs &a, hipStream_t s)
 {
     if (a.n_items == 0)
         return hipSuccess;
-#define X(DK, DV, REP)                                                                            \
-    if (!g.kv_f16 && g.dk == DK && g.dv == DV && g.rep == REP) {                                  \
+#define X(DK, DV, REP)                                                                                        \
+    if (!g.kv_f16 && g.dk == DK && g.dv == DV && g.rep == REP) {                                              \
         hipLaunchKernelGGL((decode_mfma_kernel<DK, DV, REP>), dim3(a.n_items), dim3(64), 0, s, a); \
-        return hipGetLastError();                                                                 \
+        return hipGetLastError();                                                                             \
     }
     NDA_DEC_GEOMETRIES(X)
 #undef X

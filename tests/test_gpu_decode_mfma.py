@@ -1,6 +1,7 @@
 """GPU parity of the MFMA decode of GQA groups: int8 K/V with 4 or more query
 heads per kv-head, which nda_decode runs on decode_mfma_kernel (one wave per
-(row, kv-head), the group's heads as MFMA rows). Each case stores the cache an
+row and pair of kv-heads, or per row and kv-head for odd kv-head counts; the
+heads as MFMA columns). Each case stores the cache an
 engine session at that position holds (the sinks and the ring's latest
 positions, written through nda_kv_write), decodes once, and compares the
 outputs with the oracle's attention over the same slots (ndo_attend, the
@@ -145,7 +146,8 @@ SPECS = [(0, 0), (1, 0), (30, 0), (31, 0), (32, 0), (62, 0), (63, 0), (64, 0), (
          (382, 0), (383, 0), (500, 0), (700, 4), (1000, 64), (391, 31)]
 
 
-@pytest.mark.parametrize("nh,nkv,qk", [(12, 2, 48), (8, 2, 64), (16, 2, 64), (12, 2, 64), (8, 1, 64)])
+@pytest.mark.parametrize("nh,nkv,qk", [(12, 2, 48), (8, 2, 64), (16, 2, 64), (12, 2, 64), (8, 1, 64), (16, 4, 64),
+                                       (24, 4, 48), (12, 3, 64), (18, 3, 48)])
 def test_decode_mfma_gqa_ragged_ring(nh, nkv, qk):
     say("decode mfma", nh, nkv, qk)
     order = list(range(len(SPECS)))[::-1]       # rows listed out of order
