@@ -671,15 +671,21 @@ def block_leg(N, stream, nseq=B, steps=5, warmup=2, taps=3, theta=10000.0):
             c.close()
     # the decode's algorithmic bytes per layer launch: every visible slot's
     # int8 K and V rows and their two scales, for both kv-heads (profiled
-    # steps: positions lens + warmup + steps + s, slots min(pos + 1, window))
+    # steps: positions lens + warmup + steps + s, slots min(pos + 1, window)),
+    # plus the fp32 q and gate read and the output written (12 heads, as the
+    # headline decode counts q and out)
+    nh, nkv, qk, vd = ENGINE_GEOM
     vis = [np.minimum(lens + warmup + steps + s_ + 1, W) for s_ in range(steps)]
-    dec_bytes = float(np.mean([v.sum() for v in vis])) * 2 * (48 + 64 + 8)
+    kv_bytes = float(np.mean([v.sum() for v in vis])) * nkv * (qk + vd + 8)
+    qgo_bytes = float(nseq) * nh * (qk + 2 * vd) * 4
+    dec_bytes = kv_bytes + qgo_bytes
     dec_s = per_step["decode_ms"] * 1e-3 / LAYERS
     return {"workload": "the engine's attention() per layer for %d sequences: 12/2 heads, qk 48, v 64, d_model 768, "
                         "window 384, int8 KV, 2-bit CQ projections, 3 qkv taps, L ~ U[213,383], 8 layers" % nseq,
             "tokens_per_s": round(nseq * steps / el, 1), "ms_per_step": round(el * 1e3 / steps, 4),
             "kernel_ms_per_step": per_step,
             "decode": {"kernel": "decode_mfma_kernel<48,64,rep6>", "bytes_per_launch": round(dec_bytes),
+                       "kv_bytes_per_launch": round(kv_bytes),
                        "GBps": round(dec_bytes / dec_s / 1e9, 1) if dec_s > 0 else None,
                        "frac": round(dec_bytes / dec_s / 8e12, 4) if dec_s > 0 else None, "bound": "hbm"},
             "note": "parity of the same path is held by tests/test_gpu_block.py (the engine's own attention() "

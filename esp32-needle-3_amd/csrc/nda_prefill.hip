@@ -612,12 +612,17 @@ __device__ __forceinline__ float4v mfma16k32(half8 a, half8 b, float4v c)
 // one is computed) and one in its LDS buffer. Splitting a row's tiles over
 // more waves (and merging their states) measured no faster: the launch is
 // bound by its memory stream, not by the wave count.
-template <int DK, int DV, int REP>
+//
+// RUN (pages of 16 slots, K + V + scales of a kv-head within 128 chunks of
+// 16 bytes): a half tile is a whole kv-head block of one page, 1920 bytes at
+// qk 48, read as one contiguous run by two loads.
+template <int DK, int DV, int REP, bool RUN>
 __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(4)))
 void decode_mfma_kernel(PrefillArgs a)
 {
     static_assert(DK % 16 == 0 && DK <= 64 && DV == 64 && REP <= 16,
                   "decode tiles: dk multiple of 16 up to 64, dv 64, rep <= 16");
+    static_assert(!RUN || DK + DV + 8 <= 128, "a kv-head block of a 16-slot page within two loads");
     constexpr int NS = DK / 32;                 // 32-dim steps of S (16x16x32)
     // A last 16-dim step (qk 48) runs on the same 16x16x32 instruction, its
     // upper four k slots zero in both operands. Every accumulation chain
@@ -653,7 +658,27 @@ void decode_mfma_kernel(PrefillArgs a)
     // bytes), V chunk `lane`, and scale word `lane % 32` (16 k scales, then
     // 16 v scales). Offsets are from the kv-head block of the half's page;
     // the half's first slot adds sip * DK, sip * DV and sip * 4.
+    // RUN: 16-byte chunks `lane` and 64 + lane of the block (K rows, V rows,
+    // k scales, v scales; surplus lanes repeat the last chunk), each with its
+    // LDS place per half.
     const int P = 1 << a.pg.log2_page;
+    constexpr int NRC = DK + DV + 8;           // chunks of a 16-slot kv-head block
+    auto run_lds = [&](int c, int h) __attribute__((always_inline)) -> int {
+        if (c < DK)
+            return 16 * DK * h + 16 * c;
+        if (c < DK + DV)
+            return KB + (16 * h + (c - DK) / 4) * VSTR + 16 * ((c - DK) % 4);
+        const int sc = c - DK - DV;
+        return KB + VB + 128 * (sc >> 2) + 64 * h + 16 * (sc & 3);
+    };
+    const int rc1 = min(64 + lane, NRC - 1);
+    const uint32_t rg1 = 16 * rc1;
+    int rl[2][2];
+#pragma unroll
+    for (int h = 0; h < 2; h++) {
+        rl[h][0] = run_lds(lane, h);
+        rl[h][1] = run_lds(rc1, h);
+    }
     const uint32_t kc = 16 * (lane % DK);
     const uint32_t gv = P * DK + 16 * lane;
     const int lv = KB + (lane >> 2) * VSTR + 16 * (lane & 3);
@@ -688,7 +713,7 @@ void decode_mfma_kernel(PrefillArgs a)
         tr_.sip[1] = s1 & (P - 1);
     };
     struct Stage {
-        u32x4 k[2], v[2];
+        u32x4 k[2], v[2];                       // RUN: chunks lane and 64 + lane
         float sc[2];
     };
     auto load = [&](const TileRef &t_, Stage &sg) __attribute__((always_inline)) {
@@ -697,15 +722,25 @@ void decode_mfma_kernel(PrefillArgs a)
             // a page is under 4 GiB: one 32 x 32 -> 64-bit multiply-add
             const uint8_t *hb = a.pool + (uint64_t)(uint32_t)t_.pid[h] * (uint32_t)a.pg.page_bytes +
                                 (uint64_t)kvh * a.pg.head_bytes;
-            const uint32_t sip = (uint32_t)t_.sip[h];
-            sg.k[h] = __builtin_nontemporal_load(reinterpret_cast<const u32x4 *>(hb + (kc + sip * DK)));
-            sg.v[h] = __builtin_nontemporal_load(reinterpret_cast<const u32x4 *>(hb + (gv + sip * DV)));
-            sg.sc[h] = __builtin_nontemporal_load(reinterpret_cast<const float *>(hb + (gs + sip * 4)));
+            if constexpr (RUN) {
+                sg.k[h] = __builtin_nontemporal_load(reinterpret_cast<const u32x4 *>(hb + 16 * lane));
+                sg.v[h] = __builtin_nontemporal_load(reinterpret_cast<const u32x4 *>(hb + rg1));
+            } else {
+                const uint32_t sip = (uint32_t)t_.sip[h];
+                sg.k[h] = __builtin_nontemporal_load(reinterpret_cast<const u32x4 *>(hb + (kc + sip * DK)));
+                sg.v[h] = __builtin_nontemporal_load(reinterpret_cast<const u32x4 *>(hb + (gv + sip * DV)));
+                sg.sc[h] = __builtin_nontemporal_load(reinterpret_cast<const float *>(hb + (gs + sip * 4)));
+            }
         }
     };
     auto store = [&](const Stage &sg) __attribute__((always_inline)) {
 #pragma unroll
         for (int h = 0; h < 2; h++) {
+            if constexpr (RUN) {
+                *reinterpret_cast<u32x4 *>(lds + rl[h][0]) = sg.k[h];
+                *reinterpret_cast<u32x4 *>(lds + rl[h][1]) = sg.v[h];
+                continue;
+            }
             *reinterpret_cast<u32x4 *>(lds + kc + 16 * DK * h) = sg.k[h];
             *reinterpret_cast<u32x4 *>(lds + lv + 16 * VSTR * h) = sg.v[h];
             *reinterpret_cast<float *>(lds + ls + 64 * h) = sg.sc[h];
@@ -949,10 +984,15 @@ hipError_t launch_decode_mfma(const Geo &g, const PrefillArgs &a, hipStream_t s)
 {
     if (a.n_items == 0)
         return hipSuccess;
-#define X(DK, DV, REP)                                                                                        \
-    if (!g.kv_f16 && g.dk == DK && g.dv == DV && g.rep == REP) {                                              \
-        hipLaunchKernelGGL((decode_mfma_kernel<DK, DV, REP>), dim3(a.n_items), dim3(64), 0, s, a); \
-        return hipGetLastError();                                                                             \
+    const bool p16 = a.pg.log2_page == 4;
+#define X(DK, DV, REP)                                                                                  \
+    if (!g.kv_f16 && g.dk == DK && g.dv == DV && g.rep == REP) {                                        \
+        if (p16 && DK + DV + 8 <= 128)                                                                  \
+            hipLaunchKernelGGL((decode_mfma_kernel<DK, DV, REP, (DK + DV + 8 <= 128)>), dim3(a.n_items), \
+                               dim3(64), 0, s, a);                                                      \
+        else                                                                                            \
+            hipLaunchKernelGGL((decode_mfma_kernel<DK, DV, REP, false>), dim3(a.n_items), dim3(64), 0, s, a); \
+        return hipGetLastError();                                                                       \
     }
     NDA_DEC_GEOMETRIES(X)
 #undef X

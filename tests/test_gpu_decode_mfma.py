@@ -71,7 +71,7 @@ def _visible_positions(pos, n_sink, W):
     return sinks + list(range(lo, pos + 1))
 
 
-def _run(nh, nkv, qk, W, specs, seed, gated=True, order=None, prefix=0, outlier_p=0.0):
+def _run(nh, nkv, qk, W, specs, seed, gated=True, order=None, prefix=0, outlier_p=0.0, page_size=16):
     """specs: (pos, n_sink) per sequence; with prefix > 0 every sequence is
     attached to a prefix of `prefix` sink positions built on an extra
     sequence, so its (pos, n_sink) is (pos, prefix). Returns the worst
@@ -103,7 +103,8 @@ def _run(nh, nkv, qk, W, specs, seed, gated=True, order=None, prefix=0, outlier_
 
     outs = []
     for flags in (0, N.FLAG_DECODE_VALU):
-        ctx = N.Context(1, nh, nkv, qk, vd, W, kv_dtype=N.KV_INT8, max_seqs=B + 1, flags=flags)
+        ctx = N.Context(1, nh, nkv, qk, vd, W, kv_dtype=N.KV_INT8, max_seqs=B + 1, flags=flags,
+                        page_size=page_size)
         if prefix:
             ctx.seq_set_sink(B, prefix)
         else:
@@ -179,3 +180,18 @@ def test_decode_mfma_shared_prefix():
     say("worst vs oracle: mfma", mf, "valu", va, "between", between)
     assert mf <= TOL and va <= TOL, (mf, va)
     assert between <= KERNELS_TOL, between
+
+
+@pytest.mark.parametrize("page_size", [32, 64])
+@pytest.mark.parametrize("nh,nkv,qk", [(12, 2, 48), (8, 2, 64)])
+def test_decode_mfma_page_sizes(nh, nkv, qk, page_size):
+    """Pages of 32 and 64 slots: a tile's halves share a page and its K rows,
+    V rows and scales are separate runs (the 16-slot pages of the other
+    cases are read as one run per kv-head block); rings, sinks and a shared
+    prefix whose end falls inside a page."""
+    say("decode mfma pages", page_size, nh, nkv, qk)
+    mf, va, between = _run(nh, nkv, qk, 384, SPECS, seed=page_size + qk, page_size=page_size)
+    assert mf <= TOL and va <= TOL and between <= KERNELS_TOL, (mf, va, between)
+    specs = [(213, 0), (229, 0), (245, 0), (600, 0)]
+    mf, va, between = _run(nh, nkv, qk, 384, specs + specs, seed=page_size + 3, prefix=213, page_size=page_size)
+    assert mf <= TOL and va <= TOL and between <= KERNELS_TOL, (mf, va, between)
