@@ -11,6 +11,7 @@ timed region. Prints one JSON line.
     python bench.py [--steps K] [--warmup W] [--no-cpu]
 """
 import argparse
+import gc
 import json
 import os
 import sys
@@ -584,12 +585,18 @@ def block_prefill_leg(N, stream, nseq=1024, npre=213, nmin=32, nmax=64, reps=3, 
         if prof:
             ctx.prof_enable(True)
             ctx.prof_read(reset=True)
+        # the enqueue is host time of the library's calls: no garbage
+        # collection of the interpreter's heap (which the earlier legs grow)
+        # inside it
+        gc.collect()
+        gc.disable()
         t0 = time.perf_counter()
         for li in range(LAYERS):
             ctx.prefill_block(li, nseq, n, x[li], y, stream=stream)
         enq = time.perf_counter() - t0
         ctx.sync(stream)
         el = time.perf_counter() - t0
+        gc.enable()
         if prof:
             kms, _ = ctx.prof_read(reset=True)
             ctx.prof_enable(False)

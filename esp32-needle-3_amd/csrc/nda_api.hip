@@ -88,6 +88,16 @@ struct ProfRec {
     hipEvent_t a, b;
 };
 
+// An upload in flight from the pinned ring: bytes [lo, hi) of the ring, free
+// again once `ev` (recorded behind the copy) has completed.
+struct UploadRec {
+    size_t lo, hi;
+    hipEvent_t ev;
+};
+
+constexpr size_t UPLOAD_RING_BYTES = 16u << 20;
+constexpr int UPLOAD_EVENTS = 256;
+
 } // namespace
 
 struct nda_ctx {
@@ -143,6 +153,14 @@ struct nda_ctx {
     float *d_bscr = nullptr;            // xh | q | k | v | gate | attn | attn xh, per row
     size_t bscr_cap = 0;                // floats
 
+    // pinned staging of the per-call uploads (upload()); null: none could be
+    // allocated, uploads copy from pageable memory
+    uint8_t *h_ring = nullptr;
+    size_t ring_cap = 0, ring_head = 0;
+    UploadRec ring_live[UPLOAD_EVENTS]; // in flight, in ring order: a circular list
+    int live_head = 0, live_n = 0;
+    std::vector<hipEvent_t> ring_ev;    // free events, all created with the context (capacity reserved)
+
     bool prof = false;
     std::vector<ProfRec> prof_pending;
     std::vector<hipEvent_t> ev_free;
@@ -180,6 +198,64 @@ int hip_fail(nda_ctx *c, hipError_t e, const char *what)
             return hip_fail((c), e_, #call);               \
     } while (0)
 
+// Host-to-device upload of n bytes on stream st, returning without waiting
+// for the stream. A copy from pageable memory blocks the caller until the
+// stream reaches it, which would keep the host from running ahead of the GPU
+// at every call; so the bytes are copied into the context's pinned ring and
+// sent from there. A region of the ring is written again only after the
+// event recorded behind its last copy has completed (the oldest uploads are
+// waited for when the ring wraps onto them), and the events are the
+// context's own (created with it): an upload allocates nothing. The caller's
+// buffer may be reused as soon as this returns.
+int upload(nda_ctx *c, void *dst, const void *src, size_t n, hipStream_t st)
+{
+    if (n == 0)
+        return NDA_OK;
+    const size_t need = (n + 255) & ~(size_t)255;
+    if (!c->h_ring || need > c->ring_cap / 2) {
+        HIPC(c, hipMemcpyAsync(dst, src, n, hipMemcpyHostToDevice, st));
+        return NDA_OK;
+    }
+    if (c->ring_head + need > c->ring_cap)
+        c->ring_head = 0;
+    const size_t lo = c->ring_head, hi = lo + need;
+    auto retire_front = [&](bool wait) -> hipError_t {
+        UploadRec &u = c->ring_live[c->live_head];
+        const hipError_t e = wait ? hipEventSynchronize(u.ev) : hipEventQuery(u.ev);
+        if (e == hipSuccess) {
+            c->ring_ev.push_back(u.ev);          // within the reserved capacity
+            c->live_head = (c->live_head + 1) % UPLOAD_EVENTS;
+            c->live_n--;
+        }
+        return e;
+    };
+    // completed uploads give their regions and events back
+    while (c->live_n && retire_front(false) == hipSuccess) {
+    }
+    // the oldest uploads are waited for while one still overlaps [lo, hi),
+    // or while no event is free
+    for (;;) {
+        bool blocked = c->ring_ev.empty();
+        for (int i = 0; i < c->live_n && !blocked; i++) {
+            const UploadRec &u = c->ring_live[(c->live_head + i) % UPLOAD_EVENTS];
+            blocked = u.lo < hi && lo < u.hi;
+        }
+        if (!blocked)
+            break;
+        if (hipError_t e = retire_front(true); e != hipSuccess)
+            return hip_fail(c, e, "hipEventSynchronize (upload ring)");
+    }
+    memcpy(c->h_ring + lo, src, n);
+    HIPC(c, hipMemcpyAsync(dst, c->h_ring + lo, n, hipMemcpyHostToDevice, st));
+    hipEvent_t ev = c->ring_ev.back();
+    HIPC(c, hipEventRecord(ev, st));
+    c->ring_ev.pop_back();
+    c->ring_live[(c->live_head + c->live_n) % UPLOAD_EVENTS] = UploadRec{lo, hi, ev};
+    c->live_n++;
+    c->ring_head = hi;
+    return NDA_OK;
+}
+
 void release_pages(nda_ctx *c, uint32_t seq) { c->pt.release(seq); }
 
 // Back own slots [s0, s1) of a sequence with pages. All-or-nothing.
@@ -212,20 +288,22 @@ int sync_tables(nda_ctx *c, hipStream_t st)
             tmp[i].prefix = c->seqs[i].prefix;
             tmp[i].pad = 0;
         }
-        HIPC(c, hipMemcpyAsync(c->d_seqs, tmp.data(), tmp.size() * sizeof(SeqDev), hipMemcpyHostToDevice, st));
+        if (int rc = upload(c, c->d_seqs, tmp.data(), tmp.size() * sizeof(SeqDev), st))
+            return rc;
         c->seqs_dirty = false;
     }
     if (c->pt.dirty_lo < c->pt.dirty_hi) {
         size_t off = (size_t)c->pt.dirty_lo * c->pg.pages_per_seq;
         size_t n = (size_t)(c->pt.dirty_hi - c->pt.dirty_lo) * c->pg.pages_per_seq;
-        HIPC(c, hipMemcpyAsync(c->d_pages + off, c->pt.pages.data() + off, n * sizeof(int32_t),
-                               hipMemcpyHostToDevice, st));
+        if (int rc = upload(c, c->d_pages + off, c->pt.pages.data() + off, n * sizeof(int32_t), st))
+            return rc;
         c->pt.dirty_lo = UINT32_MAX;
         c->pt.dirty_hi = 0;
     }
     if (c->pt.prefix_dirty) {
-        HIPC(c, hipMemcpyAsync(c->d_prefix_pages, c->pt.prefix_pages.data(),
-                               c->pt.prefix_pages.size() * sizeof(int32_t), hipMemcpyHostToDevice, st));
+        if (int rc = upload(c, c->d_prefix_pages, c->pt.prefix_pages.data(),
+                            c->pt.prefix_pages.size() * sizeof(int32_t), st))
+            return rc;
         c->pt.prefix_dirty = false;
     }
     return NDA_OK;
@@ -366,8 +444,8 @@ int hist_flush(nda_ctx *c, hipStream_t st)
     const size_t n = c->hist_pending.size();
     if (int rc = ensure_buf(c, c->d_hist_ops, c->hist_ops_cap, n))
         return rc;
-    HIPC(c, hipMemcpyAsync(c->d_hist_ops, c->hist_pending.data(), n * sizeof(HistOp), hipMemcpyHostToDevice,
-                           st));
+    if (int rc = upload(c, c->d_hist_ops, c->hist_pending.data(), n * sizeof(HistOp), st))
+        return rc;
     // Launch maximal runs of ops that touch disjoint blocks; a run ends where
     // an op writes a block the run reads or writes, or reads one it writes.
     std::unordered_set<const float *> dsts, srcs;
@@ -423,11 +501,13 @@ int upload_rows(nda_ctx *c, uint32_t rows, const uint32_t *row_seq, const uint32
     if (rc)
         return rc;
     if (row_seq) {
-        HIPC(c, hipMemcpyAsync(c->d_rows, row_seq, rows * sizeof(uint32_t), hipMemcpyHostToDevice, st));
+        if (int rc2 = upload(c, c->d_rows, row_seq, rows * sizeof(uint32_t), st))
+            return rc2;
         *d_seq = c->d_rows;
     }
     if (row_t) {
-        HIPC(c, hipMemcpyAsync(c->d_rows + rows, row_t, rows * sizeof(uint32_t), hipMemcpyHostToDevice, st));
+        if (int rc2 = upload(c, c->d_rows + rows, row_t, rows * sizeof(uint32_t), st))
+            return rc2;
         *d_t = c->d_rows + rows;
     }
     return NDA_OK;
@@ -664,6 +744,26 @@ int nda_create(const nda_config *cfg_in, nda_ctx **out)
         return NDA_ERR_NOMEM;
     }
     c->dev_bytes += pt * 4 + ppt * 4 + (size_t)cfg.max_seqs * sizeof(SeqDev);
+    // the pinned upload ring and its events; without them uploads copy from
+    // pageable memory (correct, but the host then waits for the stream)
+    if (hipHostMalloc((void **)&c->h_ring, UPLOAD_RING_BYTES, hipHostMallocDefault) == hipSuccess) {
+        c->ring_cap = UPLOAD_RING_BYTES;
+        c->ring_ev.reserve(UPLOAD_EVENTS);
+        for (int i = 0; i < UPLOAD_EVENTS; i++) {
+            hipEvent_t e;
+            if (hipEventCreateWithFlags(&e, hipEventDisableTiming) != hipSuccess)
+                break;
+            c->ring_ev.push_back(e);
+        }
+        if (c->ring_ev.empty()) {
+            (void)hipHostFree(c->h_ring);
+            c->h_ring = nullptr;
+            c->ring_cap = 0;
+        }
+    } else {
+        c->h_ring = nullptr;
+        (void)hipGetLastError();
+    }
     try {
         c->pt.init(cfg.max_seqs, cfg.max_prefixes, c->pg.pages_per_seq, c->pg.log2_page, c->max_pages);
         c->seqs.assign(cfg.max_seqs, SeqHost());
@@ -687,6 +787,12 @@ void nda_destroy(nda_ctx *c)
     }
     for (auto e : c->ev_free)
         (void)hipEventDestroy(e);
+    for (int i = 0; i < c->live_n; i++)
+        (void)hipEventDestroy(c->ring_live[(c->live_head + i) % UPLOAD_EVENTS].ev);
+    for (auto e : c->ring_ev)
+        (void)hipEventDestroy(e);
+    if (c->h_ring)
+        (void)hipHostFree(c->h_ring);
     void *bufs[] = {c->pool, c->d_pages, c->d_prefix_pages, c->d_seqs, c->d_rows, c->d_part,
                     c->d_stage, c->d_pf, c->d_hist, c->d_snap_hist, c->d_prefix_hist,
                     c->d_front_w, c->d_front_norm, c->d_rope, c->d_qfront, c->d_front_rows,
@@ -1141,7 +1247,8 @@ int nda_decode_noalloc(nda_ctx *c, uint32_t layer, uint32_t nseq, const uint32_t
     if (int rc = sync_tables(c, st))
         return rc;
     if (ids) {
-        HIPC(c, hipMemcpyAsync(c->scratch, ids, ids_bytes, hipMemcpyHostToDevice, st));
+        if (int rc = upload(c, c->scratch, ids, ids_bytes, st))
+            return rc;
         a.row_seq = reinterpret_cast<const uint32_t *>(c->scratch);
     }
     return run_attend(c, a, st, split ? reinterpret_cast<float *>(c->scratch + part_off) : nullptr, false);
@@ -1342,8 +1449,10 @@ int nda_prefill(nda_ctx *c, uint32_t layer, uint32_t nseq, const uint32_t *ids, 
     }
     if (int rc = ensure_pf(c, host.size() + items.size()))
         return rc;
-    HIPC(c, hipMemcpyAsync(c->d_pf, host.data(), host.size() * 4, hipMemcpyHostToDevice, st));
-    HIPC(c, hipMemcpyAsync(c->d_pf + host.size(), items.data(), items.size() * 4, hipMemcpyHostToDevice, st));
+    if (int rc = upload(c, c->d_pf, host.data(), host.size() * 4, st))
+        return rc;
+    if (int rc = upload(c, c->d_pf + host.size(), items.data(), items.size() * 4, st))
+        return rc;
     PrefillArgs pa{};
     pa.q = q;
     pa.gate = gate;
@@ -1557,7 +1666,8 @@ int nda_front(nda_ctx *c, uint32_t layer, uint32_t nseq, const uint32_t *ids, co
             host[2 * rows + r] = n;
         }
     }
-    HIPC(c, hipMemcpyAsync(c->d_front_rows, host.data(), host.size() * 4, hipMemcpyHostToDevice, st));
+    if (int rc = upload(c, c->d_front_rows, host.data(), host.size() * 4, st))
+        return rc;
     FrontArgs a = front_args(c, layer);
     a.q = q;
     a.k = k;
