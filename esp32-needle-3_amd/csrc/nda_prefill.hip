@@ -75,6 +75,18 @@ __device__ __forceinline__ uint32_t split_lo2(uint32_t hw, float p0, float p1, f
     return __builtin_bit_cast(uint32_t, l);
 }
 
+typedef short short4v __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) short4v lds_short4v;
+
+// four fp16 of a transposed 16-lane block (ds_read_b64_tr_b16): see the P.V
+// operand of the prefill kernel for the lane layout
+__device__ __forceinline__ half4 tr16_read(const _Float16 *p)
+{
+    const short4v w = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+        (lds_short4v *)(__attribute__((address_space(3))) void *)p);
+    return __builtin_bit_cast(half4, w);
+}
+
 __device__ __forceinline__ float16v mfma32(half8 a, half8 b, float16v c)
 {
     return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
@@ -87,7 +99,7 @@ typedef __fp16 fp16x2 __attribute__((ext_vector_type(2)));
 template <int ES, int DK, int DV, int NTHR>
 struct PfTile {
     static constexpr int KPAD = DK + 8;        // halves per K row in LDS
-    static constexpr int VPAD = PF_KT + 4;     // halves per V^T row in LDS
+    static constexpr int VPAD = DV + 8;        // halves per V row in LDS (row-major; read transposed)
     static constexpr int KC = DK * ES / 16;    // 16-byte chunks per stored K row
     static constexpr int VC = DV * ES / 16;
     static constexpr int EPC = 16 / ES;        // elements per chunk
@@ -172,7 +184,7 @@ struct PfIO {
         }
     }
     __device__ __forceinline__ void store(const Staged<T::CPT> &sg, _Float16 (*Ks)[T::KPAD],
-                                          _Float16 (*Vt)[T::VPAD], float *Ksc, float *Vsc) const
+                                          _Float16 (*Vr)[T::VPAD], float *Ksc, float *Vsc) const
     {
 #pragma unroll
         for (int i = 0; i < T::CPT; i++) {
@@ -199,11 +211,21 @@ struct PfIO {
                         Ksc[kl] = sg.sc[i];
                 }
             } else {
+                // V row-major, as stored: the P.V operand reads it transposed
+                if constexpr (ES == 2) {
+                    *reinterpret_cast<u32x4 *>(&Vr[kl][ch * 8]) = sg.w[i];
+                } else {
+                    half8 lo, hi;
 #pragma unroll
-                for (int e = 0; e < T::EPC; e++)
-                    Vt[ch * T::EPC + e][kl] = code_at<ES>(sg.w[i][e / (4 / ES)], e % (4 / ES));
-                if (ES == 1 && ch == 0)
-                    Vsc[kl] = sg.sc[i];
+                    for (int e = 0; e < 8; e++) {
+                        lo[e] = code_at<1>(sg.w[i][e >> 2], e & 3);
+                        hi[e] = code_at<1>(sg.w[i][2 + (e >> 2)], e & 3);
+                    }
+                    *reinterpret_cast<half8 *>(&Vr[kl][ch * 16]) = lo;
+                    *reinterpret_cast<half8 *>(&Vr[kl][ch * 16 + 8]) = hi;
+                    if (ch == 0)
+                        Vsc[kl] = sg.sc[i];
+                }
             }
         }
     }
@@ -221,7 +243,7 @@ void prefill_kernel(PrefillArgs a)
 
     // two tile buffers: one is computed on while the next tile is written
     __shared__ __attribute__((aligned(16))) _Float16 Ks2[2][PF_KT][T::KPAD];
-    __shared__ __attribute__((aligned(16))) _Float16 Vt2[2][DV][T::VPAD];
+    __shared__ __attribute__((aligned(16))) _Float16 Vr2[2][PF_KT][T::VPAD];
     __shared__ float Ksc2[2][PF_KT], Vsc2[2][PF_KT];
 
     const int tid = threadIdx.x;
@@ -322,7 +344,7 @@ void prefill_kernel(PrefillArgs a)
     io.fetch_pages(0, prn[0]);
     io.fetch_pages(PF_KT, prn[1]);
     io.load(prn[0], sg[0]);                     // tile 0
-    io.store(sg[0], Ks2[0], Vt2[0], Ksc2[0], Vsc2[0]);
+    io.store(sg[0], Ks2[0], Vr2[0], Ksc2[0], Vsc2[0]);
     io.fetch_pages(2 * PF_KT, prn[0]);
     io.load(prn[1], sg[1 % PD]);                // tile 1
     if constexpr (PD == 2) {
@@ -347,7 +369,7 @@ void prefill_kernel(PrefillArgs a)
         io.fetch_pages((j + PD + 1) * PF_KT, prn[(PJ + PD + 1) & 1]);
         io.load(prn[(PJ + PD) & 1], sg[(PJ + PD) % PD]);
         const _Float16 (*Ks)[T::KPAD] = Ks2[PJ];
-        const _Float16 (*Vt)[T::VPAD] = Vt2[PJ];
+        const _Float16 (*Vr)[T::VPAD] = Vr2[PJ];
         const float *Ksc = Ksc2[PJ], *Vsc = Vsc2[PJ];
 
         // ---- S^T = K . Q^T (keys x rows), accumulate hi then lo
@@ -451,9 +473,13 @@ void prefill_kernel(PrefillArgs a)
             const half8 ph = __builtin_bit_cast(half8, phw), pl = __builtin_bit_cast(half8, plw);
 #pragma unroll
             for (int dt = 0; dt < 2; dt++) {
-                const _Float16 *vr = &Vt[32 * dt + ln][16 * kb2 + 4 * jh];
-                const half4 v0 = *reinterpret_cast<const half4 *>(vr);
-                const half4 v1 = *reinterpret_cast<const half4 *>(vr + 8);
+                // V^T rows 32 dt + ln, keys 16 kb2 + 4 jh + [0, 4) and 8 on:
+                // in each 16-lane group ds_read_b64_tr_b16 gives output lane i
+                // element j from the address of lane 4 j + i / 4 (plus i % 4),
+                // so lane (j, q) of the group points at key j, dims 4 q on
+                const _Float16 *vr = &Vr[16 * kb2 + 4 * jh + ((lane >> 2) & 3)][32 * dt + 16 * ((lane >> 4) & 1) + 4 * (lane & 3)];
+                const half4 v0 = tr16_read(vr);
+                const half4 v1 = tr16_read(vr + 8 * T::VPAD);
                 const half8 va = {v0[0], v0[1], v0[2], v0[3], v1[0], v1[1], v1[2], v1[3]};
                 if (dt == 0) {
                     acc0 = mfma32(va, ph, acc0);
@@ -468,7 +494,7 @@ void prefill_kernel(PrefillArgs a)
         }
         __builtin_amdgcn_s_setprio(0);
         if (j + 1 < ntile)   // tile j+1 into the other buffer (its readers are done)
-            io.store(sg[(PJ + 1) % PD], Ks2[Q1], Vt2[Q1], Ksc2[Q1], Vsc2[Q1]);
+            io.store(sg[(PJ + 1) % PD], Ks2[Q1], Vr2[Q1], Ksc2[Q1], Vsc2[Q1]);
         __syncthreads();
     };
     using P0 = std::integral_constant<int, 0>;
