@@ -9,8 +9,9 @@
 //
 // A work-group owns 32*W query rows of one (sequence, kv-head); a row is one
 // (token, query head of the group) pair, so GQA heads share every K/V tile.
-// Key tiles of 32 are staged through LDS (K row-major, V transposed), then per
-// wave and tile:
+// Key tiles of 32 slots of one segment (shared prefix, then own) are staged
+// through LDS (K and V row-major; V is read transposed), then per wave and
+// tile:
 //   S^T[32 keys x 32 rows]  = K . Q^T           v_mfma_f32_32x32x16_f16
 //   O^T[64 dims x 32 rows] += V^T . P^T         v_mfma_f32_32x32x16_f16
 // Computing the transposes puts one query row in each lane (lane l and l+32
@@ -96,143 +97,239 @@ typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 typedef __fp16 fp16x2 __attribute__((ext_vector_type(2)));
 
+typedef const __attribute__((address_space(4))) int32_t *cptr;   // read through scalar loads
+
+// int8 codes as fp16, exact: 0x64 over the byte code ^ 0x80 is the fp16
+// 1024 + code + 128, so one xor, a byte permute and a packed fp16 subtract
+// per two codes.
+template <int SEL>
+__device__ __forceinline__ half2v codes2(uint32_t xs)   // xs = codes ^ 0x80808080
+{
+    const uint32_t u = __builtin_amdgcn_perm(0x64646464u, xs, (uint32_t)SEL);
+    return __builtin_bit_cast(half2v, u) - half2v{(_Float16)1152.0f, (_Float16)1152.0f};
+}
+
+// eight int8 codes (bytes 0..7 of w) as fp16, in byte order
+__device__ __forceinline__ half8 codes8(u32x2 w)
+{
+    const uint32_t x0 = w.x ^ 0x80808080u, x1 = w.y ^ 0x80808080u;
+    const half2v c0 = codes2<0x04010400>(x0), c1 = codes2<0x04030402>(x0);
+    const half2v c2 = codes2<0x04010400>(x1), c3 = codes2<0x04030402>(x1);
+    return half8{c0[0], c0[1], c1[0], c1[1], c2[0], c2[1], c3[0], c3[1]};
+}
+
+// f(integral_constant<int, 0>) ... f(integral_constant<int, N - 1>)
+template <int N, int I = 0, class F>
+__device__ __forceinline__ void static_for(F &&f)
+{
+    if constexpr (I < N) {
+        f(std::integral_constant<int, I>{});
+        static_for<N, I + 1>(f);
+    }
+}
+
+// Key tiles are 32 slots of one segment -- the shared prefix's slots, then
+// the sequence's own (own slot s holds position n_sh + s) -- aligned to 32
+// within it. A half tile (16 keys) is then 16 consecutive slots of one page,
+// and its K rows, V rows and (int8) k and v scales are contiguous runs of
+// that page's kv-head block. A thread's share of a tile is a few 16-byte
+// chunks of those runs at offsets fixed for the launch, from one base per
+// half tile that one scalar page-table read gives.
 template <int ES, int DK, int DV, int NTHR>
 struct PfTile {
     static constexpr int KPAD = DK + 8;        // halves per K row in LDS
     static constexpr int VPAD = DV + 8;        // halves per V row in LDS (row-major; read transposed)
     static constexpr int KC = DK * ES / 16;    // 16-byte chunks per stored K row
     static constexpr int VC = DV * ES / 16;
-    static constexpr int EPC = 16 / ES;        // elements per chunk
-    static constexpr int NCHUNK = PF_KT * (KC + VC);
-    static constexpr int CPT = (NCHUNK + NTHR - 1) / NTHR;   // chunks per thread
+    static constexpr int HCH = 16 * (KC + VC) + (ES == 1 ? 8 : 0);   // chunks of a half tile
+    static constexpr int HP = (HCH + 63) / 64 * 64;   // padded to whole waves: a wave's chunks share a half
+    static constexpr int CPT = (2 * HP + NTHR - 1) / NTHR;             // chunks per thread
+    // one LDS buffer: K [32][KPAD] halves, V [32][VPAD] halves, k scales, v scales
+    static constexpr int VOFF = PF_KT * KPAD * 2, SOFF = VOFF + PF_KT * VPAD * 2;
+    static constexpr int BUF = SOFF + 2 * PF_KT * 4;
     static_assert(DK * ES % 16 == 0 && DV * ES % 16 == 0, "rows are whole 16-byte chunks");
+    static_assert(NTHR % 64 == 0 && BUF % 16 == 0, "");
 };
 
-// One thread's share of a K/V tile in flight: raw 16-byte chunks + scales.
+// One thread's share of a K/V tile in flight: raw 16-byte chunks, and the
+// tile's count of slots before its segment's end (uniform).
 template <int CPT>
 struct Staged {
     u32x4 w[CPT];
-    float sc[CPT];
+    int vlim;
 };
 
-// Element i of a dword as a half: fp16 lane or an int8 code (exact in fp16).
-template <int ES>
-__device__ __forceinline__ _Float16 code_at(uint32_t w, int i)
+// Chunk c of a tile (c = tid + i * NTHR): where it is read from, relative to
+// its half tile's kv-head block at in-page slot 0, and where it goes in LDS.
+// Padding chunks (and chunks past the tile) read chunk 0 and store nothing.
+struct PfChunk {
+    int half;           // uniform per wave
+    uint32_t gofs, rb;  // byte offset, plus rb bytes per in-page slot of the half
+    int lds;            // byte offset in an LDS buffer; -1: not stored
+    int key;            // the chunk's (first) key in the tile
+    bool scale;         // four fp32 scales rather than codes
+};
+
+template <int ES, int DK, int DV, int NTHR, int I>
+__device__ __forceinline__ PfChunk pf_chunk(int tid, int wave, uint32_t P)
 {
-    if constexpr (ES == 1)
-        return (_Float16)(float)(int8_t)(w >> (8 * i));
-    else
-        return __builtin_bit_cast(_Float16, (uint16_t)(w >> (16 * i)));
+    using T = PfTile<ES, DK, DV, NTHR>;
+    PfChunk k;
+    const int c = tid + I * NTHR;
+    const int cc = c < 2 * T::HP ? c : 2 * T::HP - 1;
+    // the half is known at compile time when chunks [I NTHR, (I+1) NTHR)
+    // lie in one half; else it follows from the (uniform) wave index
+    constexpr int C0 = I * NTHR, C1 = (I + 1) * NTHR - 1;
+    constexpr int H0 = (C0 < 2 * T::HP ? C0 : 2 * T::HP - 1) / T::HP;
+    constexpr int H1 = (C1 < 2 * T::HP ? C1 : 2 * T::HP - 1) / T::HP;
+    if constexpr (H0 == H1) {
+        k.half = H0;
+    } else {
+        const int cw = 64 * wave + I * NTHR;
+        k.half = (cw < 2 * T::HP ? cw : 2 * T::HP - 1) / T::HP;
+    }
+    int q = cc % T::HP;
+    const bool pad = c >= 2 * T::HP || q >= T::HCH;
+    if (pad)
+        q = 0;
+    k.scale = false;
+    if (q < 16 * T::KC) {
+        const int row = q / T::KC, col = q % T::KC;
+        k.gofs = 16u * q;
+        k.rb = DK * ES;
+        k.key = 16 * k.half + row;
+        k.lds = k.key * T::KPAD * 2 + col * 16 * (3 - ES);
+    } else if (q < 16 * (T::KC + T::VC)) {
+        const int q2 = q - 16 * T::KC, row = q2 / T::VC, col = q2 % T::VC;
+        k.gofs = P * (DK * ES) + 16u * q2;
+        k.rb = DV * ES;
+        k.key = 16 * k.half + row;
+        k.lds = T::VOFF + k.key * T::VPAD * 2 + col * 16 * (3 - ES);
+    } else {
+        const int s = q - 16 * (T::KC + T::VC);   // 0-3: k scales, 4-7: v scales (int8 only)
+        k.gofs = P * (DK + DV) + (s >= 4 ? 4u * P : 0u) + 16u * (s & 3);
+        k.rb = 4;
+        k.key = 16 * k.half + 4 * (s & 3);
+        k.lds = T::SOFF + (s >= 4 ? 4 * PF_KT : 0) + 4 * k.key;
+        k.scale = true;
+    }
+    if (pad)
+        k.lds = -1;
+    return k;
 }
 
-
-// One thread's part in moving key tiles from the page pool to LDS: chunk
-// c = tid + i * NTHR of a tile, K chunks [key][KC] first, then V chunks
-// [key][VC]. Every load is issued, from clamped indexes: a key past kmax
-// reads key kmax-1 (a stored position, so finite data that the causal mask
-// and a zero weight remove) and a thread past the last chunk reads the last
-// chunk, and never stores it. With no conditional loads, no loaded value is
-// needed before its use a stage later, so the in-order load counter drains
-// only old loads.
 template <int ES, int DK, int DV, int NTHR>
 struct PfIO {
     using T = PfTile<ES, DK, DV, NTHR>;
-    struct PageRef {
-        int32_t page[T::CPT];
-        int off[T::CPT];
+    // A tile's page ids and first in-page slots (uniform), as read a tile
+    // before its data is requested: the ids are used only then, so their
+    // reads have a tile to land. They are vector loads (of one address):
+    // the in-order vector-memory counter lets a later wait skip them, where
+    // a scalar read would be waited for by the next LDS wait (scalar reads
+    // return out of order, so that wait must drain them all). Their address
+    // carries threadIdx.y (zero in these one-dimensional launches), so the
+    // compiler keeps the ids in vector registers and moves them to scalar
+    // ones only where load() reads them, instead of right after the read
+    // (which would wait for it there). Half 1's slot is a difference from
+    // half 0's. Choices between two fields are made as base + (c ?
+    // difference : 0) throughout: a select between two loaded fields is
+    // folded into one load through a selected field address, which leaves
+    // the whole object in scratch memory.
+    struct TileRef {
+        uint32_t p0, p1;
+        uint32_t sip0, dsip;
+        int vlim;               // slots before the segment's end, from the tile's first
     };
     const uint8_t *pool;
-    const int32_t *own_pages, *pre_pages;
-    uint32_t page_bytes, head_bytes, log2_page, g;
-    int tid, kmax, n_sh;
+    const int32_t *own_pages;
+    int64_t pre_minus_own;      // prefix page-table row - own row, in entries
+    uint32_t zero;              // threadIdx.y: 0
+    uint64_t head_off;
+    uint32_t page_bytes, log2_page;
+    int tid, wave, n_sh, own_len;
+    // processing order: full shared tiles [0, nfs), own tiles visible to
+    // every row [nfs, jfull), then the masked ones: the partial shared tile
+    // (psh = 1 if there is one), then the own tiles crossing the diagonal
+    int nfs, psh, jfull, ntile;
 
-    __device__ __forceinline__ void fetch_pages(int kt, PageRef &pr) const
+    // tile t of the processing order: segment, first slot, segment length
+    // (selects, no branches: this runs on the scalar unit every tile)
+    __device__ __forceinline__ void seg(int t, bool &sh, int &s0, int &len) const
     {
-        const int P = 1 << log2_page;
-#pragma unroll
-        for (int i = 0; i < T::CPT; i++) {
-            const int c = min(tid + i * NTHR, T::NCHUNK - 1);
-            const bool isv = c >= PF_KT * T::KC;
-            const int cc = isv ? c - PF_KT * T::KC : c;
-            const int kl = isv ? cc / T::VC : cc / T::KC;
-            const int key = min(kt + kl, kmax - 1);
-            const bool sh = key < n_sh;
-            const int sl = sh ? key : key - n_sh;
-            pr.page[i] = (sh ? pre_pages : own_pages)[sl >> log2_page];
-            pr.off[i] = sl & (P - 1);
-        }
+        const bool tail = psh != 0 && t == jfull;       // the partial shared tile
+        sh = t < nfs || tail;
+        const int own = t - nfs - (t > jfull ? psh : 0);
+        s0 = PF_KT * (sh ? (tail ? nfs : t) : own);
+        len = own_len + (sh ? n_sh - own_len : 0);
     }
-    __device__ __forceinline__ void load(const PageRef &pr, Staged<T::CPT> &sg) const
+    // page ids of tile t (past the last tile: the last tile again); a half
+    // past its segment's end rereads half 0
+    __device__ __forceinline__ void fetch(int t, TileRef &r) const
     {
-        const int P = 1 << log2_page;
-#pragma unroll
-        for (int i = 0; i < T::CPT; i++) {
-            const int c = min(tid + i * NTHR, T::NCHUNK - 1);
-            const bool isv = c >= PF_KT * T::KC;
-            const int cc = isv ? c - PF_KT * T::KC : c;
-            const int ch = isv ? cc % T::VC : cc % T::KC;
-            const int off = pr.off[i];
-            // a page is under 4 GiB: one 32 x 32 -> 64-bit multiply-add
-            const uint8_t *hb = pool + (uint64_t)(uint32_t)pr.page[i] * page_bytes + (uint64_t)g * head_bytes;
-            const uint8_t *src = isv ? hb + (uint64_t)P * DK * ES + (uint64_t)off * DV * ES
-                                     : hb + (uint64_t)off * DK * ES;
-            sg.w[i] = __builtin_nontemporal_load(reinterpret_cast<const u32x4 *>(src) + ch);
-            if constexpr (ES == 1)
-                sg.sc[i] = reinterpret_cast<const float *>(hb + (uint64_t)P * (DK + DV))[(isv ? P : 0) + off];
-            else
-                sg.sc[i] = 0.0f;
-        }
+        bool sh;
+        int s0, len;
+        seg(min(t, ntile - 1), sh, s0, len);
+        const int s1 = s0 + 16 < len ? s0 + 16 : s0;
+        const int32_t *rows = own_pages + (sh ? pre_minus_own : 0);
+        r.p0 = (uint32_t)rows[((uint32_t)s0 >> log2_page) + zero];
+        r.p1 = (uint32_t)rows[((uint32_t)s1 >> log2_page) + zero];
+        const uint32_t m = (1u << log2_page) - 1;
+        r.sip0 = (uint32_t)s0 & m;
+        r.dsip = ((uint32_t)s1 & m) - r.sip0;
+        r.vlim = len - s0;
     }
-    __device__ __forceinline__ void store(const Staged<T::CPT> &sg, _Float16 (*Ks)[T::KPAD],
-                                          _Float16 (*Vr)[T::VPAD], float *Ksc, float *Vsc) const
+    __device__ __forceinline__ void load(const TileRef &r, Staged<T::CPT> &sg) const
     {
+        const uint32_t P = 1u << log2_page;
+        // a page is under 4 GiB: one 32 x 32 -> 64-bit multiply-add
+        const uint32_t p0 = __builtin_amdgcn_readfirstlane(r.p0), p1 = __builtin_amdgcn_readfirstlane(r.p1);
+        const uint8_t *hb0 = pool + ((uint64_t)p0 * page_bytes + head_off);
+        const int64_t dhb = ((int64_t)p1 - (int64_t)p0) * (int64_t)page_bytes;
+        static_for<T::CPT>([&](auto ic) __attribute__((always_inline)) {
+            constexpr int i = decltype(ic)::value;
+            const PfChunk k = pf_chunk<ES, DK, DV, NTHR, i>(tid, wave, P);
+            const uint8_t *hb = hb0 + (k.half ? dhb : 0);
+            const uint32_t off = k.gofs + (r.sip0 + (k.half ? r.dsip : 0u)) * k.rb;
+            sg.w[i] = __builtin_nontemporal_load(reinterpret_cast<const u32x4 *>(hb + off));
+        });
+        sg.vlim = r.vlim;
+    }
+    // a staged tile's chunks into LDS buffer buf; keys past its segment's
+    // end (a partial tile: surplus slots of the same pages, whose contents
+    // may be anything) store zero V rows / zero scales, so that masked keys
+    // add exactly nothing
+    __device__ __forceinline__ void store(const Staged<T::CPT> &sg, uint8_t *buf) const
+    {
+        const int vlim = sg.vlim;
+        const uint32_t P = 1u << log2_page;
+        static_for<T::CPT>([&](auto ic) __attribute__((always_inline)) {
+            constexpr int i = decltype(ic)::value;
+            const PfChunk k = pf_chunk<ES, DK, DV, NTHR, i>(tid, wave, P);
+            if (k.lds < 0)
+                return;
+            u32x4 w = sg.w[i];
+            if constexpr (ES == 2) {
+                if (vlim < PF_KT && k.key >= vlim)
+                    w = u32x4{0u, 0u, 0u, 0u};
+                *reinterpret_cast<u32x4 *>(buf + k.lds) = w;
+            } else if (k.scale) {
+                if (vlim < PF_KT) {
 #pragma unroll
-        for (int i = 0; i < T::CPT; i++) {
-            const int c = tid + i * NTHR;
-            if (c >= T::NCHUNK)
-                continue;
-            const bool isv = c >= PF_KT * T::KC;
-            const int cc = isv ? c - PF_KT * T::KC : c;
-            const int kl = isv ? cc / T::VC : cc / T::KC;
-            const int ch = isv ? cc % T::VC : cc % T::KC;
-            if (!isv) {
-                if constexpr (ES == 2) {
-                    *reinterpret_cast<u32x4 *>(&Ks[kl][ch * 8]) = sg.w[i];
-                } else {
-                    half8 lo, hi;
-#pragma unroll
-                    for (int e = 0; e < 8; e++) {
-                        lo[e] = code_at<1>(sg.w[i][e >> 2], e & 3);
-                        hi[e] = code_at<1>(sg.w[i][2 + (e >> 2)], e & 3);
-                    }
-                    *reinterpret_cast<half8 *>(&Ks[kl][ch * 16]) = lo;
-                    *reinterpret_cast<half8 *>(&Ks[kl][ch * 16 + 8]) = hi;
-                    if (ch == 0)
-                        Ksc[kl] = sg.sc[i];
+                    for (int e = 0; e < 4; e++)
+                        if (k.key + e >= vlim)
+                            w[e] = 0u;
                 }
+                *reinterpret_cast<u32x4 *>(buf + k.lds) = w;
             } else {
-                // V row-major, as stored: the P.V operand reads it transposed
-                if constexpr (ES == 2) {
-                    *reinterpret_cast<u32x4 *>(&Vr[kl][ch * 8]) = sg.w[i];
-                } else {
-                    half8 lo, hi;
-#pragma unroll
-                    for (int e = 0; e < 8; e++) {
-                        lo[e] = code_at<1>(sg.w[i][e >> 2], e & 3);
-                        hi[e] = code_at<1>(sg.w[i][2 + (e >> 2)], e & 3);
-                    }
-                    *reinterpret_cast<half8 *>(&Vr[kl][ch * 16]) = lo;
-                    *reinterpret_cast<half8 *>(&Vr[kl][ch * 16 + 8]) = hi;
-                    if (ch == 0)
-                        Vsc[kl] = sg.sc[i];
-                }
+                *reinterpret_cast<half8 *>(buf + k.lds) = codes8(u32x2{w.x, w.y});
+                *reinterpret_cast<half8 *>(buf + k.lds + 16) = codes8(u32x2{w.z, w.w});
             }
-        }
+        });
     }
 };
 
 template <int ES, int DK, int DV, int REP, int W>
-__global__ __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(W >= 8 ? 4 : 1)))
+__global__ __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(W >= 8 ? 4 : 3)))
 void prefill_kernel(PrefillArgs a)
 {
     using T = PfTile<ES, DK, DV, 64 * W>;
@@ -242,9 +339,7 @@ void prefill_kernel(PrefillArgs a)
     constexpr int NTHR = 64 * W;
 
     // two tile buffers: one is computed on while the next tile is written
-    __shared__ __attribute__((aligned(16))) _Float16 Ks2[2][PF_KT][T::KPAD];
-    __shared__ __attribute__((aligned(16))) _Float16 Vr2[2][PF_KT][T::VPAD];
-    __shared__ float Ksc2[2][PF_KT], Vsc2[2][PF_KT];
+    __shared__ __attribute__((aligned(16))) uint8_t kvbuf[2][T::BUF];
 
     const int tid = threadIdx.x;
     const int lane = tid & 63, wave = tid >> 6;
@@ -275,6 +370,49 @@ void prefill_kernel(PrefillArgs a)
     const int qpos = pos + tok;                 // keys [0, qpos] visible
     const uint64_t qrow = (uint64_t)(a.btok0[b] + tok) * a.nh + h;
 
+    // rows of this tile: keys up to the last valid row's position
+    const int last_r = min(r0 + ROWS, nrows) - 1;
+    const int kmax = pos + last_r / REP + 1;        // keys [0, kmax) are touched
+    const int kfull = pos + r0 / REP + 1;           // keys [0, kfull) visible to every row
+
+    float16v acc0 = {}, acc1 = {};
+    float m = -FLT_MAX, lsum = 0.0f;
+    const float neg1 = opaque_neg1();
+
+    PfIO<ES, DK, DV, NTHR> io;
+    io.pool = a.pool;
+    io.own_pages = a.page_table + (uint64_t)seq * a.pg.pages_per_seq;
+    io.zero = threadIdx.y;
+    io.pre_minus_own = sd.prefix >= 0 ? (a.prefix_pages + (uint64_t)sd.prefix * a.pg.pages_per_seq) -
+                                            (a.page_table + (uint64_t)seq * a.pg.pages_per_seq) : 0;
+    io.head_off = (uint64_t)g * a.pg.head_bytes;
+    io.page_bytes = a.pg.page_bytes;
+    io.log2_page = a.pg.log2_page;
+    io.tid = tid;
+    io.wave = __builtin_amdgcn_readfirstlane(wave);
+    io.n_sh = n_sh;
+    io.own_len = kmax - n_sh;                       // own slots [0, own_len) are touched
+    io.nfs = n_sh / PF_KT;
+    io.psh = n_sh % PF_KT != 0;
+    io.jfull = io.nfs + (kfull - n_sh) / PF_KT;     // + own tiles visible to every row
+    io.ntile = io.nfs + io.psh + (io.own_len + PF_KT - 1) / PF_KT;
+    const int ntile = io.ntile, jfull = io.jfull;
+
+    // Register prefetch: tile j+1 loads while tile j is computed and waits
+    // in registers for its LDS store at the end of tile j. The 8-wave
+    // variant fits the 128 registers of 4 waves per SIMD; the 2- and 4-wave
+    // ones fit 3 waves per SIMD (about 160 registers). A second tile in
+    // flight costs those a wave per SIMD and measured slower: a
+    // shared-prefix prefill of 48-token suffixes took 0.164 ms at 2 waves
+    // per SIMD with two tiles in flight and 0.145 ms at 3 with one. Page ids
+    // sit in a ring indexed by tile parity: those of tile j+2 are read at
+    // the start of tile j, next to the data load of tile j+1. Tile 0 is
+    // requested before Q, so its latency and Q's overlap.
+    typename PfIO<ES, DK, DV, NTHR>::TileRef prn[2];
+    Staged<T::CPT> sg;
+    io.fetch(0, prn[0]);
+    io.fetch(1, prn[1]);
+    io.load(prn[0], sg);                        // tile 0
     // Q^T operand, hi and lo halves, slots = dims 16*kb + 8*jh + s: eight
     // consecutive floats per k-block, loaded as two float4 (all issued
     // before any is used; rows past the chunk read row 0 and are zeroed).
@@ -307,50 +445,7 @@ void prefill_kernel(PrefillArgs a)
         }
     }
 
-    // rows of this tile: keys up to the last valid row's position
-    const int last_r = min(r0 + ROWS, nrows) - 1;
-    const int kmax = pos + last_r / REP + 1;        // keys [0, kmax) are touched
-    const int kfull = pos + r0 / REP + 1;           // keys [0, kfull) visible to every row
-
-    float16v acc0 = {}, acc1 = {};
-    float m = -FLT_MAX, lsum = 0.0f;
-    const float neg1 = opaque_neg1();
-
-    PfIO<ES, DK, DV, NTHR> io;
-    io.pool = a.pool;
-    io.own_pages = a.page_table + (uint64_t)seq * a.pg.pages_per_seq;
-    io.pre_pages = sd.prefix >= 0 ? a.prefix_pages + (uint64_t)sd.prefix * a.pg.pages_per_seq : nullptr;
-    io.page_bytes = a.pg.page_bytes;
-    io.head_bytes = a.pg.head_bytes;
-    io.log2_page = a.pg.log2_page;
-    io.g = g;
-    io.tid = tid;
-    io.kmax = kmax;
-    io.n_sh = n_sh;
-    const int ntile = (kmax + PF_KT - 1) / PF_KT;
-    const int jfull = min(kfull / PF_KT, ntile);    // tiles [0, jfull) visible to every row
-
-    // Register prefetch: with PD = 2, tile j+1 waits in registers for its
-    // LDS store while tile j+2 loads, so each load has two tiles of compute
-    // to land; the 8-wave variant keeps one tile in flight to stay within the
-    // 128 registers of 4 waves per SIMD. Tiles in flight and their page ids
-    // sit in rings indexed by tile parity (a register copy would wait on the
-    // newest load), and a tile's page ids are fetched before the data load
-    // issued beside them, so waiting for ids fetched a tile earlier never
-    // waits for the data load that followed them.
-    constexpr int PD = W >= 8 ? 1 : 2;
-    typename PfIO<ES, DK, DV, NTHR>::PageRef prn[2];
-    Staged<T::CPT> sg[PD];
-    io.fetch_pages(0, prn[0]);
-    io.fetch_pages(PF_KT, prn[1]);
-    io.load(prn[0], sg[0]);                     // tile 0
-    io.store(sg[0], Ks2[0], Vr2[0], Ksc2[0], Vsc2[0]);
-    io.fetch_pages(2 * PF_KT, prn[0]);
-    io.load(prn[1], sg[1 % PD]);                // tile 1
-    if constexpr (PD == 2) {
-        io.fetch_pages(3 * PF_KT, prn[1]);
-        io.load(prn[0], sg[0]);                 // tile 2
-    }
+    io.store(sg, kvbuf[0]);
     __syncthreads();
 
     // One key tile j (parity PJ = j & 1); the LDS buffer of tile j is PJ.
@@ -362,15 +457,13 @@ void prefill_kernel(PrefillArgs a)
     auto tile = [&](const int j, auto pj, auto masked, auto first) __attribute__((always_inline)) {
         constexpr int PJ = decltype(pj)::value, Q1 = PJ ^ 1;
         constexpr bool REL = ES == 2 && !decltype(first)::value;   // scores relative to m
-        const int kt = j * PF_KT;
-        // ids of tile j+PD+1 into the slot of tile j+PD-1's (spent), then the
-        // data of tile j+PD; past kmax the loads read the last key (finite
-        // data, masked)
-        io.fetch_pages((j + PD + 1) * PF_KT, prn[(PJ + PD + 1) & 1]);
-        io.load(prn[(PJ + PD) & 1], sg[(PJ + PD) % PD]);
-        const _Float16 (*Ks)[T::KPAD] = Ks2[PJ];
-        const _Float16 (*Vr)[T::VPAD] = Vr2[PJ];
-        const float *Ksc = Ksc2[PJ], *Vsc = Vsc2[PJ];
+        // ids of tile j+2 into the slot of tile j's (spent), then the data of
+        // tile j+1 (past the last tile: the last tile again, never stored)
+        io.fetch(j + 2, prn[PJ]);
+        io.load(prn[Q1], sg);
+        const _Float16 (*Ks)[T::KPAD] = reinterpret_cast<const _Float16 (*)[T::KPAD]>(kvbuf[PJ]);
+        const _Float16 (*Vr)[T::VPAD] = reinterpret_cast<const _Float16 (*)[T::VPAD]>(kvbuf[PJ] + T::VOFF);
+        const float *Ksc = reinterpret_cast<const float *>(kvbuf[PJ] + T::SOFF), *Vsc = Ksc + PF_KT;
 
         // ---- S^T = K . Q^T (keys x rows), accumulate hi then lo
         float16v st;
@@ -403,10 +496,15 @@ void prefill_kernel(PrefillArgs a)
                 st[i] *= Ksc[8 * (i >> 2) + 4 * jh + (i & 3)];
         }
         if constexpr (decltype(masked)::value) {
+            // key kl of the tile is position tb + kl; visible up to lim
+            bool sh;
+            int s0, len;
+            io.seg(j, sh, s0, len);
+            const int tb = sh ? s0 : n_sh + s0, lim = sh ? n_sh - 1 : qpos;
 #pragma unroll
             for (int i = 0; i < 16; i++) {
                 const int kl = 8 * (i >> 2) + 4 * jh + (i & 3);
-                st[i] = kt + kl > qpos ? -INFINITY : st[i];
+                st[i] = tb + kl > lim ? -INFINITY : st[i];
             }
         }
         // tile max over the 16 scores (a tree of 3-input maxes: fmaxf would
@@ -494,7 +592,7 @@ void prefill_kernel(PrefillArgs a)
         }
         __builtin_amdgcn_s_setprio(0);
         if (j + 1 < ntile)   // tile j+1 into the other buffer (its readers are done)
-            io.store(sg[(PJ + 1) % PD], Ks2[Q1], Vr2[Q1], Ksc2[Q1], Vsc2[Q1]);
+            io.store(sg, kvbuf[Q1]);
         __syncthreads();
     };
     using P0 = std::integral_constant<int, 0>;
@@ -585,22 +683,6 @@ void prefill_kernel(PrefillArgs a)
 // output lane i byte j is byte i % 8 at the address of lane 2 j + i / 8). The
 // k scale multiplies S and the v scale folds into P: the engine's
 // dequantisation (engine/src/nd_model.c:2179-2180, :2250-2252).
-template <int SEL>
-__device__ __forceinline__ half2v codes2(uint32_t xs)   // xs = codes ^ 0x80808080
-{
-    const uint32_t u = __builtin_amdgcn_perm(0x64646464u, xs, (uint32_t)SEL);
-    return __builtin_bit_cast(half2v, u) - half2v{(_Float16)1152.0f, (_Float16)1152.0f};
-}
-
-// eight int8 codes (bytes 0..7 of w) as fp16, in byte order
-__device__ __forceinline__ half8 codes8(u32x2 w)
-{
-    const uint32_t x0 = w.x ^ 0x80808080u, x1 = w.y ^ 0x80808080u;
-    const half2v c0 = codes2<0x04010400>(x0), c1 = codes2<0x04030402>(x0);
-    const half2v c2 = codes2<0x04010400>(x1), c3 = codes2<0x04030402>(x1);
-    return half8{c0[0], c0[1], c1[0], c1[1], c2[0], c2[1], c3[0], c3[1]};
-}
-
 // four int8 codes as the low k slots of an operand whose upper four are zero
 __device__ __forceinline__ half8 codes4(uint32_t w)
 {
@@ -612,7 +694,6 @@ __device__ __forceinline__ half8 codes4(uint32_t w)
 typedef float float4v __attribute__((ext_vector_type(4)));
 typedef int v2i __attribute__((ext_vector_type(2)));
 typedef __attribute__((address_space(3))) v2i lds_v2i;
-typedef const __attribute__((address_space(4))) int32_t *cptr;
 
 __device__ __forceinline__ float4v mfma16k32(half8 a, half8 b, float4v c)
 {
