@@ -294,10 +294,14 @@ struct PfIO {
         });
         sg.vlim = r.vlim;
     }
-    // a staged tile's chunks into LDS buffer buf; keys past its segment's
-    // end (a partial tile: surplus slots of the same pages, whose contents
-    // may be anything) store zero V rows / zero scales, so that masked keys
-    // add exactly nothing
+    // A staged tile's chunks into LDS buffer buf. Keys past the tile's
+    // segment end (a partial tile: surplus slots of the same pages, whose
+    // contents may be anything) must not bring non-finite values, which a
+    // zero weight would not remove: fp16 rows there are not stored (ZERO:
+    // stored as zeros), so they keep an earlier tile's finite rows or the
+    // zeros the buffer starts with; int8 codes are always finite, and their
+    // scales there are stored as zeros.
+    template <bool ZERO>
     __device__ __forceinline__ void store(const Staged<T::CPT> &sg, uint8_t *buf) const
     {
         const int vlim = sg.vlim;
@@ -309,9 +313,13 @@ struct PfIO {
                 return;
             u32x4 w = sg.w[i];
             if constexpr (ES == 2) {
-                if (vlim < PF_KT && k.key >= vlim)
-                    w = u32x4{0u, 0u, 0u, 0u};
-                *reinterpret_cast<u32x4 *>(buf + k.lds) = w;
+                if constexpr (ZERO) {
+                    if (k.key >= vlim)
+                        w = u32x4{0u, 0u, 0u, 0u};
+                    *reinterpret_cast<u32x4 *>(buf + k.lds) = w;
+                } else if (k.key < vlim) {
+                    *reinterpret_cast<u32x4 *>(buf + k.lds) = w;
+                }
             } else if (k.scale) {
                 if (vlim < PF_KT) {
 #pragma unroll
@@ -430,22 +438,31 @@ void prefill_kernel(PrefillArgs a)
         for (int kb = 0; kb < NKB; kb++) {
             const float xs[8] = {qv[kb][0].x, qv[kb][0].y, qv[kb][0].z, qv[kb][0].w,
                                  qv[kb][1].x, qv[kb][1].y, qv[kb][1].z, qv[kb][1].w};
+            u32x4 hw, lw;
 #pragma unroll
-            for (int s = 0; s < 8; s++) {
-                // hi and lo must both derive from the one rounded fp32 x;
-                // the empty asm keeps the compiler from rounding the exact
-                // product straight to fp16 for one of them (fused
-                // multiply-convert), which would pair lo with another hi
-                float x = xs[s] * qs;
-                asm volatile("" : "+v"(x));
-                const _Float16 hi = (_Float16)x;
-                qh[kb][s] = hi;
-                ql[kb][s] = (_Float16)(x - (float)hi);
+            for (int s = 0; s < 8; s += 2) {
+                // hi (rounded toward zero, two per conversion) and lo = x -
+                // hi rounded to nearest, as for P. Both must derive from the
+                // one rounded fp32 x: the empty asm keeps the compiler from
+                // feeding either conversion the exact product (a fused
+                // multiply-convert), which would pair lo with another hi.
+                float x0 = xs[s] * qs, x1 = xs[s + 1] * qs;
+                asm volatile("" : "+v"(x0), "+v"(x1));
+                const uint32_t h = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_pkrtz(x0, x1));
+                hw[s >> 1] = h;
+                lw[s >> 1] = split_lo2(h, x0, x1, neg1);
             }
+            qh[kb] = __builtin_bit_cast(half8, hw);
+            ql[kb] = __builtin_bit_cast(half8, lw);
         }
     }
 
-    io.store(sg, kvbuf[0]);
+    io.template store<true>(sg, kvbuf[0]);
+    if constexpr (ES == 2) {
+        // the other buffer starts as zeros (see PfIO::store)
+        for (int o = 16 * tid; o < T::BUF; o += 16 * NTHR)
+            *reinterpret_cast<u32x4 *>(kvbuf[1] + o) = u32x4{0u, 0u, 0u, 0u};
+    }
     __syncthreads();
 
     // One key tile j (parity PJ = j & 1); the LDS buffer of tile j is PJ.
@@ -496,16 +513,17 @@ void prefill_kernel(PrefillArgs a)
                 st[i] *= Ksc[8 * (i >> 2) + 4 * jh + (i & 3)];
         }
         if constexpr (decltype(masked)::value) {
-            // key kl of the tile is position tb + kl; visible up to lim
+            // key kl of the tile is position tb + kl, visible up to lim:
+            // register i (key 8 (i / 4) + 4 jh + i % 4) is masked when
+            // 8 (i / 4) + i % 4 > lim - tb - 4 jh
             bool sh;
             int s0, len;
             io.seg(j, sh, s0, len);
             const int tb = sh ? s0 : n_sh + s0, lim = sh ? n_sh - 1 : qpos;
+            const int thr = lim - tb - 4 * jh;
 #pragma unroll
-            for (int i = 0; i < 16; i++) {
-                const int kl = 8 * (i >> 2) + 4 * jh + (i & 3);
-                st[i] = tb + kl > lim ? -INFINITY : st[i];
-            }
+            for (int i = 0; i < 16; i++)
+                st[i] = 8 * (i >> 2) + (i & 3) > thr ? -INFINITY : st[i];
         }
         // tile max over the 16 scores (a tree of 3-input maxes: fmaxf would
         // first make NaN-quieting copies of its inputs; scores are never NaN)
@@ -592,7 +610,7 @@ void prefill_kernel(PrefillArgs a)
         }
         __builtin_amdgcn_s_setprio(0);
         if (j + 1 < ntile)   // tile j+1 into the other buffer (its readers are done)
-            io.store(sg, kvbuf[Q1]);
+            io.template store<false>(sg, kvbuf[Q1]);
         __syncthreads();
     };
     using P0 = std::integral_constant<int, 0>;
