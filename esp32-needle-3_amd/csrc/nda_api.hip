@@ -1350,7 +1350,7 @@ static int prefill_reserve(nda_ctx *c, const PrefillPlan &pl)
         return reserve_attend(c, (uint32_t)pl.rows, true, pl.max_total, pl.sum_total);
     if (int rc = ensure_rows(c, pl.rows))
         return rc;
-    return ensure_pf(c, 3 * (size_t)pl.nseq + 3 * pl.n_items);
+    return ensure_pf(c, 8 * pl.n_items);
 }
 
 int nda_prefill(nda_ctx *c, uint32_t layer, uint32_t nseq, const uint32_t *ids, const uint32_t *n_tokens,
@@ -1427,31 +1427,31 @@ int nda_prefill(nda_ctx *c, uint32_t layer, uint32_t nseq, const uint32_t *ids, 
         a.row_t = d_t;
         return run_attend(c, a, st);
     }
-    std::vector<uint32_t> host(3 * (size_t)nseq);
+    // One record per work item with all a work-group needs to start (its
+    // first reads then wait on one scalar load, not a chain of three):
+    // sequence (~0: padding), kv-head, row tile, first packed token, tokens,
+    // position, shared-prefix slots, prefix id (-1: none).
     std::vector<uint32_t> items;
+    items.reserve(8 * pl.n_items);
     for (uint32_t b = 0, tok = 0; b < nseq; b++) {
-        host[b] = sid(ids, b);
-        host[nseq + b] = tok;
-        host[2 * nseq + b] = n_tokens[b];
-        tok += n_tokens[b];
+        const uint32_t qq = sid(ids, b);
+        const SeqHost &s = c->seqs[qq];
+        const Vis v = visible(s, s.pos, c->cfg.window);
         const uint32_t nt = (n_tokens[b] * rep + trows - 1) / trows;
         for (uint32_t g = 0; g < c->cfg.n_kv_heads; g++)
             for (uint32_t t = 0; t < nt; t++) {
-                items.push_back(b);
-                items.push_back(g);
-                items.push_back(t);
+                const uint32_t rec[8] = {qq, g, t, tok, n_tokens[b], s.pos, v.n_sh, (uint32_t)s.prefix};
+                items.insert(items.end(), rec, rec + 8);
             }
+        tok += n_tokens[b];
     }
-    while ((items.size() / 3) % 8) {   // the kernel's XCD remap needs a multiple of 8
-        items.push_back(0xFFFFFFFFu);
-        items.push_back(0);
-        items.push_back(0);
+    while ((items.size() / 8) % 8) {   // the kernel's XCD remap needs a multiple of 8
+        const uint32_t pad[8] = {0xFFFFFFFFu, 0, 0, 0, 0, 0, 0, 0};
+        items.insert(items.end(), pad, pad + 8);
     }
-    if (int rc = ensure_pf(c, host.size() + items.size()))
+    if (int rc = ensure_pf(c, items.size()))
         return rc;
-    if (int rc = upload(c, c->d_pf, host.data(), host.size() * 4, st))
-        return rc;
-    if (int rc = upload(c, c->d_pf + host.size(), items.data(), items.size() * 4, st))
+    if (int rc = upload(c, c->d_pf, items.data(), items.size() * 4, st))
         return rc;
     PrefillArgs pa{};
     pa.q = q;
@@ -1461,12 +1461,9 @@ int nda_prefill(nda_ctx *c, uint32_t layer, uint32_t nseq, const uint32_t *ids, 
     pa.page_table = c->d_pages;
     pa.prefix_pages = c->d_prefix_pages;
     pa.seqs = c->d_seqs;
-    pa.bseq = c->d_pf;
-    pa.btok0 = c->d_pf + nseq;
-    pa.bntok = c->d_pf + 2 * (size_t)nseq;
-    pa.items = c->d_pf + host.size();
+    pa.items = c->d_pf;
     pa.pg = c->pg;
-    pa.n_items = (uint32_t)(items.size() / 3);
+    pa.n_items = (uint32_t)(items.size() / 8);
     pa.nh = c->cfg.n_heads;
     pa.qscale = (float)(1.4426950408889634 / std::sqrt((double)c->cfg.qk_head_dim));
     ProfScope ps(c, NDA_K_PREFILL, st);

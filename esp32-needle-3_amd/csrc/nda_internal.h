@@ -68,10 +68,9 @@ struct PrefillArgs {
     const int32_t *page_table;
     const int32_t *prefix_pages;
     const SeqDev *seqs;
-    const uint32_t *items;   /* [n_items][3]: batch index (~0: empty), kv-head, row tile */
-    const uint32_t *bseq;    /* [nseq] sequence id per batch index */
-    const uint32_t *btok0;   /* [nseq] first packed token of the batch index */
-    const uint32_t *bntok;   /* [nseq] tokens of the batch index */
+    const uint32_t *items;   /* prefill: [n_items][8] sequence (~0: empty), kv-head, row tile,
+                                first packed token, tokens, position, shared-prefix slots,
+                                prefix id (-1: none) */
     const uint32_t *row_seq; /* decode launches (one wave per item): sequence of each row, or null */
     PageGeom pg;
     uint32_t n_items;

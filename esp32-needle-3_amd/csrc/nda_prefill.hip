@@ -357,18 +357,19 @@ void prefill_kernel(PrefillArgs a)
     // K/V) are given to work-groups of one XCD and share its L2.
     const uint32_t nwg = gridDim.x, wg = blockIdx.x;
     const uint32_t item = (wg % 8u) * (nwg / 8u) + wg / 8u;
-    const uint32_t b = a.items[3 * item];
-    if (b == 0xFFFFFFFFu)
+    // the work item's record, read-only during the launch (scalar loads)
+    const __attribute__((address_space(4))) uint32_t *it =
+        (const __attribute__((address_space(4))) uint32_t *)(a.items + 8 * (uint64_t)item);
+    const uint32_t seq = it[0];
+    if (seq == 0xFFFFFFFFu)
         return;
-    const uint32_t g = a.items[3 * item + 1], rtile = a.items[3 * item + 2];
-    const uint32_t seq = a.bseq[b];
-    const SeqDev sd = a.seqs[seq];
-    const int ntok = (int)a.bntok[b];
+    const uint32_t g = it[1], rtile = it[2], tok0 = it[3];
+    const int ntok = (int)it[4];
+    const int pos = (int)it[5];
+    const int n_sh = (int)it[6];                // shared-prefix keys (fixed over the chunk)
+    const int prefix = (int)it[7];
     const int nrows = ntok * REP;
     const int r0 = (int)rtile * ROWS;
-    const int pos = sd.pos;
-    const Visible vis0 = visible(sd, pos, (int)a.pg.window);
-    const int n_sh = vis0.n_sh;                 // shared-prefix keys (fixed over the chunk)
 
     // this lane's query row
     const int r = r0 + wave * 32 + ln;
@@ -376,7 +377,7 @@ void prefill_kernel(PrefillArgs a)
     const int tok = rvalid ? r / REP : 0;
     const int h = (int)g * REP + (rvalid ? r % REP : 0);
     const int qpos = pos + tok;                 // keys [0, qpos] visible
-    const uint64_t qrow = (uint64_t)(a.btok0[b] + tok) * a.nh + h;
+    const uint64_t qrow = (uint64_t)(tok0 + tok) * a.nh + h;
 
     // rows of this tile: keys up to the last valid row's position
     const int last_r = min(r0 + ROWS, nrows) - 1;
@@ -391,8 +392,8 @@ void prefill_kernel(PrefillArgs a)
     io.pool = a.pool;
     io.own_pages = a.page_table + (uint64_t)seq * a.pg.pages_per_seq;
     io.zero = threadIdx.y;
-    io.pre_minus_own = sd.prefix >= 0 ? (a.prefix_pages + (uint64_t)sd.prefix * a.pg.pages_per_seq) -
-                                            (a.page_table + (uint64_t)seq * a.pg.pages_per_seq) : 0;
+    io.pre_minus_own = prefix >= 0 ? (a.prefix_pages + (uint64_t)prefix * a.pg.pages_per_seq) -
+                                         (a.page_table + (uint64_t)seq * a.pg.pages_per_seq) : 0;
     io.head_off = (uint64_t)g * a.pg.head_bytes;
     io.page_bytes = a.pg.page_bytes;
     io.log2_page = a.pg.log2_page;
@@ -426,7 +427,7 @@ void prefill_kernel(PrefillArgs a)
     // before any is used; rows past the chunk read row 0 and are zeroed).
     half8 qh[NKB], ql[NKB];
     {
-        const float *qr = a.q + (rvalid ? qrow : (uint64_t)a.btok0[b] * a.nh + (int)g * REP) * DK + 8 * jh;
+        const float *qr = a.q + (rvalid ? qrow : (uint64_t)tok0 * a.nh + (int)g * REP) * DK + 8 * jh;
         float4 qv[NKB][2];
 #pragma unroll
         for (int kb = 0; kb < NKB; kb++) {
