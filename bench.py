@@ -561,8 +561,8 @@ def block_prefill_leg(N, stream, nseq=1024, npre=213, nmin=32, nmax=64, reps=3, 
     nda_prefill_block over all sum(n) tokens (projections over every row,
     the front per sequence chunk, store + causal attention with the gate,
     out_proj). Archive shapes, int8 KV, 8 layers. Timed: the 8 layer calls
-    of one pass, with the profiling events off (best of reps passes); the
-    attach before each pass is not."""
+    of one pass, with the profiling events off (best of reps passes after
+    one warm-up pass); the attach before each pass is not."""
     rng = np.random.default_rng(SEED + 61)
     n = rng.integers(nmin, nmax + 1, nseq)
     ctx, cqs = engine_block_ctx(N, rng, nseq + 1, taps, theta)
@@ -577,11 +577,14 @@ def block_prefill_leg(N, stream, nseq=1024, npre=213, nmin=32, nmax=64, reps=3, 
     ctx.advance(1, [builder], npre, stream=stream)
     pid = ctx.prefix_build(builder, stream=stream)
     best = None
-    for rep in range(reps + 1):
+    # pass 0 is a warm-up (the library sizes its buffers for 1024 sequences
+    # and loads this work-group size's kernels on it), then `reps` timed
+    # passes, then one more with the profiling events on for the split
+    for rep in range(reps + 2):
         for b in range(nseq):
             ctx.seq_attach(b, pid, stream=stream)
         ctx.sync(stream)
-        prof = rep == reps          # the per-kernel split from one more pass, events on
+        prof = rep == reps + 1
         if prof:
             ctx.prof_enable(True)
             ctx.prof_read(reset=True)
@@ -600,7 +603,7 @@ def block_prefill_leg(N, stream, nseq=1024, npre=213, nmin=32, nmax=64, reps=3, 
         if prof:
             kms, _ = ctx.prof_read(reset=True)
             ctx.prof_enable(False)
-        elif best is None or el < best:
+        elif rep > 0 and (best is None or el < best):
             best, best_enq = el, enq
     per_pass = {name: round(kms[k], 4) for name, k in
                 (("projections_ms", N.K_PROJ), ("front_ms", N.K_FRONT), ("append_ms", N.K_APPEND),

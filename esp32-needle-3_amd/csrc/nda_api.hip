@@ -747,6 +747,10 @@ int nda_create(const nda_config *cfg_in, nda_ctx **out)
     // the pinned upload ring and its events; without them uploads copy from
     // pageable memory (correct, but the host then waits for the stream)
     if (hipHostMalloc((void **)&c->h_ring, UPLOAD_RING_BYTES, hipHostMallocDefault) == hipSuccess) {
+        // every page touched once here: the first pass of uploads through
+        // untouched ring pages ran ~15x slower (0.44 against 0.03 ms for
+        // one layer's tables), which put milliseconds into the first calls
+        memset(c->h_ring, 0, UPLOAD_RING_BYTES);
         c->ring_cap = UPLOAD_RING_BYTES;
         c->ring_ev.reserve(UPLOAD_EVENTS);
         for (int i = 0; i < UPLOAD_EVENTS; i++) {
