@@ -678,3 +678,107 @@ def test_page_sizes_decode_and_prefill(page_size):
             want = O.attend_runs(view, np.arange(pos + 1), [npre, pos + 1 - npre], qd[b], None)
             worst = max(worst, maxdiff(got[b], want))
         assert worst <= TOL, (dt, worst)
+
+
+def _poison_free_pages(N, ctx, seqs, npages, page_size, window, nh, nkv, dk, dv):
+    """Fill `npages` free pages with non-finite K/V through throwaway
+    sequences (at most a window's pages each), then give them back: later
+    owners find them there past their stored slots."""
+    left = npages
+    for seq in seqs:
+        if left == 0:
+            break
+        take = min(left, window // page_size)
+        left -= take
+        n = take * page_size
+        bad = np.full(n * nkv * max(dk, dv), np.nan, np.float32)
+        bad[1::3] = np.inf
+        q = N.DevBuf.from_array(np.zeros((n, nh, dk), np.float32))
+        k = N.DevBuf.from_array(bad[:n * nkv * dk].reshape(n, nkv, dk))
+        v = N.DevBuf.from_array(bad[:n * nkv * dv].reshape(n, nkv, dv))
+        out = N.DevBuf(n * nh * dv * 4)
+        ctx.prefill(0, [n], q, k, v, out, seq_ids=[seq])
+        ctx.sync()
+    assert left == 0
+    for seq in seqs:
+        ctx.seq_reset(seq)
+
+
+@pytest.mark.parametrize("page_size", [16, 64])
+@pytest.mark.parametrize("geom", [(8, 8, 64, 64), (12, 2, 48, 64)])
+def test_prefill_segment_ends_over_stale_nonfinite_slots(page_size, geom):
+    """Slots past a segment's end inside its last key tile (the prefix's
+    partial tile, an own tile that ends early, a half tile wholly past the
+    end) hold whatever their page held before. Here that is NaN / inf K/V
+    left by an earlier owner: the outputs must still match the oracle on
+    the stored slots. The pool holds exactly max_pages pages; the first
+    poisoning takes all of them and the second every free one, so every
+    slot these sequences do not store holds NaN or inf. Prefix of 200 =
+    6*32 + 8 slots (at 16 slots a page, its partial tile's second half lies
+    wholly past the end); suffixes of 20 and 45 tokens; then one decode
+    step."""
+    nh, nkv, dk, dv = geom
+    say("stale slots", page_size, geom)
+    N = nda()
+    rng = np.random.default_rng(40 + page_size + nh)
+    W, npre, n = 512, 200, [20, 45]
+    per = (npre + page_size - 1) // page_size
+    pages = 2 * per + sum((x + 1 + page_size - 1) // page_size for x in n) + 2
+    for dt in (O.KV_F16, O.KV_INT8):
+        ctx = N.Context(1, nh, nkv, dk, dv, W, kv_dtype=dt, max_seqs=4, page_size=page_size,
+                        max_pages=pages)
+        _poison_free_pages(N, ctx, [3, 0], pages, page_size, W, nh, nkv, dk, dv)
+        q = rng.standard_normal((npre, nh, dk)).astype(np.float32)
+        k = rng.standard_normal((npre, nkv, dk)).astype(np.float32)
+        v = rng.standard_normal((npre, nkv, dv)).astype(np.float32)
+        dout = N.DevBuf(npre * nh * dv * 4)
+        ctx.prefill(0, [npre], N.DevBuf.from_array(q), N.DevBuf.from_array(k), N.DevBuf.from_array(v),
+                    dout, seq_ids=[2])
+        ctx.sync()
+        got = dout.to_array(np.float32, (npre, nh * dv))
+        view, keep = _views_for(ctx, 0, 2, npre - 1, nh, dt)
+        worst = 0.0
+        for t in (0, 31, 100, 191, 192, 199):
+            want = O.attend_runs(view, np.arange(t + 1), [t + 1], q[t], None)
+            worst = max(worst, maxdiff(got[t], want))
+        ctx.advance(1, [2], npre)
+        pid = ctx.prefix_build(2)
+        ctx.seq_reset(2)
+        _poison_free_pages(N, ctx, [3, 0], pages - per, page_size, W, nh, nkv, dk, dv)
+        for b in range(2):
+            ctx.seq_attach(b, pid)
+        T = sum(n)
+        q = rng.standard_normal((T, nh, dk)).astype(np.float32)
+        k = rng.standard_normal((T, nkv, dk)).astype(np.float32)
+        v = rng.standard_normal((T, nkv, dv)).astype(np.float32)
+        dout = N.DevBuf(T * nh * dv * 4)
+        ctx.prefill(0, n, N.DevBuf.from_array(q), N.DevBuf.from_array(k), N.DevBuf.from_array(v), dout,
+                    seq_ids=[0, 1])
+        ctx.sync()
+        got = dout.to_array(np.float32, (T, nh * dv))
+        assert np.isfinite(got).all(), dt
+        r = 0
+        for b in range(2):
+            view, keep = _views_for(ctx, 0, b, npre + n[b] - 1, nh, dt)
+            for t in range(n[b]):
+                pos = npre + t
+                want = O.attend_runs(view, np.arange(pos + 1), [npre, pos + 1 - npre], q[r], None)
+                worst = max(worst, maxdiff(got[r], want))
+                r += 1
+        for b in range(2):
+            ctx.advance(1, [b], n[b])
+        qd = rng.standard_normal((2, nh, dk)).astype(np.float32)
+        kd = rng.standard_normal((2, nkv, dk)).astype(np.float32)
+        vd = rng.standard_normal((2, nkv, dv)).astype(np.float32)
+        dout = N.DevBuf(2 * nh * dv * 4)
+        ctx.step(0, 2, N.DevBuf.from_array(qd), N.DevBuf.from_array(kd), N.DevBuf.from_array(vd), dout)
+        ctx.sync()
+        got = dout.to_array(np.float32, (2, nh * dv))
+        assert np.isfinite(got).all(), dt
+        for b in range(2):
+            pos = ctx.seq_state(b)[0]
+            view, keep = _views_for(ctx, 0, b, pos, nh, dt)
+            want = O.attend_runs(view, np.arange(pos + 1), [npre, pos + 1 - npre], qd[b], None)
+            worst = max(worst, maxdiff(got[b], want))
+        ctx.close()
+        assert worst <= TOL, (dt, worst)
