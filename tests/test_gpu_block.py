@@ -4,9 +4,9 @@ the gate, out_proj) against the oracle's block, which is bit-exact to the
 engine's own attention(). The projections are fp32 on MFMA, reassociated,
 so k/v reach the int8 store within a few ulps of the engine's: stored codes
 may differ by one step where a value sits on a rounding boundary (counted,
-bounded at 0.1% of codes), and outputs are held to max |delta| <= 2e-3,
-relative to the call's largest output where that exceeds 1 (out_proj sums
-hundreds of terms)."""
+bounded at 0.01% of codes; these cases see at most two in ~10^5), and
+outputs are held to max |delta| <= 1e-3, relative to the call's largest
+output where that exceeds 1 (out_proj sums hundreds of terms)."""
 import os
 import sys
 
@@ -19,7 +19,7 @@ from detgen import Stream, make_block_weights
 pytestmark = pytest.mark.gpu
 
 HERE = os.path.dirname(os.path.abspath(__file__))
-TOL = 2e-3
+TOL = 1e-3
 
 
 def nda():
@@ -147,10 +147,11 @@ def test_block_batched(kv_dtype):
                     for got_r, want_r in ((k[j], ok[li, sl]), (v[j], ov[li, sl])):
                         gv = got_r.view(np.float16).astype(np.float64)
                         wv = want_r.view(np.float16).astype(np.float64)
-                        assert np.all(np.abs(gv - wv) <= 2e-3 * np.maximum(1.0, np.abs(wv))), (b, li, p)
+                        # within one fp16 step (2^-10 relative) of the oracle's row
+                        assert np.all(np.abs(gv - wv) <= 2.0 ** -10 * np.maximum(1.0, np.abs(wv))), (b, li, p)
     say("block batched worst (relative)", worst, "code flips", flips, "of", codes, "scale rel", sc_rel)
     assert worst <= TOL, worst
-    assert flips <= max(1, codes // 1000), (flips, codes)
+    assert flips <= max(1, codes // 10000), (flips, codes)
     assert sc_rel <= 1e-5, sc_rel
     for layer in cqs:
         for c in layer:

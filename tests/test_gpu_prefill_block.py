@@ -4,9 +4,10 @@ store and causal attention with the gate, out_proj) against the oracle's
 block stepped one token at a time, which is bit-exact to the engine's own
 attention() (the engine prefills by repeated nd_model_step_hidden,
 esp32/main/main.c:233-234, :312-315). Same bar as the decode block: outputs
-within 2e-3 relative to the call's output scale, stored int8 codes within
+within 1e-3 relative to the call's output scale, stored int8 codes within
 one step where the projections' fp32 reassociation moves a value across a
-rounding boundary (counted, at most 0.1%)."""
+rounding boundary (counted, at most 0.01%; these cases see one or two in
+~10^5)."""
 import sys
 
 import numpy as np
@@ -17,7 +18,7 @@ from detgen import make_block_weights
 
 pytestmark = pytest.mark.gpu
 
-TOL = 2e-3
+TOL = 1e-3
 
 
 def nda():
@@ -135,7 +136,8 @@ class Rig:
                     else:
                         gv = g_.view(np.float16).astype(np.float64)
                         wv = w_.view(np.float16).astype(np.float64)
-                        assert np.all(np.abs(gv - wv) <= 2e-3 * np.maximum(1.0, np.abs(wv))), (b, li, p)
+                        # within one fp16 step (2^-10 relative) of the oracle's row
+                        assert np.all(np.abs(gv - wv) <= 2.0 ** -10 * np.maximum(1.0, np.abs(wv))), (b, li, p)
                 if self.kv_dtype == O.KV_INT8:
                     for g_, w_ in ((ks[0], oks[li, sl]), (vs[0], ovs[li, sl])):
                         assert np.all(np.abs(g_ - w_) <= 1e-5 * np.abs(w_) + 1e-30), (b, li, p)
@@ -168,7 +170,7 @@ def test_prefill_block_ragged_chunks(kv_dtype):
         flips, codes = flips + f, codes + c
     say("prefill block worst (relative)", R.worst, "code flips", flips, "of", codes)
     assert R.worst <= TOL, R.worst
-    assert flips <= max(1, codes // 1000), (flips, codes)
+    assert flips <= max(1, codes // 10000), (flips, codes)
     R.close()
 
 
@@ -206,7 +208,7 @@ def test_prefill_block_shared_prefix_flow():
         assert np.all(np.abs(h - want) <= 1e-4 * np.maximum(1.0, np.abs(want))), b
     say("prefill block prefix worst (relative)", R.worst, "code flips", flips, "of", codes)
     assert R.worst <= TOL, R.worst
-    assert flips <= max(1, codes // 1000), (flips, codes)
+    assert flips <= max(1, codes // 10000), (flips, codes)
     R.close()
 
 
