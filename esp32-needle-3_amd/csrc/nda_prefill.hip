@@ -278,6 +278,12 @@ struct PfIO {
         r.dsip = ((uint32_t)s1 & m) - r.sip0;
         r.vlim = len - s0;
     }
+    // Plain loads, not nontemporal ones: a tile is read again by other
+    // work-groups (every sequence reads the shared prefix's tiles; the row
+    // groups of one sequence and kv-head read the same own tiles), and L2
+    // keeps it for them. With the nontemporal hint a shared-prefix prefill
+    // of 48-token suffixes took 0.142 ms instead of 0.122, and a 512-token
+    // chunk 3-4% longer.
     __device__ __forceinline__ void load(const TileRef &r, Staged<T::CPT> &sg) const
     {
         const uint32_t P = 1u << log2_page;
@@ -290,7 +296,7 @@ struct PfIO {
             const PfChunk k = pf_chunk<ES, DK, DV, NTHR, i>(tid, wave, P);
             const uint8_t *hb = hb0 + (k.half ? dhb : 0);
             const uint32_t off = k.gofs + (r.sip0 + (k.half ? r.dsip : 0u)) * k.rb;
-            sg.w[i] = __builtin_nontemporal_load(reinterpret_cast<const u32x4 *>(hb + off));
+            sg.w[i] = *reinterpret_cast<const u32x4 *>(hb + off);
         });
         sg.vlim = r.vlim;
     }
