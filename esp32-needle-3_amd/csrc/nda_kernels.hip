@@ -63,13 +63,24 @@ struct Words {
     uint32_t w[NB / 4];
 };
 
-template <int NB>
+// NT: nontemporal loads (a row read once); plain loads where other
+// work-groups read the same rows (a shared prefix), which L2 then keeps
+template <typename V, bool NT>
+__device__ __forceinline__ V ld(const V *p)
+{
+    if constexpr (NT)
+        return __builtin_nontemporal_load(p);
+    else
+        return *p;
+}
+
+template <int NB, bool NT = true>
 __device__ __forceinline__ void load_words(Words<NB> &d, const uint8_t *p)
 {
     if constexpr (NB % 16 == 0) {
 #pragma unroll
         for (int i = 0; i < NB / 16; i++) {
-            u32x4 x = __builtin_nontemporal_load(reinterpret_cast<const u32x4 *>(p) + i);
+            u32x4 x = ld<u32x4, NT>(reinterpret_cast<const u32x4 *>(p) + i);
             d.w[4 * i + 0] = x.x;
             d.w[4 * i + 1] = x.y;
             d.w[4 * i + 2] = x.z;
@@ -78,25 +89,25 @@ __device__ __forceinline__ void load_words(Words<NB> &d, const uint8_t *p)
     } else if constexpr (NB % 8 == 0) {
 #pragma unroll
         for (int i = 0; i < NB / 8; i++) {
-            u32x2 x = __builtin_nontemporal_load(reinterpret_cast<const u32x2 *>(p) + i);
+            u32x2 x = ld<u32x2, NT>(reinterpret_cast<const u32x2 *>(p) + i);
             d.w[2 * i + 0] = x.x;
             d.w[2 * i + 1] = x.y;
         }
     } else {
 #pragma unroll
         for (int i = 0; i < NB / 4; i++)
-            d.w[i] = __builtin_nontemporal_load(reinterpret_cast<const uint32_t *>(p) + i);
+            d.w[i] = ld<uint32_t, NT>(reinterpret_cast<const uint32_t *>(p) + i);
     }
 }
 
 // The first nb bytes of a slice (whole dwords; nb may be <= 0), the rest zero:
 // a lane's part of a row whose true length is shorter than the padded one.
-template <int NB>
+template <int NB, bool NT = true>
 __device__ __forceinline__ void load_words_upto(Words<NB> &d, const uint8_t *p, int nb)
 {
 #pragma unroll
     for (int i = 0; i < NB / 4; i++)
-        d.w[i] = 4 * i < nb ? __builtin_nontemporal_load(reinterpret_cast<const uint32_t *>(p) + i) : 0u;
+        d.w[i] = 4 * i < nb ? ld<uint32_t, NT>(reinterpret_cast<const uint32_t *>(p) + i) : 0u;
 }
 
 // Element e of a loaded slice as float: int8 code or fp16 value.
@@ -136,7 +147,7 @@ struct AttnState {
 // RT: the rows are a.pg.dk / a.pg.dv elements long (multiples of 4, at most
 // DK / DV, the padded register layout); lanes load only their part of the
 // true row, and the padding reads as zero.
-template <bool MASK, bool RT, int ES, int DK, int DV, int REP, int G, int NP, int NW>
+template <bool MASK, bool RT, bool NT, int ES, int DK, int DV, int REP, int G, int NP, int NW>
 __device__ __forceinline__ void attn_step(AttnState<ES, DK, DV, REP, G, NP, NW> &st,
                                           const AttnArgs &a, const int32_t *pages, uint32_t g,
                                           int blk0, int s0, int s1, int grp, int li)
@@ -164,11 +175,11 @@ __device__ __forceinline__ void attn_step(AttnState<ES, DK, DV, REP, G, NP, NW> 
             const uint8_t *kp = hb + (uint64_t)off * dk * ES + li * C::KB;
             const uint8_t *vp = hb + (uint64_t)P * dk * ES + (uint64_t)off * dv * ES + li * C::VB;
             if constexpr (RT) {
-                load_words_upto<C::KB>(kw[j], kp, dk * ES - li * C::KB);
-                load_words_upto<C::VB>(vw[j], vp, dv * ES - li * C::VB);
+                load_words_upto<C::KB, NT>(kw[j], kp, dk * ES - li * C::KB);
+                load_words_upto<C::VB, NT>(vw[j], vp, dv * ES - li * C::VB);
             } else {
-                load_words<C::KB>(kw[j], kp);
-                load_words<C::VB>(vw[j], vp);
+                load_words<C::KB, NT>(kw[j], kp);
+                load_words<C::VB, NT>(vw[j], vp);
             }
             if constexpr (ES == 1) {
                 const float *sc = reinterpret_cast<const float *>(hb + (uint64_t)P * (dk + dv));
@@ -251,7 +262,7 @@ __device__ __forceinline__ void attn_step(AttnState<ES, DK, DV, REP, G, NP, NW> 
     }
 }
 
-template <bool RT, int ES, int DK, int DV, int REP, int G, int NP, int NW>
+template <bool RT, bool NT, int ES, int DK, int DV, int REP, int G, int NP, int NW>
 __device__ __forceinline__ void attn_run(AttnState<ES, DK, DV, REP, G, NP, NW> &st, const AttnArgs &a,
                                          const int32_t *pages, uint32_t g, int s0, int s1, int wave,
                                          int grp, int li)
@@ -261,9 +272,9 @@ __device__ __forceinline__ void attn_run(AttnState<ES, DK, DV, REP, G, NP, NW> &
     const int start = (s0 / C::PW) * C::PW;
     for (int it = start + wave * BLK; it < s1; it += NW * BLK) {
         if (it >= s0 && it + BLK <= s1)
-            attn_step<false, RT>(st, a, pages, g, it, s0, s1, grp, li);
+            attn_step<false, RT, NT>(st, a, pages, g, it, s0, s1, grp, li);
         else
-            attn_step<true, RT>(st, a, pages, g, it, s0, s1, grp, li);
+            attn_step<true, RT, NT>(st, a, pages, g, it, s0, s1, grp, li);
     }
 }
 
@@ -347,10 +358,10 @@ __global__ __launch_bounds__(64 * NW) void attend_kernel(AttnArgs a)
     }
 
     if (c0 < vis.n_sh)
-        attn_run<RT>(st, a, a.prefix_pages + (uint64_t)sd.prefix * a.pg.pages_per_seq, g, c0,
+        attn_run<RT, false>(st, a, a.prefix_pages + (uint64_t)sd.prefix * a.pg.pages_per_seq, g, c0,
                      min(c1, vis.n_sh), wave, grp, li);
     if (c1 > vis.n_sh)
-        attn_run<RT>(st, a, a.page_table + (uint64_t)seq * a.pg.pages_per_seq, g,
+        attn_run<RT, true>(st, a, a.page_table + (uint64_t)seq * a.pg.pages_per_seq, g,
                      max(c0, vis.n_sh) - vis.n_sh, c1 - vis.n_sh, wave, grp, li);
 
     // Merge the lane groups of this wave: lanes li, li+G, li+2G, ...
