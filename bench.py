@@ -294,8 +294,10 @@ def shared_prefix_leg(N, stream, nseq=1024, npre=213, nmin=32, nmax=64, dsteps=6
     t_dec = time.perf_counter() - t0
     ms2, launches2 = ctx.prof_read(reset=True)
     ctx.prof_enable(False)
-    dec_ms = ms2[N.K_DECODE] / max(1, launches2[N.K_DECODE])
-    # per decode launch: the prefix once + every sequence's own positions
+    # per layer and step: every decode launch (with a shared prefix, the
+    # prefix pass and the own-positions pass) and the merge
+    dec_ms = (ms2[N.K_DECODE] + ms2[N.K_COMBINE]) / (dsteps * layers)
+    # per decode step: the prefix once + every sequence's own positions
     own = sum(int(x) + s + 1 for x in n for s in range(dsteps)) / dsteps
     uniq = npre * 2048 + own * 2048 + nseq * H * D * 4 * 2
     logical = nseq * npre * 2048 + own * 2048 + nseq * H * D * 4 * 2

@@ -637,7 +637,7 @@ int run_attend(nda_ctx *c, AttnArgs &a, hipStream_t st, float *part = nullptr, b
         if (e != hipSuccess)
             return hip_fail(c, e, "attend kernel launch");
     }
-    if (a.max_chunks > 1) {
+    if (a.max_chunks > 1 && !(a.chunk_lo == 1 && a.max_chunks == 2)) {
         ProfScope ps(c, NDA_K_COMBINE, st, prof);
         hipError_t e = launch_combine(c->geo, a, st);
         if (e != hipSuccess)
@@ -1169,6 +1169,114 @@ static int decode_check(nda_ctx *c, uint32_t layer, uint32_t nseq, const uint32_
     return NDA_OK;
 }
 
+// A decode batch whose sequences all read one shared prefix (the engine's
+// requests on its routing schema) attends that prefix in one pass over all
+// of them: per kv-head, the prefix's key tiles against every sequence's
+// query rows on the prefill kernel's MFMA tiles, each row's softmax state
+// left as its split-KV chunk 0 (chunks of n_sh positions). The VALU kernel
+// continues with each sequence's own positions (chunks 1 on) and the merge
+// combines the chunks; otherwise the VALU kernel redoes the prefix's dot
+// products for every sequence. Taken for batches of at least 4 (row,
+// kv-head) units per CU of a shape the prefill kernel is built for and the
+// MFMA GQA decode does not serve, with a prefix of at least one full key
+// tile, and not when the append is fused into the launch.
+struct PrefixSplit {
+    bool on = false;
+    int32_t prefix = -1;
+    uint32_t n_sh = 0, max_chunks = 0, n_items = 0;
+};
+constexpr int PREFIX_PASS_WAVES = 2;    // 64-row work-groups: more of them to spread over the CUs
+
+// whether a batch's sequences qualify (append not fused; see above)
+static bool prefix_split_batch(const nda_ctx *c, uint32_t nseq, const uint32_t *ids, int32_t *pfx_out,
+                               uint32_t *nsh_out)
+{
+    if (nseq == 0 || mfma_decode_geo(c) || !prefill_mfma_supported(c->geo) ||
+        (c->cfg.flags & (NDA_FLAG_PREFILL_VALU | NDA_FLAG_DECODE_VALU)))
+        return false;
+    if ((uint64_t)nseq * c->cfg.n_kv_heads < 4ull * (uint64_t)c->cus)
+        return false;
+    int32_t pfx = -1;
+    uint32_t nsh = 0;
+    for (uint32_t b = 0; b < nseq; b++) {
+        const SeqHost &s = c->seqs[sid(ids, b)];
+        if (s.prefix < 0)
+            return false;
+        const Vis v = visible(s, s.pos, c->cfg.window);
+        if (b == 0) {
+            pfx = s.prefix;
+            nsh = v.n_sh;
+        } else if (s.prefix != pfx || v.n_sh != nsh) {
+            return false;
+        }
+    }
+    *pfx_out = pfx;
+    *nsh_out = nsh;
+    return nsh >= 32;
+}
+
+static void prefix_split_plan(nda_ctx *c, uint32_t nseq, const uint32_t *ids, bool fused, uint32_t max_total,
+                              PrefixSplit &ps)
+{
+    ps = PrefixSplit();
+    int32_t pfx;
+    uint32_t nsh;
+    if (fused || !prefix_split_batch(c, nseq, ids, &pfx, &nsh) || max_total <= nsh)
+        return;
+    ps.on = true;
+    ps.prefix = pfx;
+    ps.n_sh = nsh;
+    ps.max_chunks = (max_total + nsh - 1) / nsh;
+    const uint64_t trows = 32u * PREFIX_PASS_WAVES;
+    const uint64_t per_head = ((uint64_t)nseq * c->geo.rep + trows - 1) / trows;
+    ps.n_items = (uint32_t)((per_head * c->cfg.n_kv_heads + 7) / 8 * 8);
+}
+
+// The prefix pass: work item (kv-head, tile of 64 rows of the batch), the
+// rows being (sequence of the batch, query head of the group) pairs as the
+// decode's q holds them.
+static int prefix_pass(nda_ctx *c, const AttnArgs &a, uint32_t nseq, const uint32_t *ids, const PrefixSplit &ps,
+                       hipStream_t st)
+{
+    const uint64_t trows = 32u * PREFIX_PASS_WAVES;
+    const uint32_t per_head = (uint32_t)(((uint64_t)nseq * c->geo.rep + trows - 1) / trows);
+    std::vector<uint32_t> items;
+    items.reserve(8 * (size_t)ps.n_items);
+    const uint32_t seq0 = sid(ids, 0);
+    for (uint32_t g = 0; g < c->cfg.n_kv_heads; g++)
+        for (uint32_t t = 0; t < per_head; t++) {
+            // sequence, kv-head, row tile, first row, rows, position (unused),
+            // prefix slots, prefix id; the sequence only names a page-table
+            // row, which a pass with no own tiles never reads
+            const uint32_t rec[8] = {seq0, g, t, 0u, nseq, ps.n_sh, ps.n_sh, (uint32_t)ps.prefix};
+            items.insert(items.end(), rec, rec + 8);
+        }
+    while ((items.size() / 8) % 8) {
+        const uint32_t pad[8] = {0xFFFFFFFFu, 0, 0, 0, 0, 0, 0, 0};
+        items.insert(items.end(), pad, pad + 8);
+    }
+    if (int rc = upload(c, c->d_pf, items.data(), items.size() * 4, st))
+        return rc;
+    PrefillArgs pa{};
+    pa.q = a.q;
+    pa.pool = a.pool;
+    pa.page_table = a.page_table;
+    pa.prefix_pages = a.prefix_pages;
+    pa.seqs = a.seqs;
+    pa.items = c->d_pf;
+    pa.part = a.part;
+    pa.max_chunks = a.max_chunks;
+    pa.pg = a.pg;
+    pa.n_items = (uint32_t)(items.size() / 8);
+    pa.nh = a.nh;
+    pa.qscale = a.qscale;
+    ProfScope ps_(c, NDA_K_DECODE, st);
+    hipError_t e = launch_prefill(c->geo, pa, PREFIX_PASS_WAVES, st);
+    if (e != hipSuccess)
+        return hip_fail(c, e, "shared-prefix decode pass launch");
+    return NDA_OK;
+}
+
 static int decode_impl(nda_ctx *c, uint32_t layer, uint32_t nseq, const uint32_t *ids, const float *q,
                        const float *k, const float *v, const float *gate, float *out, void *stream)
 {
@@ -1195,6 +1303,14 @@ static int decode_impl(nda_ctx *c, uint32_t layer, uint32_t nseq, const uint32_t
         return rc;
     if (int rc = reserve_attend(c, nseq, ids != nullptr, max_total, sum_total))
         return rc;
+    PrefixSplit psp;
+    prefix_split_plan(c, nseq, ids, k != nullptr, max_total, psp);
+    if (psp.on) {
+        if (int rc = ensure_part(c, (size_t)nseq * c->cfg.n_heads * psp.max_chunks * (c->cfg.v_head_dim + 2)))
+            return rc;
+        if (int rc = ensure_pf(c, 8 * (size_t)psp.n_items))
+            return rc;
+    }
     txn.commit();
     if (k)
         for (uint32_t b = 0; b < nseq; b++) {
@@ -1212,6 +1328,15 @@ static int decode_impl(nda_ctx *c, uint32_t layer, uint32_t nseq, const uint32_t
     a.row_t = d_t;
     a.k_new = k;
     a.v_new = v;
+    if (psp.on) {
+        a.chunk = psp.n_sh;
+        a.max_chunks = psp.max_chunks;
+        a.part = c->d_part;
+        if (int rc = prefix_pass(c, a, nseq, ids, psp, st))
+            return rc;
+        a.chunk_lo = 1;
+        return run_attend(c, a, st, c->d_part);
+    }
     return run_attend(c, a, st);
 }
 
@@ -1264,14 +1389,18 @@ int nda_decode_noalloc(nda_ctx *c, uint32_t layer, uint32_t nseq, const uint32_t
 // two launches: a store plus barrier at the head of every one of tens of
 // thousands of work-groups costs more than the separate append kernel; GQA
 // groups the MFMA decode serves switch to it (and so to two launches) from
-// 4 work items per CU.
+// 4 work items per CU, and so do batches on one shared prefix that its
+// decode pass serves.
 int nda_step(nda_ctx *c, uint32_t layer, uint32_t nseq, const uint32_t *ids, const float *q,
              const float *k, const float *v, const float *gate, float *out, void *stream)
 {
     if (c && nseq && (!k || !v))
         return fail(c, NDA_ERR_ARG, "null k/v");
     const uint64_t units = c ? (uint64_t)nseq * c->cfg.n_kv_heads : 0;
-    if (c && (units >= 16ull * (uint64_t)c->cus || (mfma_decode_geo(c) && units >= 4ull * (uint64_t)c->cus))) {
+    int32_t pfx;
+    uint32_t nsh;
+    if (c && (units >= 16ull * (uint64_t)c->cus || (mfma_decode_geo(c) && units >= 4ull * (uint64_t)c->cus) ||
+              (check_ids(c, nseq, ids) == NDA_OK && prefix_split_batch(c, nseq, ids, &pfx, &nsh)))) {
         if (int rc = nda_kv_append(c, layer, nseq, ids, k, v, stream))
             return rc;
         return decode_impl(c, layer, nseq, ids, q, nullptr, nullptr, gate, out, stream);

@@ -52,6 +52,7 @@ struct AttnArgs {
     uint32_t nh;
     uint32_t chunk;          /* positions per work item */
     uint32_t max_chunks;
+    uint32_t chunk_lo;       /* first chunk launched (a shared-prefix pass wrote those below) */
     float qscale;            /* log2(e) / sqrt(dk) */
     const float *k_new;      /* [rows][nkv][dk] fused append (decode), or null */
     const float *v_new;      /* [rows][nkv][dv] */
@@ -72,6 +73,8 @@ struct PrefillArgs {
                                 first packed token, tokens, position, shared-prefix slots,
                                 prefix id (-1: none) */
     const uint32_t *row_seq; /* decode launches (one wave per item): sequence of each row, or null */
+    float *part;             /* shared-prefix decode pass: split-KV partials of chunk 0, or null */
+    uint32_t max_chunks;     /*   their stride (AttnArgs::max_chunks) */
     PageGeom pg;
     uint32_t n_items;
     uint32_t nh;

@@ -305,7 +305,7 @@ __global__ __launch_bounds__(64 * NW) void attend_kernel(AttnArgs a)
     const uint32_t nkv = a.pg.nkv;
     const uint32_t unit = blockIdx.x;
     const uint32_t row = unit / (nkv * HS), gv = unit % (nkv * HS), g = gv / HS;   // heads gv*REP..+REP
-    const uint32_t chunk = blockIdx.y;
+    const uint32_t chunk = blockIdx.y + a.chunk_lo;
 
     const uint32_t seq = a.row_seq ? a.row_seq[row] : row;
     const SeqDev sd = a.seqs[seq];
@@ -426,6 +426,25 @@ __global__ __launch_bounds__(64 * NW) void attend_kernel(AttnArgs a)
                     o[e] = z;
                 }
             }
+        } else if (a.chunk_lo == 1 && nchunks == 2) {
+            // a shared-prefix pass left chunk 0 (the prefix) and this is the
+            // row's only other chunk: merge the two here and write the row
+            const float *r0 = a.part + ((uint64_t)row * a.nh + h) * a.max_chunks * (dv + 2);
+            const float m0 = r0[dv], l0 = r0[dv + 1];
+            const float M = fmaxf(st.m[t], m0);
+            const float ca = fast_exp2(st.m[t] - M), cb = fast_exp2(m0 - M);
+            const float inv = 1.0f / (st.l[t] * ca + l0 * cb);
+            float *o = a.out + ((uint64_t)row * a.nh + h) * dv + li * C::EV;
+            const float *gt = a.gate ? a.gate + ((uint64_t)row * a.nh + h) * dv + li * C::EV : nullptr;
+#pragma unroll
+            for (int e = 0; e < C::EV; e++) {
+                if (!RT || li * C::EV + e < dv) {
+                    float z = (st.acc[t][e] * ca + r0[li * C::EV + e] * cb) * inv;
+                    if (gt)
+                        z *= sigmoid_dev(gt[e]);
+                    o[e] = z;
+                }
+            }
         } else {
             float *r = a.part + (((uint64_t)row * a.nh + h) * a.max_chunks + chunk) * (dv + 2);
 #pragma unroll
@@ -454,7 +473,7 @@ __global__ __launch_bounds__(256) void combine_kernel(AttnArgs a)
     const int p = sd.pos + (a.row_t ? (int)a.row_t[row] : 0);
     const Visible vis = visible(sd, p, (int)a.pg.window);
     const int nchunks = (vis.n_sh + vis.n_own + (int)a.chunk - 1) / (int)a.chunk;
-    if (nchunks <= 1)
+    if (nchunks <= 1 || (a.chunk_lo == 1 && nchunks == 2))    // (the attend kernel wrote the row)
         return;
     const float *base = a.part + ((uint64_t)row * a.nh + h) * a.max_chunks * (DV + 2);
     float M = -FLT_MAX;
@@ -776,7 +795,7 @@ static void launch_attend_hs(const AttnArgs &a, hipStream_t s)
 {
     constexpr int R = REP / HS;
     constexpr int G = RT ? lanes_rt<ES, R>() : lanes_per_pos<ES, DK, R>();
-    const dim3 grid(a.rows * a.pg.nkv * HS, a.max_chunks);
+    const dim3 grid(a.rows * a.pg.nkv * HS, a.max_chunks - a.chunk_lo);
     hipLaunchKernelGGL((attend_kernel<ES, DK, DV, R, G, att_np<ES, R>(), NW, HS, RT>), grid, dim3(64 * NW), 0, s,
                        a);
 }
@@ -825,7 +844,9 @@ hipError_t launch_attend(const Geo &g, const AttnArgs &a, hipStream_t s)
 
 hipError_t launch_combine(const Geo &g, const AttnArgs &a, hipStream_t s)
 {
-    if (a.rows == 0 || a.max_chunks <= 1)
+    // after a shared-prefix pass, rows of two chunks are merged by the attend
+    // kernel itself
+    if (a.rows == 0 || a.max_chunks <= 1 || (a.chunk_lo == 1 && a.max_chunks == 2))
         return hipSuccess;
     if (g.dv > 64)
         return hipErrorNotSupported;

@@ -406,10 +406,15 @@ void prefill_kernel(PrefillArgs a)
     io.tid = tid;
     io.wave = __builtin_amdgcn_readfirstlane(wave);
     io.n_sh = n_sh;
-    io.own_len = kmax - n_sh;                       // own slots [0, own_len) are touched
+    // A shared-prefix decode pass (a.part set) attends the prefix only: its
+    // rows are decode queries of sequences attached to it, packed across
+    // them, and it leaves each row's softmax state for the sequences' own
+    // positions to continue.
+    const bool partial = a.part != nullptr;
+    io.own_len = partial ? 0 : kmax - n_sh;         // own slots [0, own_len) are touched
     io.nfs = n_sh / PF_KT;
     io.psh = n_sh % PF_KT != 0;
-    io.jfull = io.nfs + (kfull - n_sh) / PF_KT;     // + own tiles visible to every row
+    io.jfull = io.nfs + (partial ? 0 : (kfull - n_sh) / PF_KT);   // + own tiles visible to every row
     io.ntile = io.nfs + io.psh + (io.own_len + PF_KT - 1) / PF_KT;
     const int ntile = io.ntile, jfull = io.jfull;
 
@@ -662,6 +667,23 @@ void prefill_kernel(PrefillArgs a)
     lsum += __shfl_xor(lsum, 32, 64);
     if (!rvalid)
         return;
+    if (partial) {
+        // split-KV chunk 0 of the row: unnormalised sums, the running max
+        // (base 2) and the sum of weights, as the decode kernel's partials
+        float *pr = a.part + qrow * a.max_chunks * (DV + 2);
+#pragma unroll
+        for (int dt = 0; dt < 2; dt++) {
+            const float16v &acc = dt == 0 ? acc0 : acc1;
+#pragma unroll
+            for (int i = 0; i < 16; i++)
+                pr[32 * dt + 8 * (i >> 2) + 4 * jh + (i & 3)] = acc[i];
+        }
+        if (jh == 0) {
+            pr[DV] = m;
+            pr[DV + 1] = lsum;
+        }
+        return;
+    }
     const float inv = 1.0f / lsum;
     float *o = a.out + qrow * DV;
     const float *gt = a.gate ? a.gate + qrow * DV : nullptr;

@@ -366,6 +366,75 @@ def test_shared_prefix_prefill_then_decode(kv_dtype):
     ctx.prefix_free(pid)
 
 
+@pytest.mark.parametrize("kv_dtype,geom,npre,own_max", [
+    (O.KV_F16, (8, 8, 64, 64), 213, 40), (O.KV_INT8, (8, 8, 64, 64), 213, 40),
+    (O.KV_F16, (8, 4, 64, 64), 213, 40), (O.KV_F16, (8, 8, 64, 64), 40, 100)])
+def test_shared_prefix_decode_pass(kv_dtype, geom, npre, own_max):
+    """A decode batch whose sequences all share one prefix (at least 4
+    (row, kv-head) units per CU) attends the prefix in one MFMA pass over all
+    of them and their own positions on the VALU kernel, merged as split-KV
+    chunks of the prefix's length. Rows of two chunks are merged by the
+    own-positions pass; with a 40-slot prefix and up to 101 own positions
+    other rows have up to four and go through the merge kernel. Every row
+    against the oracle, gated and not; the pass is taken (two decode
+    launches per call, a merge launch only when some row has more than two
+    chunks)."""
+    nh, nkv, dk, dv = geom
+    say("shared prefix decode pass", kv_dtype, geom, npre, own_max)
+    N = nda()
+    rng = np.random.default_rng(77 + nkv + npre)
+    W, B = 384, 264
+    ctx = N.Context(1, nh, nkv, dk, dv, W, kv_dtype=kv_dtype, max_seqs=B + 1)
+    q = rng.standard_normal((npre, nh, dk)).astype(np.float32)
+    k = rng.standard_normal((npre, nkv, dk)).astype(np.float32)
+    v = rng.standard_normal((npre, nkv, dv)).astype(np.float32)
+    dout = N.DevBuf(npre * nh * dv * 4)
+    ctx.prefill(0, [npre], N.DevBuf.from_array(q), N.DevBuf.from_array(k), N.DevBuf.from_array(v), dout,
+                seq_ids=[B])
+    ctx.advance(1, [B], npre)
+    pid = ctx.prefix_build(B)
+    for b in range(B):
+        ctx.seq_attach(b, pid)
+    n = rng.integers(0, own_max + 1, B)
+    ids = [b for b in range(B) if n[b] > 0]
+    T = int(n.sum())
+    q = rng.standard_normal((T, nh, dk)).astype(np.float32)
+    k = rng.standard_normal((T, nkv, dk)).astype(np.float32)
+    v = rng.standard_normal((T, nkv, dv)).astype(np.float32)
+    dout = N.DevBuf(T * nh * dv * 4)
+    ctx.prefill(0, [int(n[b]) for b in ids], N.DevBuf.from_array(q), N.DevBuf.from_array(k),
+                N.DevBuf.from_array(v), dout, seq_ids=ids)
+    for b in ids:
+        ctx.advance(1, [b], int(n[b]))
+    worst = 0.0
+    for gated in (False, True):
+        q = rng.standard_normal((B, nh, dk)).astype(np.float32)
+        k = rng.standard_normal((B, nkv, dk)).astype(np.float32)
+        v = rng.standard_normal((B, nkv, dv)).astype(np.float32)
+        g = rng.standard_normal((B, nh, dv)).astype(np.float32) if gated else None
+        dout = N.DevBuf(B * nh * dv * 4)
+        ctx.sync()
+        ctx.prof_enable(True)
+        ctx.prof_read(reset=True)
+        ctx.step(0, B, N.DevBuf.from_array(q), N.DevBuf.from_array(k), N.DevBuf.from_array(v), dout,
+                 gate=N.DevBuf.from_array(g) if gated else None)
+        ctx.sync()
+        ms, launches = ctx.prof_read(reset=True)
+        ctx.prof_enable(False)
+        max_chunks = -(-(npre + int(n.max()) + 1) // npre)
+        assert launches[N.K_DECODE] == 2, list(launches)
+        assert launches[N.K_COMBINE] == (1 if max_chunks > 2 else 0), list(launches)
+        got = dout.to_array(np.float32, (B, nh * dv))
+        for b in range(B):
+            pos = ctx.seq_state(b)[0]
+            view, keep = _views_for(ctx, 0, b, pos, nh, kv_dtype)
+            want = O.attend_runs(view, np.arange(pos + 1), [npre, pos + 1 - npre], q[b],
+                                 g[b] if gated else None)
+            worst = max(worst, maxdiff(got[b], want))
+    ctx.close()
+    assert worst <= TOL, worst
+
+
 def test_prefill_gqa_chunks_on_shared_prefix():
     """Prefill of several chunks on one shared prefix at the engine's GQA
     shape (12 q / 2 kv heads, qk 48, int8): a 100-token prefix (not a whole
