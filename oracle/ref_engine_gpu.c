@@ -18,7 +18,12 @@
  *   - in nd_model_reset / _set_sink / _snapshot / _rewind / _prefix_save /
  *     _prefix_restore / _prefix_free and the position step of
  *     nd_model_step_hidden (m->pos++, nd_model.c:3094), the matching nd_gpu_*
- *     call (engine/include/nd_model.h:193-222).
+ *     call (engine/include/nd_model.h:193-222);
+ *   - for the whole attention() on the GPU: the front's tap count, theta and
+ *     staged weights (fp16_slot[li][4..8]) handed over once, each layer's
+ *     five CQ tensors registered from the archive's own blobs and codebook
+ *     (nd_cact_data, nd_cact_codebook), and attention(m, li, xin, out)
+ *     becoming one nd_gpu_attention_block call.
  * Each eng_* call below runs the engine's own body and the binding's call
  * side by side, so one token stream drives the CPU attention and the GPU
  * drop-in through the same nd_model.
@@ -30,6 +35,8 @@
 typedef struct {
     nd_model *m;
     nd_gpu_model *gpu;
+    uint32_t d_model;
+    nda_cq **cq;        /* [layer * 5 + tensor], registered with the session */
 } eng;
 
 typedef struct {
@@ -59,9 +66,15 @@ void *eng_open(uint32_t n_layers, uint32_t nh, uint32_t nkv, uint32_t qk_hd, uin
 void eng_close(void *ve)
 {
     eng *e = (eng *)ve;
+    uint32_t i;
     if (!e)
         return;
     nd_gpu_close(e->gpu);
+    if (e->cq)      /* the tensors outlive the session that uses them */
+        for (i = 0; i < e->m->n_layers * 5; i++)
+            if (e->cq[i])
+                nda_cq_destroy(e->cq[i]);
+    free(e->cq);
     ref_session_free(e->m);
     free(e);
 }
@@ -170,4 +183,70 @@ void eng_state(void *ve, uint32_t *pos_cpu, uint32_t *sink_cpu, uint32_t *pos_gp
     *sink_cpu = e->m->n_sink;
     *pos_gpu = nd_gpu_pos(e->gpu);
     *sink_gpu = nd_gpu_n_sink(e->gpu);
+}
+
+/* ------------------------------------------------- the whole attention() */
+
+/* The attention front on both sides: the tap histories and rotary
+ * frequencies nd_model_open sets up, and the session's nd_gpu_front_init. */
+int eng_front(void *ve, uint32_t taps, float theta)
+{
+    eng *e = (eng *)ve;
+    if (ref_session_front(e->m, taps, theta))
+        return -1;
+    return nd_gpu_front_init(e->gpu, taps, theta, 0);
+}
+
+/* The engine's nd_layer CQ tensors over one nd_cact buffer (blobs[layer * 5
+ * + t], t = q, k, v, gate, out_proj; the archive's 28-float codebook) and
+ * its staged front weights front[layer * 5 + i] (tap_q, tap_k, tap_v, norm_q,
+ * norm_k in fp16_slot[li][4..8]); then, as the binding registers them, each
+ * layer's front weights and one nda_cq per tensor made from the archive's
+ * own blob and codebook slice. */
+int eng_block_setup(void *ve, uint32_t d_model, uint32_t group, const void *const *blobs, const float *codebook,
+                    const float *const *front)
+{
+    eng *e = (eng *)ve;
+    nd_model *m = e->m;
+    uint32_t li, i;
+    if (ref_block_setup(m, d_model, group, blobs, codebook))
+        return -1;
+    e->d_model = d_model;
+    e->cq = (nda_cq **)calloc((size_t)m->n_layers * 5, sizeof(nda_cq *));
+    if (!e->cq)
+        return -1;
+    for (li = 0; li < m->n_layers; li++) {
+        const nd_layer *L = &m->layer[li];
+        const nd_tensor *src[5] = { &L->q_proj, &L->k_proj, &L->v_proj, &L->gate_proj, &L->out_proj };
+        nda_cq **t = e->cq + (size_t)li * 5;
+        int rc;
+        for (i = 0; i < 5; i++)
+            m->fp16_slot[li][4 + i] = (float *)front[li * 5 + i];
+        rc = nd_gpu_front_weights(e->gpu, li, m->fp16_slot[li][4], m->fp16_slot[li][5], m->fp16_slot[li][6],
+                                  m->fp16_slot[li][7], m->fp16_slot[li][8]);
+        if (rc)
+            return rc;
+        for (i = 0; i < 5; i++) {
+            rc = nda_cq_create(src[i]->shape[0], src[i]->shape[1], src[i]->group, src[i]->bits,
+                               nd_cact_data(&m->c, src[i]), nd_cact_codebook(&m->c, src[i]->bits), &t[i]);
+            if (rc)
+                return rc;
+        }
+        rc = nd_gpu_block_weights(e->gpu, li, t[0], t[1], t[2], t[3], t[4]);
+        if (rc)
+            return rc;
+    }
+    return 0;
+}
+
+/* attention(m, li, xin, out) at the model's position: cpu_out from the
+ * engine's own function (with the rotary table of nd_model_step_hidden),
+ * gpu_out from the binding's single call. Returns the call's status. */
+int eng_attention_block(void *ve, uint32_t li, const float *xin, float *cpu_out, float *gpu_out)
+{
+    eng *e = (eng *)ve;
+    nd_model *m = e->m;
+    ref_attention_block(m, li, m->fp16_slot[li][4], m->fp16_slot[li][5], m->fp16_slot[li][6], m->fp16_slot[li][7],
+                        m->fp16_slot[li][8], xin, cpu_out);
+    return nd_gpu_attention_block(e->gpu, li, xin, e->d_model, gpu_out);
 }

@@ -8,17 +8,22 @@ against the package's libndhost.so and libndattn.so. One token stream with
 snapshots, sinks, prefix save / restore, rewind and reset drives the
 engine's CPU attention and the GPU drop-in through the same nd_model: every
 output within 1e-3 of the engine's (fp32 accumulate), positions and sink
-counts equal after every event. Skipped where the harness was not built
-(no reference tree at build time)."""
+counts equal after every event. The whole attention() binding (front
+weights and the archive's CQ tensors registered from the engine's own
+nd_layer records, one nd_gpu_attention_block call) runs beside the engine's
+attention() function itself. Skipped where the harness was not built (no
+reference tree at build time)."""
 import ctypes as C
 import os
+import sys
 
 import numpy as np
 import pytest
 
 pytestmark = pytest.mark.gpu
 
-REPO = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HERE = os.path.dirname(os.path.abspath(__file__))
+REPO = os.path.dirname(HERE)
 SO = os.path.join(REPO, "oracle", "_ref", "libndrefgpu.so")
 TOL = 1e-3
 
@@ -49,6 +54,12 @@ def lib():
         L.eng_prefix_restore.argtypes = [vp, vp, ip, ip]
         L.eng_prefix_free.argtypes = [vp]
         L.eng_state.argtypes = [vp, up, up, up, up]
+        L.eng_front.restype = C.c_int
+        L.eng_front.argtypes = [vp, u32, C.c_float]
+        L.eng_block_setup.restype = C.c_int
+        L.eng_block_setup.argtypes = [vp, u32, u32, vp, vp, vp]
+        L.eng_attention_block.restype = C.c_int
+        L.eng_attention_block.argtypes = [vp, u32, fp, fp, fp]
         _lib = L
     return _lib
 
@@ -63,7 +74,9 @@ def state(L, e):
     return tuple(x.value for x in v)
 
 
-def run(geom, script, seed, scale=1.0):
+def run(geom, script, seed, scale=1.0, block=None):
+    """block: (d_model, taps, theta, front weights, block weights, input
+    stream) to drive the whole attention() instead of the store + dispatch."""
     L = lib()
     nl, nh, nkv, qk, vd, W = geom
     e = L.eng_open(*geom)
@@ -71,9 +84,29 @@ def run(geom, script, seed, scale=1.0):
     rng = np.random.default_rng(seed)
     saved = {}
     worst = 0.0
+    keep = []
     try:
+        if block:
+            d_model, taps, theta, fw, bw, st = block
+            assert L.eng_front(e, taps, theta) == 0
+            blobs = (C.c_void_p * (5 * nl))(*[b.ctypes.data for layer in bw.blobs for b in layer])
+            front = (C.c_void_p * (5 * nl))(*[a.ctypes.data for li in range(nl) for a in fw.arrays(li)])
+            keep += [blobs, front, fw, bw]
+            assert L.eng_block_setup(e, d_model, bw.group, blobs, bw.codebook.ctypes.data, front) == 0
         for ev in script:
-            if ev[0] == "tok":
+            if ev[0] == "tok" and block:
+                for li in range(nl):
+                    x = np.ascontiguousarray(st.take(d_model), np.float32)
+                    co = np.zeros(d_model, np.float32)
+                    go = np.zeros(d_model, np.float32)
+                    rc = L.eng_attention_block(e, li, fptr(x), fptr(co), fptr(go))
+                    assert rc == 0, rc
+                    # out_proj sums hundreds of terms: relative to the call's
+                    # largest output where that exceeds 1
+                    scale_o = max(1.0, float(np.abs(co).max()))
+                    worst = max(worst, float(np.abs(co.astype(np.float64) - go).max()) / scale_o)
+                L.eng_step_end(e)
+            elif ev[0] == "tok":
                 for li in range(nl):
                     q = (rng.standard_normal(nh * qk) * scale).astype(np.float32)
                     k = (rng.standard_normal(nkv * qk) * scale).astype(np.float32)
@@ -123,6 +156,24 @@ def test_engine_binding_gqa_ring_prefixes():
               [("restore", 0)] + [("tok", True)] * 130 + [("reset",)] + [("tok", True)] * 5)
     worst = run((2, 12, 2, 48, 64, 128), script, seed=31, scale=2.0)
     print("[gpu-case] engine binding gqa worst", worst, flush=True)
+    assert worst <= TOL, worst
+
+
+def test_engine_binding_whole_attention():
+    """The engine's attention(m, li, xin, out) itself against its one-call
+    GPU binding: 12 q / 2 kv heads, qk 48, v 64, d_model 256, 3 taps, 2-bit
+    CQ projections registered from the engine's nd_layer records, 2 layers;
+    snapshot, prefix save, rewind, reset and restore."""
+    print("[gpu-case] engine binding whole attention", flush=True)
+    sys.path.insert(0, HERE)
+    from detgen import Stream, make_block_weights
+    from test_oracle_block import BLOCK, front_weights
+    nl, nh, nkv, qk, vd, W = BLOCK["geom"]
+    fw = front_weights(BLOCK["seed"] + 1, nl, nh, nkv, qk, vd, BLOCK["taps"])
+    bw = make_block_weights(BLOCK["seed"] + 2, nl, nh, nkv, qk, vd, BLOCK["d_model"])
+    worst = run(BLOCK["geom"], BLOCK["script"], seed=33,
+                block=(BLOCK["d_model"], BLOCK["taps"], BLOCK["theta"], fw, bw, Stream(BLOCK["seed"])))
+    print("[gpu-case] engine binding whole attention worst", worst, flush=True)
     assert worst <= TOL, worst
 
 
