@@ -78,6 +78,31 @@ __global__ __launch_bounds__((64 * FrontShape<DK, DV, REP>::W)) void front_kerne
     float *hist = a.hist + ((uint64_t)seq * a.n_layers + a.layer) * taps * dcol;
     const bool store = a.k_out == nullptr;
 
+    // What steps 3 and 4 read (this thread's rotary pairs and norm scales,
+    // the page of the stored slot) is requested now, beside the tap loads,
+    // so the wave waits on one round of loads rather than three.
+    constexpr int NE = (S::NH * S::HALF + 64 * S::W - 1) / (64 * S::W);   // emit elements per thread
+    const float2 *rope = a.rope + (uint64_t)pos * S::HALF;
+    float2 cs_e[NE];
+    float s1_e[NE], s2_e[NE];
+#pragma unroll
+    for (int n = 0; n < NE; n++) {
+        const int e = tid + n * 64 * S::W;
+        const int h = e / S::HALF, i = e % S::HALF;
+        if (e < S::NH * S::HALF) {
+            const float *sn = a.norm + (h < REP ? 0 : DK);
+            cs_e[n] = rope[i];
+            s1_e[n] = sn[i];
+            s2_e[n] = sn[i + S::HALF];
+        }
+    }
+    int slot = 0;
+    int32_t page = -1;
+    if (store) {
+        slot = own_slot(sd, (int)pos, (int)a.pg.window);
+        page = a.page_table[(uint64_t)seq * a.pg.pages_per_seq + (slot >> a.pg.log2_page)];
+    }
+
     // 1. tap convolution of this thread's four columns
     const bool active = tid < S::NG;
     const int lc = tid * 4;                      // column within the group
@@ -144,16 +169,18 @@ __global__ __launch_bounds__((64 * FrontShape<DK, DV, REP>::W)) void front_kerne
     __syncthreads();
 
     // 3. (1 + s) * x * inv, rotated by the position's (cos, sin)
-    const float2 *rope = a.rope + (uint64_t)pos * S::HALF;
-    for (int e = tid; e < S::NH * S::HALF; e += 64 * S::W) {
+#pragma unroll
+    for (int n = 0; n < NE; n++) {
+        const int e = tid + n * 64 * S::W;
+        if (e >= S::NH * S::HALF)
+            break;
         const int h = e / S::HALF, i = e % S::HALF;
         const bool is_q = h < REP;
-        const float *s = a.norm + (is_q ? 0 : DK);
         float *r = ylds + h * S::STRIDE;
         const float iv = invlds[h];
-        const float x1 = (1.0f + s[i]) * r[i] * iv;
-        const float x2 = (1.0f + s[i + S::HALF]) * r[i + S::HALF] * iv;
-        const float2 cs = rope[i];
+        const float x1 = (1.0f + s1_e[n]) * r[i] * iv;
+        const float x2 = (1.0f + s2_e[n]) * r[i + S::HALF] * iv;
+        const float2 cs = cs_e[n];
         const float o1 = x1 * cs.x - x2 * cs.y;
         const float o2 = x2 * cs.x + x1 * cs.y;
         if (is_q) {
@@ -176,9 +203,7 @@ __global__ __launch_bounds__((64 * FrontShape<DK, DV, REP>::W)) void front_kerne
     // 4. store this position's k/v rows of kv-head g (wave 0, lane = element)
     if (tid >= 64)
         return;
-    const int slot = own_slot(sd, (int)pos, (int)a.pg.window);
     const int P = 1 << a.pg.log2_page;
-    const int32_t page = a.page_table[(uint64_t)seq * a.pg.pages_per_seq + (slot >> a.pg.log2_page)];
     if (page < 0)
         return;   // the host backs every stored slot; never taken
     uint8_t *hb = a.pool + (uint64_t)page * a.pg.page_bytes + (uint64_t)g * a.pg.head_bytes;
