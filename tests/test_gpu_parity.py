@@ -366,24 +366,26 @@ def test_shared_prefix_prefill_then_decode(kv_dtype):
     ctx.prefix_free(pid)
 
 
-@pytest.mark.parametrize("kv_dtype,geom,npre,own_max", [
-    (O.KV_F16, (8, 8, 64, 64), 213, 40), (O.KV_INT8, (8, 8, 64, 64), 213, 40),
-    (O.KV_F16, (8, 4, 64, 64), 213, 40), (O.KV_F16, (8, 8, 64, 64), 40, 100)])
-def test_shared_prefix_decode_pass(kv_dtype, geom, npre, own_max):
+@pytest.mark.parametrize("kv_dtype,geom,npre,own_max,W,extra", [
+    (O.KV_F16, (8, 8, 64, 64), 213, 40, 384, 0), (O.KV_INT8, (8, 8, 64, 64), 213, 40, 384, 0),
+    (O.KV_F16, (8, 4, 64, 64), 213, 40, 384, 0), (O.KV_F16, (8, 8, 64, 64), 40, 100, 384, 0),
+    (O.KV_INT8, (8, 8, 64, 64), 213, 64, 277, 30)])
+def test_shared_prefix_decode_pass(kv_dtype, geom, npre, own_max, W, extra):
     """A decode batch whose sequences all share one prefix (at least 4
     (row, kv-head) units per CU) attends the prefix in one MFMA pass over all
     of them and their own positions on the VALU kernel, merged as split-KV
     chunks of the prefix's length. Rows of two chunks are merged by the
     own-positions pass; with a 40-slot prefix and up to 101 own positions
-    other rows have up to four and go through the merge kernel. Every row
-    against the oracle, gated and not; the pass is taken (two decode
-    launches per call, a merge launch only when some row has more than two
-    chunks)."""
+    other rows have up to four and go through the merge kernel. With a
+    277-slot window (213 sinks, the 64-slot minimum ring) and 30 more decode
+    steps first, the own ring wraps. Every row against the
+    oracle, gated and not; the pass is taken (two decode launches per call,
+    a merge launch only when some row has more than two chunks)."""
     nh, nkv, dk, dv = geom
-    say("shared prefix decode pass", kv_dtype, geom, npre, own_max)
+    say("shared prefix decode pass", kv_dtype, geom, npre, own_max, W)
     N = nda()
-    rng = np.random.default_rng(77 + nkv + npre)
-    W, B = 384, 264
+    rng = np.random.default_rng(77 + nkv + npre + W)
+    B = 264
     ctx = N.Context(1, nh, nkv, dk, dv, W, kv_dtype=kv_dtype, max_seqs=B + 1)
     q = rng.standard_normal((npre, nh, dk)).astype(np.float32)
     k = rng.standard_normal((npre, nkv, dk)).astype(np.float32)
@@ -406,6 +408,11 @@ def test_shared_prefix_decode_pass(kv_dtype, geom, npre, own_max):
                 N.DevBuf.from_array(v), dout, seq_ids=ids)
     for b in ids:
         ctx.advance(1, [b], int(n[b]))
+    for _ in range(extra):
+        x = [N.DevBuf.from_array(rng.standard_normal((B, d, e)).astype(np.float32))
+             for d, e in ((nh, dk), (nkv, dk), (nkv, dv))]
+        ctx.step(0, B, *x, N.DevBuf(B * nh * dv * 4))
+        ctx.advance(B, None, 1)
     worst = 0.0
     for gated in (False, True):
         q = rng.standard_normal((B, nh, dk)).astype(np.float32)
@@ -421,16 +428,23 @@ def test_shared_prefix_decode_pass(kv_dtype, geom, npre, own_max):
         ctx.sync()
         ms, launches = ctx.prof_read(reset=True)
         ctx.prof_enable(False)
-        max_chunks = -(-(npre + int(n.max()) + 1) // npre)
+        tot = max(npre + min(ctx.seq_state(b)[0] + 1 - npre, W - npre) for b in range(B))
+        max_chunks = -(-tot // npre)
         assert launches[N.K_DECODE] == 2, list(launches)
         assert launches[N.K_COMBINE] == (1 if max_chunks > 2 else 0), list(launches)
         got = dout.to_array(np.float32, (B, nh * dv))
         for b in range(B):
             pos = ctx.seq_state(b)[0]
-            view, keep = _views_for(ctx, 0, b, pos, nh, kv_dtype)
-            want = O.attend_runs(view, np.arange(pos + 1), [npre, pos + 1 - npre], q[b],
-                                 g[b] if gated else None)
+            nown = min(pos + 1 - npre, W - npre)          # the ring's newest positions
+            # the visible rows: the prefix, then the ring's positions
+            parts = [ctx.kv_read(0, b, 0, npre), ctx.kv_read(0, b, pos + 1 - nown, nown)]
+            k_, v_, ks_, vs_ = (np.concatenate([x[i] for x in parts]) for i in range(4))
+            if kv_dtype == O.KV_F16:
+                ks_ = vs_ = None
+            view = O.kv_view(k_, v_, ks_, vs_, nh, npre + nown, 0, npre + nown - 1, kv_dtype)
+            want = O.attend_runs(view, np.arange(npre + nown), [npre, nown], q[b], g[b] if gated else None)
             worst = max(worst, maxdiff(got[b], want))
+        ctx.advance(B, None, 1)
     ctx.close()
     assert worst <= TOL, worst
 
