@@ -532,6 +532,46 @@ __global__ __launch_bounds__(256) void append_kernel(AppendArgs a)
     store_row<ES>(hb, off, P, kx, vx, lane, DK, DV);
 }
 
+// fp16 store with head dims that are multiples of 4: 16 lanes per (row,
+// kv-head), four elements each (16-byte loads, 8-byte stores), four units
+// per wave. Each unit is a short chain of dependent loads (sequence state,
+// page id) before its store. A decode step's 4096 x 8 units run here as one
+// wave per four units, one round on the chip, where one wave per unit took
+// four rounds (13 us a launch). The row's K/V are loaded first: they do not
+// depend on the page. The rounding is append_kernel's.
+__global__ __launch_bounds__(256) void append_f16_kernel(AppendArgs a)
+{
+    const int DK = (int)a.pg.dk, DV = (int)a.pg.dv;
+    const int e = 4 * (int)(threadIdx.x & 15);
+    const uint64_t unit = (uint64_t)blockIdx.x * 16 + (threadIdx.x >> 4);
+    const uint32_t nkv = a.pg.nkv;
+    if (unit >= (uint64_t)a.rows * nkv)
+        return;
+    const uint32_t row = (uint32_t)(unit / nkv), g = (uint32_t)(unit % nkv);
+    float4 kx = {0.0f, 0.0f, 0.0f, 0.0f}, vx = kx;
+    if (e < DK)
+        kx = *reinterpret_cast<const float4 *>(a.k + ((uint64_t)row * nkv + g) * DK + e);
+    if (e < DV)
+        vx = *reinterpret_cast<const float4 *>(a.v + ((uint64_t)row * nkv + g) * DV + e);
+    const uint32_t seq = a.row_seq ? a.row_seq[row] : row;
+    const SeqDev sd = a.seqs[seq];
+    const int p = sd.pos + (a.row_t ? (int)a.row_t[row] : 0);
+    const int slot = own_slot(sd, p, (int)a.pg.window);
+    const int P = 1 << a.pg.log2_page;
+    const int32_t page = a.page_table[(uint64_t)seq * a.pg.pages_per_seq + (slot >> a.pg.log2_page)];
+    if (page < 0)
+        return;   // the host backs every appended slot; never taken
+    uint8_t *hb = a.pool + (uint64_t)page * a.pg.page_bytes + (uint64_t)g * a.pg.head_bytes;
+    const int off = slot & (P - 1);
+    typedef _Float16 half4v __attribute__((ext_vector_type(4)));
+    if (e < DK)
+        *reinterpret_cast<half4v *>(hb + ((uint64_t)off * DK + e) * 2) =
+            half4v{(_Float16)kx.x, (_Float16)kx.y, (_Float16)kx.z, (_Float16)kx.w};
+    if (e < DV)
+        *reinterpret_cast<half4v *>(hb + (uint64_t)P * DK * 2 + ((uint64_t)off * DV + e) * 2) =
+            half4v{(_Float16)vx.x, (_Float16)vx.y, (_Float16)vx.z, (_Float16)vx.w};
+}
+
 // ------------------------------------------------------ copies and staging
 
 // Bytes of one slot of one kv-head: K row, V row (+ the two scales).
@@ -868,8 +908,13 @@ hipError_t launch_append(const Geo &g, const AppendArgs &a, hipStream_t s)
         return hipSuccess;
     if (!geometry_supported(g))
         return hipErrorNotSupported;
-    const unsigned nb = blocks_for((uint64_t)a.rows * a.pg.nkv);
-    if (g.kv_f16)
+    const uint64_t units = (uint64_t)a.rows * a.pg.nkv;
+    const unsigned nb = blocks_for(units);
+    const bool vec = g.dk % 4 == 0 && g.dv % 4 == 0 && (reinterpret_cast<uintptr_t>(a.k) & 15) == 0 &&
+                     (reinterpret_cast<uintptr_t>(a.v) & 15) == 0;
+    if (g.kv_f16 && vec)
+        hipLaunchKernelGGL(append_f16_kernel, dim3((unsigned)((units + 15) / 16)), dim3(256), 0, s, a);
+    else if (g.kv_f16)
         hipLaunchKernelGGL((append_kernel<2>), dim3(nb), dim3(256), 0, s, a);
     else
         hipLaunchKernelGGL((append_kernel<1>), dim3(nb), dim3(256), 0, s, a);

@@ -539,6 +539,45 @@ def test_int8_store_edge_rows():
             assert np.float32(s).view(np.uint32) == np.float32(scl).view(np.uint32), b
 
 
+@pytest.mark.parametrize("geom,unaligned", [((8, 64, 64), False), ((2, 48, 64), False), ((3, 20, 36), False),
+                                             ((8, 64, 64), True)])
+def test_f16_store_rows(geom, unaligned):
+    """fp16 K/V stores (nda_kv_append): every stored element is the fp32
+    input rounded to nearest-even fp16, bit for bit, including values that
+    round to the fp16 maximum, overflow to infinity, or go subnormal.
+    Head dims that are multiples of 4 with 16-byte aligned inputs take the
+    vector kernel, the rest (qk 20 / v 36 are multiples of 4; a k pointer
+    4 bytes off alignment) the per-element one; rows in several pages, out
+    of order."""
+    nkv, dk, dv = geom
+    say("f16 store rows", geom, unaligned)
+    N = nda()
+    rng = np.random.default_rng(17 + dk)
+    n, W, steps = 300, 64, 3
+    ctx = N.Context(1, nkv, nkv, dk, dv, W, kv_dtype=O.KV_F16, max_seqs=n)
+    special = np.array([65504.0, 65519.9, 65520.0, -7e4, 6.1e-5, 6.0e-8, 2.9e-8, -3.0e-8, 0.0, -0.0,
+                        1.0 + 2.0 ** -11, 1.0 + 3 * 2.0 ** -11], np.float32)
+    ids = rng.permutation(n)[: n // 2].astype(np.uint32)
+    for step in range(steps):
+        kin = (rng.standard_normal((len(ids), nkv, dk)) * 10 ** rng.uniform(-6, 4, (len(ids), nkv, 1)))
+        vin = (rng.standard_normal((len(ids), nkv, dv)) * 10 ** rng.uniform(-6, 4, (len(ids), nkv, 1)))
+        kin, vin = kin.astype(np.float32), vin.astype(np.float32)
+        kin.reshape(-1)[: len(special)] = special
+        vin.reshape(-1)[-len(special):] = special
+        kb = N.DevBuf.from_array(np.concatenate([np.zeros(1, np.float32), kin.reshape(-1)])) if unaligned \
+            else N.DevBuf.from_array(kin)
+        kptr = kb.value + 4 if unaligned else kb
+        ctx.kv_append(0, len(ids), kptr, N.DevBuf.from_array(vin), seq_ids=list(ids))
+        for b in ids:
+            ctx.advance(1, [int(b)], 1)
+        ctx.sync()
+        for j, b in enumerate(ids):
+            k, v, _, _ = ctx.kv_read(0, int(b), step, 1)
+            assert np.array_equal(k[0].view(np.uint16), kin[j].astype(np.float16).view(np.uint16)), (step, b)
+            assert np.array_equal(v[0].view(np.uint16), vin[j].astype(np.float16).view(np.uint16)), (step, b)
+    ctx.close()
+
+
 # ------------------------------------------------------------ error handling
 
 def test_error_paths():
