@@ -1174,9 +1174,10 @@ static int decode_check(nda_ctx *c, uint32_t layer, uint32_t nseq, const uint32_
 // of them: per kv-head, the prefix's key tiles against every sequence's
 // query rows on the prefill kernel's MFMA tiles, each row's softmax state
 // left as its split-KV chunk 0 (chunks of n_sh positions). The VALU kernel
-// continues with each sequence's own positions (chunks 1 on) and the merge
-// combines the chunks; otherwise the VALU kernel redoes the prefix's dot
-// products for every sequence. Taken for batches of at least 4 (row,
+// continues with each sequence's own positions (chunks 1 on); a row of two
+// chunks it merges with chunk 0 itself, longer rows go through the merge
+// kernel. Without the pass the VALU kernel redoes the prefix's dot products
+// for every sequence. Taken for batches of at least 4 (row,
 // kv-head) units per CU of a shape the prefill kernel is built for and the
 // MFMA GQA decode does not serve, with a prefix of at least one full key
 // tile, and not when the append is fused into the launch.
