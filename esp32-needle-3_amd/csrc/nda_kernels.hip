@@ -303,15 +303,19 @@ __global__ __launch_bounds__(64 * NW) void attend_kernel(AttnArgs a)
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int grp = lane / G, li = lane % G;
     const uint32_t nkv = a.pg.nkv;
-    // Work-group w runs on XCD w % 8. Each XCD is given one contiguous run
-    // of units, so the work-groups running on an XCD at one time read
-    // neighbouring rows (and their pages, allocated in row order) rather
-    // than every eighth: the 4096-row decode takes 0.748 ms per launch
-    // instead of 0.766. (A bijection on [0, gridDim.x): XCD x takes the
-    // gridDim.x / 8 units from x * (gridDim.x / 8) + min(x, gridDim.x % 8),
-    // plus one when x < gridDim.x % 8.)
+    // Work-group w runs on XCD w % 8. With 8-wave work-groups (long rows)
+    // each XCD is given one contiguous run of units, so the work-groups
+    // running on an XCD at one time read neighbouring rows (and their pages,
+    // allocated in row order) rather than every eighth: the 4096-row decode
+    // takes 0.748 ms per launch instead of 0.766. Short rows on 2-wave
+    // work-groups keep the plain order: for them (the own positions of
+    // sequences on a shared prefix) the runs measured no better, 0.0536 and
+    // 0.0554 ms per layer step against 0.0521 and 0.0534. (The run is a
+    // bijection on [0, gridDim.x): XCD x takes the gridDim.x / 8 units from
+    // x * (gridDim.x / 8) + min(x, gridDim.x % 8), plus one when x <
+    // gridDim.x % 8.)
     const uint32_t nwg = gridDim.x, xcd = blockIdx.x % 8u;
-    const uint32_t unit = (nwg / 8u) * xcd + min(xcd, nwg % 8u) + blockIdx.x / 8u;
+    const uint32_t unit = NW >= 8 ? (nwg / 8u) * xcd + min(xcd, nwg % 8u) + blockIdx.x / 8u : blockIdx.x;
     const uint32_t row = unit / (nkv * HS), gv = unit % (nkv * HS), g = gv / HS;   // heads gv*REP..+REP
     const uint32_t chunk = blockIdx.y + a.chunk_lo;
 
