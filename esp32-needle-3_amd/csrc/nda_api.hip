@@ -120,6 +120,13 @@ struct nda_ctx {
     size_t stage_cap = 0;
     uint32_t *d_pf = nullptr;           // prefill work list staging
     size_t pf_cap = 0;                  // uint32 entries
+    // GQA decode work order (longest rows first) for batches of sequences
+    // 0..rows-1, valid while no sequence state has changed since it was built
+    uint32_t *d_order = nullptr;
+    size_t order_cap = 0;               // uint32 entries
+    uint32_t order_rows = 0;
+    uint64_t order_ver = 0;
+    uint64_t state_ver = 1;             // bumped by every change of a sequence's position, sinks or prefix
     uint64_t dev_bytes = 0;
     uint8_t *scratch = nullptr;         // this device's nda_decode_noalloc scratch
 
@@ -599,7 +606,47 @@ int reserve_attend(nda_ctx *c, uint32_t rows, bool staged, uint32_t max_total, u
     return NDA_OK;
 }
 
-int run_attend(nda_ctx *c, AttnArgs &a, hipStream_t st, float *part = nullptr, bool prof = true)
+// The GQA decode's work order for the batch of sequences 0..rows-1: rows by
+// key tiles visited, most first (a counting sort). Its waves then finish
+// together: in row order the ragged tail of the last waves cost 3% of the
+// launch. Built once per change of sequence state (the 8 layers of a step
+// share it) and uploaded on the caller's stream; any permutation of the rows
+// gives the same results, so a stale order only costs time. A failed
+// allocation just leaves the rows in order.
+static const uint32_t *decode_order(nda_ctx *c, uint32_t rows, hipStream_t st)
+{
+    if (c->d_order && c->order_rows == rows && c->order_ver == c->state_ver)
+        return c->d_order;
+    std::vector<uint32_t> tiles(rows), first;
+    uint32_t top = 0;
+    for (uint32_t b = 0; b < rows; b++) {
+        const SeqHost &s = c->seqs[b];
+        const Vis v = visible(s, s.pos, c->cfg.window);
+        tiles[b] = (v.n_sh + 31) / 32 + (v.n_own + 31) / 32;
+        top = std::max(top, tiles[b]);
+    }
+    first.assign(top + 2, 0u);
+    for (uint32_t b = 0; b < rows; b++)         // counts, then starts, by descending tiles
+        first[top - tiles[b] + 1]++;
+    for (uint32_t k = 1; k <= top + 1; k++)
+        first[k] += first[k - 1];
+    std::vector<uint32_t> ord(rows);
+    for (uint32_t b = 0; b < rows; b++)
+        ord[first[top - tiles[b]]++] = b;
+    if (grow_buf(c, c->d_order, c->order_cap, rows, std::max<size_t>(rows, 4096)) ||
+        upload(c, c->d_order, ord.data(), (size_t)rows * 4, st)) {
+        c->order_rows = 0;
+        return nullptr;
+    }
+    c->order_rows = rows;
+    c->order_ver = c->state_ver;
+    return c->d_order;
+}
+
+// ordered: the GQA decode may take the rows longest first (it then builds
+// or reuses the context's order buffer; nda_decode_noalloc does not)
+int run_attend(nda_ctx *c, AttnArgs &a, hipStream_t st, float *part = nullptr, bool prof = true,
+               bool ordered = true)
 {
     if (mfma_decode(c, a)) {
         PrefillArgs pa{};
@@ -615,6 +662,9 @@ int run_attend(nda_ctx *c, AttnArgs &a, hipStream_t st, float *part = nullptr, b
         pa.n_items = a.rows * c->cfg.n_kv_heads;
         pa.nh = a.nh;
         pa.qscale = a.qscale;
+        // enough rows for several rounds of waves, rows 0..rows-1
+        if (ordered && !a.row_seq && pa.n_items >= 4u * (uint32_t)c->cus)
+            pa.items = decode_order(c, a.rows, st);
         ProfScope ps(c, NDA_K_DECODE, st, prof);
         hipError_t e = launch_decode_mfma(c->geo, pa, st);
         if (e != hipSuccess)
@@ -800,7 +850,7 @@ void nda_destroy(nda_ctx *c)
     void *bufs[] = {c->pool, c->d_pages, c->d_prefix_pages, c->d_seqs, c->d_rows, c->d_part,
                     c->d_stage, c->d_pf, c->d_hist, c->d_snap_hist, c->d_prefix_hist,
                     c->d_front_w, c->d_front_norm, c->d_rope, c->d_qfront, c->d_front_rows,
-                    c->d_hist_ops, c->d_bscr};
+                    c->d_hist_ops, c->d_bscr, c->d_order};
     for (void *b : bufs)
         dev_free(b);
     delete c;
@@ -821,6 +871,7 @@ int nda_seq_reset(nda_ctx *c, uint32_t seq)
         c->prefixes[s.prefix].refs--;
     release_pages(c, seq);
     s = SeqHost();
+    c->state_ver++;
     c->seqs_dirty = true;
     if (c->taps)
         hist_queue(c, hist_live(c, seq), nullptr);    // nd_model_reset, nd_model.c:1575-1580
@@ -837,6 +888,7 @@ int nda_seq_set_sink(nda_ctx *c, uint32_t seq, uint32_t n)
     if (s.prefix >= 0)
         return fail(c, NDA_ERR_STATE, "sequence %u reads its sinks from prefix %d", seq, s.prefix);
     s.n_sink = clamp_sink(c->cfg.window, n);
+    c->state_ver++;
     c->seqs_dirty = true;
     return NDA_OK;
 }
@@ -865,6 +917,7 @@ int nda_seq_set_pos(nda_ctx *c, uint32_t seq, uint32_t pos)
     if (s.prefix >= 0 && pos < s.n_sink)
         return fail(c, NDA_ERR_RANGE, "pos %u inside the shared prefix (%u)", pos, s.n_sink);
     s.pos = pos;
+    c->state_ver++;
     c->seqs_dirty = true;
     return NDA_OK;
 }
@@ -900,6 +953,7 @@ int nda_advance(nda_ctx *c, uint32_t nseq, const uint32_t *ids, uint32_t n, void
             return rc;
     for (uint32_t b = 0; b < nseq; b++)
         c->seqs[sid(ids, b)].pos += n;
+    c->state_ver++;
     if (c->seqs_dirty)      // a full upload is pending anyway
         return NDA_OK;
     // Same increment on the device copy, in stream order, so steady-state
@@ -978,6 +1032,7 @@ int nda_prefix_build(nda_ctx *c, uint32_t seq, int32_t *prefix_id, void *stream)
     // nd_model_snapshot: the builder pins its own positions as sinks.
     if (s.prefix < 0)
         s.n_sink = pf.n_sink;
+    c->state_ver++;
     s.has_snap = true;
     s.snap_pos = len;
     c->seqs_dirty = true;
@@ -1018,6 +1073,7 @@ int nda_seq_attach(nda_ctx *c, uint32_t seq, int32_t id, void *stream)
         c->prefixes[s.prefix].refs--;
     release_pages(c, seq);
     s = SeqHost();
+    c->state_ver++;
     s.prefix = id;
     s.n_sink = pf.n_sink;
     s.pos = pf.len;
@@ -1073,6 +1129,7 @@ int nda_seq_rewind(nda_ctx *c, uint32_t seq)
     s.ring_lo = std::min(s.ring_lo, s.snap_pos);
     s.stored_end = std::min(s.stored_end, s.snap_pos);
     s.pos = s.snap_pos;
+    c->state_ver++;
     c->seqs_dirty = true;
     if (c->taps)
         hist_queue(c, hist_live(c, seq), hist_snap(c, seq));   // nd_model.c:1451-1453
@@ -1381,7 +1438,7 @@ int nda_decode_noalloc(nda_ctx *c, uint32_t layer, uint32_t nseq, const uint32_t
             return rc;
         a.row_seq = reinterpret_cast<const uint32_t *>(c->scratch);
     }
-    return run_attend(c, a, st, split ? reinterpret_cast<float *>(c->scratch + part_off) : nullptr, false);
+    return run_attend(c, a, st, split ? reinterpret_cast<float *>(c->scratch + part_off) : nullptr, false, false);
 }
 
 // Store, then attend. Small batches (launch latency dominates, e.g. one

@@ -71,7 +71,8 @@ struct PrefillArgs {
     const SeqDev *seqs;
     const uint32_t *items;   /* prefill: [n_items][8] sequence (~0: empty), kv-head, row tile,
                                 first packed token, tokens, position, shared-prefix slots,
-                                prefix id (-1: none) */
+                                prefix id (-1: none); GQA decode: [rows] the rows' work order,
+                                or null */
     const uint32_t *row_seq; /* decode launches (one wave per item): sequence of each row, or null */
     float *part;             /* shared-prefix decode pass: split-KV partials of chunk 0, or null */
     uint32_t max_chunks;     /*   their stride (AttnArgs::max_chunks) */

@@ -792,7 +792,10 @@ void decode_mfma_kernel(PrefillArgs a)
     const int lane = threadIdx.x;
     const int g = lane >> 4, r = lane & 15;     // MFMA: lane group, row / column
     const uint32_t nkv = a.pg.nkv;
-    const uint32_t b = blockIdx.x / nkv, kvh = blockIdx.x % nkv;
+    // a.items: the rows' work order (longest first), or null: in order
+    const uint32_t b = a.items ? *(const __attribute__((address_space(4))) uint32_t *)(a.items + blockIdx.x / nkv)
+                               : blockIdx.x / nkv;
+    const uint32_t kvh = blockIdx.x % nkv;
     // row ids, sequence state and page tables are read-only during the
     // launch and uniform per wave: read through the constant address space
     // (scalar loads)

@@ -195,3 +195,65 @@ def test_decode_mfma_page_sizes(nh, nkv, qk, page_size):
     specs = [(213, 0), (229, 0), (245, 0), (600, 0)]
     mf, va, between = _run(nh, nkv, qk, 384, specs + specs, seed=page_size + 3, prefix=213, page_size=page_size)
     assert mf <= TOL and va <= TOL and between <= KERNELS_TOL, (mf, va, between)
+
+
+def test_decode_mfma_ordered_batch():
+    """A batch large enough for the longest-first work order of the GQA
+    decode: 2048 sequences x 2 kv-heads at the engine's shape (12 q heads,
+    qk 48, int8), lengths 1-700 over a 384-slot window (short rows and
+    wrapped rings), a synthetic cache. Three decode steps through nda_step
+    (new rows stored, positions advanced between steps, so the order is
+    rebuilt), two layers each (the order reused), and before the last
+    advance a listed subset through nda_decode (rows in call order, no work
+    order). Every output against the VALU kernel on a context fed the same
+    (1e-4), and sampled rows against the oracle over the cache as stored
+    (1e-3)."""
+    say("decode mfma ordered batch")
+    N = nda()
+    nh, nkv, qk, vd, W, B, L, steps = 12, 2, 48, 64, 384, 2048, 2, 3
+    rng = np.random.default_rng(91)
+    lens = rng.integers(0, 700, B)
+    calls = [[tuple(rng.standard_normal((B, h, d)).astype(np.float32)
+                    for h, d in ((nh, qk), (nkv, qk), (nkv, vd), (nh, vd))) for li in range(L)]
+             for step in range(steps)]
+    sub = sorted(rng.choice(B, 300, replace=False).tolist(), key=lambda x: -lens[x])
+    q_sub = rng.standard_normal((len(sub), nh, qk)).astype(np.float32)
+    sample = [int(b) for b in rng.choice(B, 12, replace=False)]
+    outs = {}
+    worst = 0.0
+    for flags in (0, N.FLAG_DECODE_VALU):
+        ctx = N.Context(L, nh, nkv, qk, vd, W, kv_dtype=N.KV_INT8, max_seqs=B, flags=flags)
+        for b in range(B):
+            ctx.seq_set_pos(b, int(lens[b]))
+            ctx.seq_reserve(b, W)
+        ctx.kv_fill_normal(B, seed=92)
+        res = []
+        for step in range(steps):
+            for li in range(L):
+                q, k, v, g = calls[step][li]
+                dout = N.DevBuf(B * nh * vd * 4)
+                ctx.step(li, B, N.DevBuf.from_array(q), N.DevBuf.from_array(k), N.DevBuf.from_array(v), dout,
+                         gate=N.DevBuf.from_array(g))
+                ctx.sync()
+                got = dout.to_array(np.float32, (B, nh * vd))
+                res.append(got)
+                if flags == 0:
+                    for b in sample:
+                        pos = ctx.seq_state(b)[0]
+                        n = min(pos + 1, W)
+                        kk, vv, ks, vs = ctx.kv_read(li, b, pos + 1 - n, n)
+                        view = O.kv_view(kk, vv, ks, vs, nh, n, 0, n - 1, O.KV_INT8)
+                        want = O.attend_runs(view, np.arange(n), [n], q[b], g[b])
+                        worst = max(worst, float(np.abs(got[b].astype(np.float64) - want).max()))
+            if step == steps - 1:
+                dout = N.DevBuf(len(sub) * nh * vd * 4)
+                ctx.decode(0, len(sub), N.DevBuf.from_array(q_sub), dout, seq_ids=sub)
+                ctx.sync()
+                res.append(dout.to_array(np.float32, (len(sub), nh * vd)))
+            ctx.advance(B, None, 1)
+        outs[flags] = res
+        ctx.close()
+    between = max(float(np.abs(a.astype(np.float64) - b).max()) for a, b in zip(outs[0], outs[N.FLAG_DECODE_VALU]))
+    say("ordered batch worst vs oracle", worst, "mfma vs valu", between)
+    assert worst <= TOL, worst
+    assert between <= KERNELS_TOL, between
