@@ -576,6 +576,61 @@ __global__ __launch_bounds__(256) void append_f16_kernel(AppendArgs a)
             half4v{(_Float16)vx.x, (_Float16)vx.y, (_Float16)vx.z, (_Float16)vx.w};
 }
 
+// The int8 store in the same shape (16 lanes per unit, four elements each):
+// the row's absmax over the 16 lanes by shuffles, then the engine's step
+// sequence per element (quant_code), four codes stored as one word, the
+// scales by the unit's first lane. Codes and scales are append_kernel<1>'s
+// bit for bit: the max is exact in any order.
+__global__ __launch_bounds__(256) void append_i8_kernel(AppendArgs a)
+{
+    const int DK = (int)a.pg.dk, DV = (int)a.pg.dv;
+    const int e = 4 * (int)(threadIdx.x & 15);
+    const uint64_t unit = (uint64_t)blockIdx.x * 16 + (threadIdx.x >> 4);
+    const uint32_t nkv = a.pg.nkv;
+    if (unit >= (uint64_t)a.rows * nkv)
+        return;       // (the 16 lanes of a unit leave together)
+    const uint32_t row = (uint32_t)(unit / nkv), g = (uint32_t)(unit % nkv);
+    float4 kx = {0.0f, 0.0f, 0.0f, 0.0f}, vx = kx;
+    if (e < DK)
+        kx = *reinterpret_cast<const float4 *>(a.k + ((uint64_t)row * nkv + g) * DK + e);
+    if (e < DV)
+        vx = *reinterpret_cast<const float4 *>(a.v + ((uint64_t)row * nkv + g) * DV + e);
+    const uint32_t seq = a.row_seq ? a.row_seq[row] : row;
+    const SeqDev sd = a.seqs[seq];
+    const int p = sd.pos + (a.row_t ? (int)a.row_t[row] : 0);
+    const int slot = own_slot(sd, p, (int)a.pg.window);
+    const int P = 1 << a.pg.log2_page;
+    const int32_t page = a.page_table[(uint64_t)seq * a.pg.pages_per_seq + (slot >> a.pg.log2_page)];
+    float ak = fmaxf(fmaxf(fabsf(kx.x), fabsf(kx.y)), fmaxf(fabsf(kx.z), fabsf(kx.w)));
+    float av = fmaxf(fmaxf(fabsf(vx.x), fabsf(vx.y)), fmaxf(fabsf(vx.z), fabsf(vx.w)));
+#pragma unroll
+    for (int o = 8; o > 0; o >>= 1) {
+        ak = fmaxf(ak, __shfl_xor(ak, o, 16));
+        av = fmaxf(av, __shfl_xor(av, o, 16));
+    }
+    if (page < 0)
+        return;   // the host backs every appended slot; never taken
+    uint8_t *hb = a.pool + (uint64_t)page * a.pg.page_bytes + (uint64_t)g * a.pg.head_bytes;
+    const int off = slot & (P - 1);
+    const float sk = ak > 0.0f ? __fdiv_rn(ak, 127.0f) : 1.0f;
+    const float sv = av > 0.0f ? __fdiv_rn(av, 127.0f) : 1.0f;
+    const float rk = __fdiv_rn(1.0f, sk), rv = __fdiv_rn(1.0f, sv);
+    auto pack = [](float x0, float x1, float x2, float x3, float s_, float r_) {
+        return (uint32_t)(uint8_t)quant_code(x0, s_, r_) | (uint32_t)(uint8_t)quant_code(x1, s_, r_) << 8 |
+               (uint32_t)(uint8_t)quant_code(x2, s_, r_) << 16 | (uint32_t)(uint8_t)quant_code(x3, s_, r_) << 24;
+    };
+    if (e < DK)
+        *reinterpret_cast<uint32_t *>(hb + (uint64_t)off * DK + e) = pack(kx.x, kx.y, kx.z, kx.w, sk, rk);
+    if (e < DV)
+        *reinterpret_cast<uint32_t *>(hb + (uint64_t)P * DK + (uint64_t)off * DV + e) =
+            pack(vx.x, vx.y, vx.z, vx.w, sv, rv);
+    if (e == 0) {
+        float *sc = reinterpret_cast<float *>(hb + (uint64_t)P * (DK + DV));
+        sc[off] = sk;
+        sc[P + off] = sv;
+    }
+}
+
 // ------------------------------------------------------ copies and staging
 
 // Bytes of one slot of one kv-head: K row, V row (+ the two scales).
@@ -916,8 +971,9 @@ hipError_t launch_append(const Geo &g, const AppendArgs &a, hipStream_t s)
     const unsigned nb = blocks_for(units);
     const bool vec = g.dk % 4 == 0 && g.dv % 4 == 0 && (reinterpret_cast<uintptr_t>(a.k) & 15) == 0 &&
                      (reinterpret_cast<uintptr_t>(a.v) & 15) == 0;
-    if (g.kv_f16 && vec)
-        hipLaunchKernelGGL(append_f16_kernel, dim3((unsigned)((units + 15) / 16)), dim3(256), 0, s, a);
+    if (vec)
+        hipLaunchKernelGGL((g.kv_f16 ? append_f16_kernel : append_i8_kernel), dim3((unsigned)((units + 15) / 16)),
+                           dim3(256), 0, s, a);
     else if (g.kv_f16)
         hipLaunchKernelGGL((append_kernel<2>), dim3(nb), dim3(256), 0, s, a);
     else
