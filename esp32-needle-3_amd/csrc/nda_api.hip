@@ -1493,6 +1493,35 @@ struct PrefillPlan {
     size_t n_items = 0;
 };
 
+// Work order of the MFMA prefill items. The kernel gives work-group w the
+// item (w % 8) * (n / 8) + w / 8: XCD x (w % 8) runs the x-th eighth of the
+// list, in order. The (sequence, kv-head) groups are sorted by the keys
+// they visit (position plus chunk), most first, and dealt in turn to the
+// eight ranges; each range is padded to the longest with empty items. A
+// launch of ragged chunks (L ~ U[8K, 32K]) then ends on short items on
+// every XCD, rather than on whichever long items came last. A group's row
+// tiles stay adjacent in one range, where L2 serves their shared K/V.
+static uint32_t prefill_bins(const nda_ctx *c, uint32_t nseq, const uint32_t *ids, const uint32_t *n_tokens,
+                             uint32_t rep, uint32_t trows, std::vector<std::pair<uint32_t, uint32_t>> (&bins)[8])
+{
+    std::vector<std::pair<uint64_t, uint32_t>> key;      // (keys visited, batch index)
+    for (uint32_t b = 0; b < nseq; b++)
+        if (n_tokens[b])
+            key.push_back({(uint64_t)c->seqs[sid(ids, b)].pos + n_tokens[b], b});
+    std::stable_sort(key.begin(), key.end(), [](const auto &x, const auto &y) { return x.first > y.first; });
+    uint32_t load[8] = {}, rank = 0;
+    for (auto &bin : bins)
+        bin.clear();
+    for (const auto &kb : key) {
+        const uint32_t nt = (n_tokens[kb.second] * rep + trows - 1) / trows;
+        for (uint32_t g = 0; g < c->cfg.n_kv_heads; g++, rank++) {
+            bins[rank % 8].push_back({kb.second, g});
+            load[rank % 8] += nt;
+        }
+    }
+    return *std::max_element(load, load + 8);
+}
+
 static int prefill_plan(nda_ctx *c, uint32_t nseq, const uint32_t *ids, const uint32_t *n_tokens, PrefillPlan &pl)
 {
     pl = PrefillPlan();
@@ -1525,9 +1554,8 @@ static int prefill_plan(nda_ctx *c, uint32_t nseq, const uint32_t *ids, const ui
     pl.waves = NDA_PF_FORCE_W;
 #endif
     pl.trows = 32u * pl.waves;
-    for (uint32_t b = 0; b < nseq; b++)
-        pl.n_items += (size_t)c->cfg.n_kv_heads * ((n_tokens[b] * pl.rep + pl.trows - 1) / pl.trows);
-    pl.n_items = (pl.n_items + 7) / 8 * 8;     // the kernel's XCD remap needs a multiple of 8
+    std::vector<std::pair<uint32_t, uint32_t>> bins[8];
+    pl.n_items = 8 * (size_t)prefill_bins(c, nseq, ids, n_tokens, pl.rep, pl.trows, bins);
     return NDA_OK;
 }
 
@@ -1622,26 +1650,36 @@ int nda_prefill(nda_ctx *c, uint32_t layer, uint32_t nseq, const uint32_t *ids, 
     // first reads then wait on one scalar load, not a chain of three):
     // sequence (~0: padding), kv-head, row tile, first packed token, tokens,
     // position, shared-prefix slots, prefix id (-1: none).
-    std::vector<uint32_t> items;
-    items.reserve(8 * pl.n_items);
+    // in the order of prefill_bins (the same as planned: positions have not
+    // changed since)
+    std::vector<uint32_t> tok0(nseq);
     for (uint32_t b = 0, tok = 0; b < nseq; b++) {
-        const uint32_t qq = sid(ids, b);
-        const SeqHost &s = c->seqs[qq];
-        const Vis v = visible(s, s.pos, c->cfg.window);
-        const uint32_t nt = (n_tokens[b] * rep + trows - 1) / trows;
-        for (uint32_t g = 0; g < c->cfg.n_kv_heads; g++)
-            for (uint32_t t = 0; t < nt; t++) {
-                const uint32_t rec[8] = {qq, g, t, tok, n_tokens[b], s.pos, v.n_sh, (uint32_t)s.prefix};
-                items.insert(items.end(), rec, rec + 8);
-            }
+        tok0[b] = tok;
         tok += n_tokens[b];
     }
-    while ((items.size() / 8) % 8) {   // the kernel's XCD remap needs a multiple of 8
-        const uint32_t pad[8] = {0xFFFFFFFFu, 0, 0, 0, 0, 0, 0, 0};
-        items.insert(items.end(), pad, pad + 8);
+    std::vector<std::pair<uint32_t, uint32_t>> bins[8];
+    const uint32_t per_bin = prefill_bins(c, nseq, ids, n_tokens, rep, trows, bins);
+    std::vector<uint32_t> items;
+    items.reserve(8 * 8 * (size_t)per_bin);
+    for (const auto &bin : bins) {
+        uint32_t n = 0;
+        for (const auto &bg : bin) {
+            const uint32_t b = bg.first, qq = sid(ids, b);
+            const SeqHost &s = c->seqs[qq];
+            const Vis v = visible(s, s.pos, c->cfg.window);
+            const uint32_t nt = (n_tokens[b] * rep + trows - 1) / trows;
+            for (uint32_t t = 0; t < nt; t++, n++) {
+                const uint32_t rec[8] = {qq, bg.second, t, tok0[b], n_tokens[b], s.pos, v.n_sh, (uint32_t)s.prefix};
+                items.insert(items.end(), rec, rec + 8);
+            }
+        }
+        for (; n < per_bin; n++) {
+            const uint32_t pad[8] = {0xFFFFFFFFu, 0, 0, 0, 0, 0, 0, 0};
+            items.insert(items.end(), pad, pad + 8);
+        }
     }
-    if (int rc = ensure_pf(c, items.size()))
-        return rc;
+    if (items.size() != 8 * pl.n_items)
+        return fail(c, NDA_ERR_STATE, "prefill work list: size differs from its plan");
     if (int rc = upload(c, c->d_pf, items.data(), items.size() * 4, st))
         return rc;
     PrefillArgs pa{};
