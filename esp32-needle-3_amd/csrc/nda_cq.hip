@@ -496,7 +496,8 @@ __global__ __launch_bounds__(256) void cq_split_tables_kernel(CqTabArgs a)
 // group tables (one step ahead, in two register sets used in turn) and
 // decodes each W operand dword with one v_perm (its selector from the
 // codes by a shift, a mask and a v_perm per two dwords). The norms are inside the
-// tables, so one sum per block runs over all groups. No LDS, no barrier.
+// tables, so one sum per block runs over all groups. LDS holds only each
+// wave's output stage (below); there is no barrier.
 //
 // The grid is persistent: work-group w runs on XCD w % 8 and walks the
 // items of that XCD's contiguous range, w / 8, w / 8 + G8, ... (G8
@@ -505,7 +506,7 @@ __global__ __launch_bounds__(256) void cq_split_tables_kernel(CqTabArgs a)
 // rows from its L2. The prefetch runs across items: during an item's last
 // step the next item's first step is loaded, and every step's loads carry
 // the row and column exponents its item's stores need, so an item's end
-// waits on nothing. Loads for rows or outputs past the end read row or
+// waits on no load. Loads for rows or outputs past the end read row or
 // column 0 instead (in bounds); what they feed lands only in rows or
 // columns that are never stored.
 template <int OB>
@@ -642,30 +643,68 @@ void cq_gemm_split_kernel(CqSplitArgs a)
                     acc[rb][ob] = __builtin_amdgcn_mfma_f32_32x32x16_f16(st.x[ks][rb][0], wb[ob], acc[rb][ob], 0, 0, 0);
         }
     };
-    // An item's end: the sums out, scaled by 2^-(rexp + cexp), then zeroed.
-    // D layout: lane holds output column ln of each block, rows 8 (i/4) +
-    // 4 jh + (i%4) of the block; lane t of the wave holds row t's exponent.
+    // An item's end: the sums, scaled by 2^-(rexp + cexp), go to this
+    // wave's LDS stage as [64 rows][32 OB columns] and acc is zeroed. The
+    // stage goes out during the next item's first steps, two 16-byte
+    // streaming stores (8 / OB rows of 32 OB columns each) at a step: a
+    // quarter of the store instructions of storing from the MFMA layout,
+    // spread between the MFMA runs, and the output stream does not displace
+    // the X rows the XCD's work-groups re-read from L2. A wave reads back
+    // only its own stage, and its LDS operations complete in order.
+    constexpr int SLD = 32 * OB + 4;            // row stride of the stage, floats
+    constexpr int NG = 4 * OB;                  // groups of two stores per item
+    __shared__ float stage[4 * 64 * SLD];
+    float *const sw = stage + wave * 64 * SLD;
+    Item mo = {0, 0, 0, 0};
+    uint32_t pend = 0;
+    auto drain = [&]() __attribute__((always_inline)) {
+        const uint32_t g = NG - pend;
+        float *y = a.y[mo.ti];
+        const bool v4 = (mo.out & 3u) == 0 && (reinterpret_cast<uintptr_t>(y) & 15u) == 0;
+#pragma unroll
+        for (int h = 0; h < 2; h++) {
+            const uint32_t r = (2 * g + h) * (8 / OB) + lane / (8 * OB), c = 4 * (lane % (8 * OB));
+            const float4v v = *reinterpret_cast<const float4v *>(sw + r * SLD + c);
+            const uint32_t row = mo.r0 + wr + r, o = mo.o0 + wo + c;
+            if (row < a.rows) {
+                float *dst = y + (uint64_t)row * mo.out + o;
+                if (v4 && o + 3 < mo.out) {
+                    __builtin_nontemporal_store(v, reinterpret_cast<float4v *>(dst));
+                } else {
+                    if (o < mo.out)
+                        __builtin_nontemporal_store(v.x, dst + 0);
+                    if (o + 1 < mo.out)
+                        __builtin_nontemporal_store(v.y, dst + 1);
+                    if (o + 2 < mo.out)
+                        __builtin_nontemporal_store(v.z, dst + 2);
+                    if (o + 3 < mo.out)
+                        __builtin_nontemporal_store(v.w, dst + 3);
+                }
+            }
+        }
+        pend--;
+    };
     auto finish = [&](const Item &m, const Step &st) {
-        float *y = a.y[m.ti];
+        while (pend)
+            drain();
 #pragma unroll
         for (int rb = 0; rb < 2; rb++)
 #pragma unroll
             for (int i = 0; i < 16; i++) {
                 const int t = 32 * rb + 8 * (i >> 2) + 4 * jh + (i & 3);
                 const int rx = __shfl(st.rx, t, 64);
-                const uint32_t row = m.r0 + wr + t;
 #pragma unroll
-                for (int ob = 0; ob < OB; ob++) {
-                    const uint32_t o = m.o0 + wo + 32 * ob + ln;
-                    if (row < a.rows && o < m.out)
-                        y[(uint64_t)row * m.out + o] = ldexpf(acc[rb][ob][i], -(rx + st.ce[ob]));
-                }
+                for (int ob = 0; ob < OB; ob++)
+                    sw[t * SLD + 32 * ob + ln] = ldexpf(acc[rb][ob][i], -(rx + st.ce[ob]));
             }
+        __builtin_amdgcn_wave_barrier();
 #pragma unroll
         for (int rb = 0; rb < 2; rb++)
 #pragma unroll
             for (int ob = 0; ob < OB; ob++)
                 acc[rb][ob] = float16v{};
+        mo = m;
+        pend = NG;
     };
 
     // Loads run one step ahead of the MFMAs at (lit, ls); when nothing is
@@ -696,6 +735,8 @@ void cq_gemm_split_kernel(CqSplitArgs a)
         __builtin_amdgcn_sched_barrier(0);
         compute(s0);
         __builtin_amdgcn_sched_barrier(0);
+        if (pend)
+            drain();
         if (++cs == nsteps) {
             finish(mc, s0);
             if (cit + G8 >= last)
@@ -709,6 +750,8 @@ void cq_gemm_split_kernel(CqSplitArgs a)
         __builtin_amdgcn_sched_barrier(0);
         compute(s1);
         __builtin_amdgcn_sched_barrier(0);
+        if (pend)
+            drain();
         if (++cs == nsteps) {
             finish(mc, s1);
             if (cit + G8 >= last)
@@ -718,6 +761,8 @@ void cq_gemm_split_kernel(CqSplitArgs a)
             mc = item(cit);
         }
     }
+    while (pend)
+        drain();
 }
 
 hipError_t launch_cq_split_tables(const CqTabArgs &a, hipStream_t s)
