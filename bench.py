@@ -207,6 +207,42 @@ def prefill_leg(N, stream, nseq=256, lmin=8192, lmax=32768, chunk=512, reps=3):
             "decode": dec}
 
 
+def ceiling_leg(N, iters=200000):
+    """Measured device ceilings (libndprobe, include/ndp.h), register-only
+    loops with no memory traffic:
+    - the dense fp16 MFMA rate: 4 independent v_mfma_f32_32x32x16_f16 chains
+      per wave, at 1 and 2 waves per SIMD (the best is the ceiling);
+    - the shader clock under that load, per wave from s_memtime cycles over
+      s_memrealtime time;
+    - SIMD cycles per wave64 v_exp_f32 and v_fma_f32 (8 independent chains);
+    - MFMA with 2 or 4 independent exps issued after each MFMA by the same
+      wave: whether the VALU work hides under the matrix pipe."""
+    def mfma(bpc, wpb, nexp=0, n=iters):
+        r = N.probe_run(N.PROBE_MFMA_F16, 4, nexp, bpc, wpb, n)
+        wps = bpc * wpb / 4.0
+        return {"waves_per_simd": wps, "tflops": round(r["flops"] / (r["ms"] * 1e-3) / 1e12, 1),
+                "clock_ghz": round(r["clock_ghz"], 3), "ms": round(r["ms"], 3),
+                "simd_cycles_per_mfma": round(r["cycles_per_iter"] / 4 / wps, 2)}
+
+    def valu(kind, bpc=2, wpb=4, n=iters // 2):
+        r = N.probe_run(kind, 0, 0, bpc, wpb, n)
+        wps = bpc * wpb / 4.0
+        return {"waves_per_simd": wps, "simd_cycles_per_inst": round(r["cycles_per_iter"] / 8 / wps, 2),
+                "clock_ghz": round(r["clock_ghz"], 3),
+                "ginst_per_s": round(r["valu_insts"] / (r["ms"] * 1e-3) / 1e9, 1)}
+
+    runs = [mfma(1, 4), mfma(2, 4), mfma(1, 8)]
+    best = max(runs, key=lambda x: x["tflops"])
+    return {"workload": "device ceilings: register-only probe loops on every CU",
+            "mfma_f16_dense_tflops": best["tflops"], "clock_ghz_under_mfma": best["clock_ghz"],
+            "mfma_runs": runs,
+            "exp_f32": valu(N.PROBE_VALU_EXP), "fma_f32": valu(N.PROBE_VALU_FMA),
+            "mfma_plus_exp": {"2_per_mfma": mfma(2, 4, 2, iters // 2), "4_per_mfma": mfma(2, 4, 4, iters // 2)},
+            "nominal_mfma_f16_tflops": 2500.0,
+            "note": "FLOPs of v_mfma_f32_32x32x16_f16 = 2*32*32*16 per wave instruction; clock = s_memtime "
+                    "cycles / s_memrealtime time (device wall-clock rate), averaged over all waves"}
+
+
 def decode_long(N, ctx, stream, lens, q, k, v, out, reps):
     """One decode token per sequence at position L_s (append + attention over
     [0, L_s], split-KV at this batch), repeated `reps` times at the same
@@ -787,7 +823,8 @@ def main():
     ap.add_argument("--no-prefill", action="store_true")
     ap.add_argument("--calib", action="store_true",
                     help="first run a 4 GiB device copy (known traffic, for counter calibration)")
-    ap.add_argument("--leg", choices=["cq", "cq_prefill", "block", "block_prefill", "prefill", "front", "shared"],
+    ap.add_argument("--leg", choices=["cq", "cq_prefill", "block", "block_prefill", "prefill", "front", "shared",
+                                      "ceiling"],
                     help="run only this leg and print its JSON object (for profiling one kernel family)")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
@@ -815,7 +852,7 @@ def main():
         legs = {"cq": lambda: cq_leg(N, stream), "cq_prefill": lambda: cq_leg(N, stream, rows=49787, reps=5),
                 "block": lambda: block_leg(N, stream), "block_prefill": lambda: block_prefill_leg(N, stream),
                 "prefill": lambda: prefill_leg(N, stream), "front": lambda: front_leg(N, stream),
-                "shared": lambda: shared_prefix_leg(N, stream)}
+                "shared": lambda: shared_prefix_leg(N, stream), "ceiling": lambda: ceiling_leg(N)}
         print(json.dumps(legs[args.leg]()), flush=True)
         return
     rng = np.random.default_rng(SEED)
@@ -925,11 +962,18 @@ def main():
             "%.0f GB/s logical, sampled max |delta| %.3g" % (
                 shared["prefill_tflops"], shared["prefill_unique_GBps"], shared["decode_tokens_per_s"],
                 shared["decode_unique_GBps"], shared["decode_logical_GBps"], shared["max_abs_delta_sampled"]))
+    ceiling = ceiling_leg(N)
+    log("ceiling: dense fp16 MFMA %.1f TFLOP/s at %.3f GHz; exp %.2f, fma %.2f SIMD cycles per wave instruction" % (
+        ceiling["mfma_f16_dense_tflops"], ceiling["clock_ghz_under_mfma"],
+        ceiling["exp_f32"]["simd_cycles_per_inst"], ceiling["fma_f32"]["simd_cycles_per_inst"]))
     prefill = None
     if not args.no_prefill:
         prefill = prefill_leg(N, stream)
-        log("prefill: %.1f TFLOP/s (%.3f of 2.5 PF), kernel %.3f ms, sampled max |delta| %.3g" %
-            (prefill["tflops"], prefill["frac"], prefill["kernel_ms"], prefill["max_abs_delta_sampled"]))
+        prefill["peak_measured"] = ceiling["mfma_f16_dense_tflops"]
+        prefill["frac_measured"] = round(prefill["tflops"] / ceiling["mfma_f16_dense_tflops"], 4)
+        log("prefill: %.1f TFLOP/s (%.3f of 2.5 PF, %.3f of the measured %.0f), kernel %.3f ms, sampled max "
+            "|delta| %.3g" % (prefill["tflops"], prefill["frac"], prefill["frac_measured"], prefill["peak_measured"],
+                              prefill["kernel_ms"], prefill["max_abs_delta_sampled"]))
 
     cpu = cpu_1 = cpu_ref = cpu_long = None
     if not args.no_cpu:
@@ -985,6 +1029,7 @@ def main():
         "cpu_reference_int8": cpu_ref,
         "cpu_long_context_decode": cpu_long,
         "prefill": prefill,
+        "device_ceiling": ceiling,
         "engine_session": engine,
         "front": front,
         "cq_projections": cq,

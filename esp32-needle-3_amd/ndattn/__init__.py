@@ -14,6 +14,7 @@ PKG_DIR = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 # The in-tree build is the only library this module loads.
 LIB_PATH = os.path.join(PKG_DIR, "libndattn.so")
 HOST_LIB_PATH = os.path.join(PKG_DIR, "libndhost.so")
+PROBE_LIB_PATH = os.path.join(PKG_DIR, "libndprobe.so")
 
 NDA_OK = 0
 ERRORS = {-1: "NDA_ERR_ARG", -2: "NDA_ERR_NOMEM", -3: "NDA_ERR_HIP", -4: "NDA_ERR_RANGE",
@@ -49,6 +50,8 @@ HOST_SYMBOLS = [
     "nd_gpu_front_init", "nd_gpu_front_weights", "nd_gpu_attention_raw",
     "nd_gpu_block_weights", "nd_gpu_attention_block",
 ]
+PROBE_SYMBOLS = ["ndp_run"]
+PROBE_MFMA_F16, PROBE_VALU_EXP, PROBE_VALU_FMA = 0, 1, 2   # include/ndp.h
 
 
 class NdaError(RuntimeError):
@@ -617,6 +620,37 @@ def cq_gemm_split_many(tensors, rows, xs, ys, stream=None):
     th = (vp * n)(*[t.h for t in tensors])
     yp = (vp * n)(*[_dp(y) for y in ys])
     _check(lib().nda_cq_gemm_split_many(th, n, rows, _dp(xs), yp, stream))
+
+
+class ProbeResult(C.Structure):
+    _fields_ = [("ms", C.c_double), ("clock_ghz", C.c_double), ("cycles_per_iter", C.c_double),
+                ("flops", C.c_double), ("valu_insts", C.c_double), ("waves", C.c_uint32),
+                ("cus", C.c_uint32)]
+
+
+_probe = None
+
+
+def probe_lib():
+    """Load libndprobe.so (include/ndp.h): the device-ceiling probe."""
+    global _probe
+    if _probe is None:
+        if not os.path.exists(PROBE_LIB_PATH):
+            raise RuntimeError("libndprobe.so not built: run `make -C esp32-needle-3_amd`")
+        P = C.CDLL(PROBE_LIB_PATH)
+        P.ndp_run.restype = C.c_int
+        P.ndp_run.argtypes = [C.c_int] * 6 + [C.POINTER(ProbeResult)]
+        _probe = P
+    return _probe
+
+
+def probe_run(kind, nacc=4, nexp=0, blocks_per_cu=2, waves_per_block=4, iters=100000):
+    """One ndp_run launch; returns its ProbeResult fields as a dict."""
+    r = ProbeResult()
+    rc = probe_lib().ndp_run(kind, nacc, nexp, blocks_per_cu, waves_per_block, iters, C.byref(r))
+    if rc != 0:
+        raise NdaError(rc, "ndp_run(kind=%d)" % kind)
+    return {f: getattr(r, f) for f, _ in ProbeResult._fields_}
 
 
 class Timer:

@@ -13,7 +13,7 @@ def declared(header):
     text = open(os.path.join(REPO, "include", header)).read()
     text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
     names = re.findall(r"\b(n[a-z0-9_]+)\s*\(", text)
-    return sorted({n for n in names if n.startswith(("nda_", "nd_gpu_"))})
+    return sorted({n for n in names if n.startswith(("nda_", "nd_gpu_", "ndp_"))})
 
 
 def test_nda_exports_every_declared_symbol():
@@ -31,6 +31,15 @@ def test_host_shim_exports_every_declared_symbol():
     names = declared("nd_attn_gpu.h")
     assert sorted(ndattn.HOST_SYMBOLS) == names
     lib = C.CDLL(ndattn.HOST_LIB_PATH)
+    for n in names:
+        assert hasattr(lib, n), n
+
+
+def test_probe_exports_every_declared_symbol():
+    import ndattn
+    names = declared("ndp.h")
+    assert sorted(ndattn.PROBE_SYMBOLS) == names
+    lib = C.CDLL(ndattn.PROBE_LIB_PATH)
     for n in names:
         assert hasattr(lib, n), n
 
