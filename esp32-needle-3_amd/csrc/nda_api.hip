@@ -1324,6 +1324,7 @@ static int prefix_pass(nda_ctx *c, const AttnArgs &a, uint32_t nseq, const uint3
     pa.items = c->d_pf;
     pa.part = a.part;
     pa.max_chunks = a.max_chunks;
+    pa.tab_cap = (ps.n_sh + 31) / 32;         // the prefix's tiles only
     pa.pg = a.pg;
     pa.n_items = (uint32_t)(items.size() / 8);
     pa.nh = a.nh;
@@ -1661,12 +1662,16 @@ int nda_prefill(nda_ctx *c, uint32_t layer, uint32_t nseq, const uint32_t *ids, 
     const uint32_t per_bin = prefill_bins(c, nseq, ids, n_tokens, rep, trows, bins);
     std::vector<uint32_t> items;
     items.reserve(8 * 8 * (size_t)per_bin);
+    // key tiles of the longest item (its work-group's tile table): the
+    // shared prefix's, then the own slots up to the chunk's last token
+    uint32_t tab_cap = 0;
     for (const auto &bin : bins) {
         uint32_t n = 0;
         for (const auto &bg : bin) {
             const uint32_t b = bg.first, qq = sid(ids, b);
             const SeqHost &s = c->seqs[qq];
             const Vis v = visible(s, s.pos, c->cfg.window);
+            tab_cap = std::max<uint32_t>(tab_cap, (v.n_sh + 31) / 32 + (s.pos + n_tokens[b] - v.n_sh + 31) / 32);
             const uint32_t nt = (n_tokens[b] * rep + trows - 1) / trows;
             for (uint32_t t = 0; t < nt; t++, n++) {
                 const uint32_t rec[8] = {qq, bg.second, t, tok0[b], n_tokens[b], s.pos, v.n_sh, (uint32_t)s.prefix};
@@ -1691,6 +1696,7 @@ int nda_prefill(nda_ctx *c, uint32_t layer, uint32_t nseq, const uint32_t *ids, 
     pa.prefix_pages = c->d_prefix_pages;
     pa.seqs = c->d_seqs;
     pa.items = c->d_pf;
+    pa.tab_cap = tab_cap;
     pa.pg = c->pg;
     pa.n_items = (uint32_t)(items.size() / 8);
     pa.nh = c->cfg.n_heads;

@@ -76,6 +76,8 @@ struct PrefillArgs {
     const uint32_t *row_seq; /* decode launches (one wave per item): sequence of each row, or null */
     float *part;             /* shared-prefix decode pass: split-KV partials of chunk 0, or null */
     uint32_t max_chunks;     /*   their stride (AttnArgs::max_chunks) */
+    uint32_t tab_cap;        /* prefill: key tiles of the longest work item (its per-work-group tile
+                                table in LDS), 0: no table */
     PageGeom pg;
     uint32_t n_items;
     uint32_t nh;
@@ -263,6 +265,9 @@ struct Geo {
 hipError_t launch_append(const Geo &g, const AppendArgs &a, hipStream_t s);
 hipError_t launch_attend(const Geo &g, const AttnArgs &a, hipStream_t s);
 hipError_t launch_prefill(const Geo &g, const PrefillArgs &a, int waves, hipStream_t s);
+/* Largest prefill tile table (PrefillArgs::tab_cap * 16 bytes) a work-group
+ * size can take; a launch whose table would be larger runs without one. */
+uint32_t pf_tab_max_bytes(int waves);
 /* GQA decode on MFMA: one wave per (row, kv-head) item, n_items = rows * nkv,
  * items in (row, kv-head) order; a.row_seq as in AttnArgs. */
 bool decode_mfma_supported(const Geo &g);

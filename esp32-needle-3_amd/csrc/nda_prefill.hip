@@ -218,7 +218,7 @@ __device__ __forceinline__ PfChunk pf_chunk(int tid, int wave, uint32_t P)
     return k;
 }
 
-template <int ES, int DK, int DV, int NTHR>
+template <int ES, int DK, int DV, int NTHR, bool TAB>
 struct PfIO {
     using T = PfTile<ES, DK, DV, NTHR>;
     // A tile's page ids and first in-page slots (uniform), as read a tile
@@ -262,9 +262,27 @@ struct PfIO {
         s0 = PF_KT * (sh ? (tail ? nfs : t) : own);
         len = own_len + (sh ? n_sh - own_len : 0);
     }
+    // TAB: every tile's TileRef, built once per work-group in LDS, entries
+    // [0, tab_n); fetch() is then one broadcast LDS read instead of the
+    // segment arithmetic and two page-table loads per tile
+    const uint4 *tab;
+    int tab_n;
+    __device__ __forceinline__ void fetch(int t, TileRef &r) const
+    {
+        if constexpr (TAB) {
+            const uint4 e = tab[min(t, tab_n - 1)];
+            r.p0 = e.x;
+            r.p1 = e.y;
+            r.sip0 = e.z & 0xFFFFu;
+            r.dsip = e.z >> 16;
+            r.vlim = (int)e.w;
+        } else {
+            compute(t, r);
+        }
+    }
     // page ids of tile t (past the last tile: the last tile again); a half
     // past its segment's end rereads half 0
-    __device__ __forceinline__ void fetch(int t, TileRef &r) const
+    __device__ __forceinline__ void compute(int t, TileRef &r) const
     {
         bool sh;
         int s0, len;
@@ -342,7 +360,7 @@ struct PfIO {
     }
 };
 
-template <int ES, int DK, int DV, int REP, int W>
+template <int ES, int DK, int DV, int REP, int W, bool TAB>
 __global__ __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(W >= 8 ? 4 : 3)))
 void prefill_kernel(PrefillArgs a)
 {
@@ -394,7 +412,7 @@ void prefill_kernel(PrefillArgs a)
     float m = -FLT_MAX, lsum = 0.0f;
     const float neg1 = opaque_neg1();
 
-    PfIO<ES, DK, DV, NTHR> io;
+    PfIO<ES, DK, DV, NTHR, TAB> io;
     io.pool = a.pool;
     io.own_pages = a.page_table + (uint64_t)seq * a.pg.pages_per_seq;
     io.zero = threadIdx.y;
@@ -418,6 +436,20 @@ void prefill_kernel(PrefillArgs a)
     io.ntile = io.nfs + io.psh + (io.own_len + PF_KT - 1) / PF_KT;
     const int ntile = io.ntile, jfull = io.jfull;
 
+    // TAB: the tile table (dynamic LDS of a.tab_cap entries, at least every
+    // item's tile count), one entry per thread and pass
+    if constexpr (TAB) {
+        extern __shared__ __attribute__((aligned(16))) uint4 pf_tab[];
+        io.tab = pf_tab;
+        io.tab_n = (int)min((uint32_t)ntile, a.tab_cap);
+        for (int t = tid; t < io.tab_n; t += NTHR) {
+            typename PfIO<ES, DK, DV, NTHR, TAB>::TileRef r;
+            io.compute(t, r);
+            pf_tab[t] = uint4{r.p0, r.p1, r.sip0 | (r.dsip << 16), (uint32_t)r.vlim};
+        }
+        __syncthreads();
+    }
+
     // Register prefetch: tile j+1 loads while tile j is computed and waits
     // in registers for its LDS store at the end of tile j. The 8-wave
     // variant fits the 128 registers of 4 waves per SIMD; the 2- and 4-wave
@@ -428,7 +460,7 @@ void prefill_kernel(PrefillArgs a)
     // sit in a ring indexed by tile parity: those of tile j+2 are read at
     // the start of tile j, next to the data load of tile j+1. Tile 0 is
     // requested before Q, so its latency and Q's overlap.
-    typename PfIO<ES, DK, DV, NTHR>::TileRef prn[2];
+    typename PfIO<ES, DK, DV, NTHR, TAB>::TileRef prn[2];
     Staged<T::CPT> sg;
     io.fetch(0, prn[0]);
     io.fetch(1, prn[1]);
@@ -537,44 +569,55 @@ void prefill_kernel(PrefillArgs a)
             for (int i = 0; i < 16; i++)
                 st[i] = 8 * (i >> 2) + (i & 3) > thr ? -INFINITY : st[i];
         }
-        // tile max over the 16 scores (a tree of 3-input maxes: fmaxf would
-        // first make NaN-quieting copies of its inputs; scores are never NaN)
-        // and the partner lane's, without an LDS round trip: the swap
-        // returns (own, partner) in lanes 0-31 and (partner, own) in 32-63
-        const float x0 = max3(st[0], st[1], st[2]), x1 = max3(st[3], st[4], st[5]);
-        const float x2 = max3(st[6], st[7], st[8]), x3 = max3(st[9], st[10], st[11]);
-        const float x4 = max3(st[12], st[13], st[14]);
-        const float y0 = max3(x0, x1, x2), y1 = max3(x3, x4, st[15]);
-        float mt = max3(y0, y1, y1);
-        {
-            const auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(mt), __float_as_uint(mt), false, false);
-            mt = max3(mt, __uint_as_float(sw[0]), __uint_as_float(sw[1]));
-        }
-        // Lazy max: keep the running max unless the tile exceeds it by more
-        // than 2^8 (weights stay <= 256, exact range for fp16 and fp32), and
-        // skip the rescale sweep when no row of the wave moved.
-        const bool grow = REL ? mt > 8.0f : mt > m + 8.0f;
-        if (__builtin_expect(__ballot(grow) != 0, 0)) {
-            if constexpr (REL) {
-                const float d = grow ? mt : 0.0f;     // the running max moves by d
-                const float rs = fast_exp2(-d);
-                m += d;
-                lsum *= rs;
-#pragma unroll
-                for (int i = 0; i < 16; i++) {
-                    acc0[i] *= rs;
-                    acc1[i] *= rs;
-                    st[i] -= d;
-                }
-            } else {
-                const float mnew = grow ? mt : m;
-                const float rs = fast_exp2(m - mnew);
-                m = mnew;
-                lsum *= rs;
-#pragma unroll
-                for (int i = 0; i < 16; i++) {
-                    acc0[i] *= rs;
-                    acc1[i] *= rs;
+        // Lazy max (below): the running max moves only when a score exceeds
+        // it by more than 2^8, so weights stay <= 256 (exact range for fp16
+        // and fp32). With fp16 K/V, after the first tile, that is checked on
+        // the weights instead of the scores: each 16-key half's exps are
+        // summed for the row sum anyway, and a half whose sum is at most 256
+        // holds no weight above 256, so the tile max is needed only when a
+        // sum exceeds it (rare once the running max has settled). Otherwise
+        // the tile max decides first.
+        constexpr bool SUMCHK = REL;
+        if constexpr (!SUMCHK) {
+            // tile max over the 16 scores (a tree of 3-input maxes: fmaxf would
+            // first make NaN-quieting copies of its inputs; scores are never NaN)
+            // and the partner lane's, without an LDS round trip: the swap
+            // returns (own, partner) in lanes 0-31 and (partner, own) in 32-63
+            const float x0 = max3(st[0], st[1], st[2]), x1 = max3(st[3], st[4], st[5]);
+            const float x2 = max3(st[6], st[7], st[8]), x3 = max3(st[9], st[10], st[11]);
+            const float x4 = max3(st[12], st[13], st[14]);
+            const float y0 = max3(x0, x1, x2), y1 = max3(x3, x4, st[15]);
+            float mt = max3(y0, y1, y1);
+            {
+                const auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(mt), __float_as_uint(mt), false, false);
+                mt = max3(mt, __uint_as_float(sw[0]), __uint_as_float(sw[1]));
+            }
+            // Lazy max: keep the running max unless the tile exceeds it by more
+            // than 2^8 (weights stay <= 256, exact range for fp16 and fp32), and
+            // skip the rescale sweep when no row of the wave moved.
+            const bool grow = REL ? mt > 8.0f : mt > m + 8.0f;
+            if (__builtin_expect(__ballot(grow) != 0, 0)) {
+                if constexpr (REL) {
+                    const float d = grow ? mt : 0.0f;     // the running max moves by d
+                    const float rs = fast_exp2(-d);
+                    m += d;
+                    lsum *= rs;
+    #pragma unroll
+                    for (int i = 0; i < 16; i++) {
+                        acc0[i] *= rs;
+                        acc1[i] *= rs;
+                        st[i] -= d;
+                    }
+                } else {
+                    const float mnew = grow ? mt : m;
+                    const float rs = fast_exp2(m - mnew);
+                    m = mnew;
+                    lsum *= rs;
+    #pragma unroll
+                    for (int i = 0; i < 16; i++) {
+                        acc0[i] *= rs;
+                        acc1[i] *= rs;
+                    }
                 }
             }
         }
@@ -584,19 +627,57 @@ void prefill_kernel(PrefillArgs a)
         // ranges short. hi = p rounded toward zero to fp16, lo = the remainder.
 #pragma unroll
         for (int kb2 = 0; kb2 < 2; kb2++) {
+            float p[8];
+#pragma unroll
+            for (int i = 0; i < 8; i++)
+                p[i] = fast_exp2(REL ? st[8 * kb2 + i] : st[8 * kb2 + i] - m);
+            if constexpr (SUMCHK) {
+                float ts = ((p[0] + p[1]) + (p[2] + p[3])) + ((p[4] + p[5]) + (p[6] + p[7]));
+                if (__builtin_expect(__ballot(ts > 256.0f) != 0, 0)) {
+                    // the half's max over the row (this lane's 8 keys and its
+                    // partner's), then the running max moves as above; the
+                    // other half's scores move with it
+                    const float h0 = max3(st[8 * kb2], st[8 * kb2 + 1], st[8 * kb2 + 2]);
+                    const float h1 = max3(st[8 * kb2 + 3], st[8 * kb2 + 4], st[8 * kb2 + 5]);
+                    float mt = max3(h0, h1, __builtin_fmaxf(st[8 * kb2 + 6], st[8 * kb2 + 7]));
+                    const auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(mt), __float_as_uint(mt), false, false);
+                    mt = max3(mt, __uint_as_float(sw[0]), __uint_as_float(sw[1]));
+                    const bool grow = mt > 8.0f;
+                    if (__ballot(grow) != 0) {
+                        const float d = grow ? mt : 0.0f;     // the running max moves by d
+                        const float rs = fast_exp2(-d);
+                        m += d;
+                        lsum *= rs;
+#pragma unroll
+                        for (int i = 0; i < 16; i++) {
+                            acc0[i] *= rs;
+                            acc1[i] *= rs;
+                            st[i] -= d;
+                        }
+#pragma unroll
+                        for (int i = 0; i < 8; i++)
+                            p[i] = fast_exp2(st[8 * kb2 + i]);
+                        ts = ((p[0] + p[1]) + (p[2] + p[3])) + ((p[4] + p[5]) + (p[6] + p[7]));
+                    }
+                }
+                lsum += ts;
+            } else {
+#pragma unroll
+                for (int i = 0; i < 8; i += 2)
+                    lsum += p[i] + p[i + 1];
+            }
             u32x4 phw, plw;
 #pragma unroll
-            for (int i = 8 * kb2; i < 8 * kb2 + 8; i += 2) {
-                float p0 = fast_exp2(REL ? st[i] : st[i] - m), p1 = fast_exp2(REL ? st[i + 1] : st[i + 1] - m);
-                lsum += p0 + p1;
+            for (int i = 0; i < 8; i += 2) {
+                float p0 = p[i], p1 = p[i + 1];
                 if constexpr (ES == 1) {
-                    p0 *= Vsc[8 * (i >> 2) + 4 * jh + (i & 3)];
-                    p1 *= Vsc[8 * (i >> 2) + 4 * jh + ((i + 1) & 3)];
+                    p0 *= Vsc[8 * ((8 * kb2 + i) >> 2) + 4 * jh + (i & 3)];
+                    p1 *= Vsc[8 * ((8 * kb2 + i) >> 2) + 4 * jh + ((i + 1) & 3)];
                 }
                 const fp16x2 h = __builtin_amdgcn_cvt_pkrtz(p0, p1);
                 const uint32_t hw = __builtin_bit_cast(uint32_t, h);
-                phw[(i & 7) >> 1] = hw;
-                plw[(i & 7) >> 1] = split_lo2(hw, p0, p1, neg1);
+                phw[i >> 1] = hw;
+                plw[i >> 1] = split_lo2(hw, p0, p1, neg1);
             }
             const half8 ph = __builtin_bit_cast(half8, phw), pl = __builtin_bit_cast(half8, plw);
 #pragma unroll
@@ -1174,6 +1255,25 @@ bool prefill_mfma_supported(const Geo &g)
 // SIMD; the others run 4-wave work-groups.
 static bool pf_w8_fits(const Geo &g) { return g.kv_f16 && g.rep == 1; }
 
+template <int ES, int DK, int DV, int REP, bool TAB>
+static void launch_pf(dim3 grid, int waves, uint32_t lds, const PrefillArgs &a, hipStream_t s)
+{
+    if (waves == 2)
+        hipLaunchKernelGGL((prefill_kernel<ES, DK, DV, REP, 2, TAB>), grid, dim3(128), lds, s, a);
+    else if (waves == 8)
+        hipLaunchKernelGGL((prefill_kernel<ES, DK, DV, REP, 8, TAB>), grid, dim3(512), lds, s, a);
+    else
+        hipLaunchKernelGGL((prefill_kernel<ES, DK, DV, REP, 4, TAB>), grid, dim3(256), lds, s, a);
+}
+
+// Largest tile table (bytes of dynamic LDS) that keeps a work-group size's
+// residency: 160 KiB per CU over its resident work-groups (4 waves per SIMD
+// for 8-wave groups, 3 otherwise), less two tile buffers (at most 19 KiB).
+uint32_t pf_tab_max_bytes(int waves)
+{
+    return waves >= 8 ? 48u << 10 : waves == 4 ? 32u << 10 : 7u << 10;
+}
+
 hipError_t launch_prefill(const Geo &g, const PrefillArgs &a, int waves, hipStream_t s)
 {
     if (a.n_items == 0)
@@ -1182,14 +1282,15 @@ hipError_t launch_prefill(const Geo &g, const PrefillArgs &a, int waves, hipStre
         waves = 4;
     const int es = g.kv_f16 ? 2 : 1;
     dim3 grid(a.n_items);     // n_items: a multiple of 8 (padded with empty items)
+    // a table of a.tab_cap tiles when the host sized one that fits
+    const uint32_t tab_bytes = a.tab_cap * 16u;
+    const bool tab = a.tab_cap > 0 && tab_bytes <= pf_tab_max_bytes(waves);
 #define X(ES, DK, DV, REP)                                                                      \
     if (es == ES && g.dk == DK && g.dv == DV && g.rep == REP) {                                 \
-        if (waves == 2)                                                                          \
-            hipLaunchKernelGGL((prefill_kernel<ES, DK, DV, REP, 2>), grid, dim3(128), 0, s, a);  \
-        else if (waves == 8)                                                                     \
-            hipLaunchKernelGGL((prefill_kernel<ES, DK, DV, REP, 8>), grid, dim3(512), 0, s, a);  \
+        if (tab)                                                                                 \
+            launch_pf<ES, DK, DV, REP, true>(grid, waves, tab_bytes, a, s);                      \
         else                                                                                     \
-            hipLaunchKernelGGL((prefill_kernel<ES, DK, DV, REP, 4>), grid, dim3(256), 0, s, a);  \
+            launch_pf<ES, DK, DV, REP, false>(grid, waves, 0, a, s);                             \
         return hipGetLastError();                                                                \
     }
     NDA_PF_GEOMETRIES(X)
