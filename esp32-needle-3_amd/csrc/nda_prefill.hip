@@ -280,6 +280,18 @@ struct PfIO {
             compute(t, r);
         }
     }
+    // a table entry (as read from LDS) as uniform values
+    __device__ __forceinline__ static TileRef uniform(const uint4 &e)
+    {
+        TileRef r;
+        r.p0 = __builtin_amdgcn_readfirstlane(e.x);
+        r.p1 = __builtin_amdgcn_readfirstlane(e.y);
+        const uint32_t z = __builtin_amdgcn_readfirstlane(e.z);
+        r.sip0 = z & 0xFFFFu;
+        r.dsip = z >> 16;
+        r.vlim = (int)__builtin_amdgcn_readfirstlane(e.w);
+        return r;
+    }
     // page ids of tile t (past the last tile: the last tile again); a half
     // past its segment's end rereads half 0
     __device__ __forceinline__ void compute(int t, TileRef &r) const
@@ -462,9 +474,19 @@ void prefill_kernel(PrefillArgs a)
     // requested before Q, so its latency and Q's overlap.
     typename PfIO<ES, DK, DV, NTHR, TAB>::TileRef prn[2];
     Staged<T::CPT> sg;
-    io.fetch(0, prn[0]);
-    io.fetch(1, prn[1]);
-    io.load(prn[0], sg);                        // tile 0
+    // TAB: nxt is the table entry of the tile the next load brings, read
+    // before each tile's barrier (whose fence waits for it) and made uniform
+    // at the load; without a table, page ids sit in a ring indexed by tile
+    // parity
+    uint4 nxt = {};
+    if constexpr (TAB) {
+        io.load(io.uniform(io.tab[0]), sg);     // tile 0
+        nxt = io.tab[min(1, io.tab_n - 1)];
+    } else {
+        io.fetch(0, prn[0]);
+        io.fetch(1, prn[1]);
+        io.load(prn[0], sg);                    // tile 0
+    }
     // Q^T operand, hi and lo halves, slots = dims 16*kb + 8*jh + s: eight
     // consecutive floats per k-block, loaded as two float4 (all issued
     // before any is used; rows past the chunk read row 0 and are zeroed).
@@ -518,10 +540,15 @@ void prefill_kernel(PrefillArgs a)
     auto tile = [&](const int j, auto pj, auto masked, auto first) __attribute__((always_inline)) {
         constexpr int PJ = decltype(pj)::value, Q1 = PJ ^ 1;
         constexpr bool REL = ES == 2 && !decltype(first)::value;   // scores relative to m
-        // ids of tile j+2 into the slot of tile j's (spent), then the data of
-        // tile j+1 (past the last tile: the last tile again, never stored)
-        io.fetch(j + 2, prn[PJ]);
-        io.load(prn[Q1], sg);
+        // the data of tile j+1 (past the last tile: the last tile again,
+        // never stored); without a table, first the ids of tile j+2 into the
+        // slot of tile j's (spent)
+        if constexpr (TAB) {
+            io.load(io.uniform(nxt), sg);
+        } else {
+            io.fetch(j + 2, prn[PJ]);
+            io.load(prn[Q1], sg);
+        }
         const _Float16 (*Ks)[T::KPAD] = reinterpret_cast<const _Float16 (*)[T::KPAD]>(kvbuf[PJ]);
         const _Float16 (*Vr)[T::VPAD] = reinterpret_cast<const _Float16 (*)[T::VPAD]>(kvbuf[PJ] + T::VOFF);
         const float *Ksc = reinterpret_cast<const float *>(kvbuf[PJ] + T::SOFF), *Vsc = Ksc + PF_KT;
@@ -704,6 +731,8 @@ void prefill_kernel(PrefillArgs a)
         __builtin_amdgcn_s_setprio(0);
         if (j + 1 < ntile)   // tile j+1 into the other buffer (its readers are done)
             io.template store<false>(sg, kvbuf[Q1]);
+        if constexpr (TAB)
+            nxt = io.tab[min(j + 2, io.tab_n - 1)];
         __syncthreads();
     };
     using P0 = std::integral_constant<int, 0>;
