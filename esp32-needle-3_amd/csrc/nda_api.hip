@@ -168,6 +168,12 @@ struct nda_ctx {
     int live_head = 0, live_n = 0;
     std::vector<hipEvent_t> ring_ev;    // free events, all created with the context (capacity reserved)
 
+    // stream order: the stream of the last call that queued work, and the
+    // event a call on another stream waits for (on_stream)
+    hipStream_t last_stream = nullptr;
+    bool has_stream = false;
+    hipEvent_t order_ev = nullptr;
+
     bool prof = false;
     std::vector<ProfRec> prof_pending;
     std::vector<hipEvent_t> ev_free;
@@ -204,6 +210,24 @@ int hip_fail(nda_ctx *c, hipError_t e, const char *what)
         if (e_ != hipSuccess)                              \
             return hip_fail((c), e_, #call);               \
     } while (0)
+
+// Calls on one context are ordered as if they ran on one stream. A call
+// rewrites device tables and scratch buffers (sequence and page tables, row
+// staging, work lists, split partials, block scratch) that the previous
+// call's kernels may still be reading; so a call on a stream other than the
+// previous call's first makes its stream wait for everything queued on the
+// previous one (an event recorded there), before it uploads or launches
+// anything. Calls on one stream need nothing: stream order covers them.
+int on_stream(nda_ctx *c, hipStream_t st)
+{
+    if (c->has_stream && c->last_stream != st) {
+        HIPC(c, hipEventRecord(c->order_ev, c->last_stream));
+        HIPC(c, hipStreamWaitEvent(st, c->order_ev, 0));
+    }
+    c->last_stream = st;
+    c->has_stream = true;
+    return NDA_OK;
+}
 
 // Host-to-device upload of n bytes on stream st, returning without waiting
 // for the stream. A copy from pageable memory blocks the caller until the
@@ -330,7 +354,10 @@ int grow_buf(nda_ctx *c, T *&buf, size_t &cap, size_t need, size_t n_alloc)
     if (!nb)
         return fail(c, NDA_ERR_NOMEM, "device allocation of %zu bytes failed", n_alloc * sizeof(T));
     if (buf) {
-        (void)hipDeviceSynchronize();
+        if (hipError_t e = hipDeviceSynchronize(); e != hipSuccess) {
+            dev_free(nb);
+            return hip_fail(c, e, "hipDeviceSynchronize (buffer growth)");
+        }
         dev_free(buf);
         c->dev_bytes -= cap * sizeof(T);
     }
@@ -438,10 +465,10 @@ void hist_queue(nda_ctx *c, float *dst, const float *src)
         return;
     c->hist_pending.push_back({dst, src});
     // A context that never runs the front again would only grow the queue:
-    // past this length it is applied on the null stream, which is ordered
-    // after the work already queued on the context's (blocking) stream.
+    // past this length it is applied on the stream of the context's last
+    // call (stream order then covers it).
     if (c->hist_pending.size() >= (1u << 16))
-        (void)hist_flush(c, nullptr);
+        (void)hist_flush(c, c->has_stream ? c->last_stream : nullptr);
 }
 
 int hist_flush(nda_ctx *c, hipStream_t st)
@@ -587,10 +614,6 @@ bool mfma_decode(const nda_ctx *c, const AttnArgs &a)
            (uint64_t)a.rows * c->cfg.n_kv_heads >= MFMA_DECODE_MIN_ITEMS;
 }
 
-// part: split-KV partials of at least rows * nh * max_chunks * (v_hd + 2)
-// floats, or null for the context's own buffer (grown on demand). prof: record
-// profiling events (nda_decode_noalloc records none: creating an event may
-// allocate).
 // Device buffers an attention launch over `rows` rows needs: the row staging
 // (staged: ids or per-row offsets are uploaded) and, for rows split into
 // chunks (which the VALU kernel serves), the partials. Taken before a call
@@ -643,8 +666,11 @@ static const uint32_t *decode_order(nda_ctx *c, uint32_t rows, hipStream_t st)
     return c->d_order;
 }
 
-// ordered: the GQA decode may take the rows longest first (it then builds
-// or reuses the context's order buffer; nda_decode_noalloc does not)
+// part: split-KV partials of at least rows * nh * max_chunks * (v_hd + 2)
+// floats, or null for the context's own buffer (grown on demand). prof: record
+// profiling events (nda_decode_noalloc records none: creating an event may
+// allocate). ordered: the GQA decode may take the rows longest first (it then
+// builds or reuses the context's order buffer; nda_decode_noalloc does not).
 int run_attend(nda_ctx *c, AttnArgs &a, hipStream_t st, float *part = nullptr, bool prof = true,
                bool ordered = true)
 {
@@ -794,6 +820,11 @@ int nda_create(const nda_config *cfg_in, nda_ctx **out)
         return NDA_ERR_NOMEM;
     }
     c->dev_bytes += pt * 4 + ppt * 4 + (size_t)cfg.max_seqs * sizeof(SeqDev);
+    if (hipEventCreateWithFlags(&c->order_ev, hipEventDisableTiming) != hipSuccess) {
+        c->order_ev = nullptr;
+        nda_destroy(c);
+        return NDA_ERR_HIP;
+    }
     // the pinned upload ring and its events; without them uploads copy from
     // pageable memory (correct, but the host then waits for the stream)
     if (hipHostMalloc((void **)&c->h_ring, UPLOAD_RING_BYTES, hipHostMallocDefault) == hipSuccess) {
@@ -845,6 +876,8 @@ void nda_destroy(nda_ctx *c)
         (void)hipEventDestroy(c->ring_live[(c->live_head + i) % UPLOAD_EVENTS].ev);
     for (auto e : c->ring_ev)
         (void)hipEventDestroy(e);
+    if (c->order_ev)
+        (void)hipEventDestroy(c->order_ev);
     if (c->h_ring)
         (void)hipHostFree(c->h_ring);
     void *bufs[] = {c->pool, c->d_pages, c->d_prefix_pages, c->d_seqs, c->d_rows, c->d_part,
@@ -959,6 +992,8 @@ int nda_advance(nda_ctx *c, uint32_t nseq, const uint32_t *ids, uint32_t n, void
     // Same increment on the device copy, in stream order, so steady-state
     // decoding uploads nothing.
     hipStream_t st = (hipStream_t)stream;
+    if (int rc = on_stream(c, st))
+        return rc;
     const uint32_t *d_seq, *d_t;
     if (int rc = upload_rows(c, nseq, ids, nullptr, st, &d_seq, &d_t))
         return rc;
@@ -975,6 +1010,8 @@ int nda_prefix_build(nda_ctx *c, uint32_t seq, int32_t *prefix_id, void *stream)
     if (int rc = check_seq(c, seq))
         return rc;
     hipStream_t st = (hipStream_t)stream;
+    if (int rc = on_stream(c, st))
+        return rc;
     SeqHost &s = c->seqs[seq];
     const uint32_t len = s.pos;
     if (len == 0)
@@ -1057,6 +1094,8 @@ int nda_seq_attach(nda_ctx *c, uint32_t seq, int32_t id, void *stream)
     if (id < 0 || (uint32_t)id >= c->cfg.max_prefixes || !c->prefixes[id].used)
         return fail(c, NDA_ERR_ARG, "prefix %d does not exist", id);
     hipStream_t st = (hipStream_t)stream;
+    if (int rc = on_stream(c, st))
+        return rc;
     SeqHost &s = c->seqs[seq];
     const Prefix &pf = c->prefixes[id];
     {
@@ -1159,6 +1198,8 @@ int nda_kv_append(nda_ctx *c, uint32_t layer, uint32_t nseq, const uint32_t *ids
     if (int rc = check_ids(c, nseq, ids))
         return rc;
     hipStream_t st = (hipStream_t)stream;
+    if (int rc = on_stream(c, st))
+        return rc;
     if (ids)
         if (int rc = ensure_rows(c, nseq))
             return rc;
@@ -1237,13 +1278,18 @@ static int decode_check(nda_ctx *c, uint32_t layer, uint32_t nseq, const uint32_
 // for every sequence. Taken for batches of at least 4 (row,
 // kv-head) units per CU of a shape the prefill kernel is built for and the
 // MFMA GQA decode does not serve, with a prefix of at least one full key
-// tile, and not when the append is fused into the launch.
+// tile, and not when the append is fused into the launch. Rows longer than
+// PREFIX_PASS_MAX_CHUNKS prefix lengths keep the single VALU pass: their own
+// positions would be cut into many short work items (a prefix's length
+// each), with partials and a merge, where the prefix is a small part of
+// what they read.
 struct PrefixSplit {
     bool on = false;
     int32_t prefix = -1;
     uint32_t n_sh = 0, max_chunks = 0, n_items = 0;
 };
 constexpr int PREFIX_PASS_WAVES = 2;    // 64-row work-groups: more of them to spread over the CUs
+constexpr uint32_t PREFIX_PASS_MAX_CHUNKS = 4;
 
 // whether a batch's sequences qualify (append not fused; see above)
 static bool prefix_split_batch(const nda_ctx *c, uint32_t nseq, const uint32_t *ids, int32_t *pfx_out,
@@ -1281,10 +1327,13 @@ static void prefix_split_plan(nda_ctx *c, uint32_t nseq, const uint32_t *ids, bo
     uint32_t nsh;
     if (fused || !prefix_split_batch(c, nseq, ids, &pfx, &nsh) || max_total <= nsh)
         return;
+    const uint32_t chunks = (max_total + nsh - 1) / nsh;
+    if (chunks > PREFIX_PASS_MAX_CHUNKS)
+        return;
     ps.on = true;
     ps.prefix = pfx;
     ps.n_sh = nsh;
-    ps.max_chunks = (max_total + nsh - 1) / nsh;
+    ps.max_chunks = chunks;
     const uint64_t trows = 32u * PREFIX_PASS_WAVES;
     const uint64_t per_head = ((uint64_t)nseq * c->geo.rep + trows - 1) / trows;
     ps.n_items = (uint32_t)((per_head * c->cfg.n_kv_heads + 7) / 8 * 8);
@@ -1336,6 +1385,39 @@ static int prefix_pass(nda_ctx *c, const AttnArgs &a, uint32_t nseq, const uint3
     return NDA_OK;
 }
 
+// The longest visible run and the sum over the listed sequences, at their
+// current positions (valid ids).
+static void decode_totals(const nda_ctx *c, uint32_t nseq, const uint32_t *ids, uint32_t *max_total,
+                          uint64_t *sum_total)
+{
+    *max_total = 0;
+    *sum_total = 0;
+    for (uint32_t b = 0; b < nseq; b++) {
+        const SeqHost &s = c->seqs[sid(ids, b)];
+        const Vis vv = visible(s, s.pos, c->cfg.window);
+        *max_total = std::max(*max_total, vv.n_sh + vv.n_own);
+        *sum_total += vv.n_sh + vv.n_own;
+    }
+}
+
+// The device buffers a decode of these sequences needs (row staging, split
+// partials, the shared-prefix pass's partials and work list), grown before a
+// call changes any state; psp: the shared-prefix pass plan.
+static int decode_reserve(nda_ctx *c, uint32_t nseq, const uint32_t *ids, bool fused, uint32_t max_total,
+                          uint64_t sum_total, PrefixSplit &psp)
+{
+    if (int rc = reserve_attend(c, nseq, ids != nullptr, max_total, sum_total))
+        return rc;
+    prefix_split_plan(c, nseq, ids, fused, max_total, psp);
+    if (psp.on) {
+        if (int rc = ensure_part(c, (size_t)nseq * c->cfg.n_heads * psp.max_chunks * (c->cfg.v_head_dim + 2)))
+            return rc;
+        if (int rc = ensure_pf(c, 8 * (size_t)psp.n_items))
+            return rc;
+    }
+    return NDA_OK;
+}
+
 static int decode_impl(nda_ctx *c, uint32_t layer, uint32_t nseq, const uint32_t *ids, const float *q,
                        const float *k, const float *v, const float *gate, float *out, void *stream)
 {
@@ -1360,16 +1442,9 @@ static int decode_impl(nda_ctx *c, uint32_t layer, uint32_t nseq, const uint32_t
     uint64_t sum_total;
     if (int rc = decode_check(c, layer, nseq, ids, q, out, &max_total, &sum_total))
         return rc;
-    if (int rc = reserve_attend(c, nseq, ids != nullptr, max_total, sum_total))
-        return rc;
     PrefixSplit psp;
-    prefix_split_plan(c, nseq, ids, k != nullptr, max_total, psp);
-    if (psp.on) {
-        if (int rc = ensure_part(c, (size_t)nseq * c->cfg.n_heads * psp.max_chunks * (c->cfg.v_head_dim + 2)))
-            return rc;
-        if (int rc = ensure_pf(c, 8 * (size_t)psp.n_items))
-            return rc;
-    }
+    if (int rc = decode_reserve(c, nseq, ids, k != nullptr, max_total, sum_total, psp))
+        return rc;
     txn.commit();
     if (k)
         for (uint32_t b = 0; b < nseq; b++) {
@@ -1377,6 +1452,8 @@ static int decode_impl(nda_ctx *c, uint32_t layer, uint32_t nseq, const uint32_t
             s.stored_end = std::max(s.stored_end, s.pos + 1);
         }
     hipStream_t st = (hipStream_t)stream;
+    if (int rc = on_stream(c, st))
+        return rc;
     if (int rc = sync_tables(c, st))
         return rc;
     const uint32_t *d_seq, *d_t;
@@ -1420,6 +1497,8 @@ int nda_decode_noalloc(nda_ctx *c, uint32_t layer, uint32_t nseq, const uint32_t
     if (!c->scratch)
         return fail(c, NDA_ERR_STATE, "nda_decode_noalloc: no scratch address for this device");
     hipStream_t st = (hipStream_t)stream;
+    if (int rc = on_stream(c, st))
+        return rc;
     AttnArgs a = attn_args(c, layer, nseq, q, gate, out, max_total, sum_total);
     const uint64_t ids_bytes = ids ? (uint64_t)nseq * sizeof(uint32_t) : 0;
     const uint64_t part_off = (ids_bytes + 255) & ~(uint64_t)255;
@@ -1460,6 +1539,17 @@ int nda_step(nda_ctx *c, uint32_t layer, uint32_t nseq, const uint32_t *ids, con
     uint32_t nsh;
     if (c && (units >= 16ull * (uint64_t)c->cus || (mfma_decode_geo(c) && units >= 4ull * (uint64_t)c->cus) ||
               (check_ids(c, nseq, ids) == NDA_OK && prefix_split_batch(c, nseq, ids, &pfx, &nsh)))) {
+        // The decode's buffers first: once the append has stored this
+        // position, a decode that fails for want of memory would leave the
+        // step half done.
+        if (layer < c->cfg.n_layers && check_ids(c, nseq, ids) == NDA_OK) {
+            uint32_t max_total;
+            uint64_t sum_total;
+            decode_totals(c, nseq, ids, &max_total, &sum_total);
+            PrefixSplit psp;
+            if (int rc = decode_reserve(c, nseq, ids, false, max_total, sum_total, psp))
+                return rc;
+        }
         if (int rc = nda_kv_append(c, layer, nseq, ids, k, v, stream))
             return rc;
         return decode_impl(c, layer, nseq, ids, q, nullptr, nullptr, gate, out, stream);
@@ -1587,6 +1677,8 @@ int nda_prefill(nda_ctx *c, uint32_t layer, uint32_t nseq, const uint32_t *ids, 
     if (int rc = prefill_check(c, nseq, ids, n_tokens))
         return rc;
     hipStream_t st = (hipStream_t)stream;
+    if (int rc = on_stream(c, st))
+        return rc;
     PrefillPlan pl;
     if (int rc = prefill_plan(c, nseq, ids, n_tokens, pl))
         return rc;
@@ -1872,6 +1964,8 @@ int nda_front(nda_ctx *c, uint32_t layer, uint32_t nseq, const uint32_t *ids, co
     if (!aligned16(q) || !aligned16(k) || !aligned16(v) || !aligned16(k_out) || !aligned16(v_out))
         return fail(c, NDA_ERR_ARG, "q/k/v and k_out/v_out must be 16-byte aligned");
     hipStream_t st = (hipStream_t)stream;
+    if (int rc = on_stream(c, st))
+        return rc;
     uint64_t rows = 0;
     bool multi = false;
     for (uint32_t b = 0; b < nseq; b++) {
@@ -1955,6 +2049,8 @@ int nda_attention(nda_ctx *c, uint32_t layer, uint32_t nseq, const uint32_t *ids
     if (!aligned16(q) || !aligned16(k) || !aligned16(v))
         return fail(c, NDA_ERR_ARG, "q/k/v must be 16-byte aligned");
     hipStream_t st = (hipStream_t)stream;
+    if (int rc = on_stream(c, st))
+        return rc;
     // Buffers first (the front's q, the row staging, the decode's partials),
     // then pages: a call that fails for want of memory changes nothing.
     const size_t dq = (size_t)c->cfg.n_heads * c->cfg.qk_head_dim;
@@ -2015,6 +2111,8 @@ int nda_front_hist(nda_ctx *c, uint32_t seq, int snap, float *dst, void *stream)
     if (int rc = check_seq(c, seq))
         return rc;
     hipStream_t st = (hipStream_t)stream;
+    if (int rc = on_stream(c, st))
+        return rc;
     if (int rc = hist_flush(c, st))
         return rc;
     const float *src = snap ? hist_snap(c, seq) : hist_live(c, seq);
@@ -2028,6 +2126,10 @@ int nda_sync(nda_ctx *c, void *stream)
     hipError_t e = hipStreamSynchronize((hipStream_t)stream);
     if (e != hipSuccess)
         return hip_fail(c, e, "hipStreamSynchronize");
+    // the context's work on that stream is done: the next call, on any
+    // stream, waits for nothing (and the stream may be destroyed)
+    if (c && c->has_stream && c->last_stream == (hipStream_t)stream)
+        c->has_stream = false;
     return NDA_OK;
 }
 
@@ -2106,6 +2208,8 @@ static int kv_stage(nda_ctx *c, uint32_t layer, uint32_t seq, uint32_t p0, uint3
     a.stage_v = a.stage_k + kb;
     a.count = count;
     a.pg = c->pg;
+    if (int rc = on_stream(c, nullptr))
+        return rc;
     if (int rc = sync_tables(c, nullptr))
         return rc;
     HIPC(c, hipMemcpy((void *)a.pages_for_slot, pg.data(), count * 4, hipMemcpyHostToDevice));
@@ -2158,6 +2262,8 @@ int nda_kv_fill_normal(nda_ctx *c, uint32_t nseq, const uint32_t *ids, uint64_t 
     if (int rc = check_ids(c, nseq, ids))
         return rc;
     hipStream_t st = (hipStream_t)stream;
+    if (int rc = on_stream(c, st))
+        return rc;
     if (ids)
         if (int rc = ensure_rows(c, nseq))
             return rc;
@@ -2523,6 +2629,8 @@ int nda_attention_block(nda_ctx *c, uint32_t layer, uint32_t nseq, const uint32_
     if (!x || !out || !aligned16(x) || !aligned16(out))
         return fail(c, NDA_ERR_ARG, "x / out null or not 16-byte aligned");
     hipStream_t st = (hipStream_t)stream;
+    if (int rc = on_stream(c, st))
+        return rc;
     const auto &w = c->blk[layer];
     const nda_config &g = c->cfg;
     // scratch parts, each a multiple of 4 floats (16-byte aligned): the two
@@ -2580,6 +2688,8 @@ int nda_prefill_block(nda_ctx *c, uint32_t layer, uint32_t nseq, const uint32_t 
     if (rows == 0)
         return NDA_OK;
     hipStream_t st = (hipStream_t)stream;
+    if (int rc = on_stream(c, st))
+        return rc;
     const auto &w = c->blk[layer];
     const nda_config &g = c->cfg;
     // scratch parts as in nda_attention_block, plus the front's outputs

@@ -16,7 +16,14 @@
  *     seq_ids and n_tokens are HOST arrays (NULL seq_ids = sequences 0..nseq-1);
  *   - stream is a hipStream_t passed as void* (NULL = the default stream);
  *   - a context is used by one host thread at a time; calls on it are serial.
- *     Kernels launched by one call write disjoint (sequence, head) outputs.
+ *     Kernels launched by one call write disjoint (sequence, head) outputs;
+ *   - calls on one context are ordered as if they ran on one stream (the
+ *     engine's single-threaded contract, engine/include/nd_quant.h:221-228):
+ *     a call on a stream other than the previous call's first makes its
+ *     stream wait for the work queued on the previous one, so that stream
+ *     must still exist then (nda_sync on it releases that). The inspection
+ *     calls (nda_kv_read / nda_kv_write) run on the null stream the same way.
+ *     Contexts do not order each other.
  */
 #ifndef NDA_H
 #define NDA_H
@@ -149,8 +156,12 @@ int nda_decode(nda_ctx *ctx, uint32_t layer, uint32_t nseq, const uint32_t *seq_
 
 /* nda_decode that allocates nothing: no counterpart in the reference. For
  * callers that must not allocate device memory (tight serving loops,
- * harnesses that forbid hipMalloc). Same arguments, kernels and results as
- * nda_decode; the sequence ids and the split-KV partials (long rows cut into
+ * harnesses that forbid hipMalloc). Same arguments as nda_decode, and the
+ * same results within fp32 rounding: the same kernels, except that it never
+ * takes the shared-prefix decode pass (a batch on one shared prefix is then
+ * attended row by row) or the longest-first row order of the GQA decode,
+ * whose work buffers the context grows. The sequence ids and the split-KV
+ * partials (long rows cut into
  * chunks merged by log-sum-exp) live in one static device array of
  * NDA_NOALLOC_SCRATCH_BYTES per GPU, held until the process ends, instead of
  * context buffers grown by hipMalloc. A call whose ids (4 bytes each, after

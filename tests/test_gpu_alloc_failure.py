@@ -8,7 +8,6 @@ host; every kernel that runs still gets valid memory. After each refused call
 the test checks that positions and device bytes are as before, that the page
 pool lost nothing (it is filled to its last page afterwards), and that the
 same call then succeeds with outputs matching the oracle."""
-import ctypes as C
 import sys
 
 import numpy as np
@@ -30,50 +29,6 @@ def nda():
 def say(*a):
     print("[gpu-case]", *a, flush=True)
     sys.stdout.flush()
-
-
-ALLOC = C.CFUNCTYPE(C.c_void_p, C.c_size_t, C.c_void_p)
-FREE = C.CFUNCTYPE(None, C.c_void_p, C.c_void_p)
-
-
-class FailingAllocator:
-    """hipMalloc / hipFree; refuses every request while `armed`, or only the
-    n-th request counted from `refuse_nth` being set."""
-
-    def __init__(self):
-        self.hip = C.CDLL("libamdhip64.so")
-        self.hip.hipMalloc.argtypes = [C.POINTER(C.c_void_p), C.c_size_t]
-        self.hip.hipMalloc.restype = C.c_int
-        self.hip.hipFree.argtypes = [C.c_void_p]
-        self.hip.hipFree.restype = C.c_int
-        self.armed = False
-        self.refuse_nth = 0
-        self.seen = 0
-        self.refused = 0
-        self._alloc = ALLOC(self.alloc)
-        self._free = FREE(self.free)
-
-    def alloc(self, nbytes, user):
-        self.seen += 1
-        if self.armed or (self.refuse_nth and self.seen == self.refuse_nth):
-            self.refused += 1
-            return None
-        p = C.c_void_p()
-        return p.value if self.hip.hipMalloc(C.byref(p), nbytes) == 0 else None
-
-    def free(self, ptr, user):
-        self.hip.hipFree(ptr)
-
-
-@pytest.fixture
-def allocator():
-    N = nda()
-    a = FailingAllocator()
-    N._check(N.lib().nda_set_allocator(C.cast(a._alloc, C.c_void_p), C.cast(a._free, C.c_void_p), None))
-    yield a
-    a.armed = False
-    a.refuse_nth = 0
-    N._check(N.lib().nda_set_allocator(None, None, None))
 
 
 def _states(ctx, seqs):
@@ -256,4 +211,56 @@ def test_front_init_all_or_nothing(allocator):
     allocator.refuse_nth = 0
     ctx.front_init(3, 10000.0)
     assert ctx.device_bytes > dev_bytes
+    ctx.close()
+
+
+def test_two_launch_step_refused_before_its_append(allocator):
+    """nda_step on a batch whose decode takes the shared-prefix pass (1024
+    sequences on one 213-token prefix) runs the append and the decode as
+    two launches. With the decode's partials refused, the call fails before
+    the append: the position is still unstored, positions and device bytes
+    are as before. Then the same step succeeds and meets the oracle."""
+    N = nda()
+    nh, d, W, B, npre = 8, 64, 384, 1024, 213
+    ctx = N.Context(1, nh, nh, d, d, W, kv_dtype=O.KV_F16, max_seqs=B + 1)
+    bufs = [N.DevBuf(npre * nh * d * 4) for _ in range(4)]
+    for i, bb in enumerate(bufs[:3]):
+        bb.fill_normal(npre * nh * d, 0, 60 + i)
+    ctx.prefill(0, [npre], bufs[0], bufs[1], bufs[2], bufs[3], seq_ids=[B])
+    ctx.advance(1, [B], npre)
+    pid = ctx.prefix_build(B)
+    for b in range(B):
+        ctx.seq_attach(b, pid)
+    ctx.sync()
+    q, k, v, out = (N.DevBuf(B * nh * d * 4) for _ in range(4))
+    for i, bb in enumerate((q, k, v)):
+        bb.fill_normal(B * nh * d, 0, 70 + i)
+    seqs = list(range(B))
+    before, dev_bytes = _states(ctx, seqs), ctx.device_bytes
+    say("shared-prefix step of", B, "sequences, allocations refused")
+    allocator.armed = True
+    with pytest.raises(N.NdaError) as e:
+        ctx.step(0, B, q, k, v, out)
+    allocator.armed = False
+    assert e.value.code == NOMEM and allocator.refused >= 1
+    assert _states(ctx, seqs) == before and ctx.device_bytes == dev_bytes
+    for b in (0, B - 1):
+        with pytest.raises(N.NdaError) as e:
+            ctx.kv_read(0, b, npre, 1)         # the refused step stored nothing
+        assert e.value.code == -4
+    say("the same step with memory")
+    ctx.step(0, B, q, k, v, out)
+    ctx.sync()
+    qh = q.to_array(np.float32, (B, nh * d))
+    got = out.to_array(np.float32, (B, nh * d))
+    worst = 0.0
+    for b in (0, 517, B - 1):
+        kk, vv, _, _ = ctx.kv_read(0, b, 0, npre + 1)
+        view = O.kv_view(kk, vv, None, None, nh, npre + 1, 0, npre, O.KV_F16)
+        worst = max(worst, float(np.abs(got[b] - O.attend_view(view, qh[b])).max()))
+    say("worst", worst)
+    assert worst <= TOL
+    for b in range(B + 1):
+        ctx.seq_reset(b)
+    ctx.prefix_free(pid)
     ctx.close()

@@ -8,9 +8,13 @@ restated, engine/src/nd_model.c:2105-2359, dispatch :2451-2483).
   token through the split-KV attention and its merge, then a 512-token causal
   chunk on top. Every decode row is checked, and every chunk row of the
   32768- and 8192-key sequences.
-- Shared prefix: 1024 sequences attached to one 213-token prefix per layer (2
-  layers), causal suffixes of 32-64 tokens, then 64 decode steps; sampled
-  rows of the prefill and of every decode step are checked.
+- Shared prefix: 1024 sequences attached to one 213-token prefix per layer (8
+  layers, as the workload has), causal suffixes of 32-64 tokens, then 64
+  decode steps; sampled rows of the prefill and of every decode step are
+  checked.
+- The long-context workload at the size the benchmark times (256 sequences),
+  and a short prefix with long own tails (the decode's shared-prefix pass
+  must not be taken).
 
 Bar: max |delta| <= 1e-3 (fp32 accumulate)."""
 import os
@@ -129,7 +133,7 @@ def test_long_context_decode_then_512_token_chunk():
 
 def test_shared_prefix_1024_sequences_64_decode_steps():
     N = nda()
-    nh, d, B, npre, W, LAYERS, STEPS = 8, 64, 1024, 213, 384, 2, 64
+    nh, d, B, npre, W, LAYERS, STEPS = 8, 64, 1024, 213, 384, 8, 64
     rng = np.random.default_rng(4)
     ctx = N.Context(LAYERS, nh, nh, d, d, W, kv_dtype=O.KV_F16, max_seqs=B + 1)
     say("shared prefix: building the 213-token prefix")
@@ -183,7 +187,7 @@ def test_shared_prefix_1024_sequences_64_decode_steps():
             q = dq.to_array(np.float32, (B, nh * d))
             got = dout.to_array(np.float32, (B, nh * d))
             assert np.isfinite(got).all()
-            picks = sorted(int(x) for x in rng.choice(B, 6, replace=False))
+            picks = sorted(int(x) for x in rng.choice(B, 3, replace=False))
             for b in picks:
                 pos = ctx.seq_state(b)[0]
                 worst = max(worst, check(li, b, pos, q[b], None, got[b]))
@@ -194,4 +198,122 @@ def test_shared_prefix_1024_sequences_64_decode_steps():
     for b in range(B):
         ctx.seq_reset(b)
     ctx.prefix_free(pid)
+    ctx.close()
+
+
+def test_short_prefix_long_tails_skip_the_prefix_pass():
+    """1024 sequences on one 40-token prefix, each with 900-1400 positions of
+    its own: rows span more than four prefix lengths, so the decode keeps
+    the single VALU pass (one attention launch, no prefix pass, no merge)
+    instead of cutting every row into prefix-sized chunks. Sampled rows meet
+    the oracle."""
+    N = nda()
+    nh, d, W, B, npre = 8, 64, 1600, 1024, 40
+    rng = np.random.default_rng(6)
+    ctx = N.Context(1, nh, nh, d, d, W, kv_dtype=O.KV_F16, max_seqs=B + 1)
+    bufs = [N.DevBuf(npre * nh * d * 4) for _ in range(4)]
+    for i, bb in enumerate(bufs[:3]):
+        bb.fill_normal(npre * nh * d, 0, 3000 + i)
+    ctx.prefill(0, [npre], bufs[0], bufs[1], bufs[2], bufs[3], seq_ids=[B])
+    ctx.advance(1, [B], npre)
+    pid = ctx.prefix_build(B)
+    own = rng.integers(900, 1401, B)
+    for b in range(B):
+        ctx.seq_attach(b, pid)
+        ctx.seq_set_pos(b, npre + int(own[b]))
+    ctx.kv_fill_normal(B, seed=3100)
+    q, k, v, out = (N.DevBuf(B * nh * d * 4) for _ in range(4))
+    for i, bb in enumerate((q, k, v)):
+        bb.fill_normal(B * nh * d, 0, 3200 + i)
+    ctx.sync()
+    say("short prefix, long own tails: one decode step of", B, "sequences")
+    ctx.prof_enable(True)
+    ctx.prof_read(reset=True)
+    ctx.step(0, B, q, k, v, out)
+    ctx.sync()
+    _, launches = ctx.prof_read(reset=True)
+    ctx.prof_enable(False)
+    assert launches[N.K_DECODE] == 1 and launches[N.K_COMBINE] == 0, launches
+    qh = q.to_array(np.float32, (B, nh * d))
+    got = out.to_array(np.float32, (B, nh * d))
+    worst = 0.0
+    for b in sorted(int(x) for x in rng.choice(B, 8, replace=False)):
+        pos = ctx.seq_state(b)[0]
+        kk, vv, _, _ = ctx.kv_read(0, b, 0, pos + 1)
+        view = O.kv_view(kk, vv, None, None, nh, pos + 1, 0, pos, O.KV_F16)
+        worst = max(worst, maxdiff(got[b], O.attend_view(view, qh[b])))
+    say("worst vs oracle", worst)
+    assert worst <= TOL
+    for b in range(B + 1):
+        ctx.seq_reset(b)
+    ctx.prefix_free(pid)
+    ctx.close()
+
+
+def test_long_context_at_the_benchmarked_geometry():
+    """The long-context workload at the size the benchmark times it: 256
+    sequences with L ~ U[8192, 32768] stored positions (device-filled N(0,1)),
+    a block of 8 K rows with 8-sigma outliers (times 8, exact in fp16) per
+    sequence, one decode token (the split-KV plan of this batch and its merge),
+    then a 512-token causal chunk over every sequence (this batch's prefill
+    work order, longest items first over the eight XCD ranges). Decode rows
+    and three chunk rows of 16 sequences are checked against the oracle."""
+    N = nda()
+    nh, d, CH, B, P = 8, 64, 512, 256, 16
+    rng = np.random.default_rng(7)
+    lens = rng.integers(8192, 32769, B)
+    W = 32768 + CH + 16
+    need = int(sum((int(L) + CH + P) // P for L in lens)) + 64
+    ctx = N.Context(1, nh, nh, d, d, W, kv_dtype=O.KV_F16, max_seqs=B, page_size=P, max_pages=need)
+    for b in range(B):
+        ctx.seq_set_pos(b, int(lens[b]))
+    ctx.kv_fill_normal(B, seed=8100)
+    for b in range(B):
+        p0 = int(rng.integers(0, int(lens[b]) - 8))
+        kf = (rng.standard_normal((8, nh, d)) * 8.0).astype(np.float32)
+        vf = rng.standard_normal((8, nh, d)).astype(np.float32)
+        ctx.kv_write(0, b, p0, f16(kf), f16(vf))
+    sample = sorted(int(x) for x in rng.choice(B, 16, replace=False))
+    say("benchmarked long-context geometry: %d sequences, L %d..%d" % (B, lens.min(), lens.max()))
+    q, k, v, g, out = (N.DevBuf(B * nh * d * 4) for _ in range(5))
+    for i, bb in enumerate((q, k, v, g)):
+        bb.fill_normal(B * nh * d, 0, 8200 + i)
+    ctx.prof_enable(True)
+    ctx.prof_read(reset=True)
+    ctx.step(0, B, q, k, v, out, gate=g)
+    ctx.sync()
+    _, launches = ctx.prof_read(reset=True)
+    ctx.prof_enable(False)
+    assert launches[N.K_COMBINE] > 0, "the decode must split rows and merge them"
+    qh, gh = q.to_array(np.float32, (B, nh * d)), g.to_array(np.float32, (B, nh * d))
+    got = out.to_array(np.float32, (B, nh * d))
+    worst = 0.0
+    for b in sample:
+        L = int(lens[b])
+        kk, vv, _, _ = ctx.kv_read(0, b, 0, L + 1)
+        view = O.kv_view(kk, vv, None, None, nh, L + 1, 0, L, O.KV_F16)
+        worst = max(worst, maxdiff(got[b], O.attend_view(view, qh[b], gh[b])))
+    say("decode, 16 sequences: worst vs oracle", worst)
+    assert worst <= TOL, worst
+    ctx.advance(B, None, 1)
+
+    T = B * CH
+    q, k, v, g, out = (N.DevBuf(T * nh * d * 4) for _ in range(5))
+    for i, bb in enumerate((q, k, v, g)):
+        bb.fill_normal(T * nh * d, 0, 8300 + i)
+    say("512-token chunk on", B, "sequences")
+    ctx.prefill(0, [CH] * B, q, k, v, out, gate=g)
+    ctx.sync()
+    qh, gh = q.to_array(np.float32, (T, nh * d)), g.to_array(np.float32, (T, nh * d))
+    got = out.to_array(np.float32, (T, nh * d))
+    worst = 0.0
+    for b in sample:
+        L = int(lens[b]) + 1
+        kk, vv, _, _ = ctx.kv_read(0, b, 0, L + CH)
+        for t in (0, 255, CH - 1):
+            r = b * CH + t
+            view = O.kv_view(kk, vv, None, None, nh, L + CH, 0, L + t, O.KV_F16)
+            worst = max(worst, maxdiff(got[r], O.attend_view(view, qh[r], gh[r])))
+    say("chunk, 16 sequences x 3 rows: worst vs oracle", worst)
+    assert worst <= TOL, worst
     ctx.close()

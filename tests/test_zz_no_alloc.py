@@ -148,3 +148,85 @@ def test_noalloc_refuses_scratch_overflow():
     (ref, got), _ = _both(N, ctx, 2, [5, 3], q, None, nh)
     assert np.isfinite(ref).all() and np.array_equal(ref, got)
     ctx.close()
+
+
+def test_noalloc_allocates_nothing(allocator):
+    """A fresh context; with every device allocation refused through the
+    allocator seam, nda_decode_noalloc over listed sequences (ids in the
+    scratch) whose rows are split (partials in the scratch) succeeds twice,
+    the second call smaller, and the allocator sees no request at all. The
+    outputs then meet the oracle."""
+    N = nda()
+    nh = 8
+    rng = np.random.default_rng(33)
+    lens = rng.integers(3000, 8193, 48)
+    ctx = _context(N, lens, nh, nh, 64, O.KV_F16, seed=801)
+    calls = [(48, [int(x) for x in rng.permutation(48)]), (12, [int(x) for x in rng.permutation(48)[:12]])]
+    inputs = []
+    for nseq, ids in calls:
+        qh = rng.standard_normal((nseq, nh, 64)).astype(np.float32)
+        inputs.append((qh, N.DevBuf.from_array(qh), N.DevBuf(nseq * nh * 64 * 4)))
+    ctx.sync()
+    say("noalloc with every allocation refused")
+    allocator.seen = 0
+    allocator.armed = True
+    try:
+        for (nseq, ids), (_, q, d) in zip(calls, inputs):
+            ctx.decode_noalloc(0, nseq, q, d, seq_ids=ids)
+        ctx.sync()
+    finally:
+        allocator.armed = False
+    assert allocator.seen == 0, "nda_decode_noalloc asked the allocator for memory"
+    for (nseq, ids), (qh, _, d) in zip(calls, inputs):
+        got = d.to_array(np.float32, (nseq, nh, 64))
+        assert np.isfinite(got).all()
+        w = _oracle_rows(ctx, range(0, nseq, max(1, nseq // 4)), ids, qh, None, got, nh, O.KV_F16)
+        say(nseq, "rows: worst vs oracle", w)
+        assert w <= TOL
+    ctx.close()
+
+
+def test_noalloc_on_a_shared_prefix_batch():
+    """1024 sequences on one 213-token prefix: nda_decode attends the prefix
+    in one pass for the batch, nda_decode_noalloc row by row; the two agree
+    within fp32 reassociation and both meet the oracle."""
+    N = nda()
+    nh, d, W, B, npre = 8, 64, 384, 1024, 213
+    rng = np.random.default_rng(34)
+    ctx = N.Context(1, nh, nh, d, d, W, kv_dtype=O.KV_F16, max_seqs=B + 1)
+    bufs = [N.DevBuf(npre * nh * d * 4) for _ in range(4)]
+    for i, bb in enumerate(bufs[:3]):
+        bb.fill_normal(npre * nh * d, 0, 90 + i)
+    ctx.prefill(0, [npre], bufs[0], bufs[1], bufs[2], bufs[3], seq_ids=[B])
+    ctx.advance(1, [B], npre)
+    pid = ctx.prefix_build(B)
+    n = rng.integers(1, 40, B)
+    for b in range(B):
+        ctx.seq_attach(b, pid)
+    T = int(n.sum())
+    pb = [N.DevBuf(T * nh * d * 4) for _ in range(4)]
+    for i, bb in enumerate(pb[:3]):
+        bb.fill_normal(T * nh * d, 0, 95 + i)
+    ctx.prefill(0, n, pb[0], pb[1], pb[2], pb[3])
+    for b in range(B):
+        ctx.advance(1, [b], int(n[b]))
+    k = N.DevBuf(B * nh * d * 4)
+    k.fill_normal(B * nh * d, 0, 99)
+    ctx.kv_append(0, B, k, k)
+    ctx.sync()
+    qh = rng.standard_normal((B, nh, d)).astype(np.float32)
+    q = N.DevBuf.from_array(qh)
+    say("shared prefix: decode (prefix pass) and decode_noalloc")
+    (ref, got), (lr, lg) = _both(N, ctx, B, None, q, None, nh)
+    assert lr[N.K_DECODE] == 2, "nda_decode must take the shared-prefix pass here"
+    assert np.isfinite(ref).all() and np.isfinite(got).all()
+    diff = float(np.abs(ref - got).max())
+    say("decode vs decode_noalloc", diff)
+    assert diff <= 1e-4
+    w = _oracle_rows(ctx, (0, 311, B - 1), None, qh, None, got, nh, O.KV_F16)
+    say("worst vs oracle", w)
+    assert w <= TOL
+    for b in range(B + 1):
+        ctx.seq_reset(b)
+    ctx.prefix_free(pid)
+    ctx.close()
