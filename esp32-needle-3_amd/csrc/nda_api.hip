@@ -1810,11 +1810,6 @@ int nda_front_init(nda_ctx *c, const nda_front_config *fc)
         return fail(c, NDA_ERR_STATE, "attention front already initialised");
     if (fc->taps < 1 || fc->taps > 8)
         return fail(c, NDA_ERR_ARG, "taps %u outside 1..8", fc->taps);
-    if (!geometry_fast(c->geo))
-        return fail(c, NDA_ERR_UNSUPPORTED,
-                    "attention front: no kernel for qk %d / v %d / rep %d (the front is built for 64/64 with rep "
-                    "1, 2, 4, 6, 8 and 48/64 with rep 1, 2, 6)",
-                    c->geo.dk, c->geo.dv, c->geo.rep);
     if (!(fc->rope_theta > 0.0f))
         return fail(c, NDA_ERR_ARG, "rope_theta must be positive");
     const nda_config &g = c->cfg;

@@ -212,6 +212,126 @@ __global__ __launch_bounds__((64 * FrontShape<DK, DV, REP>::W)) void front_kerne
     store_row<ES>(hb, slot & (P - 1), P, kx, vx, tid, DK, DV);
 }
 
+// The same front for every other shape the engine defines (head dims that are
+// multiples of 4 up to 64, 1-8 query heads per kv-head), the dims read at run
+// time: one 256-thread work-group per (row, kv group), at most 8 * 64 + 64
+// + 64 = 640 columns in 160 four-column groups. Same steps and the same order of
+// every rounding as front_kernel, so the rows are bit-identical to the
+// engine's too.
+template <int ES>
+__global__ __launch_bounds__(256) void front_rt_kernel(FrontArgs a)
+{
+#pragma clang fp contract(off)
+    constexpr int MAXH = 9, MAXD = 64, STRIDE = MAXD + 4, NT = 256;
+    __shared__ __align__(16) float ylds[MAXH * STRIDE];
+    __shared__ __align__(16) float sqlds[MAXH * STRIDE];
+    __shared__ __align__(16) float vlds[MAXD];
+    __shared__ float invlds[MAXH];
+
+    const int DK = (int)a.qk, DV = (int)a.vd, nkv = (int)a.nkv, REP = (int)(a.nh / a.nkv);
+    const int NC = REP * DK + DK + DV, NG = NC / 4, NH = REP + 1, HALF = DK / 2;
+    const uint32_t row = blockIdx.x / nkv, g = blockIdx.x % nkv;
+    const int tid = threadIdx.x;
+    const uint32_t seq = a.row_seq ? a.row_seq[row] : row;
+    const uint32_t t = a.row_t ? a.row_t[row] : 0u;
+    const SeqDev sd = a.seqs[seq];
+    const uint32_t pos = (uint32_t)sd.pos + t;
+    const uint32_t taps = a.taps;
+    const uint32_t nt = min(taps, pos + 1u);
+    const uint32_t dq = nkv * REP * DK, dk = nkv * DK, dv = nkv * DV, dcol = dq + dk + dv;
+    float *hist = a.hist + ((uint64_t)seq * a.n_layers + a.layer) * taps * dcol;
+    const bool store = a.k_out == nullptr;
+
+    // 1. tap convolution of this thread's four columns (taps in order)
+    const int lc = tid * 4;                      // column within the group
+    if (tid < NG) {
+        const float *src;
+        uint32_t ld, cc, gc;                     // source row length, column in it, column in dcol
+        if (lc < REP * DK) {
+            src = a.q; ld = dq; cc = g * REP * DK + lc; gc = cc;
+        } else if (lc < REP * DK + DK) {
+            src = a.k; ld = dk; cc = g * DK + (lc - REP * DK); gc = dq + cc;
+        } else {
+            src = a.v; ld = dv; cc = g * DV + (lc - REP * DK - DK); gc = dq + dk + cc;
+        }
+        const float4 raw = ld4(src + (uint64_t)row * ld + cc);
+        float4 acc = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+        for (uint32_t j = 0; j < nt; j++) {
+            const float4 wj = ld4(a.w + (uint64_t)j * dcol + gc);
+            const float4 xj = j == 0 ? raw
+                              : j <= t ? ld4(src + (uint64_t)(row - j) * ld + cc)
+                                       : ld4(hist + (uint64_t)((pos - j) % taps) * dcol + gc);
+            acc4(acc, wj, xj);
+        }
+        if (a.hist_write)
+            *reinterpret_cast<float4 *>(hist + (uint64_t)(pos % taps) * dcol + gc) = raw;
+        if (lc < (REP + 1) * DK) {
+            const int o = (lc / DK) * STRIDE + lc % DK;
+            *reinterpret_cast<float4 *>(ylds + o) = acc;
+            *reinterpret_cast<float4 *>(sqlds + o) =
+                make_float4(acc.x * acc.x, acc.y * acc.y, acc.z * acc.z, acc.w * acc.w);
+        } else if (store) {
+            *reinterpret_cast<float4 *>(vlds + (lc - (REP + 1) * DK)) = acc;
+        } else {
+            *reinterpret_cast<float4 *>(a.v_out + (uint64_t)row * dv + cc) = acc;
+        }
+    }
+    __syncthreads();
+
+    // 2. per-head sum of squares in index order, inverse RMS
+    if (tid < NH) {
+        const float *r = sqlds + tid * STRIDE;
+        float ss = 0.0f;
+        for (int i = 0; i < DK; i++)
+            ss = ss + r[i];
+        invlds[tid] = 1.0f / __builtin_sqrtf(ss / (float)DK + 1e-6f);
+    }
+    __syncthreads();
+
+    // 3. (1 + s) * x * inv, rotated by the position's (cos, sin)
+    const float2 *rope = a.rope + (uint64_t)pos * HALF;
+    for (int e = tid; e < NH * HALF; e += NT) {
+        const int h = e / HALF, i = e % HALF;
+        const bool is_q = h < REP;
+        const float *sn = a.norm + (is_q ? 0 : DK);
+        float *r = ylds + h * STRIDE;
+        const float iv = invlds[h];
+        const float x1 = (1.0f + sn[i]) * r[i] * iv;
+        const float x2 = (1.0f + sn[i + HALF]) * r[i + HALF] * iv;
+        const float2 cs = rope[i];
+        const float o1 = x1 * cs.x - x2 * cs.y;
+        const float o2 = x2 * cs.x + x1 * cs.y;
+        if (is_q) {
+            float *qo = a.q_out + (uint64_t)row * dq + (g * REP + h) * DK;
+            qo[i] = o1;
+            qo[i + HALF] = o2;
+        } else if (store) {
+            r[i] = o1;
+            r[i + HALF] = o2;
+        } else {
+            float *ko = a.k_out + (uint64_t)row * dk + g * DK;
+            ko[i] = o1;
+            ko[i + HALF] = o2;
+        }
+    }
+    if (!store)
+        return;
+    __syncthreads();
+
+    // 4. store this position's k/v rows of kv-head g (wave 0, lane = element)
+    if (tid >= 64)
+        return;
+    const int slot = own_slot(sd, (int)pos, (int)a.pg.window);
+    const int32_t page = a.page_table[(uint64_t)seq * a.pg.pages_per_seq + (slot >> a.pg.log2_page)];
+    if (page < 0)
+        return;   // the host backs every stored slot; never taken
+    const int P = 1 << a.pg.log2_page;
+    uint8_t *hb = a.pool + (uint64_t)page * a.pg.page_bytes + (uint64_t)g * a.pg.head_bytes;
+    const float kx = tid < DK ? ylds[REP * STRIDE + tid] : 0.0f;
+    const float vx = tid < DV ? vlds[tid] : 0.0f;
+    store_row<ES>(hb, slot & (P - 1), P, kx, vx, tid, DK, DV);
+}
+
 // Raw rows of each sequence's last `taps` tokens into their history slots,
 // after a multi-token front launch has read the old history.
 __global__ __launch_bounds__(256) void hist_tail_kernel(HistTailArgs a)
@@ -260,7 +380,13 @@ hipError_t launch_front(const Geo &g, const FrontArgs &a, hipStream_t s)
     }
     NDA_FOR_GEOMETRIES(X)
 #undef X
-    return hipErrorNotSupported;
+    if (!geometry_supported(g))
+        return hipErrorNotSupported;
+    if (g.kv_f16)
+        hipLaunchKernelGGL((front_rt_kernel<2>), grid, dim3(256), 0, s, a);
+    else
+        hipLaunchKernelGGL((front_rt_kernel<1>), grid, dim3(256), 0, s, a);
+    return hipGetLastError();
 }
 
 hipError_t launch_hist_tail(const HistTailArgs &a, hipStream_t s)

@@ -41,8 +41,8 @@ extern "C" {
 #define NDA_ERR_HIP         -3   /* a HIP runtime call failed */
 #define NDA_ERR_RANGE       -4   /* position / length outside what the window holds */
 #define NDA_ERR_STATE       -5   /* call not valid in the sequence's current state */
-#define NDA_ERR_UNSUPPORTED -6   /* a shape the engine does not define, or the front / block
-                                    calls for a shape they are not built for */
+#define NDA_ERR_UNSUPPORTED -6   /* a shape the engine does not define, or a CQ tensor form
+                                    (bits, group, width) the call does not take */
 #define NDA_ERR_NODEV       -7   /* no usable gfx950 device */
 
 /* KV element types. INT8: symmetric int8 codes + fp32 scale per (slot,
@@ -215,10 +215,9 @@ typedef struct {
 
 /* Allocates the tap histories and the rotary table (cos/sin of
  * pos * theta^(-2i/qk_head_dim), as nd_model_open :1233-1236 and
- * nd_model_step_hidden :2949-2954 compute them). Once per context. The front
- * (and with it the attention block calls) is built for qk/v 64/64 with 1, 2,
- * 4, 6 or 8 query heads per kv-head and 48/64 with 1, 2 or 6; other shapes
- * return NDA_ERR_UNSUPPORTED. */
+ * nd_model_step_hidden :2949-2954 compute them). Once per context. Every
+ * shape the context accepts has a front (qk/v 64/64 and 48/64 on kernels
+ * specialised for them, the others with their dims read at run time). */
 int nda_front_init(nda_ctx *ctx, const nda_front_config *fc);
 /* One layer's weights from HOST arrays, the engine's staged fp32 slots
  * (fp16_slot[li][4..8]): tap_q [taps][n_heads*qk_head_dim],

@@ -2,7 +2,10 @@
 shim's nd_gpu_attention_raw) against the oracle: the front's q/k/v rows and
 the tap histories bit-exact, stored int8 codes and scales bit-exact,
 attention outputs within max |delta| <= 1e-3; and the engine session replay
-against the reference engine's own golden outputs."""
+against the reference engine's own golden outputs. The shapes include odd
+ones (qk 36 / v 20, 7 query heads on one kv-head, qk 16 / v 8) that run on
+the front kernel with run-time dims; the oracle's front is pinned bit-exact
+to the reference at those shapes in tests/test_oracle_front.py."""
 import os
 import sys
 
@@ -64,6 +67,13 @@ def oracle_sessions(nseq, geom, kv_dtype, taps, theta):
     ((12, 2, 48, 64), O.KV_INT8, 3, 10000.0),     # the archive's shapes
     ((8, 2, 64, 64), O.KV_INT8, 4, 1000000.0),
     ((16, 2, 64, 64), O.KV_F16, 1, 500000.0),
+    # shapes on the kernel with run-time dims
+    ((10, 2, 36, 20), O.KV_INT8, 3, 10000.0),
+    ((7, 1, 64, 64), O.KV_F16, 2, 10000.0),
+    ((8, 1, 20, 44), O.KV_INT8, 4, 1000000.0),
+    ((4, 4, 16, 8), O.KV_F16, 1, 10000.0),
+    ((16, 4, 64, 32), O.KV_INT8, 3, 10000.0),
+    ((3, 1, 48, 64), O.KV_INT8, 3, 10000.0),
 ])
 def test_front_rows_bit_exact(shape, kv_dtype, taps, theta):
     """nda_front, one token per sequence per call, sequences at different
@@ -110,15 +120,17 @@ def test_front_rows_bit_exact(shape, kv_dtype, taps, theta):
         assert np.array_equal(bits(ctx.front_hist(b)), bits(want)), b
 
 
-@pytest.mark.parametrize("kv_dtype", [O.KV_F16, O.KV_INT8])
-def test_front_multi_token_chunk(kv_dtype):
+@pytest.mark.parametrize("shape,kv_dtype", [((12, 2, 48, 64), O.KV_F16), ((12, 2, 48, 64), O.KV_INT8),
+                                             ((10, 2, 36, 20), O.KV_INT8), ((7, 1, 64, 64), O.KV_F16)])
+def test_front_multi_token_chunk(shape, kv_dtype):
     """nda_front over chunks of several tokens per sequence (a prefill chunk's
     front) equals the token-by-token oracle, including the history left for
     the next single-token call."""
     N = nda()
-    say("front multi-token chunk", kv_dtype)
+    say("front multi-token chunk", shape, kv_dtype)
     rng = np.random.default_rng(5)
-    nh, nkv, qk, vd, L, W, taps, theta = 12, 2, 48, 64, 1, 256, 3, 10000.0
+    nh, nkv, qk, vd = shape
+    L, W, taps, theta = 1, 256, 3, 10000.0
     n_tok = [5, 1, 9, 0, 3, 2]
     starts = [0, 4, 1, 8, 20, 0]
     B = len(n_tok)
@@ -158,16 +170,18 @@ def test_front_multi_token_chunk(kv_dtype):
             assert np.array_equal(bits(ctx.front_hist(b)), bits(want)), (rnd, b)
 
 
-@pytest.mark.parametrize("kv_dtype", [O.KV_INT8, O.KV_F16])
-def test_attention_batched_sessions(kv_dtype):
+@pytest.mark.parametrize("shape,kv_dtype", [((8, 2, 64, 64), O.KV_INT8), ((8, 2, 64, 64), O.KV_F16),
+                                             ((10, 2, 36, 20), O.KV_INT8), ((7, 1, 64, 64), O.KV_F16)])
+def test_attention_batched_sessions(shape, kv_dtype):
     """nda_attention (front + store + decode) over a batch of sequences for
     many steps: outputs within tolerance of the oracle's engine step, stored
     codes / fp16 rows bit-exact; then a snapshot of one sequence shared by the
     others (prefix build + attach), decoding on, a rewind and a reset."""
     N = nda()
-    say("attention batched", kv_dtype)
+    say("attention batched", shape, kv_dtype)
     rng = np.random.default_rng(9)
-    nh, nkv, qk, vd, L, W, taps, theta = 8, 2, 64, 64, 2, 96, 3, 10000.0
+    nh, nkv, qk, vd = shape
+    L, W, taps, theta = 2, 96, 3, 10000.0
     B = 4
     geom = (L, nh, nkv, qk, vd, W)
     fw = make_weights(rng, L, nh, nkv, qk, vd, taps)

@@ -223,7 +223,5 @@ def test_undefined_shapes_refused():
             N.Context(1, nh, nkv, qk, vd, 64)
         assert e.value.code in (-1, -6), (nh, nkv, qk, vd, e.value.code)
     ctx = N.Context(1, 10, 2, 36, 20, 64)
-    with pytest.raises(N.NdaError) as e:
-        ctx.front_init(3, 10000.0)
-    assert e.value.code == -6
+    ctx.front_init(3, 10000.0)                 # every defined shape has a front
     ctx.close()

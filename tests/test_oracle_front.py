@@ -38,6 +38,10 @@ def weights(seed, L, nh, nkv, qk, vd, taps):
     ((1, 8, 2, 64, 64, 64), 2, 500000.0),     # GQA 4
     ((1, 16, 2, 64, 64, 64), 4, 1000000.0),   # GQA 8, 4 taps
     ((1, 6, 3, 48, 64, 64), 5, 10000.0),
+    ((1, 10, 2, 36, 20, 64), 3, 10000.0),    # odd dims: qk 36 (9 rotary pairs per half)
+    ((1, 7, 1, 64, 64, 64), 2, 10000.0),     # 7 query heads on one kv-head
+    ((1, 8, 1, 20, 44, 64), 4, 1000000.0),
+    ((1, 4, 4, 16, 8, 64), 1, 10000.0),
 ])
 def test_front_matches_reference(geom, taps, theta):
     L, nh, nkv, qk, vd, W = geom
