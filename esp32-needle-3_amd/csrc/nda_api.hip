@@ -2490,6 +2490,47 @@ int nda_cq_gemm(const nda_cq *t, uint32_t rows, const float *xh, float *y, void 
 }
 
 static bool cq_split_ok(const nda_cq *t) { return t->bits == 2 && t->group >= 32; }
+static bool cq_lut2_ok(const nda_cq *t) { return t->bits == 2 && t->in_pad <= (uint32_t)CQ_LUT_MAX_IN; }
+
+int nda_cq_gemv_lut2(const nda_cq *const *ts, uint32_t n, uint32_t rows, const float *xh, float *const *ys,
+                     void *stream)
+{
+    if (!ts || !ys || n == 0 || n > (uint32_t)CQ_MAX_T || (rows && !xh) || ((uintptr_t)xh & 15))
+        return NDA_ERR_ARG;
+    const nda_cq *t0 = ts[0];
+    if (!t0)
+        return NDA_ERR_ARG;
+    if (rows > 65535)
+        return NDA_ERR_UNSUPPORTED;
+    CqGemmArgs a{};
+    a.xh = xh;
+    a.rows = rows;
+    a.in_pad = t0->in_pad;
+    a.group = t0->group;
+    a.ngroup = t0->ngroup;
+    a.bits = t0->bits;
+    a.rowbytes = t0->rowbytes;
+    a.nt = n;
+    uint32_t tiles = 0;
+    for (uint32_t i = 0; i < n; i++) {
+        const nda_cq *t = ts[i];
+        if (!t || (rows && !ys[i]))
+            return NDA_ERR_ARG;
+        if (t->in != t0->in || t->group != t0->group || t->bits != t0->bits)
+            return NDA_ERR_ARG;     // one prepared activation serves them all
+        if (!cq_lut2_ok(t))
+            return NDA_ERR_UNSUPPORTED;
+        a.y[i] = ys[i];
+        a.packed[i] = t->packed;
+        a.norms[i] = t->norms;
+        a.cb[i] = t->cb;
+        a.out[i] = t->out;
+        a.tile0[i] = tiles;
+        tiles += (t->out + CQ_LUT_OT - 1) / CQ_LUT_OT;
+    }
+    a.tile0[n] = tiles;
+    return launch_cq_lut2(a, (hipStream_t)stream) == hipSuccess ? NDA_OK : NDA_ERR_HIP;
+}
 
 // rows rounded up to a block of 32: operand blocks (4 bytes per element), then the exponents
 static size_t split_rows(uint32_t rows) { return ((size_t)rows + 31) & ~(size_t)31; }
@@ -2565,14 +2606,25 @@ int nda_cq_gemm_split(const nda_cq *t, uint32_t rows, const void *xs, float *y, 
 }
 
 // n tensors sharing one input (q/k/v/gate, or out_proj alone) for the block
-// paths: the split-precision kernels where every tensor allows them, the
-// fp32 ones otherwise. xs holds nda_cq_split_bytes(ts[0], rows).
+// paths: the engine's own LUT order for up to CQ_LUT_ROWS rows (bit-identical
+// projections, so the front and the int8 store see the engine's values), the
+// split-precision GEMM above that where every tensor allows it, the fp32 GEMM
+// otherwise. xs holds nda_cq_split_bytes(ts[0], rows), at least the fp32
+// prepared form's rows * in_pad floats.
+constexpr uint32_t CQ_LUT_ROWS = 64;
 static int cq_project(const nda_cq *const *ts, uint32_t n, uint32_t rows, const float *x, void *xs,
                       float *const *ys, hipStream_t st)
 {
-    bool split = true;
-    for (uint32_t i = 0; i < n; i++)
+    bool split = true, lut = rows <= CQ_LUT_ROWS;
+    for (uint32_t i = 0; i < n; i++) {
         split = split && cq_split_ok(ts[i]);
+        lut = lut && cq_lut2_ok(ts[i]);
+    }
+    if (lut) {
+        if (int rc = nda_cq_prepare(ts[0], rows, x, (float *)xs, st))
+            return rc;
+        return nda_cq_gemv_lut2(ts, n, rows, (const float *)xs, ys, st);
+    }
     if (split) {
         if (int rc = nda_cq_prepare_split(ts[0], rows, x, xs, st))
             return rc;

@@ -13,6 +13,8 @@
 //                       fw_scale, :36-65, :99-116), so xh is bit-identical
 //   cq_gemm_kernel      y[r][o] = sum_k cb[idx[o][k]] * norm[o][k/group] *
 //                       xh[r][k] over all rows r of the batch
+//   cq_lut2_kernel      the same for 2-bit tensors and a few rows, summed in
+//                       the engine's own order (bit-identical y)
 //
 // The engine runs one row against the weights (a GEMV that streams the
 // compressed weights); a batch of rows makes it a GEMM in which every weight
@@ -763,6 +765,75 @@ void cq_gemm_split_kernel(CqSplitArgs a)
     }
     while (pend)
         drain();
+}
+
+// ------------------------------------------------ the engine's LUT order
+
+// 2-bit matvecs for a few rows (one decode step's tokens) computed the way
+// the engine computes them (nd_cq_lut_build + nd_lut2_rows_c, engine/src/
+// nd_quant.c:75-94, :722-764), so y is bit-identical to the engine's: per
+// row the pair table T[p][i0 + 4 i1] = cb[i0] xh[2p] + cb[i1] xh[2p+1] in
+// LDS; per output the groups in order, each group's 32-bit words in order,
+// nibble k of a word added into accumulator k % 4 from table block k, and
+// acc = acc + norm * ((s0 + s1) + (s2 + s3)). One work-group per
+// (256-output tile, row), one output per thread; every product and sum
+// rounds on its own.
+__global__ __launch_bounds__(256) void cq_lut2_kernel(CqGemmArgs a)
+{
+#pragma clang fp contract(off)
+    extern __shared__ float lut[];   // [in_pad / 2][16]
+    const uint32_t tile = blockIdx.x, row = blockIdx.y;
+    uint32_t t = 0;
+    while (t + 1 < a.nt && tile >= a.tile0[t + 1])
+        t++;
+    const float *xh = a.xh + (uint64_t)row * a.in_pad;
+    const float *cb = a.cb[t];
+    for (uint32_t e = threadIdx.x; e < a.in_pad * 8; e += 256) {
+        const uint32_t p = e >> 4;
+        const float x0 = xh[2 * p], x1 = xh[2 * p + 1];
+        const float lo = cb[e & 3] * x0, hi = cb[(e >> 2) & 3] * x1;
+        lut[e] = lo + hi;
+    }
+    __syncthreads();
+    const uint32_t o = (tile - a.tile0[t]) * CQ_LUT_OT + threadIdx.x;
+    if (o >= a.out[t])
+        return;
+    const uint32_t *q = reinterpret_cast<const uint32_t *>(a.packed[t] + (uint64_t)o * a.rowbytes);
+    const uint16_t *nrm = a.norms[t] + (uint64_t)o * a.ngroup;
+    const uint32_t gw = a.group / 16;          // words per group
+    const float *T = lut;
+    float acc = 0.0f;
+    for (uint32_t gi = 0; gi < a.ngroup; gi++) {
+        const float nf = half_bits_to_float(nrm[gi]);
+        float s0 = 0.0f, s1 = 0.0f, s2 = 0.0f, s3 = 0.0f;
+        for (uint32_t j = 0; j < gw; j++) {
+            const uint32_t w = q[j];
+            s0 = s0 + T[w & 15u];
+            s1 = s1 + T[16 + ((w >> 4) & 15u)];
+            s2 = s2 + T[32 + ((w >> 8) & 15u)];
+            s3 = s3 + T[48 + ((w >> 12) & 15u)];
+            T += 64;
+            s0 = s0 + T[(w >> 16) & 15u];
+            s1 = s1 + T[16 + ((w >> 20) & 15u)];
+            s2 = s2 + T[32 + ((w >> 24) & 15u)];
+            s3 = s3 + T[48 + (w >> 28)];
+            T += 64;
+        }
+        q += gw;
+        acc = acc + nf * ((s0 + s1) + (s2 + s3));
+    }
+    a.y[t][(uint64_t)row * a.out[t] + o] = acc;
+}
+
+hipError_t launch_cq_lut2(const CqGemmArgs &a, hipStream_t s)
+{
+    if (a.rows == 0 || a.nt == 0 || a.tile0[a.nt] == 0)
+        return hipSuccess;
+    if (a.bits != 2 || a.group % 16 || a.in_pad > CQ_LUT_MAX_IN || a.rows > 65535)
+        return hipErrorInvalidValue;
+    hipLaunchKernelGGL(cq_lut2_kernel, dim3(a.tile0[a.nt], a.rows), dim3(256), (size_t)a.in_pad * 8 * sizeof(float),
+                       s, a);
+    return hipGetLastError();
 }
 
 hipError_t launch_cq_split_tables(const CqTabArgs &a, hipStream_t s)

@@ -178,14 +178,17 @@ struct CqPrepArgs {
 };
 
 /* Up to CQ_MAX_T tensors sharing one prepared activation (same in, group,
- * bits) in one launch: grid.y walks their 64-output tiles in order. */
+ * bits) in one launch: the grid walks their output tiles in order (64
+ * outputs per tile in the GEMM, CQ_LUT_OT in the engine-order kernel). */
 constexpr int CQ_MAX_T = 8;
+constexpr int CQ_LUT_OT = 256;        /* engine-order kernel: outputs per work-group */
+constexpr int CQ_LUT_MAX_IN = 2048;   /* its pair table, in_pad * 32 bytes of LDS, within 64 KiB */
 struct CqGemmArgs {
     const float *xh;                    /* [rows][in_pad] prepared activations */
     float *y[CQ_MAX_T];                 /* [rows][out[t]] */
     const uint8_t *packed[CQ_MAX_T];    /* [out][rowbytes] LSB-first index bitstream */
     const uint16_t *norms[CQ_MAX_T];    /* [out][ngroup] fp16 bits */
-    const float *cb[CQ_MAX_T];          /* [1 << bits] codebook (scaled by 1/sqrt(group)) */
+    const float *cb[CQ_MAX_T];          /* [1 << bits] codebook (H's 1/sqrt(group) is in xh) */
     uint32_t out[CQ_MAX_T];
     uint32_t tile0[CQ_MAX_T + 1];       /* first grid.y tile of each tensor; tile0[nt] = total */
     uint32_t nt;
@@ -239,6 +242,7 @@ constexpr int CQ_SPLIT_NT = 64 * CQ_SPLIT_OB;   /* outputs per work-group */
 
 hipError_t launch_cq_prepare(const CqPrepArgs &a, hipStream_t s);
 hipError_t launch_cq_gemm(const CqGemmArgs &a, hipStream_t s);
+hipError_t launch_cq_lut2(const CqGemmArgs &a, hipStream_t s);
 hipError_t launch_cq_prepare_split(const CqPrepSplitArgs &a, hipStream_t s);
 hipError_t launch_cq_gemm_split(const CqSplitArgs &a, hipStream_t s);
 hipError_t launch_cq_split_tables(const CqTabArgs &a, hipStream_t s);

@@ -40,6 +40,7 @@ ABI_SYMBOLS = [
     "nda_front_init", "nda_front_weights", "nda_front", "nda_attention", "nda_front_hist",
     "nda_cq_create", "nda_cq_destroy", "nda_cq_in_pad", "nda_cq_prepare", "nda_cq_gemm", "nda_cq_gemm_many",
     "nda_cq_split_bytes", "nda_cq_prepare_split", "nda_cq_gemm_split", "nda_cq_gemm_split_many",
+    "nda_cq_gemv_lut2",
     "nda_event_create", "nda_event_destroy", "nda_event_record", "nda_event_elapsed",
     "nda_block_weights", "nda_attention_block", "nda_prefill_block",
 ]
@@ -141,6 +142,7 @@ def lib():
             "nda_cq_prepare_split": (C.c_int, [vp, u32, vp, vp, vp]),
             "nda_cq_gemm_split": (C.c_int, [vp, u32, vp, vp, vp]),
             "nda_cq_gemm_split_many": (C.c_int, [vp, u32, u32, vp, vp, vp]),
+            "nda_cq_gemv_lut2": (C.c_int, [vp, u32, u32, vp, vp, vp]),
             "nda_event_create": (C.c_int, [C.POINTER(vp)]),
             "nda_event_destroy": (C.c_int, [vp]),
             "nda_event_record": (C.c_int, [vp, vp]),
@@ -620,6 +622,15 @@ def cq_gemm_split_many(tensors, rows, xs, ys, stream=None):
     th = (vp * n)(*[t.h for t in tensors])
     yp = (vp * n)(*[_dp(y) for y in ys])
     _check(lib().nda_cq_gemm_split_many(th, n, rows, _dp(xs), yp, stream))
+
+
+def cq_gemv_lut2(tensors, rows, xh, ys, stream=None):
+    """The engine's own 2-bit LUT matvec (bit-identical) for tensors sharing
+    a prepared activation (nda_cq_prepare's form): ys[i] = W_i . x."""
+    n = len(tensors)
+    th = (vp * n)(*[t.h for t in tensors])
+    yp = (vp * n)(*[_dp(y) for y in ys])
+    _check(lib().nda_cq_gemv_lut2(th, n, rows, _dp(xh), yp, stream))
 
 
 class ProbeResult(C.Structure):

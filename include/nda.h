@@ -290,12 +290,23 @@ int nda_cq_gemm_many(const nda_cq *const *ts, uint32_t n, uint32_t rows, const f
  * are split the same way, per (row, group), when the tensor is created; the
  * fourth product (lo x lo, 2^-22 relative) is dropped, so the result is
  * within a few 2^-22 of sum |w x| of the engine's. The attention block calls
- * take this path when all five tensors allow it. */
+ * take this path above 64 rows when all five tensors allow it. */
 size_t nda_cq_split_bytes(const nda_cq *t, uint32_t rows);
 int nda_cq_prepare_split(const nda_cq *t, uint32_t rows, const float *x, void *xs, void *stream);
 int nda_cq_gemm_split(const nda_cq *t, uint32_t rows, const void *xs, float *y, void *stream);
 int nda_cq_gemm_split_many(const nda_cq *const *ts, uint32_t n, uint32_t rows, const void *xs,
                            float *const *ys, void *stream);
+/* The engine's own 2-bit matvec, bit for bit: nd_cq_lut_build +
+ * nd_cq_gemv_lut2 (engine/src/nd_quant.c:667-677, :809-821; the table rows
+ * lutb_rows :75-94, the row walk nd_lut2_rows_c :722-764) for each row of xh (nda_cq_prepare's form,
+ * device, 16-byte aligned): y_i = W_i . x into ys[i][rows][out_i] for
+ * n <= 8 tensors sharing in and group, 2-bit, in_pad <= 2048, rows <=
+ * 65535 (otherwise NDA_ERR_UNSUPPORTED). Each output is a serial sum, so
+ * this is the path for a few rows (one token per sequence); the attention
+ * block calls take it for at most 64 rows, where the stored int8 codes then
+ * equal the engine's exactly. */
+int nda_cq_gemv_lut2(const nda_cq *const *ts, uint32_t n, uint32_t rows, const float *xh, float *const *ys,
+                     void *stream);
 
 /* ---- the whole attention block (attention(), engine/src/nd_model.c:2382-2502) ----
  * Register one layer's five CQ tensors (borrowed: they must outlive the

@@ -130,6 +130,76 @@ def test_cq_golden_reference_outputs():
         assert np.all(np.abs(y[0].astype(np.float64) - ref) <= 1e-5 * sc + 1e-6)
 
 
+@pytest.mark.parametrize("shapes,inp,group,rows", [
+    ([576, 96, 128, 768], 768, 128, 5),       # the archive's q/k/v/gate from d_model 768
+    ([768], 576, 128, 3),                     # its out_proj
+    ([360, 72, 40, 200], 256, 128, 64),       # 10 q / 2 kv heads, qk 36, v 20; 64 rows
+    ([256], 200, 128, 2),                     # out_proj over 200 inputs (padded to 256)
+    ([300, 17], 2048, 256, 4),                # the largest table (in_pad 2048)
+    ([33], 100, 16, 9),                       # group 16, padded
+    ([70, 70], 96, 32, 1),
+])
+def test_cq_lut2_bit_exact(shapes, inp, group, rows):
+    """nda_cq_gemv_lut2: every output bit-identical to the engine's
+    nd_cq_gemv_lut2 (the oracle's restatement, pinned bit-exact to the
+    reference), special norms (subnormal, negative, zero) included."""
+    N = nda()
+    say("cq lut2", shapes, inp, group, rows)
+    ts = [make_cq_tensor(900 + 7 * i + inp, o, inp, group, 2, special_norms=True) for i, o in enumerate(shapes)]
+    qs = [N.CQ(o, inp, group, 2, t.blob, t.cb()) for o, t in zip(shapes, ts)]
+    x = np.stack([det_normal(300 + r, inp) for r in range(rows)]) * np.float32(2.5)
+    dx = N.DevBuf.from_array(x)
+    dxh = N.DevBuf(rows * qs[0].in_pad * 4)
+    qs[0].prepare(rows, dx, dxh)
+    ys = [N.DevBuf(rows * o * 4) for o in shapes]
+    N.cq_gemv_lut2(qs, rows, dxh, ys)
+    N.device_sync()
+    xh = dxh.to_array(np.float32, (rows, qs[0].in_pad))
+    for t, o, y in zip(ts, shapes, ys):
+        got = y.to_array(np.float32, (rows, o))
+        for r in range(rows):
+            want = O.cq_gemv_lut2(t, xh[r])
+            assert np.array_equal(bits(got[r]), bits(want)), (o, r)
+    for q in qs:
+        q.close()
+
+
+def test_cq_lut2_golden_and_refusals():
+    """The reference's own nd_cq_gemv_lut2 outputs for the committed 2-bit
+    vectors, bit for bit; widths and table sizes the kernel does not take
+    are refused with NDA_ERR_UNSUPPORTED."""
+    N = nda()
+    say("cq lut2 golden")
+    G = np.load(os.path.join(HERE, "golden", "golden.npz"))
+    seen = 0
+    for i, shape in enumerate(G["cq_shapes"]):
+        out, inp, group, b = (int(v) for v in shape)
+        if b != 2:
+            continue
+        q = N.CQ(out, inp, group, b, G["cq_blob_%d" % i], G["cq_cb_%d" % i])
+        if q.in_pad > 2048:
+            q.close()
+            continue
+        dxh = N.DevBuf.from_array(G["cq_xh_%d" % i][None, :].astype(np.float32))
+        dy = N.DevBuf(out * 4)
+        N.cq_gemv_lut2([q], 1, dxh, [dy])
+        N.device_sync()
+        assert np.array_equal(bits(dy.to_array(np.float32, (1, out))[0]), bits(G["cq_y2_%d" % i])), i
+        seen += 1
+        q.close()
+    assert seen > 0
+    t3 = make_cq_tensor(5, 16, 64, 32, 3)
+    q3 = N.CQ(16, 64, 32, 3, t3.blob, t3.cb())
+    t4 = make_cq_tensor(6, 8, 4096, 128, 2)
+    q4 = N.CQ(8, 4096, 128, 2, t4.blob, t4.cb())
+    buf = N.DevBuf(4096 * 4 * 2)
+    for q in (q3, q4):
+        with pytest.raises(N.NdaError) as e:
+            N.cq_gemv_lut2([q], 1, buf, [buf])
+        assert e.value.code == -6
+        q.close()
+
+
 def test_cq_error_paths():
     N = nda()
     say("cq errors")

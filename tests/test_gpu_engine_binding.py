@@ -159,15 +159,19 @@ def test_engine_binding_gqa_ring_prefixes():
     assert worst <= TOL, worst
 
 
-def test_engine_binding_whole_attention():
+@pytest.mark.parametrize("odd", [False, True], ids=["12x2_48_64", "10x2_36_20"])
+def test_engine_binding_whole_attention(odd):
     """The engine's attention(m, li, xin, out) itself against its one-call
-    GPU binding: 12 q / 2 kv heads, qk 48, v 64, d_model 256, 3 taps, 2-bit
-    CQ projections registered from the engine's nd_layer records, 2 layers;
+    GPU binding: 12 q / 2 kv heads, qk 48, v 64 (and 10 q / 2 kv heads, qk
+    36, v 20, whose front has run-time dims), d_model 256, 3 taps, 2-bit CQ
+    projections registered from the engine's nd_layer records, 2 layers;
     snapshot, prefix save, rewind, reset and restore."""
-    print("[gpu-case] engine binding whole attention", flush=True)
+    print("[gpu-case] engine binding whole attention", "odd" if odd else "", flush=True)
     sys.path.insert(0, HERE)
     from detgen import Stream, make_block_weights
-    from test_oracle_block import BLOCK, front_weights
+    from test_oracle_block import BLOCK, BLOCK_ODD, front_weights
+    if odd:
+        BLOCK = BLOCK_ODD
     nl, nh, nkv, qk, vd, W = BLOCK["geom"]
     fw = front_weights(BLOCK["seed"] + 1, nl, nh, nkv, qk, vd, BLOCK["taps"])
     bw = make_block_weights(BLOCK["seed"] + 2, nl, nh, nkv, qk, vd, BLOCK["d_model"])

@@ -149,12 +149,15 @@ class Rig:
                 c.close()
 
 
-@pytest.mark.parametrize("kv_dtype", [O.KV_INT8, O.KV_F16])
-def test_prefill_block_ragged_chunks(kv_dtype):
+@pytest.mark.parametrize("shape,kv_dtype", [((12, 2, 48, 64), O.KV_INT8), ((12, 2, 48, 64), O.KV_F16),
+                                             ((10, 2, 36, 20), O.KV_INT8), ((8, 1, 20, 44), O.KV_F16)])
+def test_prefill_block_ragged_chunks(shape, kv_dtype):
     """Sequences at different positions prefill ragged chunks (1 to 70
-    tokens) in one call per layer, then decode on through the block."""
-    say("prefill block ragged", kv_dtype)
-    R = Rig(kv_dtype, B=5)
+    tokens) in one call per layer, then decode on through the block; at the
+    engine's shape and at two shapes whose front has run-time dims."""
+    say("prefill block ragged", shape, kv_dtype)
+    nh, nkv, qk, vd = shape
+    R = Rig(kv_dtype, B=5, nh=nh, nkv=nkv, qk=qk, vd=vd)
     R.decode([1, 3])                     # two sequences start a few tokens in
     R.decode([1, 3])
     R.decode([3])

@@ -31,6 +31,10 @@ BLOCK = dict(geom=(2, 12, 2, 48, 64, 64), d_model=256, taps=3, theta=10000.0, se
                     [("tok",)] * 3 + [("reset",)] + [("tok",)] * 4 + [("restore", 0)] + [("tok",)] * 3)
 
 
+# an odd shape: qk 36 / v 20, 5 query heads per kv-head, out_proj over 200 inputs
+BLOCK_ODD = dict(BLOCK, geom=(2, 10, 2, 36, 20, 64), seed=907)
+
+
 def replay_block(S, spec):
     L, nh, nkv, qk, vd, W = spec["geom"]
     S.front_init(spec["taps"], spec["theta"])
@@ -59,11 +63,12 @@ def replay_block(S, spec):
 
 
 @pytest.mark.skipif(not O.have_ref(), reason="reference harness not built")
-def test_block_matches_engine_attention():
-    o = O.OracleSession(*BLOCK["geom"])
-    r = O.RefSession(*BLOCK["geom"])
-    a, sa = replay_block(o, BLOCK)
-    b, sb = replay_block(r, BLOCK)
+@pytest.mark.parametrize("spec", [BLOCK, BLOCK_ODD], ids=["12x2_48_64", "10x2_36_20"])
+def test_block_matches_engine_attention(spec):
+    o = O.OracleSession(*spec["geom"])
+    r = O.RefSession(*spec["geom"])
+    a, sa = replay_block(o, spec)
+    b, sb = replay_block(r, spec)
     assert np.array_equal(bits(a), bits(b))
     for x, y in zip(o.cache(), r.cache()):
         assert np.array_equal(np.asarray(x), np.asarray(y))
