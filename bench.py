@@ -111,7 +111,7 @@ def cpu_reference_int8(lens_all, seconds, threads):
     if not O.have_ref():
         return None
     rng = np.random.default_rng(SEED + 2)
-    S = 64
+    S = max(64, 4 * max(threads))
     lens = rng.choice(lens_all, S)
     sess = []
     for L in lens:
@@ -141,6 +141,148 @@ def cpu_reference_int8(lens_all, seconds, threads):
     for r in sess:
         r.close()
     return res
+
+
+def usable_cores():
+    """Cores the CPU legs may use on this host: the process's CPU affinity,
+    bounded by a cgroup CPU quota when one is set and by the thread share the
+    host declares in OMP_NUM_THREADS when that is set. Returns (cores, how)."""
+    n = len(os.sched_getaffinity(0))
+    how = ["affinity %d" % n]
+    try:
+        quota, period = open("/sys/fs/cgroup/cpu.max").read().split()[:2]
+        if quota != "max":
+            q = max(1, int(-(-int(quota) // int(period))))
+            how.append("cgroup quota %d" % q)
+            n = min(n, q)
+    except (OSError, ValueError):
+        pass
+    omp = os.environ.get("OMP_NUM_THREADS", "")
+    if omp.isdigit() and int(omp) > 0:
+        how.append("OMP_NUM_THREADS %s" % omp)
+        n = min(n, int(omp))
+    return n, ", ".join(how)
+
+
+def median_of(fn, repeats=5):
+    """fn() -> seconds of one run; one warm-up, then the median of `repeats`."""
+    fn()
+    ts = sorted(fn() for _ in range(repeats))
+    return ts[len(ts) // 2], ts
+
+
+def cpu_reference_prefill_int8(threads, S=256, layers=LAYERS, repeats=5):
+    """The 256-token single-sequence prefill (8 layers, MHA 8 x 64) through
+    the reference engine's own code (oracle/_ref): the prompt fed one token
+    at a time, each token's store + attention() dispatch in every layer, the
+    heads through nd_parallel_rows - serial for 1 thread, the harness's
+    n-thread splitter in that seam otherwise (so at most 8 threads work: one
+    per head). Timed in C with CLOCK_MONOTONIC; median of `repeats` after one
+    warm-up. Returns {threads: object} or None without the harness."""
+    import ndoracle as O
+    if not O.have_ref():
+        return None
+    rng = np.random.default_rng(SEED + 21)
+    q, k, v = (rng.standard_normal((S, H * D)).astype(np.float32) for _ in range(3))
+    out = np.zeros((S, H * D), np.float32)
+    flops = layers * H * 2 * (D + D) * S * (S + 1) / 2
+    res = {}
+    for nt in threads:
+        r = O.RefSession(layers, H, H, D, D, S)
+        if nt > 1 and O.ref().ref_pool_start(nt) != 0:
+            r.close()
+            continue
+
+        def one():
+            O.ref().ref_reset(r.m)
+            return O.ref().ref_prefill_rounds(r.m, S, q.ctypes.data, k.ctypes.data, v.ctypes.data, out.ctypes.data)
+        try:
+            t, ts = median_of(one, repeats)
+        finally:
+            if nt > 1:
+                O.ref().ref_pool_stop()
+        r.close()
+        res[nt] = {"value": round(S / t, 1), "unit": "prompt tokens/s (8 layers)", "cores": nt,
+                   "kind": "reference", "ms_per_prefill": round(t * 1e3, 2),
+                   "attention_GFLOPs": round(flops / t / 1e9, 3),
+                   "sample": "the whole workload: 1 sequence x %d tokens x %d layers, int8 KV; median of %d "
+                             "(%.1f-%.1f ms)" % (S, layers, repeats, ts[0] * 1e3, ts[-1] * 1e3)}
+    return res
+
+
+def cpu_port_prefill_f16(pre, ntok, nthreads, seed_off, repeats=5):
+    """Token-by-token causal prefill through the oracle's fp16 attention
+    port (the engine's attn_heads with fp16 KV; one call stores the token's
+    k/v and attends over everything before it, as the engine prefills a
+    prompt): sequence s has pre[s] stored positions and takes ntok[s] new
+    tokens; sequences split over nthreads threads as independent sessions.
+    Each round is one token of every sequence still prefilling, timed around
+    the attention calls (CLOCK_MONOTONIC); median of `repeats` after one
+    warm-up. Returns (seconds, attention FLOPs, repeat times)."""
+    import ndoracle as O
+    rng = np.random.default_rng(SEED + seed_off)
+    S = len(pre)
+    tot = np.asarray(pre, np.int64) + np.asarray(ntok, np.int64)
+    koff = np.zeros(S, np.uint64)
+    koff[1:] = np.cumsum(tot[:-1] * H * D).astype(np.uint64)
+    pool = rng.standard_normal(1 << 22, dtype=np.float32).astype(np.float16).view(np.uint16)
+    n_el = int(tot.sum()) * H * D
+    kbase = np.resize(pool, n_el)
+    vbase = np.resize(pool[::-1], n_el)
+    T = int(max(ntok))
+    q = rng.standard_normal((T, S * H * D), dtype=np.float32)
+    kn = rng.standard_normal((T, S * H * D), dtype=np.float32)
+    vn = rng.standard_normal((T, S * H * D), dtype=np.float32)
+    out = np.zeros(S * H * D, np.float32)
+    rounds = []
+    for t in range(T):
+        act = [s for s in range(S) if ntok[s] > t]
+        lens = np.array([pre[s] + t + 1 for s in act], np.uint32)
+        sel = np.concatenate([np.arange(s * H * D, (s + 1) * H * D) for s in act])
+        rounds.append((lens, koff[act], np.ascontiguousarray(q[t, sel]), np.ascontiguousarray(kn[t, sel]),
+                       np.ascontiguousarray(vn[t, sel])))
+    flops = float(sum(H * 2 * (D + D) * (int(pre[s]) * int(ntok[s]) + int(ntok[s]) * (int(ntok[s]) + 1) / 2)
+                      for s in range(S)))
+
+    def one():
+        el = 0.0
+        for lens, ko, qq, kk, vv in rounds:
+            t0 = time.perf_counter()
+            O.decode_batch_f16(H, H, D, D, lens, kbase, vbase, ko, ko, qq, kk, vv, None, out, nthreads)
+            el += time.perf_counter() - t0
+        return el
+    t, ts = median_of(one, repeats)
+    return t, flops, ts
+
+
+def config2_leg(N, stream, S=256, layers=LAYERS, reps=10):
+    """The single-sequence causal prefill (1 sequence x 256 tokens, 8 layers,
+    MHA 8 x 64, int8 K/V, the engine's own dtype): nda_prefill per layer on
+    an empty sequence, whole 8-layer prefills timed back to back. A latency
+    workload (one work-group column per head), not a throughput one."""
+    rng = np.random.default_rng(SEED + 21)
+    ctx = N.Context(layers, H, H, D, D, S, kv_dtype=N.KV_INT8, max_seqs=1)
+    q, k, v, out = (N.DevBuf(S * H * D * 4) for _ in range(4))
+    for i, b in enumerate((q, k, v)):
+        b.upload(rng.standard_normal((S, H * D)).astype(np.float32))
+
+    def one():
+        ctx.seq_reset(0)
+        for li in range(layers):
+            ctx.prefill(li, [S], q, k, v, out, stream=stream)
+        ctx.advance(1, [0], S, stream=stream)
+    one()
+    ctx.sync(stream)
+    t0 = time.perf_counter()
+    for _ in range(reps):
+        one()
+    ctx.sync(stream)
+    el = (time.perf_counter() - t0) / reps
+    ctx.close()
+    flops = layers * H * 2 * (D + D) * S * (S + 1) / 2
+    return {"workload": "causal prefill: 1 sequence x %d tokens, %d layers, 8 heads x 64, int8 K/V" % (S, layers),
+            "ms_per_prefill": round(el * 1e3, 3), "prompt_tokens_per_s": round(S / el, 1),
+            "tflops": round(flops / el / 1e12, 4), "flop_per_prefill": flops}
 
 
 def prefill_leg(N, stream, nseq=256, lmin=8192, lmax=32768, chunk=512, reps=3):
@@ -975,9 +1117,14 @@ def main():
             "|delta| %.3g" % (prefill["tflops"], prefill["frac"], prefill["frac_measured"], prefill["peak_measured"],
                               prefill["kernel_ms"], prefill["max_abs_delta_sampled"]))
 
-    cpu = cpu_1 = cpu_ref = cpu_long = None
+    cfg2 = config2_leg(N, stream)
+    log("config 2 prefill (1 x 256 tokens, 8 layers, int8): %.3f ms, %.0f prompt tok/s" % (
+        cfg2["ms_per_prefill"], cfg2["prompt_tokens_per_s"]))
+
+    cpu = cpu_1 = cpu_ref = cpu_long = cpu_long_1 = cpu_cfg = None
     if not args.no_cpu:
-        ncores = min(16, os.cpu_count() or 1)
+        ncores, cores_how = usable_cores()
+        log("cpu legs: %d cores (%s)" % (ncores, cores_how))
         sec = args.cpu_seconds
         c_tok, _, sample = cpu_port_f16(lens, sec * 0.3, ncores)
         cpu = {"value": round(c_tok, 1), "unit": "tokens/s", "cores": ncores, "kind": "port",
@@ -993,13 +1140,55 @@ def main():
                 cpu_ref["1"]["value"], cpu_ref[str(ncores)]["value"], ncores))
         # the long-context decode (8K-32K positions), a 16-sequence subsample
         rng_l = np.random.default_rng(SEED + 5)
-        lt, lf, lsample = cpu_port_f16(rng_l.integers(8192, 32769, 256), sec * 0.2, ncores, nseq=16,
+        lt, lf, lsample = cpu_port_f16(rng_l.integers(8192, 32769, 256), sec * 0.2, ncores, nseq=max(16, ncores),
                                        seed_off=5)
         cpu_long = {"value": round(lt * LAYERS, 1), "unit": "tokens/s per layer", "cores": ncores,
                     "kind": "port", "attention_GFLOPs": round(lf / 1e9, 2),
                     "sample": lsample + ", fp16 KV, L ~ U[8192, 32768], one layer"}
         log("cpu long-context decode (port): %.1f tok/s per layer, %.1f GFLOP/s on %d threads" % (
             lt * LAYERS, lf / 1e9, ncores))
+        lt1, lf1, lsample1 = cpu_port_f16(rng_l.integers(8192, 32769, 256), sec * 0.15, 1, nseq=2, seed_off=5)
+        cpu_long_1 = {"value": round(lt1 * LAYERS, 1), "unit": "tokens/s per layer", "cores": 1,
+                      "kind": "port", "attention_GFLOPs": round(lf1 / 1e9, 2),
+                      "sample": lsample1 + ", fp16 KV, L ~ U[8192, 32768], one layer"}
+        log("cpu long-context decode (port): %.1f tok/s per layer on 1 thread" % (lt1 * LAYERS))
+        cpu_cfg = {"cores_available": ncores, "cores_source": cores_how}
+        # config 2: the reference's own token-by-token prefill, int8
+        c2 = cpu_reference_prefill_int8((1, ncores) if ncores > 1 else (1,))
+        if c2:
+            cpu_cfg["config2_prefill_reference_int8"] = {str(k): v for k, v in c2.items()}
+            log("cpu config 2 prefill (reference, int8): %s" % ", ".join(
+                "%.1f ms on %d" % (v["ms_per_prefill"], k) for k, v in c2.items()))
+        # config 4: suffix prefill after the shared 213-token prefix, subsamples
+        rng4 = np.random.default_rng(SEED + 9)
+        n4 = rng4.integers(32, 65, 1024)
+        c4 = {}
+        for nt, S in ((1, 16), (ncores, max(128, 8 * ncores))):
+            t, f, ts = cpu_port_prefill_f16([213] * S, n4[:S], nt, seed_off=31)
+            c4[str(nt)] = {"value": round(float(n4[:S].sum()) / t, 1), "unit": "prompt tokens/s per layer",
+                           "cores": nt, "kind": "port", "attention_GFLOPs": round(f / t / 1e9, 3),
+                           "sample": "the first %d of the 1024 sequences (n ~ U[32,64], %d tokens) after the "
+                                     "213-token prefix, one layer, fp16 KV; median of 5 (%.3f-%.3f s)"
+                                     % (S, int(n4[:S].sum()), ts[0], ts[-1])}
+        cpu_cfg["config4_suffix_prefill_port_f16"] = c4
+        log("cpu config 4 suffix prefill (port): %s" % ", ".join(
+            "%.1f GFLOP/s on %s" % (v["attention_GFLOPs"], k) for k, v in c4.items()))
+        # config 5: the 512-token chunk over 8K-32K stored positions, subsamples
+        rng5 = np.random.default_rng(SEED + 5)
+        L5 = rng5.integers(8192, 32769, 256) + 1
+        c5 = {}
+        for nt, S, Tk in ((1, 1, 8), (ncores, ncores, 8)):
+            t, f, ts = cpu_port_prefill_f16(L5[:S], [Tk] * S, nt, seed_off=41)
+            full = float(sum(H * 2 * (D + D) * (512 * int(L) + 512 * 513 / 2) for L in L5))
+            c5[str(nt)] = {"value": round(f / t / 1e9, 3), "unit": "attention GFLOP/s",
+                           "cores": nt, "kind": "port", "chunk_tokens_per_s": round(S * Tk / t, 2),
+                           "full_chunk_s_estimate": round(full / (f / t), 1),
+                           "sample": "the first %d tokens of the 512-token chunk of the first %d of the 256 "
+                                     "sequences (L ~ U[8192,32768]), one layer, fp16 KV; median of 5 (%.3f-%.3f "
+                                     "s); the full chunk scaled by its FLOPs" % (Tk, S, ts[0], ts[-1])}
+        cpu_cfg["config5_chunk_prefill_port_f16"] = c5
+        log("cpu config 5 chunk (port): %s" % ", ".join(
+            "%.2f GFLOP/s on %s" % (v["value"], k) for k, v in c5.items()))
 
     res = {
         "metric": "decode attn tokens/s + HBM GB/s (% peak) at B=4096; prefill TFLOP/s",
@@ -1028,6 +1217,9 @@ def main():
         "cpu_baseline_1core": cpu_1,
         "cpu_reference_int8": cpu_ref,
         "cpu_long_context_decode": cpu_long,
+        "cpu_long_context_decode_1core": cpu_long_1,
+        "cpu_prefill_configs": cpu_cfg,
+        "config2_prefill": cfg2,
         "prefill": prefill,
         "device_ceiling": ceiling,
         "engine_session": engine,

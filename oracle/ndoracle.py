@@ -193,6 +193,11 @@ def ref():
         R.ref_attention_rounds.restype = C.c_double
         R.ref_attention_rounds.argtypes = [C.c_void_p, C.c_uint32, C.c_uint32] + [C.c_void_p] * 4 + \
             [C.c_uint32] * 3
+        R.ref_pool_start.restype = C.c_int
+        R.ref_pool_start.argtypes = [C.c_int]
+        R.ref_pool_stop.argtypes = []
+        R.ref_prefill_rounds.restype = C.c_double
+        R.ref_prefill_rounds.argtypes = [C.c_void_p, C.c_uint32] + [C.c_void_p] * 4
         _ref = R
     return _ref
 

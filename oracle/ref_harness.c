@@ -438,3 +438,133 @@ double ref_attention_rounds(void **models, uint32_t n, uint32_t li, const float 
     clock_gettime(CLOCK_MONOTONIC, &t1);
     return (double)(t1.tv_sec - t0.tv_sec) + 1e-9 * (double)(t1.tv_nsec - t0.tv_nsec);
 }
+
+/* ---- the engine's row seam on the host's cores ----
+ *
+ * nd_parallel_rows (engine/include/nd_quant.h:213-230) is the engine's only
+ * parallelism: an installed splitter runs fn over disjoint row ranges at once
+ * and the caller waits for all of them (the ESP32 build installs a two-core
+ * one, esp32/main/main.c:191). ref_pool_start(n) installs the same contract
+ * over n host threads - the caller's thread takes range 0, n - 1 persistent
+ * workers the others, contiguous and as even as the row count allows, with a
+ * barrier before and after - so attention()'s own dispatch,
+ * nd_parallel_rows(attn_heads, &actx, nh) (engine/src/nd_model.c:2481), runs
+ * its heads on n cores. ref_pool_stop() restores the serial splitter. */
+static pthread_t pool_th[256];
+static int pool_n = 0, pool_quit = 0;
+static pthread_barrier_t pool_go, pool_done;
+static nd_row_fn pool_fn;
+static void *pool_ctx;
+static uint32_t pool_rows;
+static void (*pool_saved)(nd_row_fn, void *, uint32_t);
+
+static void pool_slice(int t)
+{
+    uint32_t r0 = (uint32_t)((uint64_t)pool_rows * (uint32_t)t / (uint32_t)pool_n);
+    uint32_t r1 = (uint32_t)((uint64_t)pool_rows * (uint32_t)(t + 1) / (uint32_t)pool_n);
+    if (r0 < r1)
+        pool_fn(pool_ctx, r0, r1);
+}
+
+static void *pool_worker(void *arg)
+{
+    int t = (int)(intptr_t)arg;
+    for (;;) {
+        pthread_barrier_wait(&pool_go);
+        if (pool_quit)
+            return NULL;
+        pool_slice(t);
+        pthread_barrier_wait(&pool_done);
+    }
+}
+
+static void pool_split(nd_row_fn fn, void *ctx, uint32_t nrows)
+{
+    pool_fn = fn;
+    pool_ctx = ctx;
+    pool_rows = nrows;
+    pthread_barrier_wait(&pool_go);
+    pool_slice(0);
+    pthread_barrier_wait(&pool_done);
+}
+
+int ref_pool_start(int n)
+{
+    int t;
+    if (pool_n || n < 2 || n > 256)
+        return -1;
+    pool_n = n;
+    pool_quit = 0;
+    pthread_barrier_init(&pool_go, NULL, (unsigned)n);
+    pthread_barrier_init(&pool_done, NULL, (unsigned)n);
+    for (t = 1; t < n; t++)
+        if (pthread_create(&pool_th[t], NULL, pool_worker, (void *)(intptr_t)t))
+            return -1;
+    pool_saved = nd_parallel_rows;
+    nd_parallel_rows = pool_split;
+    return 0;
+}
+
+void ref_pool_stop(void)
+{
+    int t;
+    if (!pool_n)
+        return;
+    nd_parallel_rows = pool_saved;
+    pool_quit = 1;
+    pthread_barrier_wait(&pool_go);
+    for (t = 1; t < pool_n; t++)
+        pthread_join(pool_th[t], NULL);
+    pthread_barrier_destroy(&pool_go);
+    pthread_barrier_destroy(&pool_done);
+    pool_n = 0;
+}
+
+/* The engine's prefill of one sequence: S tokens, each through every layer
+ * (store + attention() dispatch with the heads through nd_parallel_rows, as
+ * nd_model.c:2426-2483 does), pos advancing after each token
+ * (esp32/main/main.c:312-315 feeds a prompt one token at a time). q/k/v hold
+ * one row per token, reused by every layer; out receives the last layer's
+ * rows. Wall time of the whole prefill in seconds, CLOCK_MONOTONIC. */
+double ref_prefill_rounds(void *vm, uint32_t S, const float *q, const float *k, const float *v, float *out)
+{
+    nd_model *m = (nd_model *)vm;
+    struct timespec t0, t1;
+    uint32_t t, li, nh = m->n_heads, rcap = m->window - m->n_sink;
+    clock_gettime(CLOCK_MONOTONIC, &t0);
+    for (t = 0; t < S; t++) {
+        for (li = 0; li < m->n_layers; li++) {
+            attn_ctx c;
+            uint32_t i;
+            ref_kv_store(vm, li, k + (size_t)t * m->n_kv_heads * m->qk_head_dim,
+                         v + (size_t)t * m->n_kv_heads * m->v_head_dim);
+            memcpy(m->q, q + (size_t)t * nh * m->qk_head_dim, sizeof(float) * nh * m->qk_head_dim);
+            for (i = 0; i < nh * m->v_head_dim; i++)
+                m->gate[i] = INFINITY;
+            c.m = m;
+            c.li = li;
+            c.nkv = m->n_kv_heads;
+            c.rep = nh / m->n_kv_heads;
+            c.nh = nh;
+            c.qk_hd = m->qk_head_dim;
+            c.v_hd = m->v_head_dim;
+            c.scale = 1.0f / sqrtf((float)m->qk_head_dim);
+            c.sinks = m->n_sink < m->pos + 1u ? m->n_sink : m->pos + 1u;
+            if (m->pos + 1u <= m->n_sink) {
+                c.rfirst = m->pos + 1u;
+                c.rcount = 0;
+            } else {
+                c.rcount = m->pos + 1u - m->n_sink;
+                if (c.rcount > rcap)
+                    c.rcount = rcap;
+                c.rfirst = m->pos + 1u - c.rcount;
+            }
+            nd_parallel_rows(attn_heads, &c, nh);
+            if (li + 1 == m->n_layers)
+                memcpy(out + (size_t)t * nh * m->v_head_dim, m->attn, sizeof(float) * nh * m->v_head_dim);
+        }
+        m->pos++;
+    }
+    clock_gettime(CLOCK_MONOTONIC, &t1);
+    return (double)(t1.tv_sec - t0.tv_sec) + 1e-9 * (double)(t1.tv_nsec - t0.tv_nsec);
+}

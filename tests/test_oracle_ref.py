@@ -165,3 +165,38 @@ def test_prefix_switching_bit_exact():
                 [("tok", True, 1.0)] * 5 + [("restore", 0), ("tok", True, 1.0), ("rewind",), ("tok", False, 8.0),
                                             ("restore", 1)] + [("tok", True, 2.0)] * 400 + [("rewind",), ("tok", True, 1.0)])
     _run_pair((1, 12, 2, 48, 64, 384), 0, ev, seed=99)
+
+
+def test_prefill_timer_on_the_row_seam_bit_exact():
+    """The CPU-baseline driver of the reference (ref_prefill_rounds: a prompt
+    fed one token at a time through every layer, the heads dispatched through
+    nd_parallel_rows) gives the same rows serially and on a 4-thread splitter
+    installed in the engine's seam (disjoint head ranges, the contract of
+    engine/include/nd_quant.h:213-230), and both equal the oracle's replay of
+    the same tokens."""
+    L, nh, S = 2, 8, 40
+    rng = np.random.default_rng(8)
+    q = rng.standard_normal((S, nh * 64)).astype(np.float32)
+    k = rng.standard_normal((S, nh * 64)).astype(np.float32)
+    v = rng.standard_normal((S, nh * 64)).astype(np.float32)
+    outs = []
+    for threads in (1, 4):
+        r = O.RefSession(L, nh, nh, 64, 64, 64)
+        out = np.zeros((S, nh * 64), np.float32)
+        if threads > 1:
+            assert O.ref().ref_pool_start(threads) == 0
+        try:
+            t = O.ref().ref_prefill_rounds(r.m, S, q.ctypes.data, k.ctypes.data, v.ctypes.data, out.ctypes.data)
+        finally:
+            if threads > 1:
+                O.ref().ref_pool_stop()
+        assert t > 0 and r.pos == S
+        outs.append(out)
+        r.close()
+    assert np.array_equal(bits(outs[0]), bits(outs[1]))
+    o = O.OracleSession(L, nh, nh, 64, 64, 64)
+    for t in range(S):
+        for li in range(L):
+            got = o.attention(li, q[t], k[t], v[t], None)
+        o.step_end()
+        assert np.array_equal(bits(got), bits(outs[0][t])), t
