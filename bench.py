@@ -176,8 +176,8 @@ def cpu_reference_prefill_int8(threads, S=256, layers=LAYERS, repeats=5):
     the reference engine's own code (oracle/_ref): the prompt fed one token
     at a time, each token's store + attention() dispatch in every layer, the
     heads through nd_parallel_rows - serial for 1 thread, the harness's
-    n-thread splitter in that seam otherwise (so at most 8 threads work: one
-    per head). Timed in C with CLOCK_MONOTONIC; median of `repeats` after one
+    n-thread splitter in that seam otherwise (8 heads: at most 8 threads have
+    work). Timed in C with CLOCK_MONOTONIC; median of `repeats` after one
     warm-up. Returns {threads: object} or None without the harness."""
     import ndoracle as O
     if not O.have_ref():
@@ -1154,7 +1154,8 @@ def main():
         log("cpu long-context decode (port): %.1f tok/s per layer on 1 thread" % (lt1 * LAYERS))
         cpu_cfg = {"cores_available": ncores, "cores_source": cores_how}
         # config 2: the reference's own token-by-token prefill, int8
-        c2 = cpu_reference_prefill_int8((1, ncores) if ncores > 1 else (1,))
+        nt2 = min(ncores, H)               # the seam splits 8 heads: more threads have no work
+        c2 = cpu_reference_prefill_int8((1, nt2) if nt2 > 1 else (1,))
         if c2:
             cpu_cfg["config2_prefill_reference_int8"] = {str(k): v for k, v in c2.items()}
             log("cpu config 2 prefill (reference, int8): %s" % ", ".join(

@@ -446,17 +446,23 @@ double ref_attention_rounds(void **models, uint32_t n, uint32_t li, const float 
  * and the caller waits for all of them (the ESP32 build installs a two-core
  * one, esp32/main/main.c:191). ref_pool_start(n) installs the same contract
  * over n host threads - the caller's thread takes range 0, n - 1 persistent
- * workers the others, contiguous and as even as the row count allows, with a
- * barrier before and after - so attention()'s own dispatch,
+ * workers the others, contiguous and as even as the row count allows, the
+ * caller returning once all are done - so attention()'s own dispatch,
  * nd_parallel_rows(attn_heads, &actx, nh) (engine/src/nd_model.c:2481), runs
  * its heads on n cores. ref_pool_stop() restores the serial splitter. */
 static pthread_t pool_th[256];
 static int pool_n = 0, pool_quit = 0;
-static pthread_barrier_t pool_go, pool_done;
+static uint32_t pool_gen = 0, pool_done = 0;   /* __atomic: the dispatch and its completion count */
 static nd_row_fn pool_fn;
 static void *pool_ctx;
 static uint32_t pool_rows;
 static void (*pool_saved)(nd_row_fn, void *, uint32_t);
+
+#if defined(__x86_64__) || defined(__i386__)
+#define POOL_RELAX() __builtin_ia32_pause()
+#else
+#define POOL_RELAX() ((void)0)
+#endif
 
 static void pool_slice(int t)
 {
@@ -466,15 +472,22 @@ static void pool_slice(int t)
         pool_fn(pool_ctx, r0, r1);
 }
 
+/* Workers spin on the dispatch counter (each has a core of its own: the
+ * pool is sized to the cores the process may use), so a dispatch costs a
+ * cache-line handoff rather than a futex wake-up per thread. */
 static void *pool_worker(void *arg)
 {
     int t = (int)(intptr_t)arg;
+    uint32_t seen = 0;
     for (;;) {
-        pthread_barrier_wait(&pool_go);
-        if (pool_quit)
+        uint32_t g;
+        while ((g = __atomic_load_n(&pool_gen, __ATOMIC_ACQUIRE)) == seen)
+            POOL_RELAX();
+        seen = g;
+        if (__atomic_load_n(&pool_quit, __ATOMIC_ACQUIRE))
             return NULL;
         pool_slice(t);
-        pthread_barrier_wait(&pool_done);
+        __atomic_fetch_add(&pool_done, 1u, __ATOMIC_ACQ_REL);
     }
 }
 
@@ -483,9 +496,11 @@ static void pool_split(nd_row_fn fn, void *ctx, uint32_t nrows)
     pool_fn = fn;
     pool_ctx = ctx;
     pool_rows = nrows;
-    pthread_barrier_wait(&pool_go);
+    __atomic_store_n(&pool_done, 0u, __ATOMIC_RELAXED);
+    __atomic_fetch_add(&pool_gen, 1u, __ATOMIC_RELEASE);
     pool_slice(0);
-    pthread_barrier_wait(&pool_done);
+    while (__atomic_load_n(&pool_done, __ATOMIC_ACQUIRE) != (uint32_t)(pool_n - 1))
+        POOL_RELAX();
 }
 
 int ref_pool_start(int n)
@@ -495,8 +510,7 @@ int ref_pool_start(int n)
         return -1;
     pool_n = n;
     pool_quit = 0;
-    pthread_barrier_init(&pool_go, NULL, (unsigned)n);
-    pthread_barrier_init(&pool_done, NULL, (unsigned)n);
+    pool_gen = 0;
     for (t = 1; t < n; t++)
         if (pthread_create(&pool_th[t], NULL, pool_worker, (void *)(intptr_t)t))
             return -1;
@@ -511,12 +525,10 @@ void ref_pool_stop(void)
     if (!pool_n)
         return;
     nd_parallel_rows = pool_saved;
-    pool_quit = 1;
-    pthread_barrier_wait(&pool_go);
+    __atomic_store_n(&pool_quit, 1, __ATOMIC_RELEASE);
+    __atomic_fetch_add(&pool_gen, 1u, __ATOMIC_RELEASE);
     for (t = 1; t < pool_n; t++)
         pthread_join(pool_th[t], NULL);
-    pthread_barrier_destroy(&pool_go);
-    pthread_barrier_destroy(&pool_done);
     pool_n = 0;
 }
 
