@@ -1,5 +1,6 @@
-/* nda_internal.h - shared definitions between the C-ABI layer (nda_api.hip)
- * and the gfx950 kernels (nda_kernels.hip). Not installed. */
+/* nda_internal.h - shared definitions between the C-ABI layer (nda_api_*.hip)
+ * and the gfx950 kernels (nda_kernels.hip, nda_prefill.hip, nda_front.hip,
+ * nda_cq.hip). Not installed. */
 #pragma once
 
 #include <hip/hip_runtime.h>
