@@ -855,6 +855,24 @@ def block_leg(N, stream, nseq=B, steps=5, warmup=2, taps=3, theta=10000.0):
     per_step = {name: round(ms[k] / steps, 4) for name, k in
                 (("projections_ms", N.K_PROJ), ("front_store_ms", N.K_FRONT), ("decode_ms", N.K_DECODE),
                  ("combine_ms", N.K_COMBINE))}
+    # The same decode launches back to back, without the per-kernel events:
+    # nda_decode over the 8 layers at the positions reached, on synthetic q
+    # and gate (a decode call stores nothing, so repeats read the same cache)
+    nh, nkv, qk, vd = ENGINE_GEOM
+    qd, gd, od = N.DevBuf(nseq * nh * qk * 4), N.DevBuf(nseq * nh * vd * 4), N.DevBuf(nseq * nh * vd * 4)
+    qd.fill_normal(nseq * nh * qk, 0, SEED + 44, stream=stream)
+    gd.fill_normal(nseq * nh * vd, 0, SEED + 45, stream=stream)
+    for li in range(LAYERS):
+        ctx.decode(li, nseq, qd, od, gate=gd, stream=stream)
+    tm = N.Timer()
+    tm.start(stream)
+    for _ in range(steps):
+        for li in range(LAYERS):
+            ctx.decode(li, nseq, qd, od, gate=gd, stream=stream)
+    tm.stop(stream)
+    b2b_s = tm.ms() * 1e-3 / (steps * LAYERS)
+    for buf in (qd, gd, od):
+        buf.free()
     ctx.close()
     for layer in cqs:
         for c in layer:
@@ -864,9 +882,9 @@ def block_leg(N, stream, nseq=B, steps=5, warmup=2, taps=3, theta=10000.0):
     # steps: positions lens + warmup + steps + s, slots min(pos + 1, window)),
     # plus the fp32 q and gate read and the output written (12 heads, as the
     # headline decode counts q and out)
-    nh, nkv, qk, vd = ENGINE_GEOM
     vis = [np.minimum(lens + warmup + steps + s_ + 1, W) for s_ in range(steps)]
     kv_bytes = float(np.mean([v.sum() for v in vis])) * nkv * (qk + vd + 8)
+    b2b_bytes = float(np.minimum(lens + warmup + 2 * steps + 1, W).sum()) * nkv * (qk + vd + 8)
     qgo_bytes = float(nseq) * nh * (qk + 2 * vd) * 4
     dec_bytes = kv_bytes + qgo_bytes
     dec_s = per_step["decode_ms"] * 1e-3 / LAYERS
@@ -877,7 +895,12 @@ def block_leg(N, stream, nseq=B, steps=5, warmup=2, taps=3, theta=10000.0):
             "decode": {"kernel": "decode_mfma_kernel<48,64,rep6>", "bytes_per_launch": round(dec_bytes),
                        "kv_bytes_per_launch": round(kv_bytes),
                        "GBps": round(dec_bytes / dec_s / 1e9, 1) if dec_s > 0 else None,
-                       "frac": round(dec_bytes / dec_s / 8e12, 4) if dec_s > 0 else None, "bound": "hbm"},
+                       "frac": round(dec_bytes / dec_s / 8e12, 4) if dec_s > 0 else None, "bound": "hbm",
+                       "back_to_back_ms": round(b2b_s * 1e3, 4),
+                       "back_to_back_frac": round((b2b_bytes + qgo_bytes) / b2b_s / 8e12, 4),
+                       "note": "frac: the in-step launches timed by per-kernel events (each pair adds a gap); "
+                               "back_to_back: the 8 layers' decode calls alone, one event pair around "
+                               "%d steps" % steps},
             "note": "parity of the same path is held by tests/test_gpu_block.py (the engine's own attention() "
                     "golden session replayed within 5e-6)"}
 

@@ -1084,8 +1084,12 @@ void decode_mfma_kernel(PrefillArgs a)
     // tile j: the load of the next tile (references fetched a tile ago), the
     // references of the one after, the tile's arithmetic, then the next tile
     // into LDS; the last tile loads the gate instead
-    auto tile = [&](const int j, auto masked, auto last) __attribute__((always_inline)) {
+    // Scores are kept relative to the running max m: after the first tile
+    // (which sets m to its own max), one fma per score applies the k scale
+    // and subtracts m, and the lazy check compares with 8 alone.
+    auto tile = [&](const int j, auto masked, auto last, auto first) __attribute__((always_inline)) {
         constexpr bool more = !decltype(last)::value;
+        constexpr bool FIRST = decltype(first)::value;
         const int rem = remaining(j) - 8 * g;   // this lane's visible keys of the tile
         if constexpr (more) {
             load(tref, sg);
@@ -1119,11 +1123,19 @@ void decode_mfma_kernel(PrefillArgs a)
         // scores of keys 8 g + 4 kb + i: k scales, then the mask (a masked
         // key's v scale, possibly never written, becomes 0)
         float vsc[8];
+        const float nm = -m;
 #pragma unroll
         for (int kb = 0; kb < 2; kb++) {
             const float4 ks = *reinterpret_cast<const float4 *>(lds + soff + 16 * kb);
             const float4 vs = *reinterpret_cast<const float4 *>(lds + soff + 128 + 16 * kb);
-            st[kb] *= float4v{ks.x, ks.y, ks.z, ks.w};
+            if constexpr (FIRST) {
+                st[kb] *= float4v{ks.x, ks.y, ks.z, ks.w};
+            } else {
+                st[kb][0] = __builtin_fmaf(st[kb][0], ks.x, nm);
+                st[kb][1] = __builtin_fmaf(st[kb][1], ks.y, nm);
+                st[kb][2] = __builtin_fmaf(st[kb][2], ks.z, nm);
+                st[kb][3] = __builtin_fmaf(st[kb][3], ks.w, nm);
+            }
             vsc[4 * kb + 0] = vs.x;
             vsc[4 * kb + 1] = vs.y;
             vsc[4 * kb + 2] = vs.z;
@@ -1148,22 +1160,34 @@ void decode_mfma_kernel(PrefillArgs a)
             const auto sw2 = __builtin_amdgcn_permlane32_swap(__float_as_uint(mt), __float_as_uint(mt), false, false);
             mt = max3(mt, __uint_as_float(sw2[0]), __uint_as_float(sw2[1]));
         }
-        const bool grow = mt > m + 8.0f;
-        if (__builtin_expect(__ballot(grow) != 0, 0)) {
-            const float mnew = grow ? mt : m;
-            const float rs = fast_exp2(m - mnew);
-            m = mnew;
-            lsum *= rs;
+        if constexpr (FIRST) {
+            // the first tile sets m (nothing is accumulated yet)
+            m = mt;
 #pragma unroll
-            for (int d = 0; d < 4; d++)
-                acc[d] *= rs;
+            for (int kb = 0; kb < 2; kb++)
+                st[kb] -= mt;
+        } else {
+            // scores relative to m: it moves only when one exceeds it by 2^8
+            const bool grow = mt > 8.0f;
+            if (__builtin_expect(__ballot(grow) != 0, 0)) {
+                const float d = grow ? mt : 0.0f;
+                const float rs = fast_exp2(-d);
+                m += d;
+                lsum *= rs;
+#pragma unroll
+                for (int dd = 0; dd < 4; dd++)
+                    acc[dd] *= rs;
+#pragma unroll
+                for (int kb = 0; kb < 2; kb++)
+                    st[kb] -= d;
+            }
         }
         float p[8];
 #pragma unroll
         for (int kb = 0; kb < 2; kb++)
 #pragma unroll
             for (int i = 0; i < 4; i++)
-                p[4 * kb + i] = fast_exp2(st[kb][i] - m);
+                p[4 * kb + i] = fast_exp2(st[kb][i]);
         lsum += ((p[0] + p[1]) + (p[2] + p[3])) + ((p[4] + p[5]) + (p[6] + p[7]));
 #pragma unroll
         for (int i = 0; i < 8; i++)
@@ -1201,16 +1225,29 @@ void decode_mfma_kernel(PrefillArgs a)
         }
     };
     store(sg);
-    for (int j = 0; j + 1 < ntile; j++) {
-        if (remaining(j) >= PF_KT)
-            tile(j, std::false_type{}, std::false_type{});
+    using Yes = std::true_type;
+    using No = std::false_type;
+    if (ntile == 1) {
+        if (remaining(0) >= PF_KT)
+            tile(0, No{}, Yes{}, Yes{});
         else
-            tile(j, std::true_type{}, std::false_type{});
+            tile(0, Yes{}, Yes{}, Yes{});
+    } else {
+        if (remaining(0) >= PF_KT)
+            tile(0, No{}, No{}, Yes{});
+        else
+            tile(0, Yes{}, No{}, Yes{});
+        for (int j = 1; j + 1 < ntile; j++) {
+            if (remaining(j) >= PF_KT)
+                tile(j, No{}, No{}, No{});
+            else
+                tile(j, Yes{}, No{}, No{});
+        }
+        if (remaining(ntile - 1) >= PF_KT)
+            tile(ntile - 1, No{}, Yes{}, No{});
+        else
+            tile(ntile - 1, Yes{}, Yes{}, No{});
     }
-    if (remaining(ntile - 1) >= PF_KT)
-        tile(ntile - 1, std::false_type{}, std::true_type{});
-    else
-        tile(ntile - 1, std::true_type{}, std::true_type{});
 
     lsum += __shfl_xor(lsum, 16, 64);
     lsum += __shfl_xor(lsum, 32, 64);
