@@ -940,6 +940,18 @@ void decode_mfma_kernel(PrefillArgs a)
     };
     const int rc1 = min(64 + lane, NRC - 1);
     const uint32_t rg1 = 16 * rc1;
+    // RUN: the first slot a chunk holds (K rows, V rows, then 4 slots of k
+    // or v scales per chunk); a chunk whose slots are all past the half's
+    // visible ones is not fetched (its lane reads chunk 0 instead, one line
+    // for the wave): the keys it would feed are masked
+    auto run_slot = [&](int c) __attribute__((always_inline)) -> int {
+        if (c < DK)
+            return c * 16 / DK;
+        if (c < DK + DV)
+            return (c - DK) * 16 / DV;
+        return 4 * ((c - DK - DV) & 3);
+    };
+    const int rs0 = run_slot(lane), rs1 = run_slot(rc1);
     int rl[2][2];
 #pragma unroll
     for (int h = 0; h < 2; h++) {
@@ -965,7 +977,7 @@ void decode_mfma_kernel(PrefillArgs a)
     // the segment's end rereads half 0)
     struct TileRef {
         int32_t pid[2];
-        int sip[2];
+        int sip[2], vis[2];                     // vis: the half's visible slots (RUN)
     };
     auto fetch = [&](int j, TileRef &tr_) __attribute__((always_inline)) {
         j = min(j, ntile - 1);
@@ -978,6 +990,8 @@ void decode_mfma_kernel(PrefillArgs a)
         tr_.pid[1] = rows[s1 >> a.pg.log2_page];
         tr_.sip[0] = s0 & (P - 1);
         tr_.sip[1] = s1 & (P - 1);
+        tr_.vis[0] = min(16, len - s0);
+        tr_.vis[1] = s1 != s0 ? min(16, len - s1) : 0;
     };
     struct Stage {
         u32x4 k[2], v[2];                       // RUN: chunks lane and 64 + lane
@@ -990,8 +1004,9 @@ void decode_mfma_kernel(PrefillArgs a)
             const uint8_t *hb = a.pool + (uint64_t)(uint32_t)t_.pid[h] * (uint32_t)a.pg.page_bytes +
                                 (uint64_t)kvh * a.pg.head_bytes;
             if constexpr (RUN) {
-                sg.k[h] = __builtin_nontemporal_load(reinterpret_cast<const u32x4 *>(hb + 16 * lane));
-                sg.v[h] = __builtin_nontemporal_load(reinterpret_cast<const u32x4 *>(hb + rg1));
+                const uint32_t o0 = rs0 < t_.vis[h] ? 16 * lane : 0u, o1 = rs1 < t_.vis[h] ? rg1 : 0u;
+                sg.k[h] = __builtin_nontemporal_load(reinterpret_cast<const u32x4 *>(hb + o0));
+                sg.v[h] = __builtin_nontemporal_load(reinterpret_cast<const u32x4 *>(hb + o1));
             } else {
                 const uint32_t sip = (uint32_t)t_.sip[h];
                 sg.k[h] = __builtin_nontemporal_load(reinterpret_cast<const u32x4 *>(hb + (kc + sip * DK)));
