@@ -355,6 +355,28 @@ __global__ __launch_bounds__(64 * NW) void attend_kernel(AttnArgs a)
         }
     }
 
+    // A shared-prefix pass left chunk 0 (the prefix's softmax state) and this
+    // is the row's only other chunk: the epilogue merges the two. Wave 0's
+    // first lane group requests chunk 0 now, so that its latency overlaps
+    // the row's own loads rather than ending the work-group (REP <= 2: its
+    // REP * (EV + 2) registers).
+    constexpr bool PRE0 = REP <= 2;
+    const bool merge0 = a.chunk_lo == 1 && nchunks == 2;
+    float p0[PRE0 ? REP : 1][C::EV + 2] = {};
+    if constexpr (PRE0) {
+        if (merge0 && wave == 0 && lane < G) {
+#pragma unroll
+            for (int t = 0; t < REP; t++) {
+                const float *r0 = a.part + ((uint64_t)row * a.nh + gv * REP + t) * a.max_chunks * (dv + 2);
+#pragma unroll
+                for (int e = 0; e < C::EV; e++)
+                    p0[t][e] = (!RT || li * C::EV + e < dv) ? r0[li * C::EV + e] : 0.0f;
+                p0[t][C::EV] = r0[dv];
+                p0[t][C::EV + 1] = r0[dv + 1];
+            }
+        }
+    }
+
     AttnState<ES, DK, DV, REP, G, NP, NW> st;
 #pragma unroll
     for (int t = 0; t < REP; t++) {
@@ -438,11 +460,11 @@ __global__ __launch_bounds__(64 * NW) void attend_kernel(AttnArgs a)
                     o[e] = z;
                 }
             }
-        } else if (a.chunk_lo == 1 && nchunks == 2) {
-            // a shared-prefix pass left chunk 0 (the prefix) and this is the
-            // row's only other chunk: merge the two here and write the row
+        } else if (merge0) {
+            // merge chunk 0 (above) into this chunk and write the row
             const float *r0 = a.part + ((uint64_t)row * a.nh + h) * a.max_chunks * (dv + 2);
-            const float m0 = r0[dv], l0 = r0[dv + 1];
+            const float m0 = PRE0 ? p0[PRE0 ? t : 0][C::EV] : r0[dv];
+            const float l0 = PRE0 ? p0[PRE0 ? t : 0][C::EV + 1] : r0[dv + 1];
             const float M = fmaxf(st.m[t], m0);
             const float ca = fast_exp2(st.m[t] - M), cb = fast_exp2(m0 - M);
             const float inv = 1.0f / (st.l[t] * ca + l0 * cb);
@@ -451,7 +473,8 @@ __global__ __launch_bounds__(64 * NW) void attend_kernel(AttnArgs a)
 #pragma unroll
             for (int e = 0; e < C::EV; e++) {
                 if (!RT || li * C::EV + e < dv) {
-                    float z = (st.acc[t][e] * ca + r0[li * C::EV + e] * cb) * inv;
+                    const float a0 = PRE0 ? p0[PRE0 ? t : 0][e] : r0[li * C::EV + e];
+                    float z = (st.acc[t][e] * ca + a0 * cb) * inv;
                     if (gt)
                         z *= sigmoid_dev(gt[e]);
                     o[e] = z;
