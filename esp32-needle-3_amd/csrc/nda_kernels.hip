@@ -867,8 +867,11 @@ constexpr int att_nw(bool long_items)
 }
 constexpr uint32_t ATT_LONG_ITEM = 448;
 
-// Positions per lane group per step: as many loads in flight as registers
-// allow without spilling (the int8 and wide-GQA states are larger).
+// Positions per lane group per step. fp16 at rep <= 2: 4 (80 registers, 6
+// waves per SIMD); 8 also fits without spilling (120 registers) but leaves 4
+// waves per SIMD, and the 4096-row decode then ran 14% slower (7.33 against
+// 6.30 ms per step): waves in flight count for more than loads per wave. The
+// int8 and wide-GQA states are larger.
 template <int ES, int REP>
 constexpr int att_np()
 {
