@@ -201,7 +201,9 @@ static int decode_check(nda_ctx *c, uint32_t layer, uint32_t nseq, const uint32_
 // for every sequence. Taken for batches of at least 4 (row,
 // kv-head) units per CU of a shape the prefill kernel is built for and the
 // MFMA GQA decode does not serve, with a prefix of at least one full key
-// tile, and not when the append is fused into the launch. Rows longer than
+// tile. A fused append stores in the own pass (the work-group whose chunk
+// holds the new slot, as in a single pass); the prefix pass reads no own
+// slot. Rows longer than
 // PREFIX_PASS_MAX_CHUNKS prefix lengths keep the single VALU pass: their own
 // positions would be cut into many short work items (a prefix's length
 // each), with partials and a merge, where the prefix is a small part of
@@ -214,9 +216,10 @@ struct PrefixSplit {
 constexpr int PREFIX_PASS_WAVES = 2;    // 64-row work-groups: more of them to spread over the CUs
 constexpr uint32_t PREFIX_PASS_MAX_CHUNKS = 4;
 
-// whether a batch's sequences qualify (append not fused; see above)
+// whether a batch's sequences qualify (see above); max_total: the longest
+// visible run
 static bool prefix_split_batch(const nda_ctx *c, uint32_t nseq, const uint32_t *ids, int32_t *pfx_out,
-                               uint32_t *nsh_out)
+                               uint32_t *nsh_out, uint32_t *max_total)
 {
     if (nseq == 0 || mfma_decode_geo(c) || !prefill_mfma_supported(c->geo) ||
         (c->cfg.flags & (NDA_FLAG_PREFILL_VALU | NDA_FLAG_DECODE_VALU)))
@@ -225,11 +228,13 @@ static bool prefix_split_batch(const nda_ctx *c, uint32_t nseq, const uint32_t *
         return false;
     int32_t pfx = -1;
     uint32_t nsh = 0;
+    *max_total = 0;
     for (uint32_t b = 0; b < nseq; b++) {
         const SeqHost &s = c->seqs[sid(ids, b)];
         if (s.prefix < 0)
             return false;
         const Vis v = visible(s, s.pos, c->cfg.window);
+        *max_total = std::max(*max_total, v.n_sh + v.n_own);
         if (b == 0) {
             pfx = s.prefix;
             nsh = v.n_sh;
@@ -242,17 +247,22 @@ static bool prefix_split_batch(const nda_ctx *c, uint32_t nseq, const uint32_t *
     return nsh >= 32;
 }
 
-static void prefix_split_plan(nda_ctx *c, uint32_t nseq, const uint32_t *ids, bool fused, uint32_t max_total,
+// whether the pass is taken: a qualifying batch whose rows run past the
+// prefix by at most PREFIX_PASS_MAX_CHUNKS - 1 prefix lengths
+static bool prefix_split_on(uint32_t nsh, uint32_t max_total)
+{
+    return max_total > nsh && (max_total + nsh - 1) / nsh <= PREFIX_PASS_MAX_CHUNKS;
+}
+
+static void prefix_split_plan(nda_ctx *c, uint32_t nseq, const uint32_t *ids, uint32_t max_total,
                               PrefixSplit &ps)
 {
     ps = PrefixSplit();
     int32_t pfx;
-    uint32_t nsh;
-    if (fused || !prefix_split_batch(c, nseq, ids, &pfx, &nsh) || max_total <= nsh)
+    uint32_t nsh, mt;
+    if (!prefix_split_batch(c, nseq, ids, &pfx, &nsh, &mt) || !prefix_split_on(nsh, max_total))
         return;
     const uint32_t chunks = (max_total + nsh - 1) / nsh;
-    if (chunks > PREFIX_PASS_MAX_CHUNKS)
-        return;
     ps.on = true;
     ps.prefix = pfx;
     ps.n_sh = nsh;
@@ -326,12 +336,12 @@ static void decode_totals(const nda_ctx *c, uint32_t nseq, const uint32_t *ids, 
 // The device buffers a decode of these sequences needs (row staging, split
 // partials, the shared-prefix pass's partials and work list), grown before a
 // call changes any state; psp: the shared-prefix pass plan.
-static int decode_reserve(nda_ctx *c, uint32_t nseq, const uint32_t *ids, bool fused, uint32_t max_total,
+static int decode_reserve(nda_ctx *c, uint32_t nseq, const uint32_t *ids, uint32_t max_total,
                           uint64_t sum_total, PrefixSplit &psp)
 {
     if (int rc = reserve_attend(c, nseq, ids != nullptr, max_total, sum_total))
         return rc;
-    prefix_split_plan(c, nseq, ids, fused, max_total, psp);
+    prefix_split_plan(c, nseq, ids, max_total, psp);
     if (psp.on) {
         if (int rc = ensure_part(c, (size_t)nseq * c->cfg.n_heads * psp.max_chunks * (c->cfg.v_head_dim + 2)))
             return rc;
@@ -366,7 +376,7 @@ int decode_impl(nda_ctx *c, uint32_t layer, uint32_t nseq, const uint32_t *ids, 
     if (int rc = decode_check(c, layer, nseq, ids, q, out, &max_total, &sum_total))
         return rc;
     PrefixSplit psp;
-    if (int rc = decode_reserve(c, nseq, ids, k != nullptr, max_total, sum_total, psp))
+    if (int rc = decode_reserve(c, nseq, ids, max_total, sum_total, psp))
         return rc;
     txn.commit();
     if (k)
@@ -455,8 +465,11 @@ int nda_decode_noalloc(nda_ctx *c, uint32_t layer, uint32_t nseq, const uint32_t
 // two launches: a store plus barrier at the head of every one of tens of
 // thousands of work-groups costs more than the separate append kernel; GQA
 // groups the MFMA decode serves switch to it (and so to two launches) from
-// 4 work items per CU, and so do batches on one shared prefix that its
-// decode pass serves.
+// 4 work items per CU. Batches on one shared prefix that its decode pass
+// serves fuse the store into the own-positions pass: about the same GPU
+// time as a separate append (1024 sequences on a 213-token prefix: 53.6-56.2
+// against 54.4 us per layer step), one launch fewer to enqueue (whole steps
+// 1.65-1.70 M against 1.23-1.45 M tokens/s, host-bound).
 int nda_step(nda_ctx *c, uint32_t layer, uint32_t nseq, const uint32_t *ids, const float *q,
              const float *k, const float *v, const float *gate, float *out, void *stream)
 {
@@ -464,9 +477,11 @@ int nda_step(nda_ctx *c, uint32_t layer, uint32_t nseq, const uint32_t *ids, con
         return fail(c, NDA_ERR_ARG, "null k/v");
     const uint64_t units = c ? (uint64_t)nseq * c->cfg.n_kv_heads : 0;
     int32_t pfx;
-    uint32_t nsh;
-    if (c && (units >= 16ull * (uint64_t)c->cus || (mfma_decode_geo(c) && units >= 4ull * (uint64_t)c->cus) ||
-              (check_ids(c, nseq, ids) == NDA_OK && prefix_split_batch(c, nseq, ids, &pfx, &nsh)))) {
+    uint32_t nsh, mt;
+    if (c && layer < c->cfg.n_layers && check_ids(c, nseq, ids) == NDA_OK &&
+        prefix_split_batch(c, nseq, ids, &pfx, &nsh, &mt) && prefix_split_on(nsh, mt))
+        return decode_impl(c, layer, nseq, ids, q, k, v, gate, out, stream);
+    if (c && (units >= 16ull * (uint64_t)c->cus || (mfma_decode_geo(c) && units >= 4ull * (uint64_t)c->cus))) {
         // The decode's buffers first: once the append has stored this
         // position, a decode that fails for want of memory would leave the
         // step half done.
@@ -475,7 +490,7 @@ int nda_step(nda_ctx *c, uint32_t layer, uint32_t nseq, const uint32_t *ids, con
             uint64_t sum_total;
             decode_totals(c, nseq, ids, &max_total, &sum_total);
             PrefixSplit psp;
-            if (int rc = decode_reserve(c, nseq, ids, false, max_total, sum_total, psp))
+            if (int rc = decode_reserve(c, nseq, ids, max_total, sum_total, psp))
                 return rc;
         }
         if (int rc = nda_kv_append(c, layer, nseq, ids, k, v, stream))
