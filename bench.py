@@ -462,7 +462,10 @@ def shared_prefix_leg(N, stream, nseq=1024, npre=213, nmin=32, nmax=64, dsteps=6
     ctx.sync(stream)
     pf_flops = float(sum(H * 2 * (D + D) * (npre * int(x) + int(x) * (int(x) + 1) / 2) for x in n))
     pf_unique = (npre + int(n.sum())) * 2048 + int(n.sum()) * H * D * 4 * 2   # K/V once + q, out
-    ctx.prof_read(reset=True)
+    # the dsteps decode steps timed with the per-kernel events off (each
+    # event pair adds enqueue work to these host-bound steps), then the
+    # per-kernel split from psteps further steps with them on
+    ctx.prof_enable(False)
     t0 = time.perf_counter()
     for _ in range(dsteps):
         for li in range(layers):
@@ -470,13 +473,23 @@ def shared_prefix_leg(N, stream, nseq=1024, npre=213, nmin=32, nmax=64, dsteps=6
         ctx.advance(nseq, None, 1, stream=stream)
     ctx.sync(stream)
     t_dec = time.perf_counter() - t0
+    psteps = 8
+    ctx.prof_enable(True)
+    ctx.prof_read(reset=True)
+    for _ in range(psteps):
+        for li in range(layers):
+            ctx.step(li, nseq, q, k, v, out, stream=stream)
+        ctx.advance(nseq, None, 1, stream=stream)
+    ctx.sync(stream)
     ms2, launches2 = ctx.prof_read(reset=True)
     ctx.prof_enable(False)
     # per layer and step: every decode launch (with a shared prefix, the
-    # prefix pass and the own-positions pass) and the merge
-    dec_ms = (ms2[N.K_DECODE] + ms2[N.K_COMBINE]) / (dsteps * layers)
-    # per decode step: the prefix once + every sequence's own positions
-    own = sum(int(x) + s + 1 for x in n for s in range(dsteps)) / dsteps
+    # prefix pass and the own-positions pass, which stores the new row) and
+    # the merge
+    dec_ms = (ms2[N.K_DECODE] + ms2[N.K_COMBINE]) / (psteps * layers)
+    # per profiled decode step: the prefix once + every sequence's own
+    # positions (steps dsteps .. dsteps + psteps - 1)
+    own = sum(int(x) + dsteps + s + 1 for x in n for s in range(psteps)) / psteps
     uniq = npre * 2048 + own * 2048 + nseq * H * D * 4 * 2
     logical = nseq * npre * 2048 + own * 2048 + nseq * H * D * 4 * 2
     import ndoracle as O
@@ -501,6 +514,7 @@ def shared_prefix_leg(N, stream, nseq=1024, npre=213, nmin=32, nmax=64, dsteps=6
             "prefill_wall_ms": round(t_pf * 1e3, 2),
             "decode_tokens_per_s": round(nseq * dsteps / t_dec, 1),
             "decode_kernel_ms": round(dec_ms, 4),
+            "decode_kernel_note": "per layer step, from %d further steps with per-kernel events" % psteps,
             "decode_unique_GBps": round(uniq / (dec_ms * 1e-3) / 1e9, 1),
             "decode_logical_GBps": round(logical / (dec_ms * 1e-3) / 1e9, 1),
             "max_abs_delta_sampled": worst}
