@@ -171,7 +171,9 @@ __device__ __forceinline__ void attn_step(AttnState<ES, DK, DV, REP, G, NP, NW> 
         const int32_t page = (!MASK || blk < s1) ? pages[blk >> a.pg.log2_page] : -1;
         if (page >= 0) {
             const uint8_t *hb = a.pool + (uint64_t)page * a.pg.page_bytes + (uint64_t)g * a.pg.head_bytes;
-            const int off = s & (P - 1);
+            // a masked lane reads the nearest slot in [s0, s1), inside the
+            // same block, so that HBM serves only visible slots
+            const int off = (MASK ? min(max(s, s0), s1 - 1) : s) & (P - 1);
             const uint8_t *kp = hb + (uint64_t)off * dk * ES + li * C::KB;
             const uint8_t *vp = hb + (uint64_t)P * dk * ES + (uint64_t)off * dv * ES + li * C::VB;
             if constexpr (RT) {
