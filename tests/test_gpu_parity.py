@@ -380,7 +380,8 @@ def test_shared_prefix_decode_pass(kv_dtype, geom, npre, own_max, W, extra):
     277-slot window (213 sinks, the 64-slot minimum ring) and 30 more decode
     steps first, the own ring wraps. Every row against the
     oracle, gated and not; the pass is taken (two decode launches per call,
-    a merge launch only when some row has more than two chunks)."""
+    the second storing the new row, no append launch, a merge launch only
+    when some row has more than two chunks)."""
     nh, nkv, dk, dv = geom
     say("shared prefix decode pass", kv_dtype, geom, npre, own_max, W)
     N = nda()
@@ -431,6 +432,7 @@ def test_shared_prefix_decode_pass(kv_dtype, geom, npre, own_max, W, extra):
         tot = max(npre + min(ctx.seq_state(b)[0] + 1 - npre, W - npre) for b in range(B))
         max_chunks = -(-tot // npre)
         assert launches[N.K_DECODE] == 2, list(launches)
+        assert launches[N.K_APPEND] == 0, list(launches)
         assert launches[N.K_COMBINE] == (1 if max_chunks > 2 else 0), list(launches)
         got = dout.to_array(np.float32, (B, nh * dv))
         for b in range(B):
