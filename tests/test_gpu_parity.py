@@ -369,7 +369,7 @@ def test_shared_prefix_prefill_then_decode(kv_dtype):
 @pytest.mark.parametrize("kv_dtype,geom,npre,own_max,W,extra", [
     (O.KV_F16, (8, 8, 64, 64), 213, 40, 384, 0), (O.KV_INT8, (8, 8, 64, 64), 213, 40, 384, 0),
     (O.KV_F16, (8, 4, 64, 64), 213, 40, 384, 0), (O.KV_F16, (8, 8, 64, 64), 40, 100, 384, 0),
-    (O.KV_INT8, (8, 8, 64, 64), 213, 64, 277, 30)])
+    (O.KV_INT8, (8, 8, 64, 64), 213, 64, 277, 30), (O.KV_F16, (8, 8, 64, 64), 100, 250, 384, 0)])
 def test_shared_prefix_decode_pass(kv_dtype, geom, npre, own_max, W, extra):
     """A decode batch whose sequences all share one prefix (at least 4
     (row, kv-head) units per CU) attends the prefix in one MFMA pass over all
@@ -378,7 +378,9 @@ def test_shared_prefix_decode_pass(kv_dtype, geom, npre, own_max, W, extra):
     own-positions pass; with a 40-slot prefix and up to 101 own positions
     other rows have up to four and go through the merge kernel. With a
     277-slot window (213 sinks, the 64-slot minimum ring) and 30 more decode
-    steps first, the own ring wraps. Every row against the
+    steps first, the own ring wraps; with a 100-slot prefix and up to 250
+    own positions, rows of three and four chunks go through the merge
+    kernel. Every row against the
     oracle, gated and not; the pass is taken (two decode launches per call,
     the second storing the new row, no append launch, a merge launch only
     when some row has more than two chunks)."""
