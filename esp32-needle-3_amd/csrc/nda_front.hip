@@ -46,6 +46,8 @@ struct FrontShape {
     static_assert(W <= 4, "one group per thread");
 };
 
+typedef float float4v __attribute__((ext_vector_type(4)));
+
 __device__ __forceinline__ float4 ld4(const float *p) { return *reinterpret_cast<const float4 *>(p); }
 
 __device__ __forceinline__ void acc4(float4 &a, const float4 &w, const float4 &x)
@@ -144,8 +146,11 @@ __global__ __launch_bounds__((64 * FrontShape<DK, DV, REP>::W)) void front_kerne
                                      : ld4(hist + (uint64_t)((pos - j) % taps) * dcol + gc);
             acc4(acc, wj, xj);
         }
+        // the raw row into the tap history, read again only at the next
+        // step's front: streamed past L2 (2-6% off the 4096-row front)
         if (a.hist_write)
-            *reinterpret_cast<float4 *>(hist + (uint64_t)(pos % taps) * dcol + gc) = raw;
+            __builtin_nontemporal_store(float4v{raw.x, raw.y, raw.z, raw.w},
+                                        reinterpret_cast<float4v *>(hist + (uint64_t)(pos % taps) * dcol + gc));
         if (lc < (REP + 1) * DK) {
             const int o = (lc / DK) * S::STRIDE + lc % DK;
             *reinterpret_cast<float4 *>(ylds + o) = acc;
