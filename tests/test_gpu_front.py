@@ -170,6 +170,60 @@ def test_front_multi_token_chunk(shape, kv_dtype):
             assert np.array_equal(bits(ctx.front_hist(b)), bits(want)), (rnd, b)
 
 
+@pytest.mark.parametrize("shape,kv_dtype", [((12, 2, 48, 64), O.KV_F16), ((12, 2, 48, 64), O.KV_INT8),
+                                             ((8, 8, 64, 64), O.KV_F16)])
+def test_front_multi_token_large_launch(shape, kv_dtype):
+    """A multi-token front launch of at least 4096 (row, kv group) units runs
+    two rows per work-group: bit-exact against the token-by-token oracle over
+    an odd row count (the last work-group's second row is past the end),
+    sequences of 0 and 1 tokens (pairs straddle sequences) and a second round
+    reading the history the first one left."""
+    N = nda()
+    say("front multi-token large launch", shape, kv_dtype)
+    rng = np.random.default_rng(17)
+    nh, nkv, qk, vd = shape
+    L, W, taps, theta = 1, 256, 3, 10000.0
+    B = 48 if nkv == 2 else 16
+    n_tok = [int(x) for x in rng.integers(20, 90, B)]
+    n_tok[3], n_tok[7], n_tok[8] = 0, 1, 1
+    if sum(n_tok) % 2 == 0:
+        n_tok[0] += 1
+    T = sum(n_tok)
+    assert T * nkv >= 4096 and T % 2 == 1
+    starts = [int(x) for x in rng.integers(0, 40, B)]
+    fw = make_weights(rng, L, nh, nkv, qk, vd, taps)
+    ctx = front_ctx(N, L, nh, nkv, qk, vd, W, kv_dtype, B, taps, theta, fw)
+    orc = oracle_sessions(B, (L, nh, nkv, qk, vd, W), kv_dtype, taps, theta)
+    dq, dk, dv = nh * qk, nkv * qk, nkv * vd
+    for b, p in enumerate(starts):
+        ctx.seq_set_pos(b, p)
+        orc[b].s.pos = p
+    for rnd in range(2):
+        q = rng.standard_normal((T, dq)).astype(np.float32)
+        k = rng.standard_normal((T, dk)).astype(np.float32)
+        v = rng.standard_normal((T, dv)).astype(np.float32)
+        bq, bk, bv = N.DevBuf.from_array(q), N.DevBuf.from_array(k), N.DevBuf.from_array(v)
+        oq, ok_, ov = (N.DevBuf(T * d * 4) for d in (dq, dk, dv))
+        ctx.front(0, B, bq, bk, bv, oq, ok_, ov, n_tokens=n_tok)
+        ctx.sync()
+        gq, gk, gv = oq.to_array(np.float32, (T, dq)), ok_.to_array(np.float32, (T, dk)), \
+            ov.to_array(np.float32, (T, dv))
+        r = 0
+        for b in range(B):
+            for t in range(n_tok[b]):
+                wq, wk, wv = orc[b].front(0, fw, q[r], k[r], v[r])
+                assert np.array_equal(bits(gq[r]), bits(wq)), (rnd, b, t)
+                assert np.array_equal(bits(gk[r]), bits(wk)), (rnd, b, t)
+                assert np.array_equal(bits(gv[r]), bits(wv)), (rnd, b, t)
+                orc[b].step_end()
+                r += 1
+        for b in range(B):
+            if n_tok[b]:
+                ctx.advance(1, seq_ids=[b], n=n_tok[b])
+            want = np.concatenate([h.reshape(L, taps, -1) for h in orc[b].hist()], axis=2)
+            assert np.array_equal(bits(ctx.front_hist(b)), bits(want)), (rnd, b)
+
+
 @pytest.mark.parametrize("shape,kv_dtype", [((8, 2, 64, 64), O.KV_INT8), ((8, 2, 64, 64), O.KV_F16),
                                              ((10, 2, 36, 20), O.KV_INT8), ((7, 1, 64, 64), O.KV_F16)])
 def test_attention_batched_sessions(shape, kv_dtype):
