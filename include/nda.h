@@ -174,8 +174,9 @@ int nda_decode_noalloc(nda_ctx *ctx, uint32_t layer, uint32_t nseq, const uint32
                        const float *q, const float *gate, float *out, void *stream);
 
 /* nda_kv_append + nda_decode, in the order attention() runs them (store
- * first; the current token is attended). Small batches run it as one fused
- * launch, large ones as the two kernels; the results are the same. */
+ * first; the current token is attended). Small batches, and batches on one
+ * shared prefix that take the prefix pass, store inside the decode launch;
+ * other large ones run the two kernels; the results are the same. */
 int nda_step(nda_ctx *ctx, uint32_t layer, uint32_t nseq, const uint32_t *seq_ids,
              const float *q, const float *k, const float *v, const float *gate,
              float *out, void *stream);
