@@ -1,7 +1,7 @@
 /* nd_oracle.c - CPU restatement of the Needle attention / KV-cache path.
  *
- * TEST INFRASTRUCTURE ONLY (see nd_oracle.h): the checker for libndattn, never
- * part of the product. Must be compiled with -ffp-contract=off so that every
+ * TEST INFRASTRUCTURE ONLY (see nd_oracle.h): the oracle libndattn is tested
+ * against, never part of the product. Must be compiled with -ffp-contract=off so that every
  * multiply and add rounds separately, as the reference's x86 host build does
  * (host/CMakeLists.txt:4-11: C99, no FMA target flags).
  */

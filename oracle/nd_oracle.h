@@ -1,6 +1,6 @@
 /* nd_oracle.h - CPU restatement of the Needle engine's attention / KV-cache path.
  *
- * TEST INFRASTRUCTURE ONLY. This is the checker the HIP library is compared
+ * TEST INFRASTRUCTURE ONLY. This is the oracle the HIP library is compared
  * against; only tests/, the package smoke check and bench.py's cpu_baseline leg
  * may load it. The product (libndattn) never links or calls it.
  *
