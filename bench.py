@@ -1007,7 +1007,7 @@ def main():
                     help="run only this leg and print its JSON object (for profiling one kernel family)")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
-        print("bench.py measures one GPU: this build has no multi-GPU path "
+        print("bench.py measures one GPU: this library has no multi-GPU path "
               "(decode would shard by sequence with no exchange between GPUs)", file=sys.stderr)
         sys.exit(2)
 

@@ -1,6 +1,6 @@
 """Writes tests/golden/golden.npz from the reference engine's own attention
 code (oracle/_ref/libndref.so, compiled by oracle/ref.mk from the reference
-sources). Run in the build container, where the reference tree exists:
+sources). Run where the reference tree exists (/root/reference):
 
     make -C oracle && python tests/golden/gen_golden.py
 
