@@ -216,8 +216,8 @@ struct PrefixSplit {
 constexpr int PREFIX_PASS_WAVES = 2;    // 64-row work-groups: more of them to spread over the CUs
 constexpr uint32_t PREFIX_PASS_MAX_CHUNKS = 4;
 
-// whether a batch's sequences qualify (see above); max_total: the longest
-// visible run
+// whether a batch's sequences qualify (see above); max_total (may be null):
+// the longest visible run
 static bool prefix_split_batch(const nda_ctx *c, uint32_t nseq, const uint32_t *ids, int32_t *pfx_out,
                                uint32_t *nsh_out, uint32_t *max_total)
 {
@@ -227,14 +227,13 @@ static bool prefix_split_batch(const nda_ctx *c, uint32_t nseq, const uint32_t *
     if ((uint64_t)nseq * c->cfg.n_kv_heads < 4ull * (uint64_t)c->cus)
         return false;
     int32_t pfx = -1;
-    uint32_t nsh = 0;
-    *max_total = 0;
+    uint32_t nsh = 0, mt = 0;
     for (uint32_t b = 0; b < nseq; b++) {
         const SeqHost &s = c->seqs[sid(ids, b)];
         if (s.prefix < 0)
             return false;
         const Vis v = visible(s, s.pos, c->cfg.window);
-        *max_total = std::max(*max_total, v.n_sh + v.n_own);
+        mt = std::max(mt, v.n_sh + v.n_own);
         if (b == 0) {
             pfx = s.prefix;
             nsh = v.n_sh;
@@ -244,6 +243,8 @@ static bool prefix_split_batch(const nda_ctx *c, uint32_t nseq, const uint32_t *
     }
     *pfx_out = pfx;
     *nsh_out = nsh;
+    if (max_total)
+        *max_total = mt;
     return nsh >= 32;
 }
 
@@ -259,8 +260,8 @@ static void prefix_split_plan(nda_ctx *c, uint32_t nseq, const uint32_t *ids, ui
 {
     ps = PrefixSplit();
     int32_t pfx;
-    uint32_t nsh, mt;
-    if (!prefix_split_batch(c, nseq, ids, &pfx, &nsh, &mt) || !prefix_split_on(nsh, max_total))
+    uint32_t nsh;
+    if (!prefix_split_batch(c, nseq, ids, &pfx, &nsh, nullptr) || !prefix_split_on(nsh, max_total))
         return;
     const uint32_t chunks = (max_total + nsh - 1) / nsh;
     ps.on = true;
