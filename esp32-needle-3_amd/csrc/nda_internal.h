@@ -271,8 +271,9 @@ hipError_t launch_append(const Geo &g, const AppendArgs &a, hipStream_t s);
 hipError_t launch_attend(const Geo &g, const AttnArgs &a, hipStream_t s);
 hipError_t launch_prefill(const Geo &g, const PrefillArgs &a, int waves, hipStream_t s);
 /* Largest prefill tile table (PrefillArgs::tab_cap * 16 bytes) a work-group
- * size can take; a launch whose table would be larger runs without one. */
-uint32_t pf_tab_max_bytes(int waves);
+ * size can take (dma: tiles loaded straight into LDS, fp16 at qk 64); a
+ * launch whose table would be larger runs without one. */
+uint32_t pf_tab_max_bytes(int waves, bool dma);
 /* GQA decode on MFMA: one wave per (row, kv-head) item, n_items = rows * nkv,
  * items in (row, kv-head) order; a.row_seq as in AttnArgs. */
 bool decode_mfma_supported(const Geo &g);

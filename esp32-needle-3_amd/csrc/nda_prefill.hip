@@ -88,6 +88,42 @@ __device__ __forceinline__ half4 tr16_read(const _Float16 *p)
     return __builtin_bit_cast(half4, w);
 }
 
+// s_waitcnt vmcnt(0), the other counters unconstrained (gfx9 encoding:
+// vmcnt bits 3:0 and 15:14, expcnt 6:4, lgkmcnt 11:8), fenced so that
+// neither the optimiser nor the scheduler moves memory accesses across it
+__device__ __forceinline__ void wait_vmcnt0()
+{
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_sched_barrier(0);
+    __builtin_amdgcn_s_waitcnt((7 << 4) | (15 << 8));
+    __builtin_amdgcn_sched_barrier(0);
+    asm volatile("" ::: "memory");
+}
+
+typedef __attribute__((address_space(3))) void lds_void;
+
+__device__ __forceinline__ uint32_t lds_addr(const void *p)
+{
+    return (uint32_t)(uintptr_t)(lds_void *)p;
+}
+
+// A direct-to-LDS load: lane l's 16 bytes at base + voff land at LDS byte
+// m0 + 16 l. Issued from inline asm, which the compiler's wait insertion
+// does not follow into LDS: without alias information it would wait for
+// every such load in flight before any LDS read. The caller waits for
+// completion (wait_vmcnt0); waits the compiler places for its own loads stay
+// correct, since extra loads in the in-order count only make them stricter.
+// m0 is written by a scalar instruction one wait state ahead of the load
+// (nothing else in this kernel uses m0).
+#pragma clang diagnostic push
+#pragma clang diagnostic ignored "-Winline-asm"
+__device__ __forceinline__ void lds_dma16(const uint8_t *base, uint32_t voff, uint32_t m0)
+{
+    asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, %1" ::"v"(voff), "s"(base), "s"(m0)
+                 : "memory", "m0");
+}
+#pragma clang diagnostic pop
+
 __device__ __forceinline__ float16v mfma32(half8 a, half8 b, float16v c)
 {
     return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
@@ -135,7 +171,20 @@ __device__ __forceinline__ void static_for(F &&f)
 // that page's kv-head block. A thread's share of a tile is a few 16-byte
 // chunks of those runs at offsets fixed for the launch, from one base per
 // half tile that one scalar page-table read gives.
-template <int ES, int DK, int DV, int NTHR>
+// DMA: fp16 rows of 64 halves go from global memory straight into LDS
+// (global_load_lds_dwordx4), with no staging registers, for 2- and 4-wave
+// groups with a tile table, which then fit 4 waves per SIMD instead of 3 (a
+// shared-prefix prefill of 48-token suffixes: 0.112-0.114 against
+// 0.118-0.119 ms). One buffer is then K [32][64] and V [32][64] halves,
+// unpadded, a row's 16-byte chunk c at chunk position c ^ (row % 8) (see
+// PfIO::load_lds). The 8-wave groups, at 4 waves per SIMD either way, keep
+// their one staged chunk per thread: direct loads made the 512-token chunk
+// 3% slower (563-566 against 581-585 TFLOP/s). Without a table the page ids'
+// ring spills at 128 registers, so those groups stay staged too.
+template <int ES, int DK, int DV, int NTHR, bool TAB>
+constexpr bool pf_direct = ES == 2 && DK == 64 && DV == 64 && NTHR < 512 && TAB;
+
+template <int ES, int DK, int DV, int NTHR, bool DIRECT = false>
 struct PfTile {
     static constexpr int KPAD = DK + 8;        // halves per K row in LDS
     static constexpr int VPAD = DV + 8;        // halves per V row in LDS (row-major; read transposed)
@@ -144,9 +193,11 @@ struct PfTile {
     static constexpr int HCH = 16 * (KC + VC) + (ES == 1 ? 8 : 0);   // chunks of a half tile
     static constexpr int HP = (HCH + 63) / 64 * 64;   // padded to whole waves: a wave's chunks share a half
     static constexpr int CPT = (2 * HP + NTHR - 1) / NTHR;             // chunks per thread
-    // one LDS buffer: K [32][KPAD] halves, V [32][VPAD] halves, k scales, v scales
-    static constexpr int VOFF = PF_KT * KPAD * 2, SOFF = VOFF + PF_KT * VPAD * 2;
-    static constexpr int BUF = SOFF + 2 * PF_KT * 4;
+    static constexpr bool DMA = DIRECT;   // see pf_direct
+    // one LDS buffer otherwise: K [32][KPAD] halves, V [32][VPAD] halves,
+    // k scales, v scales
+    static constexpr int VOFF = DMA ? PF_KT * 128 : PF_KT * KPAD * 2, SOFF = VOFF + PF_KT * VPAD * 2;
+    static constexpr int BUF = DMA ? 2 * PF_KT * 128 : SOFF + 2 * PF_KT * 4;
     static_assert(DK * ES % 16 == 0 && DV * ES % 16 == 0, "rows are whole 16-byte chunks");
     static_assert(NTHR % 64 == 0 && BUF % 16 == 0, "");
 };
@@ -220,7 +271,7 @@ __device__ __forceinline__ PfChunk pf_chunk(int tid, int wave, uint32_t P)
 
 template <int ES, int DK, int DV, int NTHR, bool TAB>
 struct PfIO {
-    using T = PfTile<ES, DK, DV, NTHR>;
+    using T = PfTile<ES, DK, DV, NTHR, pf_direct<ES, DK, DV, NTHR, TAB>>;
     // A tile's page ids and first in-page slots (uniform), as read a tile
     // before its data is requested: the ids are used only then, so their
     // reads have a tile to land. They are vector loads (of one address):
@@ -330,6 +381,37 @@ struct PfIO {
         });
         sg.vlim = r.vlim;
     }
+    // DMA: tile r straight into LDS buffer buf, from inside its tile j-1
+    // (the buffer's last readers passed the barrier that ended tile j-2).
+    // The buffer is eight 1 KiB blocks: K rows 8 b .. 8 b + 7 in block b < 4,
+    // V rows 8 (b - 4) on in the others, each block 8 consecutive slots of
+    // one page's kv-head block (a half tile is 16 slots of one page). One
+    // load per block: lane l lands at byte 16 l of it, as row l / 8, chunk
+    // position l % 8, and reads that row's chunk (l % 8) ^ (l / 8) (loff), so
+    // row k's chunk c sits at position c ^ (k % 8) and the K and transposed
+    // V reads spread over the banks without padding. Rows past the tile's
+    // segment end are not loaded and keep finite values (see store). The
+    // caller waits (wait_vmcnt0) before the barrier that publishes the tile.
+    __device__ __forceinline__ void load_lds(const TileRef &r, uint8_t *buf, uint32_t loff) const
+    {
+        static_assert(T::DMA, "direct loads: fp16 rows of 64 halves");
+        constexpr int W = NTHR / 64;
+        const uint32_t P = 1u << log2_page;
+        const uint32_t p0 = __builtin_amdgcn_readfirstlane(r.p0), p1 = __builtin_amdgcn_readfirstlane(r.p1);
+        const uint8_t *hb0 = pool + ((uint64_t)p0 * page_bytes + head_off);
+        const int64_t dhb = ((int64_t)p1 - (int64_t)p0) * (int64_t)page_bytes;
+        const int vlim = __builtin_amdgcn_readfirstlane(r.vlim);
+        const int lane = tid & 63;
+#pragma unroll
+        for (int i = 0; i < 8 / W; i++) {
+            const int b = wave + W * i;                 // uniform
+            const int half = (b >> 1) & 1;
+            const uint32_t slot = __builtin_amdgcn_readfirstlane(r.sip0 + (half ? r.dsip : 0u) + 8u * (uint32_t)(b & 1));
+            const uint8_t *base = hb0 + (half ? dhb : 0) + (b >= 4 ? P * 128u : 0u) + slot * 128u;
+            if (8 * (b & 3) + (lane >> 3) < vlim)
+                lds_dma16(base, loff, lds_addr(buf + 1024 * b));
+        }
+    }
     // A staged tile's chunks into LDS buffer buf. Keys past the tile's
     // segment end (a partial tile: surplus slots of the same pages, whose
     // contents may be anything) must not bring non-finite values, which a
@@ -372,11 +454,14 @@ struct PfIO {
     }
 };
 
+// 4 waves per SIMD for 8-wave groups and for direct-loaded tiles (no
+// staging registers); 3 otherwise (about 160 registers)
 template <int ES, int DK, int DV, int REP, int W, bool TAB>
-__global__ __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(W >= 8 ? 4 : 3)))
+__global__ __launch_bounds__(64 * W)
+__attribute__((amdgpu_waves_per_eu(W >= 8 || pf_direct<ES, DK, DV, 64 * W, TAB> ? 4 : 3)))
 void prefill_kernel(PrefillArgs a)
 {
-    using T = PfTile<ES, DK, DV, 64 * W>;
+    using T = PfTile<ES, DK, DV, 64 * W, pf_direct<ES, DK, DV, 64 * W, TAB>>;
     static_assert(DK % 16 == 0 && DV == 64, "prefill tiles: dk multiple of 16, dv 64");
     constexpr int ROWS = 32 * W;
     constexpr int NKB = DK / 16;               // k-blocks of the QK MFMA
@@ -476,10 +561,31 @@ void prefill_kernel(PrefillArgs a)
     Staged<T::CPT> sg;
     // TAB: nxt is the table entry of the tile the next load brings, read
     // before each tile's barrier (whose fence waits for it) and made uniform
-    // at the load; without a table, page ids sit in a ring indexed by tile
-    // parity
+    // at the load (DMA: made uniform at once, nref, so that it waits in
+    // scalar registers); without a table, page ids sit in a ring indexed by
+    // tile parity
     uint4 nxt = {};
-    if constexpr (TAB) {
+    typename PfIO<ES, DK, DV, NTHR, TAB>::TileRef nref = {};
+    // DMA: lane's source chunk within a 1 KiB block (see PfIO::load_lds)
+    const uint32_t loff = (uint32_t)(lane >> 3) * 128u + 16u * (uint32_t)((lane & 7) ^ (lane >> 3));
+    if constexpr (T::DMA) {
+        typename PfIO<ES, DK, DV, NTHR, TAB>::TileRef r0;
+        if constexpr (TAB) {
+            r0 = io.uniform(io.tab[0]);
+            nref = io.uniform(io.tab[min(1, io.tab_n - 1)]);
+        } else {
+            io.fetch(0, prn[0]);
+            io.fetch(1, prn[1]);
+            r0 = prn[0];
+        }
+        // buffer 1, and buffer 0's rows past tile 0's segment end (which
+        // its load leaves alone), start as zeros (see PfIO::store)
+        const int vlim0 = __builtin_amdgcn_readfirstlane(r0.vlim);
+        for (int o = tid; o < 2 * T::BUF / 16; o += NTHR)
+            if (o >= T::BUF / 16 || ((o >> 3) & (PF_KT - 1)) >= vlim0)
+                *reinterpret_cast<u32x4 *>(&kvbuf[0][0] + 16 * o) = u32x4{0u, 0u, 0u, 0u};
+        io.load_lds(r0, kvbuf[0], loff);        // tile 0
+    } else if constexpr (TAB) {
         io.load(io.uniform(io.tab[0]), sg);     // tile 0
         nxt = io.tab[min(1, io.tab_n - 1)];
     } else {
@@ -523,11 +629,15 @@ void prefill_kernel(PrefillArgs a)
         }
     }
 
-    io.template store<true>(sg, kvbuf[0]);
-    if constexpr (ES == 2) {
-        // the other buffer starts as zeros (see PfIO::store)
-        for (int o = 16 * tid; o < T::BUF; o += 16 * NTHR)
-            *reinterpret_cast<u32x4 *>(kvbuf[1] + o) = u32x4{0u, 0u, 0u, 0u};
+    if constexpr (T::DMA) {
+        wait_vmcnt0();
+    } else {
+        io.template store<true>(sg, kvbuf[0]);
+        if constexpr (ES == 2) {
+            // the other buffer starts as zeros (see PfIO::store)
+            for (int o = 16 * tid; o < T::BUF; o += 16 * NTHR)
+                *reinterpret_cast<u32x4 *>(kvbuf[1] + o) = u32x4{0u, 0u, 0u, 0u};
+        }
     }
     __syncthreads();
 
@@ -543,7 +653,12 @@ void prefill_kernel(PrefillArgs a)
         // the data of tile j+1 (past the last tile: the last tile again,
         // never stored); without a table, first the ids of tile j+2 into the
         // slot of tile j's (spent)
-        if constexpr (TAB) {
+        if constexpr (T::DMA) {
+            if constexpr (!TAB)
+                io.fetch(j + 2, prn[PJ]);
+            if (j + 1 < ntile)
+                io.load_lds(TAB ? nref : prn[Q1], kvbuf[Q1], loff);
+        } else if constexpr (TAB) {
             io.load(io.uniform(nxt), sg);
         } else {
             io.fetch(j + 2, prn[PJ]);
@@ -570,7 +685,8 @@ void prefill_kernel(PrefillArgs a)
         __builtin_amdgcn_s_setprio(0);
 #pragma unroll
         for (int kb = 0; kb < NKB; kb++) {
-            const half8 ka = *reinterpret_cast<const half8 *>(&Ks[ln][16 * kb + 8 * jh]);
+            const half8 ka = T::DMA ? *reinterpret_cast<const half8 *>(kvbuf[PJ] + ln * 128 + 16 * ((2 * kb + jh) ^ (ln & 7)))
+                                    : *reinterpret_cast<const half8 *>(&Ks[ln][16 * kb + 8 * jh]);
             st = mfma32(ka, qh[kb], st);
             st = mfma32(ka, ql[kb], st);
         }
@@ -713,9 +829,14 @@ void prefill_kernel(PrefillArgs a)
                 // in each 16-lane group ds_read_b64_tr_b16 gives output lane i
                 // element j from the address of lane 4 j + i / 4 (plus i % 4),
                 // so lane (j, q) of the group points at key j, dims 4 q on
-                const _Float16 *vr = &Vr[16 * kb2 + 4 * jh + ((lane >> 2) & 3)][32 * dt + 16 * ((lane >> 4) & 1) + 4 * (lane & 3)];
+                // (DMA: row k's 16-byte chunk c at position c ^ (k % 8), the
+                // same for the rows 8 on)
+                const int vk = 16 * kb2 + 4 * jh + ((lane >> 2) & 3);
+                const int vc = 4 * dt + 2 * ((lane >> 4) & 1) + ((lane & 3) >> 1);
+                const _Float16 *vr = T::DMA ? reinterpret_cast<const _Float16 *>(kvbuf[PJ] + T::VOFF + vk * 128 + 16 * (vc ^ (vk & 7)) + 8 * (lane & 1))
+                                            : &Vr[vk][32 * dt + 16 * ((lane >> 4) & 1) + 4 * (lane & 3)];
                 const half4 v0 = tr16_read(vr);
-                const half4 v1 = tr16_read(vr + 8 * T::VPAD);
+                const half4 v1 = tr16_read(vr + (T::DMA ? 8 * 64 : 8 * T::VPAD));
                 const half8 va = {v0[0], v0[1], v0[2], v0[3], v1[0], v1[1], v1[2], v1[3]};
                 if (dt == 0) {
                     acc0 = mfma32(va, ph, acc0);
@@ -729,9 +850,13 @@ void prefill_kernel(PrefillArgs a)
                 __builtin_amdgcn_sched_barrier(0);
         }
         __builtin_amdgcn_s_setprio(0);
-        if (j + 1 < ntile)   // tile j+1 into the other buffer (its readers are done)
+        if constexpr (T::DMA)
+            wait_vmcnt0();       // tile j+1's direct loads have landed
+        else if (j + 1 < ntile)  // tile j+1 into the other buffer (its readers are done)
             io.template store<false>(sg, kvbuf[Q1]);
-        if constexpr (TAB)
+        if constexpr (TAB && T::DMA)
+            nref = io.uniform(io.tab[min(j + 2, io.tab_n - 1)]);
+        else if constexpr (TAB)
             nxt = io.tab[min(j + 2, io.tab_n - 1)];
         __syncthreads();
     };
@@ -777,31 +902,42 @@ void prefill_kernel(PrefillArgs a)
     lsum += __shfl_xor(lsum, 32, 64);
     if (!rvalid)
         return;
+    // the row's output index and lane half again, from an opaque copy of the
+    // thread id: held across the tiles, they were spilled (DMA variants)
+    uint64_t qrow_e = qrow;
+    int jh_e = jh;
+    if constexpr (T::DMA) {
+        int te = tid;
+        asm volatile("" : "+v"(te));
+        const int re = r0 + (te >> 6) * 32 + (te & 31);
+        qrow_e = (uint64_t)(tok0 + re / REP) * a.nh + (int)g * REP + re % REP;
+        jh_e = (te >> 5) & 1;
+    }
     if (partial) {
         // split-KV chunk 0 of the row: unnormalised sums, the running max
         // (base 2) and the sum of weights, as the decode kernel's partials
-        float *pr = a.part + qrow * a.max_chunks * (DV + 2);
+        float *pr = a.part + qrow_e * a.max_chunks * (DV + 2);
 #pragma unroll
         for (int dt = 0; dt < 2; dt++) {
             const float16v &acc = dt == 0 ? acc0 : acc1;
 #pragma unroll
             for (int i = 0; i < 16; i++)
-                pr[32 * dt + 8 * (i >> 2) + 4 * jh + (i & 3)] = acc[i];
+                pr[32 * dt + 8 * (i >> 2) + 4 * jh_e + (i & 3)] = acc[i];
         }
-        if (jh == 0) {
+        if (jh_e == 0) {
             pr[DV] = m;
             pr[DV + 1] = lsum;
         }
         return;
     }
     const float inv = 1.0f / lsum;
-    float *o = a.out + qrow * DV;
-    const float *gt = a.gate ? a.gate + qrow * DV : nullptr;
+    float *o = a.out + qrow_e * DV;
+    const float *gt = a.gate ? a.gate + qrow_e * DV : nullptr;
 #pragma unroll
     for (int dt = 0; dt < 2; dt++) {
 #pragma unroll
         for (int i4 = 0; i4 < 4; i4++) {
-            const int d0 = 32 * dt + 8 * i4 + 4 * jh;
+            const int d0 = 32 * dt + 8 * i4 + 4 * jh_e;
             float4 z;
             const float16v &acc = dt == 0 ? acc0 : acc1;
             z.x = acc[4 * i4 + 0] * inv;
@@ -1351,11 +1487,17 @@ static void launch_pf(dim3 grid, int waves, uint32_t lds, const PrefillArgs &a, 
 }
 
 // Largest tile table (bytes of dynamic LDS) that keeps a work-group size's
-// residency: 160 KiB per CU over its resident work-groups (4 waves per SIMD
-// for 8-wave groups, 3 otherwise), less two tile buffers (at most 19 KiB).
-uint32_t pf_tab_max_bytes(int waves)
+// residency: 160 KiB per CU over its resident work-groups, less two tile
+// buffers. 8-wave groups and the 2- and 4-wave ones with direct-loaded
+// tiles (dma: fp16, qk 64; 16 KiB of buffers) run 4 waves per SIMD; the
+// others 3. Staged buffers take at most 19 KiB.
+uint32_t pf_tab_max_bytes(int waves, bool dma)
 {
-    return waves >= 8 ? 48u << 10 : waves == 4 ? 32u << 10 : 7u << 10;
+    if (waves >= 8)
+        return 48u << 10;   // staged tiles: 19 KiB of buffers
+    if (dma)
+        return waves == 4 ? 22u << 10 : 3584u;
+    return waves == 4 ? 32u << 10 : 7u << 10;
 }
 
 hipError_t launch_prefill(const Geo &g, const PrefillArgs &a, int waves, hipStream_t s)
@@ -1368,7 +1510,7 @@ hipError_t launch_prefill(const Geo &g, const PrefillArgs &a, int waves, hipStre
     dim3 grid(a.n_items);     // n_items: a multiple of 8 (padded with empty items)
     // a table of a.tab_cap tiles when the host sized one that fits
     const uint32_t tab_bytes = a.tab_cap * 16u;
-    const bool tab = a.tab_cap > 0 && tab_bytes <= pf_tab_max_bytes(waves);
+    const bool tab = a.tab_cap > 0 && tab_bytes <= pf_tab_max_bytes(waves, es == 2 && g.dk == 64 && g.dv == 64);
 #define X(ES, DK, DV, REP)                                                                      \
     if (es == ES && g.dk == DK && g.dv == DV && g.rep == REP) {                                 \
         if (tab)                                                                                 \
