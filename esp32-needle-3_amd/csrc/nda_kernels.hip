@@ -297,7 +297,7 @@ __device__ __forceinline__ void merge_state(float &m, float &l, float *acc, int 
 // the group): each reads the kv-head's K/V, so the per-lane state of a wide
 // GQA group (heads x head dim) divides by HS and more units fit a CU.
 // RT: head dims read at run time (a.pg.dk, a.pg.dv), DK / DV the padding.
-template <int ES, int DK, int DV, int REP, int G, int NP, int NW, int HS, bool RT>
+template <int ES, int DK, int DV, int REP, int G, int NP, int NW, int HS, bool RT, bool PRE = false>
 __global__ __launch_bounds__(64 * NW) void attend_kernel(AttnArgs a)
 {
     using C = AttnCfg<ES, DK, DV, REP, G, NP, NW>;
@@ -358,11 +358,13 @@ __global__ __launch_bounds__(64 * NW) void attend_kernel(AttnArgs a)
     }
 
     // A shared-prefix pass left chunk 0 (the prefix's softmax state) and this
-    // is the row's only other chunk: the epilogue merges the two. Wave 0's
-    // first lane group requests chunk 0 now, so that its latency overlaps
-    // the row's own loads rather than ending the work-group (REP <= 2: its
-    // REP * (EV + 2) registers).
-    constexpr bool PRE0 = REP <= 2;
+    // is the row's only other chunk: the epilogue merges the two. In the
+    // launches after such a pass (PRE), wave 0's first lane group requests
+    // chunk 0 now, so that its latency overlaps the row's own loads rather
+    // than ending the work-group (REP <= 2: its REP * (EV + 2) registers,
+    // which other launches do not carry: held by the 4096-row decode's
+    // kernel they cost it a wave per SIMD and 2-4%).
+    constexpr bool PRE0 = PRE && REP <= 2;
     const bool merge0 = a.chunk_lo == 1 && nchunks == 2;
     float p0[PRE0 ? REP : 1][C::EV + 2] = {};
     if constexpr (PRE0) {
@@ -925,14 +927,14 @@ constexpr int att_hs()
 template <int ES, int REP>
 constexpr int lanes_rt() { return 8; }
 
-template <int ES, int DK, int DV, int REP, int HS, int NW, bool RT>
+template <int ES, int DK, int DV, int REP, int HS, int NW, bool RT, bool PRE = false>
 static void launch_attend_hs(const AttnArgs &a, hipStream_t s)
 {
     constexpr int R = REP / HS;
     constexpr int G = RT ? lanes_rt<ES, R>() : lanes_per_pos<ES, DK, R>();
     const dim3 grid(a.rows * a.pg.nkv * HS, a.max_chunks - a.chunk_lo);
-    hipLaunchKernelGGL((attend_kernel<ES, DK, DV, R, G, att_np<ES, R>(), NW, HS, RT>), grid, dim3(64 * NW), 0, s,
-                       a);
+    hipLaunchKernelGGL((attend_kernel<ES, DK, DV, R, G, att_np<ES, R>(), NW, HS, RT, PRE>), grid, dim3(64 * NW), 0,
+                       s, a);
 }
 
 template <int ES, int DK, int DV, int REP, bool RT>
@@ -942,8 +944,15 @@ static void launch_attend_geo(const AttnArgs &a, bool long_items, hipStream_t s)
         launch_attend_hs<ES, DK, DV, REP, att_hs<REP>(), 1, RT>(a, s);
     else if (long_items)
         launch_attend_hs<ES, DK, DV, REP, 1, att_nw<REP>(true), RT>(a, s);
-    else
+    else {
+        if constexpr (REP <= 2) {
+            if (a.chunk_lo == 1) {      // after a shared-prefix pass: chunk 0 requested early
+                launch_attend_hs<ES, DK, DV, REP, 1, att_nw<REP>(false), RT, true>(a, s);
+                return;
+            }
+        }
         launch_attend_hs<ES, DK, DV, REP, 1, att_nw<REP>(false), RT>(a, s);
+    }
 }
 
 // Shapes outside NDA_FOR_GEOMETRIES: dims padded to 64, one instance per
