@@ -744,6 +744,19 @@ def test_prefill_mfma_long_context_outliers():
     assert worst <= TOL, worst
 
 
+@pytest.mark.parametrize("hist,ntok", [([6000], [20]), ([8000], [40]), ([8000], [100])])
+def test_prefill_small_groups_direct_and_staged_tiles(hist, ntok):
+    """fp16 qk-64 chunks of at most 64 rows (2-wave groups) and 65-255 rows
+    (4-wave groups) load their key tiles straight into LDS when the tile
+    table fits the LDS their residency leaves (224 tiles at 2 waves), and
+    stage them through registers without a table otherwise: 6000 + 20
+    positions (189 tiles, direct), 8000 + 40 (252 tiles, staged), 8000 + 100
+    at 4 waves (direct), with 8-sigma keys."""
+    say("prefill small groups", hist, ntok)
+    worst, _ = _prefill_case(O.KV_F16, 8, 8, 64, hist, ntok, seed=31 + ntok[0], outlier_p=1e-3)
+    assert worst <= TOL, worst
+
+
 def test_prefill_mfma_matches_valu_path():
     say("prefill mfma vs valu")
     hist, ntok = [17, 300], [90, 45]
