@@ -361,7 +361,17 @@ __global__ __launch_bounds__(512) void cq_prepare_split_reg_kernel(CqPrepSplitAr
             for (int h = 0; h < NH; h++)
 #pragma unroll
                 for (int s = 0; s < 8; s++) {
-                    const float w = __shfl_xor(v[h][s], m, 64);
+                    // lg is fixed in each unrolled stage: one cross-lane
+                    // operation of distance m
+                    float w;
+                    switch (lg) {
+                    case 3: w = xor_lanes<1>(v[h][s], lane); break;
+                    case 4: w = xor_lanes<2>(v[h][s], lane); break;
+                    case 5: w = xor_lanes<4>(v[h][s], lane); break;
+                    case 6: w = xor_lanes<8>(v[h][s], lane); break;
+                    case 7: w = xor_lanes<16>(v[h][s], lane); break;
+                    default: w = xor_lanes<32>(v[h][s], lane); break;
+                    }
                     v[h][s] = fmaf(sg, v[h][s], w);     // lower lane: v + w; upper: w - v
                 }
         } else {

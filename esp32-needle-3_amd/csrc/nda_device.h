@@ -40,12 +40,51 @@ __device__ __forceinline__ int own_slot(const SeqDev &s, int p, int window)
     return s.n_sink + (p - s.n_sink) % (window - s.n_sink);
 }
 
+// v of lane (lane ^ M) of the wave, on VALU cross-lane operations rather
+// than through the LDS crossbar (ds_bpermute): DPP within each 16-lane row
+// (quad permutes for 1 and 2, the row shifted by 4 either way for 4, the row
+// rotated by 8 for 8), row swaps for 16 and 32 (each returns (own, partner)
+// in the lanes whose bit M is clear, (partner, own) in the others).
+template <int M>
+__device__ __forceinline__ float xor_lanes(float v, int lane)
+{
+    static_assert(M == 1 || M == 2 || M == 4 || M == 8 || M == 16 || M == 32, "lane distance");
+    const int x = __builtin_bit_cast(int, v);
+    int r;
+    if constexpr (M == 1) {
+        r = __builtin_amdgcn_update_dpp(0, x, 0xB1, 0xF, 0xF, true);    // quad_perm [1, 0, 3, 2]
+    } else if constexpr (M == 2) {
+        r = __builtin_amdgcn_update_dpp(0, x, 0x4E, 0xF, 0xF, true);    // quad_perm [2, 3, 0, 1]
+    } else if constexpr (M == 4) {
+        const int dn = __builtin_amdgcn_update_dpp(0, x, 0x114, 0xF, 0xF, true);   // row_shr:4, lane - 4
+        const int up = __builtin_amdgcn_update_dpp(0, x, 0x104, 0xF, 0xF, true);   // row_shl:4, lane + 4
+        r = (lane & 4) ? dn : up;
+    } else if constexpr (M == 8) {
+        r = __builtin_amdgcn_update_dpp(0, x, 0x128, 0xF, 0xF, true);   // row_ror:8
+    } else if constexpr (M == 16) {
+        const auto sw = __builtin_amdgcn_permlane16_swap(x, x, false, false);
+        r = (lane & 16) ? (int)sw[0] : (int)sw[1];
+    } else {
+        const auto sw = __builtin_amdgcn_permlane32_swap(x, x, false, false);
+        r = (lane & 32) ? (int)sw[0] : (int)sw[1];
+    }
+    return __builtin_bit_cast(float, r);
+}
+
+__device__ __forceinline__ int lane_id()
+{
+    return (int)__builtin_amdgcn_mbcnt_hi(~0u, __builtin_amdgcn_mbcnt_lo(~0u, 0u));
+}
+
 __device__ __forceinline__ float wave_max(float x)
 {
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1)
-        x = fmaxf(x, __shfl_xor(x, o, 64));
-    return x;
+    const int lane = lane_id();
+    x = fmaxf(x, xor_lanes<32>(x, lane));
+    x = fmaxf(x, xor_lanes<16>(x, lane));
+    x = fmaxf(x, xor_lanes<8>(x, lane));
+    x = fmaxf(x, xor_lanes<4>(x, lane));
+    x = fmaxf(x, xor_lanes<2>(x, lane));
+    return fmaxf(x, xor_lanes<1>(x, lane));
 }
 
 // One wave per (row, kv-head), lane = element. INT8: absmax over the row,
